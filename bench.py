@@ -1,0 +1,227 @@
+"""Benchmark: ms per CP-ALS iteration + sparse MTTKRP HBM GB/s, order-3 R=128.
+
+One "step" = one full ALS iteration (3 x (Gram/Hadamard, MTTKRP, solve,
+normalise), Gram fit) of BASELINE config 3 (12092 x 9184 x 28818, 76.9 M nnz,
+Zipf(1.1), log-normal values, R = 128, dense threshold 0.03) with every input
+resident in HBM.  Prints ONE JSON line on stdout; progress goes to stderr.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--R 128]
+                  [--cpu-iters 1] [--no-cpu]
+
+The CPU baseline runs the CPU oracle's OpenMP ALS (the reference's semantics)
+on the same row-sorted views, copied from the device, for --cpu-iters
+iterations on the full tensor.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor figure
+
+CONFIG_SPEC = {
+    1: dict(R=32, thr=0.03, name="cfg1: order-3 256^3 CP-rank-8 + noise, p=0.9 (~15.1M nnz)"),
+    2: dict(R=32, thr=0.03, name="cfg2: order-3 512^3, 2000 16^3 blocks + 2e-4 background"),
+    3: dict(R=128, thr=0.03,
+            name="cfg3: order-3 12092x9184x28818, 76.9M nnz, Zipf(1.1), log-normal values"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gather_bytes(nnz: int, dim_n: int, R: int, N: int = 3) -> float:
+    """No-reuse gather model: COO stream + (N-1) factor rows per nnz + output rows."""
+    return nnz * (4 * N + 8) + nnz * (N - 1) * R * 8 + dim_n * R * 8
+
+
+def load_traffic(workload: str):
+    """HBM bytes per sparse-kernel launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "mttkrp_sparse3_cfg3_pmc.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+        if d.get("workload") != workload:
+            return None
+        return d.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIG_SPEC))
+    ap.add_argument("--R", type=int, default=0)
+    ap.add_argument("--cpu-iters", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here "
+              "has one GPU); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import cptc_amd as ca
+
+    if ca.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    spec = CONFIG_SPEC[args.config]
+    R = args.R or spec["R"]
+    thr = spec["thr"]
+
+    t0 = time.perf_counter()
+    t = ca.synth_config(args.config, 42)
+    log(f"generated config {args.config}: dims {t.dims} nnz {t.nnz} in "
+        f"{time.perf_counter() - t0:.1f} s")
+
+    t0 = time.perf_counter()
+    h = ca.Als3(t, R=R, threshold=thr)
+    info = h.info
+    setup_s = time.perf_counter() - t0
+    use_mfma = bool(info.use_mfma) and int(info.num_dense_tiles) > 0
+    log(f"setup (upload, CADR, partition, views) {setup_s:.2f} s: tiles {info.num_dense_tiles} "
+        f"dense_nnz {info.dense_nnz} sparse_nnz {info.sparse_nnz} avg_fill {info.avg_fill:.4f} "
+        f"fill_min {info.fill_min:.4f} -> {'MFMA+FP64' if use_mfma else 'FP64'}; "
+        f"segments {list(info.segments)} CUs {info.num_cus}")
+
+    if args.warmup:
+        h.run(args.warmup)
+        log(f"warmup {args.warmup} iterations done")
+    h.kernel_times(reset=True)
+
+    # timed region: exactly K ALS iterations; the driver's stream is
+    # synchronised at the end of each iteration (fit readback)
+    try:
+        import torch
+        torch.cuda.synchronize()
+    except Exception:  # torch is plumbing only
+        torch = None
+    t0 = time.perf_counter()
+    fits, ms_iter, ms_mtt = h.run(args.steps)
+    if torch is not None:
+        torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    sp_ms, mt_ms, kit = h.kernel_times(reset=True)
+    assert kit == args.steps
+    log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter (host wall), event median "
+        f"{float(np.median(ms_iter)):.3f} ms, MTTKRP median {float(np.median(ms_mtt)):.3f} ms, "
+        f"fit {fits[-1]:.6f}")
+
+    dims = t.dims
+    nnz = t.nnz
+    # headline: all MTTKRP launches of an iteration vs the gather model over all nnz
+    b_iter = sum(gather_bytes(nnz, dims[m], R) for m in range(3))
+    mtt_ms_iter = float(np.sum(mt_ms)) / kit
+    mtt_gbs = b_iter / (mtt_ms_iter * 1e-3) / 1e9
+    # dominant kernel: the FP64 residual-view sparse MTTKRP, per launch (one mode)
+    snnz = int(info.sparse_nnz)
+    b_launch = [gather_bytes(snnz, dims[m], R) for m in range(3)]
+    launch_ms = [float(sp_ms[m]) / kit for m in range(3)]
+    achieved = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
+    workload = f"cfg{args.config}-R{R}"
+    traffic = load_traffic(workload)
+
+    cpu = None
+    if not args.no_cpu and args.cpu_iters > 0:
+        cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma)
+
+    line = {
+        "metric": "ms per ALS iteration + sparse MTTKRP HBM GB/s (% of peak), order-3 R=128",
+        "value": round(ms_per_step, 4),
+        "unit": "ms/iteration",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64" if not use_mfma else "f64 (dense tiles: fp32 MFMA, f64 epilogue)",
+        "data": "synthetic (deterministic generator, seed 42)",
+        "config": {
+            "workload": spec["name"] if R == spec["R"] else f"{spec['name']} (R={R})",
+            "R": R, "nnz": nnz, "dims": list(dims), "dense_threshold": thr,
+            "dense_tiles": int(info.num_dense_tiles), "dense_nnz": int(info.dense_nnz),
+            "sparse_nnz": snnz, "path": "mfma+fp64" if use_mfma else "fp64",
+            "parallelism": "single GPU",
+        },
+        "ms_per_iter_event_median": round(float(np.median(ms_iter)), 4),
+        "mttkrp_ms_per_iter": round(mtt_ms_iter, 4),
+        "mttkrp_gather_model_GBs": round(mtt_gbs, 1),
+        "mttkrp_frac_of_hbm_peak": round(mtt_gbs / HBM_PEAK_GBS, 4),
+        "fit_last": float(fits[-1]),
+        "roofline": {
+            "kernel": "mttkrp3_seg_kernel (FP64 residual view), per launch = one mode",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "launch_ms": [round(x, 4) for x in launch_ms],
+            "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
+        },
+        "cpu_baseline": cpu,
+    }
+    h.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(ca, h, t, R, iters, use_mfma):
+    """The oracle's OpenMP ALS over the device-built views (test infrastructure
+    used as the CPU baseline only), timed on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle", "_build"))
+    import cptc_oracle as orc
+
+    t0 = time.perf_counter()
+    views = [h.view(0, m) for m in range(3)]
+    dv = None
+    tiles = None
+    if int(h.info.num_dense_tiles) > 0:
+        if use_mfma:
+            tl = h.tiles()
+            tl["cutoff"] = int(h.info.dense_cutoff)
+            tiles = tl
+        else:
+            dv = [h.view(1, m) for m in range(3)]
+    F = [h.factor(m).ravel() for m in range(3)]
+    lam = h.lam()
+    x_sq = float(np.sum(t.val * t.val))
+    o = orc.Als3(views, dv, tiles, x_sq, t.dims, R, F[0], F[1], F[2], lam)
+    del views, dv, tiles
+    threads = orc.max_threads()
+    log(f"CPU baseline: data staged in {time.perf_counter() - t0:.1f} s; running {iters} "
+        f"ALS iteration(s) with {threads} OpenMP threads")
+    _, ms, mm = o.iterate(iters)
+    ms = [float(x) for x in ms]
+    log(f"CPU baseline: {ms} ms/iter (MTTKRP {[round(float(x), 1) for x in mm]} ms)")
+    return {
+        "value": round(float(np.mean(ms)), 1),
+        "unit": "ms/iteration",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{iters} full ALS iteration(s) of the same workload (all {t.nnz} nnz, R={R}), "
+                  f"starting from the GPU run's factors; views built on the GPU and copied to host",
+        "mttkrp_ms": round(float(np.mean(mm)), 1),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

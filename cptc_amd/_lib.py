@@ -1,0 +1,139 @@
+"""ctypes binding of libcptc.so (the C ABI declared in include/cptc_hip.h).
+
+The library is loaded from the package's own ``lib/`` directory; if it is
+missing the import fails loudly — there is no Python or CPU fallback for any
+entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libcptc.so")
+CLI_PATH = os.path.join(_HERE, "bin", "cptc_opt")
+
+CPTC_MAX_MODES = 8
+CPTC_SEG = 1024
+OK, ERR_ARG, ERR_HIP, ERR_UNSUPPORTED, ERR_IO, ERR_NUMERIC, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
+VAL_LOGNORMAL, VAL_NORMAL, VAL_POISSON1P2 = 0, 1, 2
+
+
+class CptcError(RuntimeError):
+    def __init__(self, where: str, rc: int, msg: str):
+        super().__init__(f"{where} failed ({rc}): {msg}")
+        self.rc = rc
+
+
+class Coo(C.Structure):
+    _fields_ = [
+        ("nmodes", C.c_int),
+        ("dims", C.c_uint64 * CPTC_MAX_MODES),
+        ("nnz", C.c_uint64),
+        ("idx", C.POINTER(C.c_uint32)),
+        ("val", C.POINTER(C.c_double)),
+    ]
+
+
+class Als3Opts(C.Structure):
+    _fields_ = [
+        ("R", C.c_int),
+        ("threshold", C.c_double),
+        ("path", C.c_int),
+        ("fill_min", C.c_double),
+        ("skip_dense", C.c_int),
+        ("skip_sparse", C.c_int),
+        ("cadr", C.c_int),
+        ("seed", C.c_uint64),
+        ("verbose", C.c_int),
+    ]
+
+
+class Als3Info(C.Structure):
+    _fields_ = [
+        ("dims", C.c_uint64 * 3),
+        ("nnz", C.c_uint64),
+        ("sparse_nnz", C.c_uint64),
+        ("dense_nnz", C.c_uint64),
+        ("num_dense_tiles", C.c_int64),
+        ("dense_cutoff", C.c_int),
+        ("avg_fill", C.c_double),
+        ("fill_min", C.c_double),
+        ("use_mfma", C.c_int),
+        ("segments", C.c_uint64 * 3),
+        ("dense_view_segments", C.c_uint64 * 3),
+        ("num_cus", C.c_int),
+    ]
+
+
+_P = C.c_void_p
+_I = C.c_int
+_Z = C.c_size_t
+_D = C.c_double
+_U64 = C.c_uint64
+
+# name -> (restype, argtypes); every symbol declared in include/cptc_hip.h
+SIGNATURES = {
+    "cptc_coo_free": (None, [C.POINTER(Coo)]),
+    "cptc_version": (C.c_char_p, []),
+    "cptc_last_error": (C.c_char_p, []),
+    "cptc_device_count": (_I, []),
+    "cptc_tns_load3": (_I, [C.c_char_p, C.POINTER(Coo)]),
+    "cptc_tns_probe_nmodes": (_I, [C.c_char_p]),
+    "cptc_tns_load_generic": (_I, [C.c_char_p, C.POINTER(Coo)]),
+    "cptc_tns_write": (_I, [C.c_char_p, C.POINTER(Coo)]),
+    "cptc_synth_config": (_I, [_I, _U64, C.POINTER(Coo)]),
+    "cptc_synth_zipf": (_I, [_I, _P, _P, _U64, _I, _U64, C.POINTER(Coo)]),
+    "cptc_synth_lowrank3": (_I, [_U64, _I, _D, _D, _U64, C.POINTER(Coo)]),
+    "cptc_synth_blocks3": (_I, [_U64, _I, _D, _D, _D, _U64, C.POINTER(Coo)]),
+    "cptc_synth_units5": (_I, [_P, _I, _D, _D, _U64, _I, _U64, C.POINTER(Coo)]),
+    "cptc_cadr3": (_I, [_P, _P, _P, _Z, _P, _P, _P, _P, _I]),
+    "cptc_unpermute_factor": (_I, [_P, _P, _P, _Z, _I, _P]),
+    "cptc_mttkrp_sparse3": (_I, [_I, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _P]),
+    "cptc_mttkrp_dense_tiles3": (_I, [_I, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
+    "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),
+    "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
+    "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
+    "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),
+    "cptc_colnorms": (_I, [_P, _Z, _I, _P, _P]),
+    "cptc_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P]),
+    "cptc_fit_gram": (_I, [_P, _P, _Z, _P, _P, _I, _I, _P, _P]),
+    "cptc_residual3_view": (_I, [_P, _P, _Z, _P, _P, _P, _P, _I, _P, _P]),
+    "cptc_residual3_tiles": (_I, [_P, _P, _P, _P, _Z, _P, _P, _P, _P, _I, _P, _P]),
+    "cptc_als3_default_opts": (None, [C.POINTER(Als3Opts)]),
+    "cptc_als3_create": (_I, [C.POINTER(Coo), C.POINTER(Als3Opts), C.POINTER(_P)]),
+    "cptc_als3_info_get": (_I, [_P, C.POINTER(Als3Info)]),
+    "cptc_als3_run": (_I, [_P, _I, _P, _P, _P]),
+    "cptc_als3_mttkrp": (_I, [_P, _I, _P]),
+    "cptc_als3_kernel_times": (_I, [_P, _P, C.POINTER(_I), _I]),
+    "cptc_als3_factor": (_I, [_P, _I, _I, _P]),
+    "cptc_als3_set_factor": (_I, [_P, _I, _P]),
+    "cptc_als3_lambda": (_I, [_P, _P]),
+    "cptc_als3_residual": (_I, [_P, C.POINTER(_D), C.POINTER(_D)]),
+    "cptc_als3_perm": (_I, [_P, _I, _P]),
+    "cptc_als3_view": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "cptc_als3_tiles": (_I, [_P, _P, _P, _P, _P]),
+    "cptc_als3_destroy": (_I, [_P]),
+}
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libcptc.so not built at {LIB_PATH}; run `python -c 'import __graft_entry__ as g; g.build()'`"
+        )
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(rc: int, where: str) -> None:
+    if rc != OK:
+        raise CptcError(where, rc, lib.cptc_last_error().decode(errors="replace"))

@@ -1,0 +1,601 @@
+// Order-3 CP-ALS driver: setup (CADR relabel, factor init, hybrid partition,
+// row-sorted views, fill-rate path selection) and the ALS iteration.
+//
+// Follows main.cu:136-672 (setup and selection) and als.cu:362-821 (the
+// iteration).  MI355X-native differences, none of which changes a result
+// beyond floating-point reassociation:
+//   * one HIP stream per driver; MTTKRP launches (MFMA tiles, FP64 residual,
+//     FP64 dense view) are queued back to back with no host synchronisation
+//     inside an iteration; the host waits once per iteration for the fit;
+//   * Grams are cached per mode and refreshed right after that mode's update
+//     (the reference recomputes the same matrices from the same factors);
+//   * the solve is an on-device pseudoinverse (Cholesky inverse with an exact
+//     Jacobi fallback) instead of cuSOLVER gesvdj.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "cptc_hip.h"
+#include "hip_util.hpp"
+#include "layout.hpp"
+
+namespace cptc {
+
+namespace {
+
+int env_flag(const char* name)
+{
+    const char* v = std::getenv(name);
+    return v != nullptr ? 1 : 0;
+}
+
+struct Als3
+{
+    cptc_als3_opts o{};
+    int R = 0;
+    uint64_t dims[3] = {0, 0, 0};
+    size_t nnz = 0;
+    hipStream_t s = nullptr;
+    int num_cus = 0;
+
+    std::vector<int32_t> perm[3];
+    int32_t* d_perm[3] = {nullptr, nullptr, nullptr};
+    DevPartition3 part;
+    DevViews3 views, dviews;
+    float* d_tile_f32 = nullptr;
+    bool use_mfma = false;
+    double fill_min = 0.08, avg_fill = 0.0;
+    int64_t tiles_total = 0;
+    uint64_t dense_nnz_total = 0;
+    bool skip_dense = false, skip_sparse = false;
+
+    double* d_F = nullptr;  // [A | B | C]
+    double* F[3] = {nullptr, nullptr, nullptr};
+    double* d_lambda = nullptr;
+    double* d_G = nullptr;  // 3 x R x R
+    bool gram_ok[3] = {false, false, false};
+    double* d_FtF = nullptr;
+    double* d_FtV = nullptr;
+    double* d_norms = nullptr;
+    double* d_scal = nullptr;  // fit iprod/model2 (2) + residual (2)
+    double x_sq = 0.0;
+    hipEvent_t ev[8] = {};
+    // around the FP64 residual-view kernel of each mode, accumulated
+    hipEvent_t kev[6] = {};
+    double k_sparse_ms[3] = {0, 0, 0}, k_mttkrp_ms[3] = {0, 0, 0};
+    int k_iters = 0;
+    bool timing_kernels = false;
+
+    double* G(int m) const { return d_G + size_t(m) * R * R; }
+};
+
+int mttkrp_launch(Als3& h, int mode)
+{
+    const int R = h.R;
+    const uint64_t dim = h.dims[mode];
+    CPTC_HIP(hipMemsetAsync(h.d_FtV, 0, dim * size_t(R) * sizeof(double), h.s));
+    const double* A = h.F[0];
+    const double* B = h.F[1];
+    const double* C = h.F[2];
+    if (h.use_mfma && !h.skip_dense && h.part.ntiles > 0)
+        CPTC_TRY(cptc_mttkrp_dense_tiles3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
+                                          A, B, C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
+                                          int(h.dims[2]), h.s));
+    if (!h.skip_sparse)
+    {
+        const double* F1 = mode == 0 ? B : A;
+        const double* F2 = mode == 2 ? B : C;
+        for (const DevViews3* v : {&h.views, &h.dviews})
+        {
+            if (!v->ready) continue;
+            const bool timed = h.timing_kernels && v == &h.views;
+            if (timed) CPTC_HIP(hipEventRecord(h.kev[2 * mode], h.s));
+            CPTC_TRY(cptc_mttkrp_sparse3(mode, v->d_coords[mode], v->d_vals[mode],
+                                         v->d_blk_row[mode], v->d_blk_start[mode],
+                                         v->d_blk_cnt[mode], v->nseg[mode], F1, F2, h.d_FtV, R,
+                                         h.s));
+            if (timed) CPTC_HIP(hipEventRecord(h.kev[2 * mode + 1], h.s));
+        }
+    }
+    return CPTC_OK;
+}
+
+// ||X - Xhat||^2 and ||X||^2 over every stored element into d_scal[2..3]
+int residual_launch(Als3& h, bool with_lambda)
+{
+    double* out = h.d_scal + 2;
+    CPTC_HIP(hipMemsetAsync(out, 0, 2 * sizeof(double), h.s));
+    const double* lam = with_lambda ? h.d_lambda : nullptr;
+    for (const DevViews3* v : {&h.views, &h.dviews})
+        if (v->ready)
+            CPTC_TRY(cptc_residual3_view(v->d_coords[0], v->d_vals[0], v->nnz, h.F[0], h.F[1],
+                                         h.F[2], lam, h.R, out, h.s));
+    if (h.use_mfma && h.part.ntiles > 0)
+        CPTC_TRY(cptc_residual3_tiles(h.part.d_tiles4, h.part.d_pool_off, h.part.d_pool_lid,
+                                      h.part.d_pool_val, size_t(h.part.ntiles), h.F[0], h.F[1],
+                                      h.F[2], lam, h.R, out, h.s));
+    return CPTC_OK;
+}
+
+void destroy(Als3* h)
+{
+    if (!h) return;
+    if (h->s) (void)hipStreamSynchronize(h->s);
+    free_partition(h->part);
+    free_views(h->views);
+    free_views(h->dviews);
+    for (auto& p : h->d_perm)
+        if (p) (void)hipFree(p);
+    for (void* p : {(void*)h->d_tile_f32, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
+                    (void*)h->d_FtF, (void*)h->d_FtV, (void*)h->d_norms, (void*)h->d_scal})
+        if (p) (void)hipFree(p);
+    for (auto& e : h->ev)
+        if (e) (void)hipEventDestroy(e);
+    for (auto& e : h->kev)
+        if (e) (void)hipEventDestroy(e);
+    if (h->s) (void)hipStreamDestroy(h->s);
+    delete h;
+}
+
+int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
+{
+    cptc_als3_opts o;
+    cptc_als3_default_opts(&o);
+    if (opts) o = *opts;
+    h->o = o;
+    CPTC_REQUIRE(coo && coo->nmodes == 3, CPTC_ERR_ARG, "cptc_als3_create: order-3 COO expected");
+    CPTC_REQUIRE(o.R >= 1 && o.R <= 512, CPTC_ERR_ARG, "cptc_als3_create: R %d not in 1..512", o.R);
+    h->R = o.R;
+    for (int m = 0; m < 3; ++m) h->dims[m] = coo->dims[m];
+    h->nnz = coo->nnz;
+    for (int m = 0; m < 3; ++m)
+        CPTC_REQUIRE(h->dims[m] >= 1 && h->dims[m] < (uint64_t(1) << 31), CPTC_ERR_ARG,
+                     "cptc_als3_create: dim %d = %llu", m, (unsigned long long)h->dims[m]);
+    CPTC_REQUIRE(coo->nnz <= size_t(UINT32_MAX), CPTC_ERR_UNSUPPORTED,
+                 "cptc_als3_create: nnz %llu exceeds uint32 range", (unsigned long long)coo->nnz);
+    CPTC_REQUIRE(coo->nnz == 0 || (coo->idx && coo->val), CPTC_ERR_ARG,
+                 "cptc_als3_create: null COO arrays");
+    // every index must lie inside its mode (the device layout kernels index by it)
+    for (int m = 0; m < 3; ++m)
+    {
+        const uint32_t* c = coo->idx + size_t(m) * coo->nnz;
+        uint64_t mx = 0;
+        #pragma omp parallel for reduction(max : mx) schedule(static)
+        for (int64_t e = 0; e < int64_t(coo->nnz); ++e) mx = std::max<uint64_t>(mx, c[e]);
+        CPTC_REQUIRE(coo->nnz == 0 || mx < h->dims[m], CPTC_ERR_ARG,
+                     "cptc_als3_create: mode %d index %llu >= dim %llu", m,
+                     (unsigned long long)mx, (unsigned long long)h->dims[m]);
+    }
+    CPTC_HIP(hipStreamCreateWithFlags(&h->s, hipStreamNonBlocking));
+    for (auto& e : h->ev) CPTC_HIP(hipEventCreate(&e));
+    for (auto& e : h->kev) CPTC_HIP(hipEventCreate(&e));
+    int dev = 0;
+    CPTC_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop{};
+    CPTC_HIP(hipGetDeviceProperties(&prop, dev));
+    h->num_cus = prop.multiProcessorCount;
+
+    // 1. COO -> device, CADR (main.cu:176-192)
+    DevCoo3 c;
+    CPTC_TRY(upload_coo3(coo->idx, coo->val, coo->nnz, coo->dims, c, h->s));
+    if (o.cadr)
+    {
+        const int rc = cadr3_device(c, h->perm, h->d_perm, 1, h->s);
+        if (rc != CPTC_OK)
+        {
+            free_coo(c);
+            return rc;
+        }
+    }
+    else
+    {
+        for (int m = 0; m < 3; ++m)
+        {
+            h->perm[m].resize(h->dims[m]);
+            for (uint64_t x = 0; x < h->dims[m]; ++x) h->perm[m][x] = int32_t(x);
+            CPTC_HIP(hipMalloc(&h->d_perm[m], h->dims[m] * sizeof(int32_t)));
+            CPTC_HIP(hipMemcpyAsync(h->d_perm[m], h->perm[m].data(), h->dims[m] * sizeof(int32_t),
+                                    hipMemcpyHostToDevice, h->s));
+        }
+    }
+
+    // 2. factors in the relabelled space (common.cu:66-123, main.cu:228-264)
+    const int R = h->R;
+    const size_t tot = (h->dims[0] + h->dims[1] + h->dims[2]) * size_t(R);
+    {
+        std::vector<double> hf(tot);
+        std::mt19937 gen(unsigned(o.seed));
+        std::uniform_real_distribution<double> dis(0.0, 1.0);
+        for (size_t x = 0; x < tot; ++x) hf[x] = dis(gen);
+        CPTC_HIP(hipMalloc(&h->d_F, tot * sizeof(double)));
+        CPTC_HIP(hipMemcpy(h->d_F, hf.data(), tot * sizeof(double), hipMemcpyHostToDevice));
+        h->F[0] = h->d_F;
+        h->F[1] = h->F[0] + h->dims[0] * R;
+        h->F[2] = h->F[1] + h->dims[1] * R;
+    }
+
+    // 3. hybrid partition, then the COO is released (main.cu:268-301)
+    {
+        const int rc = partition3_device(c, o.threshold, h->num_cus, h->part, h->s);
+        free_coo(c);
+        CPTC_TRY(rc);
+    }
+    h->tiles_total = h->part.ntiles;
+    h->dense_nnz_total = h->part.dense_nnz;
+
+    // 4. residual views (main.cu:304-314)
+    if (h->part.sparse_nnz > 0)
+        CPTC_TRY(views3_device(h->part.d_sp[0], h->part.d_sp[1], h->part.d_sp[2],
+                               h->part.d_sp_val, h->part.sparse_nnz, h->dims, h->views, h->s));
+    for (int m = 0; m < 3; ++m)
+        if (h->part.d_sp[m])
+        {
+            CPTC_HIP(hipFree(h->part.d_sp[m]));
+            h->part.d_sp[m] = nullptr;
+        }
+    if (h->part.d_sp_val)
+    {
+        CPTC_HIP(hipFree(h->part.d_sp_val));
+        h->part.d_sp_val = nullptr;
+    }
+
+    // 5. fill-rate path selection (main.cu:334-426): the SM-count scaling
+    // becomes a CU-count scaling, 0.11 / sqrt(CUs / 24) floored at 0.08
+    h->avg_fill = h->part.ntiles > 0
+                      ? double(h->part.dense_nnz) / (double(h->part.ntiles) * 4096.0)
+                      : 0.0;
+    if (o.fill_min >= 0.0)
+        h->fill_min = o.fill_min;
+    else if (const char* fm = std::getenv("ALS_FILL_MIN"))
+        h->fill_min = std::atof(fm);
+    else
+    {
+        h->fill_min = 0.11 / std::sqrt(double(h->num_cus) / 24.0);
+        if (h->fill_min < 0.08) h->fill_min = 0.08;
+    }
+    int path = o.path;
+    if (path < 0) path = env_flag("ALS_FORCE_WMMA") ? 1 : env_flag("ALS_FORCE_CUDA") ? 2 : 0;
+    h->use_mfma = (path == 1) ? true : (path == 2) ? false : (h->avg_fill >= h->fill_min);
+    h->skip_dense = o.skip_dense < 0 ? env_flag("ALS_NO_DENSE") != 0 : o.skip_dense != 0;
+    h->skip_sparse = o.skip_sparse < 0 ? env_flag("ALS_NO_SPARSE") != 0 : o.skip_sparse != 0;
+    if (h->part.ntiles > 0)
+    {
+        if (h->use_mfma)
+        {
+            CPTC_HIP(hipMalloc(&h->d_tile_f32, size_t(h->part.ntiles) * 4096 * sizeof(float)));
+            CPTC_TRY(cptc_dense_tiles_pack3(h->part.d_pool_lid, h->part.d_pool_val,
+                                            h->part.d_pool_off, size_t(h->part.ntiles),
+                                            h->d_tile_f32, h->s));
+        }
+        else
+        {
+            // FP64 dense views of the pool (partition.cu:2387-2517); the pool
+            // stays allocated for the layout getters but no kernel reads it
+            CPTC_TRY(dense_views3_device(h->part, h->dims, h->dviews, h->s));
+        }
+    }
+
+    // 6. ALS buffers (als.cu:389-430)
+    const size_t RR = size_t(R) * R;
+    const uint64_t maxdim = std::max({h->dims[0], h->dims[1], h->dims[2]});
+    CPTC_HIP(hipMalloc(&h->d_lambda, size_t(R) * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_G, 3 * RR * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_FtF, RR * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_FtV, maxdim * size_t(R) * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_norms, size_t(R) * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_scal, 4 * sizeof(double)));
+    {
+        std::vector<double> ones(size_t(R), 1.0);
+        CPTC_HIP(hipMemcpyAsync(h->d_lambda, ones.data(), size_t(R) * sizeof(double),
+                                hipMemcpyHostToDevice, h->s));
+    }
+    // ||X||^2 once (als.cu:439-450)
+    CPTC_TRY(residual_launch(*h, false));
+    double r2[2] = {0, 0};
+    CPTC_HIP(hipMemcpyAsync(r2, h->d_scal + 2, 2 * sizeof(double), hipMemcpyDeviceToHost, h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    h->x_sq = r2[1];
+    if (o.verbose)
+        std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
+                    "-> %s\n",
+                    (unsigned long long)h->dense_nnz_total, h->part.sparse_nnz,
+                    (long long)h->tiles_total, h->avg_fill, h->fill_min,
+                    h->use_mfma ? "MFMA tiles + FP64 residual" : "FP64 only");
+    return CPTC_OK;
+}
+
+int update_mode(Als3& h, int mode)
+{
+    const int R = h.R;
+    const uint64_t dim = h.dims[mode];
+    // solve (pinv) and divide by lambda, column norms, normalise + absorb,
+    // then refresh this mode's Gram (als.cu:480-517)
+    CPTC_TRY(cptc_solve_pinv(h.d_FtF, h.d_FtV, h.F[mode], dim, R, h.d_lambda, h.s));
+    CPTC_TRY(cptc_colnorms(h.F[mode], dim, R, h.d_norms, h.s));
+    CPTC_TRY(cptc_normalize_absorb(h.F[mode], dim, R, h.d_norms, h.d_lambda, h.s));
+    CPTC_TRY(cptc_gram(h.F[mode], dim, R, h.G(mode), h.s));
+    h.gram_ok[mode] = true;
+    return CPTC_OK;
+}
+
+int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
+{
+    const int R = h.R;
+    const size_t RR = size_t(R) * R;
+    const double Xn = std::sqrt(h.x_sq);
+    h.timing_kernels = h.views.ready;
+    for (int it = 0; it < iters; ++it)
+    {
+        CPTC_HIP(hipEventRecord(h.ev[0], h.s));
+        for (int mode = 0; mode < 3; ++mode)
+        {
+            const int p = mode == 0 ? 1 : 0, q = mode == 2 ? 1 : 2;
+            for (int g : {p, q})
+                if (!h.gram_ok[g])
+                {
+                    CPTC_TRY(cptc_gram(h.F[g], h.dims[g], R, h.G(g), h.s));
+                    h.gram_ok[g] = true;
+                }
+            CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+            CPTC_HIP(hipEventRecord(h.ev[1 + 2 * mode], h.s));
+            CPTC_TRY(mttkrp_launch(h, mode));
+            CPTC_HIP(hipEventRecord(h.ev[2 + 2 * mode], h.s));
+            CPTC_TRY(update_mode(h, mode));
+        }
+        // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP
+        CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, h.d_scal, h.s));
+        CPTC_HIP(hipEventRecord(h.ev[7], h.s));
+        double sc[2] = {0, 0};
+        CPTC_HIP(hipMemcpyAsync(sc, h.d_scal, 2 * sizeof(double), hipMemcpyDeviceToHost, h.s));
+        CPTC_HIP(hipStreamSynchronize(h.s));
+        const double res = std::max(h.x_sq - 2.0 * sc[0] + sc[1], 0.0);
+        const double fit = Xn > 0.0 ? 1.0 - std::sqrt(res) / Xn : 0.0;
+        float ms = 0.0f, mt = 0.0f;
+        CPTC_HIP(hipEventElapsedTime(&ms, h.ev[0], h.ev[7]));
+        for (int m = 0; m < 3; ++m)
+        {
+            float x = 0.0f;
+            CPTC_HIP(hipEventElapsedTime(&x, h.ev[1 + 2 * m], h.ev[2 + 2 * m]));
+            mt += x;
+            h.k_mttkrp_ms[m] += x;
+            if (h.timing_kernels)
+            {
+                float k = 0.0f;
+                CPTC_HIP(hipEventElapsedTime(&k, h.kev[2 * m], h.kev[2 * m + 1]));
+                h.k_sparse_ms[m] += k;
+            }
+        }
+        h.k_iters++;
+        if (fit_out) fit_out[it] = fit;
+        if (ms_out) ms_out[it] = ms;
+        if (mtt_out) mtt_out[it] = mt;
+        if (h.o.verbose) std::printf("[ALS] iter %d/%d time=%g ms fit=%.10g\n", it + 1, iters, ms, fit);
+        if (h.o.verbose && std::getenv("ALS_PROFILE"))
+            std::printf("[ALS][profile] iter %d mttkrp=%g (iter=%g)\n", it + 1, mt, ms);
+    }
+    return CPTC_OK;
+}
+
+Als3* as_h(void* p) { return static_cast<Als3*>(p); }
+
+}  // namespace
+}  // namespace cptc
+
+using cptc::Als3;
+
+extern "C" void cptc_als3_default_opts(cptc_als3_opts* o)
+{
+    if (!o) return;
+    o->R = 32;
+    o->threshold = 0.03;
+    o->path = -1;
+    o->fill_min = -1.0;
+    o->skip_dense = -1;
+    o->skip_sparse = -1;
+    o->cadr = 1;
+    o->seed = 42;
+    o->verbose = 0;
+}
+
+extern "C" int cptc_als3_create(const cptc_coo* coo, const cptc_als3_opts* opts, void** handle)
+{
+    CPTC_REQUIRE(handle, CPTC_ERR_ARG, "cptc_als3_create: null handle");
+    *handle = nullptr;
+    Als3* h = new Als3();
+    const int rc = cptc::create(coo, opts, h);
+    if (rc != CPTC_OK)
+    {
+        cptc::destroy(h);
+        return rc;
+    }
+    *handle = h;
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_destroy(void* handle)
+{
+    cptc::destroy(cptc::as_h(handle));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && info, CPTC_ERR_ARG, "cptc_als3_info_get: null argument");
+    std::memset(info, 0, sizeof(*info));
+    for (int m = 0; m < 3; ++m)
+    {
+        info->dims[m] = h->dims[m];
+        info->segments[m] = h->views.ready ? h->views.nseg[m] : 0;
+        info->dense_view_segments[m] = h->dviews.ready ? h->dviews.nseg[m] : 0;
+    }
+    info->nnz = h->nnz;
+    info->sparse_nnz = h->part.sparse_nnz;
+    info->dense_nnz = h->dense_nnz_total;
+    info->num_dense_tiles = h->tiles_total;
+    info->dense_cutoff = h->part.cutoff;
+    info->avg_fill = h->avg_fill;
+    info->fill_min = h->fill_min;
+    info->use_mfma = h->use_mfma ? 1 : 0;
+    info->num_cus = h->num_cus;
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter,
+                             float* ms_mttkrp)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && iters >= 0, CPTC_ERR_ARG, "cptc_als3_run: bad arguments");
+    return cptc::run(*h, iters, fit, ms_iter, ms_mttkrp);
+}
+
+extern "C" int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && out6 && iters, CPTC_ERR_ARG, "cptc_als3_kernel_times: bad arguments");
+    for (int m = 0; m < 3; ++m)
+    {
+        out6[m] = h->k_sparse_ms[m];
+        out6[3 + m] = h->k_mttkrp_ms[m];
+    }
+    *iters = h->k_iters;
+    if (reset)
+    {
+        for (int m = 0; m < 3; ++m) h->k_sparse_ms[m] = h->k_mttkrp_ms[m] = 0.0;
+        h->k_iters = 0;
+    }
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_mttkrp(void* handle, int mode, double* host_out)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && host_out && mode >= 0 && mode < 3, CPTC_ERR_ARG,
+                 "cptc_als3_mttkrp: bad arguments");
+    h->timing_kernels = false;
+    CPTC_TRY(cptc::mttkrp_launch(*h, mode));
+    CPTC_HIP(hipMemcpyAsync(host_out, h->d_FtV, h->dims[mode] * size_t(h->R) * sizeof(double),
+                            hipMemcpyDeviceToHost, h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_factor(void* handle, int mode, int unpermuted, double* host_out)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && host_out && mode >= 0 && mode < 3, CPTC_ERR_ARG,
+                 "cptc_als3_factor: bad arguments");
+    const size_t n = h->dims[mode] * size_t(h->R);
+    if (!unpermuted)
+    {
+        CPTC_HIP(hipMemcpyAsync(host_out, h->F[mode], n * sizeof(double), hipMemcpyDeviceToHost,
+                                h->s));
+        CPTC_HIP(hipStreamSynchronize(h->s));
+        return CPTC_OK;
+    }
+    double* tmp = nullptr;
+    CPTC_HIP(hipMalloc(&tmp, n * sizeof(double)));
+    int rc = cptc_unpermute_factor(h->F[mode], tmp, h->d_perm[mode], h->dims[mode], h->R, h->s);
+    if (rc == CPTC_OK)
+    {
+        if (hipMemcpyAsync(host_out, tmp, n * sizeof(double), hipMemcpyDeviceToHost, h->s) !=
+                hipSuccess ||
+            hipStreamSynchronize(h->s) != hipSuccess)
+            rc = CPTC_ERR_HIP;
+    }
+    (void)hipFree(tmp);
+    return rc;
+}
+
+extern "C" int cptc_als3_set_factor(void* handle, int mode, const double* host_in)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && host_in && mode >= 0 && mode < 3, CPTC_ERR_ARG,
+                 "cptc_als3_set_factor: bad arguments");
+    CPTC_HIP(hipMemcpyAsync(h->F[mode], host_in, h->dims[mode] * size_t(h->R) * sizeof(double),
+                            hipMemcpyHostToDevice, h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    h->gram_ok[mode] = false;
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_lambda(void* handle, double* host_out)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && host_out, CPTC_ERR_ARG, "cptc_als3_lambda: bad arguments");
+    CPTC_HIP(hipMemcpyAsync(host_out, h->d_lambda, size_t(h->R) * sizeof(double),
+                            hipMemcpyDeviceToHost, h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_residual(void* handle, double* res_sq, double* x_sq)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && res_sq && x_sq, CPTC_ERR_ARG, "cptc_als3_residual: bad arguments");
+    CPTC_TRY(cptc::residual_launch(*h, true));
+    double r2[2] = {0, 0};
+    CPTC_HIP(hipMemcpyAsync(r2, h->d_scal + 2, 2 * sizeof(double), hipMemcpyDeviceToHost, h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    *res_sq = r2[0];
+    *x_sq = r2[1];
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_perm(void* handle, int mode, int32_t* host_out)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && host_out && mode >= 0 && mode < 3, CPTC_ERR_ARG,
+                 "cptc_als3_perm: bad arguments");
+    std::memcpy(host_out, h->perm[mode].data(), h->perm[mode].size() * sizeof(int32_t));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_view(void* handle, int which, int mode, uint64_t* coords, double* vals,
+                              uint32_t* blk_row, uint32_t* blk_start, uint32_t* blk_cnt)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && mode >= 0 && mode < 3 && (which == 0 || which == 1), CPTC_ERR_ARG,
+                 "cptc_als3_view: bad arguments");
+    const cptc::DevViews3& v = which == 0 ? h->views : h->dviews;
+    if (!v.ready) return CPTC_OK;
+    auto cp = [&](void* dst, const void* src, size_t bytes) -> int {
+        if (dst && src && bytes)
+            CPTC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->s));
+        return CPTC_OK;
+    };
+    CPTC_TRY(cp(coords, v.d_coords[mode], v.nnz * 8));
+    CPTC_TRY(cp(vals, v.d_vals[mode], v.nnz * 8));
+    CPTC_TRY(cp(blk_row, v.d_blk_row[mode], v.nseg[mode] * 4));
+    CPTC_TRY(cp(blk_start, v.d_blk_start[mode], v.nseg[mode] * 4));
+    CPTC_TRY(cp(blk_cnt, v.d_blk_cnt[mode], v.nseg[mode] * 4));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_tiles(void* handle, int32_t* tiles4, uint64_t* pool_off,
+                               int32_t* pool_lid, double* pool_val)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h, CPTC_ERR_ARG, "cptc_als3_tiles: null handle");
+    const cptc::DevPartition3& p = h->part;
+    if (tiles4 && !p.h_tiles4.empty())
+        std::memcpy(tiles4, p.h_tiles4.data(), p.h_tiles4.size() * sizeof(int32_t));
+    if (pool_off && !p.h_pool_off.empty())
+        std::memcpy(pool_off, p.h_pool_off.data(), p.h_pool_off.size() * sizeof(uint64_t));
+    if (pool_lid && p.d_pool_lid && p.dense_nnz)
+        CPTC_HIP(hipMemcpyAsync(pool_lid, p.d_pool_lid, p.dense_nnz * 4, hipMemcpyDeviceToHost,
+                                h->s));
+    if (pool_val && p.d_pool_val && p.dense_nnz)
+        CPTC_HIP(hipMemcpyAsync(pool_val, p.d_pool_val, p.dense_nnz * 8, hipMemcpyDeviceToHost,
+                                h->s));
+    CPTC_HIP(hipStreamSynchronize(h->s));
+    return CPTC_OK;
+}

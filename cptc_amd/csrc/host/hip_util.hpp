@@ -1,0 +1,75 @@
+// Error plumbing shared by the C ABI: every entry point returns an int status
+// and records a message retrievable with cptc_last_error().
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "cptc_hip.h"
+
+namespace cptc {
+
+void set_error(const char* fmt, ...);
+
+// Kernel launches and HIP calls inside entry points.
+#define CPTC_HIP(call)                                                                     \
+    do                                                                                     \
+    {                                                                                      \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+        {                                                                                  \
+            ::cptc::set_error("%s:%d %s -> %s", __FILE__, __LINE__, #call,                 \
+                              hipGetErrorString(e_));                                      \
+            return CPTC_ERR_HIP;                                                           \
+        }                                                                                  \
+    } while (0)
+
+#define CPTC_LAUNCHED()                                                                    \
+    do                                                                                     \
+    {                                                                                      \
+        hipError_t e_ = hipGetLastError();                                                 \
+        if (e_ != hipSuccess)                                                              \
+        {                                                                                  \
+            ::cptc::set_error("%s:%d launch -> %s", __FILE__, __LINE__,                    \
+                              hipGetErrorString(e_));                                      \
+            return CPTC_ERR_HIP;                                                           \
+        }                                                                                  \
+    } while (0)
+
+#define CPTC_REQUIRE(cond, code, ...)                                                      \
+    do                                                                                     \
+    {                                                                                      \
+        if (!(cond))                                                                       \
+        {                                                                                  \
+            ::cptc::set_error(__VA_ARGS__);                                                \
+            return (code);                                                                 \
+        }                                                                                  \
+    } while (0)
+
+#define CPTC_TRY(expr)                                                                     \
+    do                                                                                     \
+    {                                                                                      \
+        int rc_ = (expr);                                                                  \
+        if (rc_ != CPTC_OK) return rc_;                                                    \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(size_t n, unsigned block, unsigned cap = 1u << 20)
+{
+    size_t g = (n + block - 1) / block;
+    if (g == 0) g = 1;
+    if (g > cap) g = cap;
+    return unsigned(g);
+}
+
+// Library-owned device scratch, one growing buffer per (device, slot),
+// freed at process exit.  Slots separate buffers that are live at the same
+// time within one entry point.
+enum ScratchSlot { SCR_GRAM = 0, SCR_PINV, SCR_FLAGS, SCR_REDUCE, SCR_LAYOUT_A, SCR_LAYOUT_B, SCR_NSLOTS };
+int scratch_get(int slot, size_t bytes, void** out);
+
+}  // namespace cptc

@@ -1,0 +1,78 @@
+// Host-side helpers shared by the generators, the loader and the drivers.
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include <omp.h>
+
+namespace cptc {
+
+inline uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Counter-based stream: independent 64-bit words for any (seed, stream, ctr).
+inline uint64_t rng_u64(uint64_t seed, uint64_t stream, uint64_t ctr)
+{
+    return mix64(mix64(seed ^ (stream * 0xD1B54A32D192ED03ull)) + ctr);
+}
+
+// [0, 1) with 53 random bits.
+inline double u01(uint64_t x) { return double(x >> 11) * (1.0 / 9007199254740992.0); }
+
+// Stable LSD radix sort of (key, payload) pairs on the low `key_bits` bits,
+// 11 bits per pass, OpenMP-parallel with per-thread histograms.
+template <class V>
+void radix_sort_pairs_u64(std::vector<uint64_t>& keys, std::vector<V>& vals, int key_bits)
+{
+    const size_t n = keys.size();
+    if (n < 2 || key_bits <= 0) return;
+    constexpr int DB = 11;
+    constexpr int NB = 1 << DB;
+    std::vector<uint64_t> k2(n);
+    std::vector<V> v2(n);
+    const int nt = std::max(1, omp_get_max_threads());
+    std::vector<size_t> hist(size_t(nt) * NB);
+    for (int shift = 0; shift < key_bits; shift += DB)
+    {
+        std::fill(hist.begin(), hist.end(), 0);
+        #pragma omp parallel num_threads(nt)
+        {
+            const int t = omp_get_thread_num();
+            const size_t lo = n * t / nt, hi = n * (t + 1) / nt;
+            size_t* h = &hist[size_t(t) * NB];
+            for (size_t i = lo; i < hi; ++i) ++h[(keys[i] >> shift) & (NB - 1)];
+        }
+        size_t run = 0;
+        for (int d = 0; d < NB; ++d)
+            for (int t = 0; t < nt; ++t)
+            {
+                const size_t c = hist[size_t(t) * NB + d];
+                hist[size_t(t) * NB + d] = run;
+                run += c;
+            }
+        #pragma omp parallel num_threads(nt)
+        {
+            const int t = omp_get_thread_num();
+            const size_t lo = n * t / nt, hi = n * (t + 1) / nt;
+            size_t* h = &hist[size_t(t) * NB];
+            for (size_t i = lo; i < hi; ++i)
+            {
+                const size_t p = h[(keys[i] >> shift) & (NB - 1)]++;
+                k2[p] = keys[i];
+                v2[p] = vals[i];
+            }
+        }
+        keys.swap(k2);
+        vals.swap(v2);
+    }
+}
+
+}  // namespace cptc

@@ -1,0 +1,226 @@
+// Order-3 FP64 sparse MTTKRP over row-sorted segments, for CDNA4 wave64.
+//
+// Semantics (sparse.cu:614-711 and 271-333): for every segment b of one
+// mode's row-sorted view, acc_r = sum_e (v_e * F1[o0_e, r]) * F2[o1_e, r] and
+// FtV[blk_row[b], r] += acc_r (one atomic per (row, rank, segment), skipped
+// when acc_r == 0).  Any R >= 1.
+//
+// Mapping.  A lane owns VEC consecutive ranks (VEC = 2: one 16-byte load per
+// factor row per lane, so a wave reads a 1 KB R=128 row as 64 x 16 B fully
+// coalesced).  LPE = RT / VEC lanes cover one element's rank tile RT; a wave
+// carries EPW = 64 / LPE elements at a time ("rank-dependent element
+// packing": R=128 -> 1, 64 -> 2, 32 -> 4, 16 -> 8, 8 -> 16 elements per wave).
+// WAVES waves of a workgroup stride over the segment; partial sums meet in
+// registers (xor-shuffles across the EPW slots of a wave) and then in LDS
+// across waves.  R > RT runs RT-wide rank blocks on grid.y.
+#include <hip/hip_runtime.h>
+
+#include "../host/hip_util.hpp"
+
+namespace {
+
+constexpr int WAVE = 64;
+
+template <int RT, int VEC, int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
+    int mode, const uint64_t* __restrict__ coords, const double* __restrict__ vals,
+    const uint32_t* __restrict__ blk_row, const uint32_t* __restrict__ blk_start,
+    const uint32_t* __restrict__ blk_cnt, const double* __restrict__ F1,
+    const double* __restrict__ F2, double* __restrict__ FtV, int R)
+{
+    constexpr int LPE = RT / VEC;          // lanes per element
+    constexpr int EPW = WAVE / LPE;        // elements per wave step
+    constexpr int STEP = EPW * WAVES;      // elements per workgroup step
+    static_assert(WAVE % LPE == 0, "rank tile must divide the wave");
+
+    const uint32_t seg = blockIdx.x;
+    const uint32_t row = blk_row[seg];
+    const uint32_t start = blk_start[seg];
+    const uint32_t end = start + blk_cnt[seg];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
+    const int slot = lane / LPE;
+    const int r0 = int(blockIdx.y) * RT + (lane % LPE) * VEC;   // first rank of this lane
+    const bool rank_ok = r0 < R;
+
+    // per-mode field shifts of the packed (i<<30 | j<<15 | k) coordinate
+    const int sh0 = (mode == 0) ? 15 : 30;   // o0 = j (mode 0) or i
+    const int sh1 = (mode == 2) ? 15 : 0;    // o1 = k (modes 0,1) or j
+
+    double acc[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = 0.0;
+
+    uint32_t e = start + uint32_t(wave * EPW + slot);
+    for (; e + uint32_t((UNROLL - 1) * STEP) < end; e += uint32_t(UNROLL * STEP))
+    {
+        uint64_t pc[UNROLL];
+        double v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            pc[u] = coords[e + u * STEP];
+            v[u] = vals[e + u * STEP];
+        }
+        if (rank_ok)
+        {
+            double a[UNROLL][VEC], b[UNROLL][VEC];
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+            {
+                const uint32_t o0 = uint32_t(pc[u] >> sh0) & 0x7FFFu;
+                const uint32_t o1 = uint32_t(pc[u] >> sh1) & 0x7FFFu;
+                const double* p1 = F1 + size_t(o0) * R + r0;
+                const double* p2 = F2 + size_t(o1) * R + r0;
+                if constexpr (VEC == 2)
+                {
+                    const double2 x = *reinterpret_cast<const double2*>(p1);
+                    const double2 y = *reinterpret_cast<const double2*>(p2);
+                    a[u][0] = x.x; a[u][1] = x.y;
+                    b[u][0] = y.x; b[u][1] = y.y;
+                }
+                else
+                {
+                    a[u][0] = *p1;
+                    b[u][0] = *p2;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+                for (int q = 0; q < VEC; ++q)
+                    if (VEC == 1 || r0 + q < R) acc[q] += v[u] * a[u][q] * b[u][q];
+        }
+    }
+    for (; e < end; e += uint32_t(STEP))
+    {
+        const uint64_t pc = coords[e];
+        const double v = vals[e];
+        if (rank_ok)
+        {
+            const uint32_t o0 = uint32_t(pc >> sh0) & 0x7FFFu;
+            const uint32_t o1 = uint32_t(pc >> sh1) & 0x7FFFu;
+            const double* p1 = F1 + size_t(o0) * R + r0;
+            const double* p2 = F2 + size_t(o1) * R + r0;
+            if constexpr (VEC == 2)
+            {
+                const double2 x = *reinterpret_cast<const double2*>(p1);
+                const double2 y = *reinterpret_cast<const double2*>(p2);
+                acc[0] += v * x.x * y.x;
+                if (r0 + 1 < R) acc[1] += v * x.y * y.y;
+            }
+            else
+            {
+                acc[0] += v * *p1 * *p2;
+            }
+        }
+    }
+
+    // reduce the EPW element slots of the wave (lanes l, l^LPE, l^2LPE, ...)
+#pragma unroll
+    for (int off = LPE; off < WAVE; off <<= 1)
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) acc[q] += __shfl_xor(acc[q], off, WAVE);
+
+    if constexpr (WAVES == 1)
+    {
+        if (slot == 0 && rank_ok)
+        {
+            double* out = FtV + size_t(row) * R + r0;
+#pragma unroll
+            for (int q = 0; q < VEC; ++q)
+                if ((VEC == 1 || r0 + q < R) && acc[q] != 0.0) atomicAdd(out + q, acc[q]);
+        }
+    }
+    else
+    {
+        __shared__ double red[WAVES][RT];
+        if (slot == 0)
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) red[wave][(lane % LPE) * VEC + q] = acc[q];
+        __syncthreads();
+        for (int x = tid; x < RT; x += WAVE * WAVES)
+        {
+            const int r = int(blockIdx.y) * RT + x;
+            if (r >= R) continue;
+            double t = 0.0;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) t += red[w][x];
+            if (t != 0.0) atomicAdd(FtV + size_t(row) * R + r, t);
+        }
+    }
+}
+
+template <int RT, int VEC>
+hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const uint32_t* br,
+                     const uint32_t* bs, const uint32_t* bc, size_t nblocks, const double* F1,
+                     const double* F2, double* FtV, int R, hipStream_t s)
+{
+    constexpr int WAVES = 4;
+    constexpr int UNROLL = 4;
+    const unsigned ry = unsigned((R + RT - 1) / RT);
+    dim3 grid(unsigned(nblocks), ry);
+    hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid, dim3(WAVE * WAVES), 0,
+                       s, mode, coords, vals, br, bs, bc, F1, F2, FtV, R);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int cptc_mttkrp_sparse3(int mode, const uint64_t* d_coords, const double* d_vals,
+                                   const uint32_t* d_blk_row, const uint32_t* d_blk_start,
+                                   const uint32_t* d_blk_cnt, size_t nblocks, const double* d_F1,
+                                   const double* d_F2, double* d_FtV, int R, void* stream)
+{
+    CPTC_REQUIRE(mode >= 0 && mode < 3, CPTC_ERR_ARG, "cptc_mttkrp_sparse3: mode %d", mode);
+    CPTC_REQUIRE(R >= 1, CPTC_ERR_ARG, "cptc_mttkrp_sparse3: R %d", R);
+    if (nblocks == 0) return CPTC_OK;
+    CPTC_REQUIRE(nblocks < (size_t(1) << 31), CPTC_ERR_ARG, "cptc_mttkrp_sparse3: %zu segments",
+                 nblocks);
+    CPTC_REQUIRE(d_coords && d_vals && d_blk_row && d_blk_start && d_blk_cnt && d_F1 && d_F2 &&
+                     d_FtV,
+                 CPTC_ERR_ARG, "cptc_mttkrp_sparse3: null pointer");
+    hipStream_t s = cptc::as_stream(stream);
+    // 16-byte rows need an even R and 16-byte aligned factor bases.
+    const bool vec2 = (R % 2 == 0) && ((reinterpret_cast<uintptr_t>(d_F1) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(d_F2) & 15) == 0);
+    hipError_t e;
+    if (vec2)
+    {
+        if (R <= 8)
+            e = launch_rt<8, 2>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt, nblocks,
+                                d_F1, d_F2, d_FtV, R, s);
+        else if (R <= 16)
+            e = launch_rt<16, 2>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+        else if (R <= 32)
+            e = launch_rt<32, 2>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+        else if (R <= 64)
+            e = launch_rt<64, 2>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+        else
+            e = launch_rt<128, 2>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                  nblocks, d_F1, d_F2, d_FtV, R, s);
+    }
+    else
+    {
+        if (R <= 8)
+            e = launch_rt<8, 1>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt, nblocks,
+                                d_F1, d_F2, d_FtV, R, s);
+        else if (R <= 16)
+            e = launch_rt<16, 1>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+        else if (R <= 32)
+            e = launch_rt<32, 1>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+        else
+            e = launch_rt<64, 1>(mode, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                 nblocks, d_F1, d_F2, d_FtV, R, s);
+    }
+    CPTC_REQUIRE(e == hipSuccess, CPTC_ERR_HIP, "cptc_mttkrp_sparse3 launch: %s",
+                 hipGetErrorString(e));
+    return CPTC_OK;
+}

@@ -1,0 +1,670 @@
+// Small dense FP64 kernels of one ALS mode update: Gram, Hadamard, the R x R
+// pseudoinverse solve, column norms, normalisation and the Gram fit.
+//
+// All reductions are two-stage with a fixed order (per-workgroup partials,
+// then one ordered sum), so every result is bit-reproducible run to run.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+
+#include "../host/hip_util.hpp"
+
+namespace {
+
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------
+// Gram: G = F^T F.  Stage 1: workgroup p sums rows [p*rpw, (p+1)*rpw) into
+// partial[p] (one RT x RT output tile per grid.y); stage 2 sums partials in
+// p order.  16 x 16 threads, TPT x TPT outputs per thread (RT = 16 * TPT).
+// ---------------------------------------------------------------------------
+template <int TPT>
+__global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restrict__ F,
+                                                           size_t rows, int R, size_t rpw,
+                                                           int ntile, double* __restrict__ part)
+{
+    constexpr int RT = 16 * TPT;
+    constexpr int CH = 16;
+    __shared__ double sa[CH][RT + 1];
+    __shared__ double sb[CH][RT + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int bi = int(blockIdx.y) / ntile, bj = int(blockIdx.y) % ntile;
+    const int ci = bi * RT, cj = bj * RT;
+    const size_t r_lo = size_t(blockIdx.x) * rpw;
+    const size_t r_hi = (r_lo + rpw < rows) ? r_lo + rpw : rows;
+    double acc[TPT][TPT];
+#pragma unroll
+    for (int a = 0; a < TPT; ++a)
+#pragma unroll
+        for (int b = 0; b < TPT; ++b) acc[a][b] = 0.0;
+    for (size_t i0 = r_lo; i0 < r_hi; i0 += CH)
+    {
+        for (int x = threadIdx.x; x < CH * RT; x += 256)
+        {
+            const int rr = x / RT, cc = x % RT;
+            const size_t i = i0 + rr;
+            const bool ok = i < r_hi;
+            sa[rr][cc] = (ok && ci + cc < R) ? F[i * R + ci + cc] : 0.0;
+            sb[rr][cc] = (ok && cj + cc < R) ? F[i * R + cj + cc] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int rr = 0; rr < CH; ++rr)
+        {
+            double va[TPT], vb[TPT];
+#pragma unroll
+            for (int a = 0; a < TPT; ++a) va[a] = sa[rr][ty + 16 * a];
+#pragma unroll
+            for (int b = 0; b < TPT; ++b) vb[b] = sb[rr][tx + 16 * b];
+#pragma unroll
+            for (int a = 0; a < TPT; ++a)
+#pragma unroll
+                for (int b = 0; b < TPT; ++b) acc[a][b] += va[a] * vb[b];
+        }
+        __syncthreads();
+    }
+    double* out = part + size_t(blockIdx.x) * size_t(R) * R;
+#pragma unroll
+    for (int a = 0; a < TPT; ++a)
+#pragma unroll
+        for (int b = 0; b < TPT; ++b)
+        {
+            const int r = ci + ty + 16 * a, s = cj + tx + 16 * b;
+            if (r < R && s < R) out[size_t(r) * R + s] = acc[a][b];
+        }
+}
+
+__global__ void sum_partials_kernel(const double* __restrict__ part, int P, size_t n,
+                                    double* __restrict__ out)
+{
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
+         x += size_t(gridDim.x) * blockDim.x)
+    {
+        double s = 0.0;
+        for (int p = 0; p < P; ++p) s += part[size_t(p) * n + x];
+        out[x] = s;
+    }
+}
+
+__global__ void hadamard_kernel(const double* A, const double* B, double* C, size_t n)
+{
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
+         x += size_t(gridDim.x) * blockDim.x)
+        C[x] = A[x] * B[x];
+}
+
+// ---------------------------------------------------------------------------
+// pinv, fast path: Cholesky A = L L^T (right-looking, one workgroup, A in
+// LDS for R <= 128 or in global scratch), then Ainv = L^-T L^-1 column by
+// column.  Any pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1
+// and leaves Ainv to the Jacobi kernel.
+// ---------------------------------------------------------------------------
+constexpr int PINV_THREADS = 1024;
+
+__global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double* __restrict__ Ain,
+                                                                    int R, double* work,
+                                                                    double* __restrict__ Ainv,
+                                                                    int* fallback, int use_lds)
+{
+    extern __shared__ double lds[];
+    double* A = use_lds ? lds : work;
+    __shared__ int ok;
+    __shared__ double tau;
+    const int tid = threadIdx.x;
+    const int n2 = R * R;
+    for (int x = tid; x < n2; x += PINV_THREADS) A[x] = Ain[x];
+    if (tid == 0) *fallback = 0;
+    __syncthreads();
+    if (tid == 0)
+    {
+        double md = 0.0;
+        for (int k = 0; k < R; ++k) md = fmax(md, A[k * R + k]);
+        tau = 1e-10 * md;
+        ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
+    }
+    __syncthreads();
+    // `ok` is written only by thread 0 before the first barrier of an
+    // iteration and read by everyone between that barrier and the next, so
+    // every thread leaves the loop at the same k.
+    for (int k = 0; k < R; ++k)
+    {
+        if (tid == 0 && ok)
+        {
+            const double d = A[k * R + k];
+            if (!(d > tau) || !isfinite(d))
+                ok = 0;
+            else
+                A[k * R + k] = sqrt(d);
+        }
+        __syncthreads();
+        if (!ok) break;
+        const double lkk = A[k * R + k];
+        for (int i = k + 1 + tid; i < R; i += PINV_THREADS) A[i * R + k] /= lkk;
+        __syncthreads();
+        // trailing lower triangle: (i, j) with k < j <= i < R
+        const int m = R - k - 1;
+        const int cnt = m * (m + 1) / 2;
+        for (int t = tid; t < cnt; t += PINV_THREADS)
+        {
+            // row-major enumeration of the lower triangle of size m
+            int ii = int((sqrt(8.0 * t + 1.0) - 1.0) * 0.5);
+            while ((ii + 1) * (ii + 2) / 2 <= t) ++ii;
+            while (ii * (ii + 1) / 2 > t) --ii;
+            const int jj = t - ii * (ii + 1) / 2;
+            const int i = k + 1 + ii, j = k + 1 + jj;
+            A[i * R + j] -= A[i * R + k] * A[j * R + k];
+        }
+        __syncthreads();
+    }
+    if (!ok)
+    {
+        if (tid == 0) *fallback = 1;
+        return;
+    }
+    // column c of L^-T L^-1: forward solve L y = e_c, back solve L^T x = y;
+    // the working vector lives in Ainv[:, c]
+    for (int c = tid; c < R; c += PINV_THREADS)
+    {
+        for (int j = 0; j < c; ++j) Ainv[j * R + c] = 0.0;
+        for (int j = c; j < R; ++j)
+        {
+            double s = (j == c) ? 1.0 : 0.0;
+            for (int q = c; q < j; ++q) s -= A[j * R + q] * Ainv[q * R + c];
+            Ainv[j * R + c] = s / A[j * R + j];
+        }
+        for (int j = R - 1; j >= 0; --j)
+        {
+            double s = Ainv[j * R + c];
+            for (int q = j + 1; q < R; ++q) s -= A[q * R + j] * Ainv[q * R + c];
+            Ainv[j * R + c] = s / A[j * R + j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// pinv, exact path (runs only when *fallback != 0): parallel cyclic Jacobi
+// (round-robin pair ordering, Brent & Luk 1985) on A = V diag(l) V^T, then
+// Ainv = sum_{|l_i| > R ulp(max|l|)} v_i v_i^T / l_i — the truncated SVD
+// pseudoinverse of a symmetric matrix (solver.cu:764-775, 900-1002).
+// A in LDS (R <= 128) or global scratch; V in global scratch.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double* __restrict__ Ain,
+                                                                   int R, double* work,
+                                                                   double* V,
+                                                                   double* __restrict__ Ainv,
+                                                                   const int* fallback,
+                                                                   int use_lds)
+{
+    if (*fallback == 0) return;
+    extern __shared__ double lds[];
+    double* A = use_lds ? lds : work;
+    __shared__ double red[PINV_THREADS / WAVE];
+    __shared__ double s_off, s_fro;
+    __shared__ int pair_p[256], pair_q[256];
+    __shared__ double rot_c[256], rot_s[256];
+    const int tid = threadIdx.x;
+    const int n2 = R * R;
+    const int Rp = R + (R & 1);  // even with a dummy index R when R is odd
+    const int npairs = Rp / 2;
+    for (int x = tid; x < n2; x += PINV_THREADS)
+    {
+        A[x] = Ain[x];
+        V[x] = ((x / R) == (x % R)) ? 1.0 : 0.0;
+    }
+    __syncthreads();
+    auto block_sum = [&](double v) -> double {
+        for (int off = WAVE / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+        if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = v;
+        __syncthreads();
+        double t = 0.0;
+        for (int w = 0; w < PINV_THREADS / WAVE; ++w) t += red[w];
+        __syncthreads();
+        return t;
+    };
+    {
+        double f = 0.0;
+        for (int x = tid; x < n2; x += PINV_THREADS) f += A[x] * A[x];
+        f = block_sum(f);
+        if (tid == 0) s_fro = sqrt(f);
+    }
+    __syncthreads();
+    for (int sweep = 0; sweep < 100; ++sweep)
+    {
+        double o = 0.0;
+        for (int x = tid; x < n2; x += PINV_THREADS)
+            if ((x / R) != (x % R)) o += A[x] * A[x];
+        o = block_sum(o);
+        if (tid == 0) s_off = sqrt(o);
+        __syncthreads();
+        if (!(s_off > 1e-15 * s_fro)) break;
+        for (int round = 0; round < Rp - 1; ++round)
+        {
+            // round-robin: index 0 fixed, others rotate
+            for (int k = tid; k < npairs; k += PINV_THREADS)
+            {
+                auto at = [&](int pos) { return pos == 0 ? 0 : 1 + (pos - 1 + round) % (Rp - 1); };
+                int p = at(k), q = at(Rp - 1 - k);
+                if (p > q) { const int t = p; p = q; q = t; }
+                double c = 1.0, s = 0.0;
+                if (q < R)
+                {
+                    const double apq = A[p * R + q];
+                    if (apq != 0.0)
+                    {
+                        const double theta = (A[q * R + q] - A[p * R + p]) / (2.0 * apq);
+                        const double t = (theta >= 0.0 ? 1.0 : -1.0) /
+                                         (fabs(theta) + sqrt(theta * theta + 1.0));
+                        c = 1.0 / sqrt(t * t + 1.0);
+                        s = t * c;
+                    }
+                }
+                pair_p[k] = p;
+                pair_q[k] = q;
+                rot_c[k] = c;
+                rot_s[k] = s;
+            }
+            __syncthreads();
+            // A <- A J (columns p, q)
+            for (int x = tid; x < npairs * R; x += PINV_THREADS)
+            {
+                const int k = x / R, r = x % R;
+                const int p = pair_p[k], q = pair_q[k];
+                if (q >= R || rot_s[k] == 0.0) continue;
+                const double c = rot_c[k], s = rot_s[k];
+                const double arp = A[r * R + p], arq = A[r * R + q];
+                A[r * R + p] = c * arp - s * arq;
+                A[r * R + q] = s * arp + c * arq;
+                const double vrp = V[r * R + p], vrq = V[r * R + q];
+                V[r * R + p] = c * vrp - s * vrq;
+                V[r * R + q] = s * vrp + c * vrq;
+            }
+            __syncthreads();
+            // A <- J^T A (rows p, q)
+            for (int x = tid; x < npairs * R; x += PINV_THREADS)
+            {
+                const int k = x / R, r = x % R;
+                const int p = pair_p[k], q = pair_q[k];
+                if (q >= R || rot_s[k] == 0.0) continue;
+                const double c = rot_c[k], s = rot_s[k];
+                const double apr = A[p * R + r], aqr = A[q * R + r];
+                A[p * R + r] = c * apr - s * aqr;
+                A[q * R + r] = s * apr + c * aqr;
+            }
+            __syncthreads();
+        }
+    }
+    __shared__ double s_tol;
+    if (tid == 0)
+    {
+        double smax = 0.0;
+        for (int k = 0; k < R; ++k) smax = fmax(smax, fabs(A[k * R + k]));
+        s_tol = double(R) * (nextafter(smax, smax + 1.0) - smax);
+    }
+    __syncthreads();
+    for (int x = tid; x < n2; x += PINV_THREADS)
+    {
+        const int r = x / R, c = x % R;
+        double s = 0.0;
+        for (int k = 0; k < R; ++k)
+        {
+            const double l = A[k * R + k];
+            if (fabs(l) > s_tol) s += V[r * R + k] * (1.0 / l) * V[c * R + k];
+        }
+        Ainv[x] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// F = FtV * Ainv (row-major dim x R times R x R), then F[:, r] /= div[r].
+// 64 x 64 output tile per workgroup, 4 x 4 per thread, K in chunks of 16.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void apply_kernel(const double* __restrict__ Y,
+                                                    const double* __restrict__ Ainv,
+                                                    double* __restrict__ F, size_t dim, int R,
+                                                    const double* __restrict__ div)
+{
+    constexpr int TM = 64, TN = 64, TK = 16;
+    __shared__ double sy[TK][TM + 1];
+    __shared__ double sa[TK][TN + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const size_t i0 = size_t(blockIdx.x) * TM;
+    const int c0 = int(blockIdx.y) * TN;
+    double acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
+    for (int k0 = 0; k0 < R; k0 += TK)
+    {
+        for (int x = threadIdx.x; x < TM * TK; x += 256)
+        {
+            const int rr = x / TK, kk = x % TK;
+            const size_t i = i0 + rr;
+            sy[kk][rr] = (i < dim && k0 + kk < R) ? Y[i * R + k0 + kk] : 0.0;
+        }
+        for (int x = threadIdx.x; x < TK * TN; x += 256)
+        {
+            const int kk = x / TN, cc = x % TN;
+            sa[kk][cc] = (k0 + kk < R && c0 + cc < R) ? Ainv[size_t(k0 + kk) * R + c0 + cc] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < TK; ++kk)
+        {
+            double y[4], a[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] = sy[kk][ty + 16 * q];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) a[q] = sa[kk][tx + 16 * q];
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[p][q] += y[p] * a[q];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+    {
+        const size_t i = i0 + ty + 16 * p;
+        if (i >= dim) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const int c = c0 + tx + 16 * q;
+            if (c >= R) continue;
+            const double v = acc[p][q];
+            F[i * R + c] = div ? v / div[c] : v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Column reductions: partial[p][r] over a row range, then ordered sums.
+// mode 0: sum F^2;  mode 1: sum F * M.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void col_partial_kernel(const double* __restrict__ F,
+                                                          const double* __restrict__ M,
+                                                          size_t rows, int R, size_t rpw,
+                                                          double* __restrict__ part)
+{
+    // thread t handles ranks r = t % R' ... with R' = min(R, 256) lanes per row
+    const int lanes = R < 256 ? R : 256;
+    const int rows_per_pass = 256 / lanes;
+    const int sub = threadIdx.x / lanes;
+    const int rl = threadIdx.x % lanes;
+    const size_t r_lo = size_t(blockIdx.x) * rpw;
+    const size_t r_hi = (r_lo + rpw < rows) ? r_lo + rpw : rows;
+    __shared__ double red[256];
+    for (int rb = 0; rb < R; rb += lanes)
+    {
+        const int r = rb + rl;
+        double s = 0.0;
+        if (sub < rows_per_pass && r < R)
+            for (size_t i = r_lo + sub; i < r_hi; i += rows_per_pass)
+            {
+                const double f = F[i * R + r];
+                s += M ? f * M[i * R + r] : f * f;
+            }
+        red[threadIdx.x] = s;
+        __syncthreads();
+        if (threadIdx.x < lanes && rb + threadIdx.x < R)
+        {
+            double t = 0.0;
+            for (int q = 0; q < rows_per_pass; ++q) t += red[q * lanes + threadIdx.x];
+            part[size_t(blockIdx.x) * R + rb + threadIdx.x] = t;
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void norms_finalize_kernel(const double* __restrict__ part, int P, int R,
+                                      double* __restrict__ norms)
+{
+    for (int r = threadIdx.x; r < R; r += blockDim.x)
+    {
+        double s = 0.0;
+        for (int p = 0; p < P; ++p) s += part[size_t(p) * R + r];
+        norms[r] = sqrt(s);
+    }
+}
+
+// als.cu:308-342
+__global__ void normalize_absorb_kernel(double* __restrict__ F, size_t rows, int R,
+                                        const double* __restrict__ norms,
+                                        double* __restrict__ lambda)
+{
+    const size_t total = rows * size_t(R);
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < total;
+         x += size_t(gridDim.x) * blockDim.x)
+    {
+        const int r = int(x % size_t(R));
+        const double n = norms[r];
+        F[x] = (n < 1e-14) ? 0.0 : F[x] / n;
+    }
+    if (blockIdx.x == 0)
+        for (int r = threadIdx.x; r < R; r += blockDim.x)
+        {
+            const double n = norms[r];
+            lambda[r] = (n < 1e-14) ? 0.0 : lambda[r] * n;
+        }
+}
+
+// iprod and model^2 of the Gram fit (als.cu:659-715)
+__global__ void fit_finalize_kernel(const double* __restrict__ part, int P, int R,
+                                    const double* __restrict__ lambda,
+                                    const double* __restrict__ grams, int ngram,
+                                    double* __restrict__ out2)
+{
+    __shared__ double red[256];
+    double ip = 0.0;
+    for (int r = threadIdx.x; r < R; r += blockDim.x)
+    {
+        double d = 0.0;
+        for (int p = 0; p < P; ++p) d += part[size_t(p) * R + r];
+        ip += lambda[r] * d;
+    }
+    double md = 0.0;
+    const int RR = R * R;
+    for (int x = threadIdx.x; x < RR; x += blockDim.x)
+    {
+        double v = lambda[x / R] * lambda[x % R];
+        for (int g = 0; g < ngram; ++g) v *= grams[size_t(g) * RR + x];
+        md += v;
+    }
+    red[threadIdx.x] = ip;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        double t = 0.0;
+        for (int q = 0; q < int(blockDim.x); ++q) t += red[q];
+        out2[0] = t;
+    }
+    __syncthreads();
+    red[threadIdx.x] = md;
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        double t = 0.0;
+        for (int q = 0; q < int(blockDim.x); ++q) t += red[q];
+        out2[1] = t;
+    }
+}
+
+int partials_for(size_t rows, size_t min_rows)
+{
+    size_t p = (rows + min_rows - 1) / min_rows;
+    if (p < 1) p = 1;
+    if (p > 256) p = 256;
+    return int(p);
+}
+
+}  // namespace
+
+extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && d_F && d_G, CPTC_ERR_ARG, "cptc_gram: bad arguments");
+    hipStream_t s = cptc::as_stream(stream);
+    const size_t RR = size_t(R) * R;
+    if (rows == 0)
+    {
+        CPTC_HIP(hipMemsetAsync(d_G, 0, RR * sizeof(double), s));
+        return CPTC_OK;
+    }
+    const int P = partials_for(rows, 64);
+    const size_t rpw = (rows + P - 1) / P;
+    void* part = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(P) * RR * sizeof(double), &part));
+    double* pd = static_cast<double*>(part);
+    if (R <= 16)
+    {
+        hipLaunchKernelGGL(gram_partial_kernel<1>, dim3(P, 1), dim3(256), 0, s, d_F, rows, R, rpw,
+                           1, pd);
+    }
+    else if (R <= 32)
+    {
+        hipLaunchKernelGGL(gram_partial_kernel<2>, dim3(P, 1), dim3(256), 0, s, d_F, rows, R, rpw,
+                           1, pd);
+    }
+    else if (R <= 64)
+    {
+        hipLaunchKernelGGL(gram_partial_kernel<4>, dim3(P, 1), dim3(256), 0, s, d_F, rows, R, rpw,
+                           1, pd);
+    }
+    else
+    {
+        const int nt = (R + 127) / 128;
+        hipLaunchKernelGGL(gram_partial_kernel<8>, dim3(P, nt * nt), dim3(256), 0, s, d_F, rows,
+                           R, rpw, nt, pd);
+    }
+    CPTC_LAUNCHED();
+    hipLaunchKernelGGL(sum_partials_kernel, dim3(cptc::grid_for(RR, 256, 1024)), dim3(256), 0, s,
+                       pd, P, RR, d_G);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_hadamard(const double* d_A, const double* d_B, double* d_C, size_t n,
+                             void* stream)
+{
+    CPTC_REQUIRE(d_A && d_B && d_C, CPTC_ERR_ARG, "cptc_hadamard: null pointer");
+    if (n == 0) return CPTC_OK;
+    hipLaunchKernelGGL(hadamard_kernel, dim3(cptc::grid_for(n, 256, 4096)), dim3(256), 0,
+                       cptc::as_stream(stream), d_A, d_B, d_C, n);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+namespace {
+int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStream_t s)
+{
+    const size_t RR = size_t(R) * R;
+    const bool use_lds = RR * sizeof(double) <= 128 * 1024;
+    // scratch: [work RR (global A when R > 128)] [V RR] [flag]
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, (2 * RR + 2) * sizeof(double), &buf));
+    double* work = static_cast<double*>(buf);
+    double* V = work + RR;
+    int* flag = d_path ? d_path : reinterpret_cast<int*>(V + RR);
+    const size_t lds = use_lds ? RR * sizeof(double) : 0;
+    static bool attr_set = false;
+    if (!attr_set)
+    {
+        CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(chol_inverse_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
+        CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(jacobi_pinv_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(chol_inverse_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work,
+                       d_Ainv, flag, int(use_lds));
+    CPTC_LAUNCHED();
+    hipLaunchKernelGGL(jacobi_pinv_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work, V,
+                       d_Ainv, flag, int(use_lds));
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+}  // namespace
+
+extern "C" int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path,
+                             void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 512 && d_FtF && d_Ainv, CPTC_ERR_ARG,
+                 "cptc_pinv_sym: bad arguments (R %d, supported 1..512)", R);
+    return pinv_launch(d_FtF, d_Ainv, R, d_path, cptc::as_stream(stream));
+}
+
+extern "C" int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
+                               int R, const double* d_div, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 512 && d_FtF && d_FtV && d_F, CPTC_ERR_ARG,
+                 "cptc_solve_pinv: bad arguments (R %d, supported 1..512)", R);
+    hipStream_t s = cptc::as_stream(stream);
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_FLAGS, size_t(R) * R * sizeof(double) + 64, &buf));
+    double* Ainv = static_cast<double*>(buf);
+    CPTC_TRY(pinv_launch(d_FtF, Ainv, R, nullptr, s));
+    if (dim == 0) return CPTC_OK;
+    dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
+    hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, s, d_FtV, Ainv, d_F, dim, R, d_div);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+namespace {
+int col_reduce(const double* F, const double* M, size_t rows, int R, hipStream_t s, double** part,
+               int* P_out)
+{
+    const int P = partials_for(rows, 256);
+    const size_t rpw = (rows + P - 1) / P;
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_REDUCE, size_t(P) * R * sizeof(double), &buf));
+    double* pd = static_cast<double*>(buf);
+    hipLaunchKernelGGL(col_partial_kernel, dim3(P), dim3(256), 0, s, F, M, rows, R, rpw, pd);
+    CPTC_LAUNCHED();
+    *part = pd;
+    *P_out = P;
+    return CPTC_OK;
+}
+}  // namespace
+
+extern "C" int cptc_colnorms(const double* d_F, size_t rows, int R, double* d_norms, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && d_F && d_norms, CPTC_ERR_ARG, "cptc_colnorms: bad arguments");
+    hipStream_t s = cptc::as_stream(stream);
+    double* part = nullptr;
+    int P = 0;
+    CPTC_TRY(col_reduce(d_F, nullptr, rows, R, s, &part, &P));
+    hipLaunchKernelGGL(norms_finalize_kernel, dim3(1), dim3(256), 0, s, part, P, R, d_norms);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_normalize_absorb(double* d_F, size_t rows, int R, const double* d_norms,
+                                     double* d_lambda, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && d_F && d_norms && d_lambda, CPTC_ERR_ARG,
+                 "cptc_normalize_absorb: bad arguments");
+    const size_t n = rows * size_t(R);
+    hipLaunchKernelGGL(normalize_absorb_kernel, dim3(cptc::grid_for(n, 256, 4096)), dim3(256), 0,
+                       cptc::as_stream(stream), d_F, rows, R, d_norms, d_lambda);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_fit_gram(const double* d_F, const double* d_M, size_t rows,
+                             const double* d_lambda, const double* d_grams, int ngram, int R,
+                             double* d_out2, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && d_F && d_M && d_lambda && d_grams && d_out2 && ngram >= 1,
+                 CPTC_ERR_ARG, "cptc_fit_gram: bad arguments");
+    hipStream_t s = cptc::as_stream(stream);
+    double* part = nullptr;
+    int P = 0;
+    CPTC_TRY(col_reduce(d_F, d_M, rows, R, s, &part, &P));
+    hipLaunchKernelGGL(fit_finalize_kernel, dim3(1), dim3(256), 0, s, part, P, R, d_lambda,
+                       d_grams, ngram, d_out2);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}

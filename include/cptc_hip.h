@@ -1,0 +1,284 @@
+/*
+ * cptc_hip.h — the C ABI of the MI355X CP-ALS engine (libcptc.so).
+ *
+ * Plain pointers, sizes and an opaque HIP stream (`void* stream`, a
+ * hipStream_t; NULL = the null stream).  Every entry point returns an int
+ * status: CPTC_OK (0) or a negative CPTC_ERR_* code; none of them exits the
+ * process.  The C++ interface in include/{tensor,cadr,partition,sparse,dense,
+ * solver,als,common,compute_fit,generic}.hpp sits on top of these and keeps
+ * the fatal-exit behaviour of the reference's C++ API.
+ *
+ * Layout conventions (identical to the reference's, cited per entry point):
+ *   factor matrices   row-major [row * R + r], fp64
+ *   Gram / FtF        R x R, fp64, symmetric
+ *   packed coords     (i << 30) | (j << 15) | k, 15-bit fields, uint64
+ *   row segments      blk_row / blk_start / blk_cnt, <= 1024 elements each
+ *   FtV               zeroed by the caller before a mode's MTTKRP launches;
+ *                     kernels only accumulate into it.
+ *
+ * Device pointers are marked d_; everything else is host memory.
+ */
+#ifndef CPTC_HIP_H
+#define CPTC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CPTC_MAX_MODES 8
+#define CPTC_SEG 1024 /* row-segment length: MTTKRP_CHUNK, sparse.hpp:14-24 */
+
+enum {
+    CPTC_OK = 0,
+    CPTC_ERR_ARG = -1,
+    CPTC_ERR_HIP = -2,
+    CPTC_ERR_UNSUPPORTED = -3,
+    CPTC_ERR_IO = -4,
+    CPTC_ERR_NUMERIC = -5,
+    CPTC_ERR_STATE = -6
+};
+
+enum { CPTC_VAL_LOGNORMAL = 0, CPTC_VAL_NORMAL = 1, CPTC_VAL_POISSON1P2 = 2 };
+
+/* Host COO tensor: idx is mode-major, idx[m * nnz + e], 0-based. */
+typedef struct cptc_coo {
+    int nmodes;
+    uint64_t dims[CPTC_MAX_MODES];
+    uint64_t nnz;
+    uint32_t* idx;
+    double* val;
+} cptc_coo;
+
+/* Frees idx/val of a cptc_coo filled by this library. */
+void cptc_coo_free(cptc_coo* c);
+
+/* Library status ---------------------------------------------------------- */
+const char* cptc_version(void);
+/* Last error message of the calling thread ("" if none). */
+const char* cptc_last_error(void);
+/* Number of visible HIP devices (0 on a host without a GPU; never faults). */
+int cptc_device_count(void);
+
+/* ========================================================================
+ * Ingest.
+ * ======================================================================== */
+
+/* Order-3 `.tns` parser with the reference's semantics: `i j k v` per line,
+ * ' '/'\t' separators, '#' lines and lines without a parsable value skipped,
+ * index m -> (m > 0 ? m - 1 : 0), dims = max + 1.
+ * Replaces load_tns_file (tensor.cu:39-271; tensor.hpp:346-349). */
+int cptc_tns_load3(const char* path, cptc_coo* out);
+
+/* Number of index columns of the first numeric line, or < 0.
+ * Replaces probe_tns_nmodes (generic.cu:983-1021; generic.hpp:30). */
+int cptc_tns_probe_nmodes(const char* path);
+
+/* N-order `.tns` parser with the generic driver's semantics.
+ * Replaces load_tns_generic (generic.cu:1023-1155; generic.hpp:31-34). */
+int cptc_tns_load_generic(const char* path, cptc_coo* out);
+
+/* Writes 1-based `.tns` text (shortest round-trip values). */
+int cptc_tns_write(const char* path, const cptc_coo* c);
+
+/* ========================================================================
+ * Synthetic inputs (deterministic for a seed; no reference counterpart).
+ * ======================================================================== */
+int cptc_synth_config(int config, uint64_t seed, cptc_coo* out);
+int cptc_synth_zipf(int nmodes, const uint64_t* dims, const double* exponents, uint64_t nnz,
+                    int value_kind, uint64_t seed, cptc_coo* out);
+int cptc_synth_lowrank3(uint64_t n, int rank, double keep_p, double noise_sigma, uint64_t seed,
+                        cptc_coo* out);
+int cptc_synth_blocks3(uint64_t n, int nblocks, double fill_lo, double fill_hi, double bg_density,
+                       uint64_t seed, cptc_coo* out);
+int cptc_synth_units5(const uint64_t* dims, int nunits, double fill_lo, double fill_hi,
+                      uint64_t total_nnz, int signal_rank, uint64_t seed, cptc_coo* out);
+
+/* ========================================================================
+ * Layout (bit-exact with the reference).
+ * ======================================================================== */
+
+/* CADR degree-descending relabel of an order-3 COO (host arrays).  Degrees
+ * are counted on the device; the relabel order is the reference's
+ * std::sort(iota, deg[a] > deg[b]) run on the host.  perm[m][old] = new.
+ * If `relabel` != 0 the coordinates are rewritten in place.
+ * Replaces compute_cadr_reordering + apply_cadr_reordering (cadr.cu:23-81). */
+int cptc_cadr3(int32_t* m0, int32_t* m1, int32_t* m2, size_t nnz, const uint64_t dims[3],
+               int32_t* perm0, int32_t* perm1, int32_t* perm2, int relabel);
+
+/* orig[old, :] = perm_factor[perm[old], :] on the device.
+ * Replaces unpermute_factor_kernel / unpermute_factor_matrices (cadr.cu:9-20, 84-103). */
+int cptc_unpermute_factor(const double* d_perm_factor, double* d_orig, const int32_t* d_perm,
+                          size_t dim, int R, void* stream);
+
+/* ========================================================================
+ * Order-3 kernels.
+ * ======================================================================== */
+
+/* FtV[row, r] += sum_e v_e * F1[o0_e, r] * F2[o1_e, r] over the row segments
+ * of one mode's row-sorted view; (F1, F2) = (B, C), (A, C), (A, B) for
+ * mode 0, 1, 2 and (o0, o1) = (j, k), (i, k), (i, j).  Any R >= 1.
+ * Replaces compute_sparse_mttkrp_async -> launch_mttkrp_rowsorted ->
+ * mttkrp_rowsorted_coalesced_kernel<R> / mttkrp_rowsorted_generic_kernel
+ * (sparse.cu:271-333, 614-711, 717-854). */
+int cptc_mttkrp_sparse3(int mode, const uint64_t* d_coords, const double* d_vals,
+                        const uint32_t* d_blk_row, const uint32_t* d_blk_start,
+                        const uint32_t* d_blk_cnt, size_t nblocks, const double* d_F1,
+                        const double* d_F2, double* d_FtV, int R, void* stream);
+
+/* Dense 16^3 tiles of an order-3 tensor on FP32 MFMA with an FP64 epilogue.
+ * d_tiles: ntiles x {bi, bj, bk, nnz} int32; d_tile_f32: ntiles x 4096 fp32
+ * cell values (layout (li*16 + lj)*16 + lk), built by cptc_dense_tiles_pack3.
+ * Replaces compute_dense_mttkrp_async -> dense_mttkrp_wmma_kernel ->
+ * dense_tile_mttkrp_wmma (dense.cu:89-1077, 1569-1621, 2072-2246). */
+int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const float* d_tile_f32,
+                             size_t ntiles, const double* d_A, const double* d_B,
+                             const double* d_C, double* d_FtV, int R, int dimI, int dimJ,
+                             int dimK, void* stream);
+
+/* Materialises dense tiles: cell (lid) of tile t holds the value of the last
+ * pool entry with that lid (pool order), clamped to +-FLT_MAX, as fp32;
+ * untouched cells are 0.  d_pool_off: ntiles+1 offsets into the pools.
+ * Same tile contents as the reference's per-call shared-memory build
+ * (dense.cu:150-190). */
+int cptc_dense_tiles_pack3(const int32_t* d_pool_lid, const double* d_pool_val,
+                           const uint64_t* d_pool_off, size_t ntiles, float* d_tile_f32,
+                           void* stream);
+
+/* G = F^T F for row-major F (rows x R); deterministic (fixed reduction order).
+ * Replaces compute_gram_matrix (cublasDgemm, als.cu:115-134) and g_gram_kernel
+ * (generic.cu:203-258). */
+int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, void* stream);
+
+/* C = A o B elementwise over n doubles (C may alias A or B).
+ * Replaces elementwise_mult_kernel (als.cu:101-106) and g_mul_kernel
+ * (generic.cu:50-88). */
+int cptc_hadamard(const double* d_A, const double* d_B, double* d_C, size_t n, void* stream);
+
+/* F = FtV * pinv(FtF) (row-major dim x R), then F[:, r] /= div[r] when
+ * d_div != NULL.  pinv by the truncated rule of the reference: singular
+ * values <= R * ulp(sigma_max) are dropped.  SPD fast path (Cholesky
+ * inverse) when every pivot exceeds 1e-9 * max diag; otherwise an on-device
+ * cyclic Jacobi eigen-decomposition applies the truncation rule exactly.
+ * Replaces solve_als_system_svd / _nosync + factor_divide_lambda_kernel
+ * (solver.cu:900-1096; als.cu:345-360, 485-499). */
+int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim, int R,
+                    const double* d_div, void* stream);
+
+/* Writes pinv(FtF) (R x R) to d_Ainv with the same rule as cptc_solve_pinv;
+ * *d_path (device int, may be NULL) receives 0 = Cholesky, 1 = Jacobi. */
+int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path, void* stream);
+
+/* norms[r] = ||F[:, r]||_2.  Replaces column_norms_kernel2 (als.cu:258-303). */
+int cptc_colnorms(const double* d_F, size_t rows, int R, double* d_norms, void* stream);
+
+/* F[:, r] /= n_r (0 if n_r < 1e-14); lambda[r] *= n_r (0 if n_r < 1e-14).
+ * Replaces normalize_absorb_lambda_kernel (als.cu:308-342). */
+int cptc_normalize_absorb(double* d_F, size_t rows, int R, const double* d_norms,
+                          double* d_lambda, void* stream);
+
+/* Gram fit scalars: out[0] = iprod = sum_r lambda_r <F[:, r], M[:, r]>,
+ * out[1] = model^2 = sum_{r,s} lambda_r lambda_s prod_m G_m[r, s]
+ * over the `ngram` Grams in d_grams (consecutive R x R blocks).
+ * Replaces the Gram fit of als.cu:659-715 and generic.cu:2174-2214. */
+int cptc_fit_gram(const double* d_F, const double* d_M, size_t rows, const double* d_lambda,
+                  const double* d_grams, int ngram, int R, double* d_out2, void* stream);
+
+/* Exact residual over one row-sorted order-3 view (any mode's view):
+ * out[0] += sum (v - sum_r lambda_r A B C)^2, out[1] += sum v^2.
+ * d_lambda NULL = no weights.  Replaces residual_sparse_view_kernel +
+ * sumsq_sparse_view_kernel (common.cu:251-342, 442-474). */
+int cptc_residual3_view(const uint64_t* d_coords, const double* d_vals, size_t nnz,
+                        const double* d_A, const double* d_B, const double* d_C,
+                        const double* d_lambda, int R, double* d_out2, void* stream);
+
+/* The same over dense-tile pools (entries, duplicates included).
+ * Replaces residual_dense_tiles_kernel + sumsq_dense_tiles_kernel
+ * (common.cu:345-439, 477-505). */
+int cptc_residual3_tiles(const int32_t* d_tiles, const uint64_t* d_pool_off,
+                         const int32_t* d_pool_lid, const double* d_pool_val, size_t ntiles,
+                         const double* d_A, const double* d_B, const double* d_C,
+                         const double* d_lambda, int R, double* d_out2, void* stream);
+
+/* ========================================================================
+ * Order-3 CP-ALS driver (main.cu:136-672 + als.cu:362-821).
+ * ======================================================================== */
+
+typedef struct cptc_als3_opts {
+    int R;               /* rank (main.cu:37: default 32) */
+    double threshold;    /* dense cutoff fraction (main.cu:44: 0.03); <= 0 auto-balance */
+    int path;            /* -1 env/auto, 0 auto, 1 force MFMA tiles, 2 force FP64 */
+    double fill_min;     /* < 0: env ALS_FILL_MIN or the CU-scaled default */
+    int skip_dense;      /* -1 env ALS_NO_DENSE, 0/1 */
+    int skip_sparse;     /* -1 env ALS_NO_SPARSE, 0/1 */
+    int cadr;            /* 1 = CADR relabel (the reference always does) */
+    uint64_t seed;       /* factor-init seed (common.cu:83: 42) */
+    int verbose;         /* 1 = reference-style stdout lines */
+} cptc_als3_opts;
+
+void cptc_als3_default_opts(cptc_als3_opts* o);
+
+/* Builds CADR relabel, factor init, partition, row-sorted views and path
+ * selection from a host order-3 COO.  *handle owns all device memory. */
+int cptc_als3_create(const cptc_coo* coo, const cptc_als3_opts* opts, void** handle);
+
+/* Layout and selection summary. */
+typedef struct cptc_als3_info {
+    uint64_t dims[3];
+    uint64_t nnz;
+    uint64_t sparse_nnz;      /* residual (FP64 kernel) */
+    uint64_t dense_nnz;       /* dense pool entries */
+    int64_t num_dense_tiles;
+    int dense_cutoff;
+    double avg_fill;
+    double fill_min;
+    int use_mfma;             /* 1 = dense tiles on MFMA, 0 = FP64 dense view */
+    uint64_t segments[3];     /* residual view segments per mode */
+    uint64_t dense_view_segments[3];
+    int num_cus;
+} cptc_als3_info;
+int cptc_als3_info_get(void* handle, cptc_als3_info* info);
+
+/* Runs `iters` ALS iterations (continuing from the current state).  Arrays
+ * of length iters (may be NULL): fit, ms per iteration (hipEvent span of
+ * als.cu:613, 722-726), ms of MTTKRP per iteration (sum over modes). */
+int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter, float* ms_mttkrp);
+
+/* Kernel times accumulated over cptc_als3_run iterations (hipEvents on the
+ * driver's stream): out6[m] = ms of the FP64 residual-view sparse MTTKRP
+ * kernel of mode m, out6[3 + m] = ms of all MTTKRP launches of mode m;
+ * *iters = iterations accumulated.  reset != 0 zeroes the sums after reading.
+ * No reference counterpart (measurement plumbing; ALS_PROFILE's
+ * per-phase events, als.cu:642-651, are the closest). */
+int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset);
+
+/* One mode's MTTKRP with the current factors into a host buffer (dim x R),
+ * through the same launches as the ALS loop.  For parity tests. */
+int cptc_als3_mttkrp(void* handle, int mode, double* host_out);
+
+/* Current factor `mode` (dim x R) to host; unpermuted=1 maps rows back to
+ * the input's index order (cadr.cu:84-103). */
+int cptc_als3_factor(void* handle, int mode, int unpermuted, double* host_out);
+int cptc_als3_set_factor(void* handle, int mode, const double* host_in);
+int cptc_als3_lambda(void* handle, double* host_out);
+
+/* Exact final fit report quantities: res^2, X^2 (common.cu:517-650). */
+int cptc_als3_residual(void* handle, double* res_sq, double* x_sq);
+
+/* Copies of the layout for bit-exactness tests.  Sizes via *_info first. */
+int cptc_als3_perm(void* handle, int mode, int32_t* host_out);
+int cptc_als3_view(void* handle, int which /*0 residual, 1 dense-fp64*/, int mode,
+                   uint64_t* coords, double* vals, uint32_t* blk_row, uint32_t* blk_start,
+                   uint32_t* blk_cnt);
+int cptc_als3_tiles(void* handle, int32_t* tiles4, uint64_t* pool_off, int32_t* pool_lid,
+                    double* pool_val);
+
+int cptc_als3_destroy(void* handle);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CPTC_HIP_H */

@@ -1,0 +1,275 @@
+// Python bindings of the CPU oracle — TEST INFRASTRUCTURE ONLY.
+// Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <omp.h>
+
+#include "cptc_oracle.hpp"
+
+namespace py = pybind11;
+using namespace oracle;
+
+template <class T>
+using arr = py::array_t<T, py::array::c_style | py::array::forcecast>;
+
+template <class T>
+std::vector<T> vec(const arr<T>& a)
+{
+    return std::vector<T>(a.data(), a.data() + a.size());
+}
+
+template <class T>
+arr<T> np(const std::vector<T>& v)
+{
+    arr<T> a(v.size());
+    if (!v.empty()) std::memcpy(a.mutable_data(), v.data(), v.size() * sizeof(T));
+    return a;
+}
+
+static void dims_from(const py::sequence& d, size_t out[3])
+{
+    for (int m = 0; m < 3; ++m) out[m] = d[m].cast<size_t>();
+}
+
+static Coo3 coo_from(arr<int32_t> m0, arr<int32_t> m1, arr<int32_t> m2, arr<double> v,
+                     py::sequence dims)
+{
+    Coo3 t;
+    t.m0 = vec(m0);
+    t.m1 = vec(m1);
+    t.m2 = vec(m2);
+    t.val = vec(v);
+    dims_from(dims, t.dims);
+    return t;
+}
+
+static py::dict part_to_dict(const Partition3& p)
+{
+    py::dict d;
+    d["cutoff"] = p.cutoff;
+    std::vector<int32_t> t4;
+    std::vector<uint64_t> off;
+    for (const Tile& t : p.tiles)
+    {
+        t4.insert(t4.end(), {t.b[0], t.b[1], t.b[2], t.nnz});
+        off.push_back(t.off);
+    }
+    off.push_back(p.pool_lid.size());
+    d["tiles"] = np(t4).attr("reshape")(py::make_tuple(-1, 4));
+    d["pool_off"] = np(off);
+    d["pool_lid"] = np(p.pool_lid);
+    d["pool_val"] = np(p.pool_val);
+    d["sp_i"] = np(p.sp_i);
+    d["sp_j"] = np(p.sp_j);
+    d["sp_k"] = np(p.sp_k);
+    d["sp_val"] = np(p.sp_val);
+    return d;
+}
+
+static Partition3 part_from_dict(const py::dict& d)
+{
+    Partition3 p;
+    p.cutoff = d["cutoff"].cast<int>();
+    auto t4 = d["tiles"].cast<arr<int32_t>>();
+    auto off = d["pool_off"].cast<arr<uint64_t>>();
+    const size_t nt = t4.size() / 4;
+    for (size_t t = 0; t < nt; ++t)
+    {
+        Tile tl;
+        for (int q = 0; q < 3; ++q) tl.b[q] = t4.data()[t * 4 + q];
+        tl.nnz = t4.data()[t * 4 + 3];
+        tl.off = off.data()[t];
+        p.tiles.push_back(tl);
+    }
+    p.pool_lid = vec(d["pool_lid"].cast<arr<int32_t>>());
+    p.pool_val = vec(d["pool_val"].cast<arr<double>>());
+    return p;
+}
+
+static py::list view_to_list(const View3& v)
+{
+    py::list l;
+    for (int m = 0; m < 3; ++m)
+    {
+        py::dict d;
+        d["coords"] = np(v.coords[m]);
+        d["vals"] = np(v.vals[m]);
+        d["blk_row"] = np(v.blk_row[m]);
+        d["blk_start"] = np(v.blk_start[m]);
+        d["blk_cnt"] = np(v.blk_cnt[m]);
+        l.append(d);
+    }
+    return l;
+}
+
+static View3 view_from_list(const py::list& l)
+{
+    View3 v;
+    for (int m = 0; m < 3; ++m)
+    {
+        py::dict d = l[m];
+        v.coords[m] = vec(d["coords"].cast<arr<uint64_t>>());
+        v.vals[m] = vec(d["vals"].cast<arr<double>>());
+        v.blk_row[m] = vec(d["blk_row"].cast<arr<uint32_t>>());
+        v.blk_start[m] = vec(d["blk_start"].cast<arr<uint32_t>>());
+        v.blk_cnt[m] = vec(d["blk_cnt"].cast<arr<uint32_t>>());
+        v.nnz = v.vals[m].size();
+    }
+    return v;
+}
+
+struct PyAls3
+{
+    View3 residual, dense_view;
+    Partition3 tiles;
+    bool has_dv = false, has_tiles = false;
+    Als3State st;
+    double x_sq = 0.0;
+
+    Als3Input input() const
+    {
+        Als3Input in;
+        in.residual = &residual;
+        in.dense_view = has_dv ? &dense_view : nullptr;
+        in.tiles = has_tiles ? &tiles : nullptr;
+        in.x_sq = x_sq;
+        return in;
+    }
+};
+
+PYBIND11_MODULE(cptc_oracle, m)
+{
+    m.doc() = "CPU oracle of the cpTC CP-ALS hot path (test infrastructure only)";
+
+    m.def("set_threads", [](int n) { omp_set_num_threads(n); });
+    m.def("max_threads", []() { return omp_get_max_threads(); });
+    m.def("set_num_cus", &set_num_cus);
+
+    m.def("load_tns3", [](const std::string& path) {
+        Coo3 t;
+        if (!load_tns3(path, t)) throw std::runtime_error("cannot open " + path);
+        return py::make_tuple(np(t.m0), np(t.m1), np(t.m2), np(t.val),
+                              py::make_tuple(t.dims[0], t.dims[1], t.dims[2]));
+    });
+
+    m.def("cadr3", [](arr<int32_t> m0, arr<int32_t> m1, arr<int32_t> m2, py::sequence dims) {
+        Coo3 t = coo_from(m0, m1, m2, arr<double>(0), dims);
+        t.val.resize(t.m0.size());
+        std::vector<int32_t> p[3];
+        cadr3(t, p);
+        return py::make_tuple(np(p[0]), np(p[1]), np(p[2]));
+    });
+
+    m.def("init_factors3", [](py::sequence dims, int R, unsigned seed) {
+        size_t d[3];
+        dims_from(dims, d);
+        std::vector<double> F[3];
+        init_factors3(d, R, seed, F);
+        return py::make_tuple(np(F[0]), np(F[1]), np(F[2]));
+    });
+
+    m.def("partition3", [](arr<int32_t> m0, arr<int32_t> m1, arr<int32_t> m2, arr<double> v,
+                           py::sequence dims, double thr) {
+        Coo3 t = coo_from(m0, m1, m2, v, dims);
+        Partition3 p;
+        partition3(t, thr, p);
+        return part_to_dict(p);
+    });
+
+    m.def("views3", [](arr<uint32_t> i, arr<uint32_t> j, arr<uint32_t> k, arr<double> v,
+                       py::sequence dims) {
+        size_t d[3];
+        dims_from(dims, d);
+        View3 out;
+        views3(vec(i), vec(j), vec(k), vec(v), d, out);
+        return view_to_list(out);
+    });
+
+    m.def("dense_views3", [](py::dict part, py::sequence dims) {
+        size_t d[3];
+        dims_from(dims, d);
+        Partition3 p = part_from_dict(part);
+        View3 out;
+        dense_views3(p, d, out);
+        return view_to_list(out);
+    });
+
+    m.def("mttkrp3_view", [](py::list view, int mode, arr<double> A, arr<double> B,
+                             arr<double> C, int R, size_t dim) {
+        View3 v = view_from_list(view);
+        std::vector<double> out(dim * size_t(R), 0.0);
+        mttkrp3_view(v, mode, A.data(), B.data(), C.data(), R, out.data());
+        return np(out);
+    });
+
+    m.def("mttkrp3_tiles", [](py::dict part, int mode, arr<double> A, arr<double> B,
+                              arr<double> C, int R, py::sequence dims) {
+        size_t d[3];
+        dims_from(dims, d);
+        Partition3 p = part_from_dict(part);
+        std::vector<double> out(d[mode] * size_t(R), 0.0);
+        mttkrp3_tiles(p, mode, A.data(), B.data(), C.data(), R, d, out.data());
+        return np(out);
+    });
+
+    m.def("gram", [](arr<double> F, int R) {
+        const size_t rows = F.size() / size_t(R);
+        std::vector<double> G(size_t(R) * R);
+        gram(F.data(), rows, R, G.data());
+        return np(G);
+    });
+
+    m.def("pinv_sym", [](arr<double> A, int R) {
+        std::vector<double> out(size_t(R) * R);
+        const int sweeps = pinv_sym(A.data(), R, out.data());
+        return py::make_tuple(np(out), sweeps);
+    });
+
+    py::class_<PyAls3>(m, "Als3")
+        .def(py::init([](py::list residual, py::object dense_view, py::object tiles, double x_sq,
+                         py::sequence dims, int R, arr<double> A, arr<double> B, arr<double> C,
+                         py::object lam) {
+            auto* s = new PyAls3();
+            s->residual = view_from_list(residual);
+            if (!dense_view.is_none())
+            {
+                s->dense_view = view_from_list(dense_view.cast<py::list>());
+                s->has_dv = true;
+            }
+            if (!tiles.is_none())
+            {
+                s->tiles = part_from_dict(tiles.cast<py::dict>());
+                s->has_tiles = !s->tiles.tiles.empty();
+            }
+            s->x_sq = x_sq;
+            s->st.R = R;
+            dims_from(dims, s->st.dims);
+            s->st.F[0] = vec(A);
+            s->st.F[1] = vec(B);
+            s->st.F[2] = vec(C);
+            if (lam.is_none())
+                s->st.lambda.assign(size_t(R), 1.0);
+            else
+                s->st.lambda = vec(lam.cast<arr<double>>());
+            return s;
+        }))
+        .def("iterate",
+             [](PyAls3& s, int iters) {
+                 std::vector<double> f(iters), ms(iters), mm(iters);
+                 Als3Input in = s.input();
+                 {
+                     py::gil_scoped_release rel;
+                     als3_iterate(in, s.st, iters, f.data(), ms.data(), mm.data());
+                 }
+                 return py::make_tuple(np(f), np(ms), np(mm));
+             })
+        .def("factor", [](PyAls3& s, int m) { return np(s.st.F[m]); })
+        .def("lam", [](PyAls3& s) { return np(s.st.lambda); })
+        .def("residual", [](PyAls3& s, bool with_lambda) {
+            double r = 0, x = 0;
+            residual3(s.input(), s.st, with_lambda, &r, &x);
+            return py::make_tuple(r, x);
+        });
+}

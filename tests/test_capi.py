@@ -1,0 +1,85 @@
+"""The C ABI library: loads, exports every symbol include/cptc_hip.h declares,
+and rejects bad arguments with CPTC_ERR_ARG before touching a device (so
+these run on a host without a GPU)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    syms = set()
+    for name in os.listdir(os.path.join(ROOT, "include")):
+        if name.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", name)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            syms |= set(re.findall(r"\b(cptc_[a-z0-9_]+)\s*\(", text))
+    return syms
+
+
+def test_library_exports_every_declared_symbol(ca):
+    lib = C.CDLL(ca.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 30
+    for s in sorted(syms):
+        assert hasattr(lib, s), f"{s} declared but not exported"
+    assert syms == set(ca.SIGNATURES), "Python bindings out of sync with the header"
+
+
+def test_version_and_no_device_here(ca):
+    assert b"gfx950" in ca.lib.cptc_version()
+    assert ca.lib.cptc_device_count() >= 0
+
+
+@pytest.mark.parametrize("call", [
+    lambda l: l.cptc_mttkrp_sparse3(3, 0, 0, 0, 0, 0, 10, 0, 0, 0, 32, None),
+    lambda l: l.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 10, 0, 0, 0, 0, None),
+    lambda l: l.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 10, 0, 0, 0, 32, None),
+    lambda l: l.cptc_mttkrp_dense_tiles3(5, 0, 0, 1, 0, 0, 0, 0, 16, 1, 1, 1, None),
+    lambda l: l.cptc_mttkrp_dense_tiles3(0, 0, 0, 1, 0, 0, 0, 0, 16, 1, 1, 1, None),
+    lambda l: l.cptc_gram(0, 10, 8, 0, None),
+    lambda l: l.cptc_hadamard(0, 0, 0, 10, None),
+    lambda l: l.cptc_solve_pinv(0, 0, 0, 10, 8, 0, None),
+    lambda l: l.cptc_pinv_sym(0, 0, 1024, 0, None),
+    lambda l: l.cptc_colnorms(0, 10, 8, 0, None),
+    lambda l: l.cptc_normalize_absorb(0, 10, 8, 0, 0, None),
+    lambda l: l.cptc_fit_gram(0, 0, 10, 0, 0, 3, 8, 0, None),
+    lambda l: l.cptc_residual3_view(0, 0, 10, 0, 0, 0, 0, 8, 0, None),
+    lambda l: l.cptc_residual3_tiles(0, 0, 0, 0, 1, 0, 0, 0, 0, 8, 0, None),
+    lambda l: l.cptc_unpermute_factor(0, 0, 0, 10, 8, None),
+    lambda l: l.cptc_dense_tiles_pack3(0, 0, 0, 4, 0, None),
+    lambda l: l.cptc_als3_run(None, 1, None, None, None),
+    lambda l: l.cptc_als3_info_get(None, None),
+])
+def test_bad_arguments_rejected(ca, call):
+    assert call(ca.lib) == -1
+    assert ca.lib.cptc_last_error() != b""
+
+
+def test_empty_work_is_ok(ca):
+    # zero segments / tiles: nothing to launch, success
+    assert ca.lib.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 32, None) == 0
+    assert ca.lib.cptc_mttkrp_dense_tiles3(0, 0, 0, 0, 0, 0, 0, 0, 16, 1, 1, 1, None) == 0
+    assert ca.lib.cptc_hadamard(1, 1, 1, 0, None) == 0
+
+
+def test_als3_create_rejects_non_order3(ca):
+    t = ca.Tensor((4, 4, 4, 4), np.zeros((4, 1), np.uint32), np.ones(1))
+    with pytest.raises(ca.CptcError):
+        ca.Als3(t, R=4)
+
+
+def test_als3_create_rejects_out_of_range_index(ca):
+    t = ca.Tensor((4, 4, 4), np.array([[0, 4], [1, 1], [2, 2]], np.uint32), np.ones(2))
+    with pytest.raises(ca.CptcError, match="index"):
+        ca.Als3(t, R=4)
+
+
+def test_cadr3_rejects_out_of_range_index(ca):
+    t = ca.Tensor((4, 4, 4), np.array([[0, 1], [1, 9], [2, 2]], np.uint32), np.ones(2))
+    with pytest.raises(ca.CptcError, match="index"):
+        ca.cadr3(t)

@@ -1,0 +1,148 @@
+"""Driver-level parity (cptc_als3_*): the device layout is bit-exact with the
+oracle (CADR permutations, partition tiles and pools, row-sorted views), the
+MTTKRP of every mode matches, and 20 ALS iterations reach the oracle's fit
+within 1e-4 (FP64 path and MFMA dense-tile path)."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_layout(orc, t, thr, cadr=True):
+    idx = t.idx.astype(np.int32)
+    if cadr:
+        perms = orc.cadr3(idx[0], idx[1], idx[2], t.dims)
+        idx = np.stack([perms[m][idx[m]] for m in range(3)]).astype(np.int32)
+    else:
+        perms = [np.arange(d, dtype=np.int32) for d in t.dims]
+    p = orc.partition3(idx[0], idx[1], idx[2], t.val, t.dims, thr)
+    v = orc.views3(p["sp_i"], p["sp_j"], p["sp_k"], p["sp_val"], t.dims)
+    return perms, p, v
+
+
+def clustered(ca, seed=0, n=64, blocks=12):
+    return ca.synth_blocks3(n, blocks, 0.1, 0.6, 2e-3, seed)
+
+
+CASES = [
+    ("zipf", 0.03), ("zipf", 0.0), ("blocks", 0.03), ("blocks", 0.001), ("blocks", 0.3),
+]
+
+
+def make(ca, kind, seed=1):
+    if kind == "zipf":
+        return ca.synth_zipf((700, 400, 1500), (1.1, 1.1, 1.1), 120000, 0, seed)
+    return clustered(ca, seed)
+
+
+@pytest.mark.parametrize("kind,thr", CASES)
+def test_layout_bit_exact(ca, orc, dev, kind, thr):
+    t = make(ca, kind)
+    perms, p, v = oracle_layout(orc, t, thr)
+    with ca.Als3(t, R=8, threshold=thr, path=2) as h:     # FP64 path: dense views too
+        for m in range(3):
+            assert np.array_equal(h.perm(m), perms[m]), f"perm {m}"
+        assert int(h.info.dense_cutoff) == p["cutoff"]
+        tl = h.tiles()
+        assert np.array_equal(tl["tiles"], p["tiles"])
+        assert np.array_equal(tl["pool_off"], p["pool_off"])
+        assert np.array_equal(tl["pool_lid"], p["pool_lid"])
+        assert np.array_equal(tl["pool_val"], p["pool_val"])
+        assert int(h.info.sparse_nnz) == len(p["sp_val"])
+        for m in range(3):
+            got = h.view(0, m)
+            for k in ("coords", "vals", "blk_row", "blk_start", "blk_cnt"):
+                assert np.array_equal(got[k], np.asarray(v[m][k])), (m, k)
+        if len(p["pool_val"]):
+            dv = orc.dense_views3(p, t.dims)
+            for m in range(3):
+                got = h.view(1, m)
+                for k in ("coords", "vals", "blk_row", "blk_start", "blk_cnt"):
+                    assert np.array_equal(got[k], np.asarray(dv[m][k])), ("dense", m, k)
+
+
+def test_cadr_entry_point_matches_oracle(ca, orc, dev):
+    t = ca.synth_zipf((300, 256, 999), (1.1, 0.0, 1.3), 50000, 0, 2)
+    perms, idx = ca.cadr3(t)
+    ref = orc.cadr3(*(t.idx[m].astype(np.int32) for m in range(3)), t.dims)
+    for m in range(3):
+        assert np.array_equal(perms[m], ref[m])
+        assert np.array_equal(idx[m], ref[m][t.idx[m]])
+
+
+def test_views_reject_wide_dims(ca, dev):
+    t = ca.Tensor((40000, 3, 3), np.array([[39999, 0], [0, 1], [0, 2]], np.uint32),
+                  np.array([1.0, 2.0]))
+    with pytest.raises(ca.CptcError):
+        ca.Als3(t, R=4, cadr=False)
+
+
+@pytest.mark.parametrize("kind,path,R", [("zipf", 2, 16), ("zipf", 2, 128), ("blocks", 1, 32),
+                                         ("blocks", 2, 32), ("zipf", 1, 20)])
+def test_mttkrp_every_mode(ca, orc, dev, kind, path, R):
+    t = make(ca, kind, 3)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+        F = [h.factor(m) for m in range(3)]
+        ref_init = orc.init_factors3(t.dims, R, 42)
+        for m in range(3):
+            assert np.array_equal(F[m].ravel(), ref_init[m])
+        mfma = int(h.info.use_mfma) == 1 and len(p["tiles"]) > 0
+        dv = orc.dense_views3(p, t.dims) if (not mfma and len(p["pool_val"])) else None
+        for mode in range(3):
+            ref = orc.mttkrp3_view(v, mode, *(f.ravel() for f in F), R, t.dims[mode])
+            if mfma:
+                ref = ref + orc.mttkrp3_tiles(p, mode, *(f.ravel() for f in F), R, t.dims)
+            elif dv is not None:
+                ref = ref + orc.mttkrp3_view(dv, mode, *(f.ravel() for f in F), R, t.dims[mode])
+            got = h.mttkrp(mode)
+            tol = 1e-5 if mfma else 1e-10
+            assert rel_err(got, ref.reshape(t.dims[mode], R)) <= tol, mode
+
+
+@pytest.mark.parametrize("kind,path,R", [("zipf", 2, 16), ("blocks", 1, 16), ("blocks", 2, 16),
+                                         ("zipf", 0, 64)])
+def test_als_fit_matches_oracle_20_iters(ca, orc, dev, kind, path, R):
+    t = make(ca, kind, 4)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+        F = [h.factor(m).ravel() for m in range(3)]
+        mfma = int(h.info.use_mfma) == 1 and len(p["tiles"]) > 0
+        tiles = p if mfma else None
+        dv = orc.dense_views3(p, t.dims) if (not mfma and len(p["pool_val"])) else None
+        o = orc.Als3(v, dv, tiles, float(np.sum(t.val ** 2)), t.dims, R, *F, None)
+        fit, ms, mt = h.run(20)
+        ofit, _, _ = o.iterate(20)
+        assert np.max(np.abs(fit - ofit)) <= 1e-4, (fit[-3:], ofit[-3:])
+        assert np.all(ms > 0) and np.all(mt > 0) and np.all(mt <= ms)
+        res, x2 = h.residual()
+        ores, ox2 = o.residual(True)
+        assert abs(x2 - ox2) <= 1e-12 * ox2
+        assert abs(res - ores) <= 1e-3 * ores
+        lam = h.lam()
+        assert rel_err(lam, o.lam()) <= 1e-3
+        # unpermuted export: row x of the exported factor = row perm[x] in the relabelled space
+        for m in range(3):
+            assert np.array_equal(h.factor(m, unpermuted=True), h.factor(m)[perms[m]])
+
+
+def test_cli_runs_and_exports(ca, dev, tmp_path):
+    t = make(ca, "zipf", 5)
+    path = str(tmp_path / "t.tns")
+    ca.write_tns(path, t)
+    env = dict(os.environ, ALS_EXPORT_FACTORS=str(tmp_path / "f"))
+    out = subprocess.run([ca.CLI_PATH, path, "3", "8"], env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert out.returncode == 0, out.stderr
+    iters = [l for l in out.stdout.splitlines() if l.startswith("[ALS] iter ")]
+    assert len(iters) == 3 and "time=" in iters[0] and "fit=" in iters[0]
+    lines = open(str(tmp_path / "f.0.out")).read().split("\n")
+    assert lines[0] == "matrix" and lines[1] == "2" and lines[2] == f"{t.dims[0]} 8"
+    assert len([x for x in lines[3:] if x]) == t.dims[0] * 8
+    lam = open(str(tmp_path / "f.lambda.out")).read().split("\n")
+    assert lam[:3] == ["vector", "1", "8"]
