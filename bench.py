@@ -104,17 +104,12 @@ def main() -> int:
         log(f"warmup {args.warmup} iterations done")
     h.kernel_times(reset=True)
 
-    # timed region: exactly K ALS iterations; the driver's stream is
-    # synchronised at the end of each iteration (fit readback)
-    try:
-        import torch
-        torch.cuda.synchronize()
-    except Exception:  # torch is plumbing only
-        torch = None
+    # timed region: exactly K ALS iterations between two device-wide
+    # synchronisations (one GPU: no barrier across ranks is needed)
+    ca.sync()
     t0 = time.perf_counter()
     fits, ms_iter, ms_mtt = h.run(args.steps)
-    if torch is not None:
-        torch.cuda.synchronize()
+    ca.sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
     sp_ms, mt_ms, kit = h.kernel_times(reset=True)

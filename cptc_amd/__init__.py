@@ -19,6 +19,7 @@ __all__ = [
     "lib", "LIB_PATH", "CLI_PATH", "SIGNATURES", "CptcError", "Tensor", "synth_config",
     "synth_zipf", "synth_lowrank3", "synth_blocks3", "synth_units5", "load_tns3",
     "load_tns_generic", "probe_nmodes", "write_tns", "cadr3", "Als3", "device_count", "ptr",
+    "DevBuf", "sync",
 ]
 
 
@@ -27,12 +28,59 @@ def device_count() -> int:
 
 
 def ptr(x) -> int:
-    """Raw device/host address of a torch tensor or numpy array (None -> 0)."""
+    """Raw address of a DevBuf, numpy array or object with data_ptr() (None -> 0)."""
     if x is None:
         return 0
     if isinstance(x, np.ndarray):
         return x.ctypes.data
     return int(x.data_ptr())
+
+
+def sync() -> None:
+    check(lib.cptc_dev_sync(), "cptc_dev_sync")
+
+
+class DevBuf:
+    """A device allocation made by libcptc's own HIP runtime."""
+
+    def __init__(self, nbytes: int, dtype=np.uint8, shape=None):
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (nbytes // self.dtype.itemsize,)
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(lib.cptc_dev_malloc(self.nbytes, C.byref(p)), "cptc_dev_malloc")
+        self._p = p
+
+    @classmethod
+    def from_numpy(cls, a) -> "DevBuf":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, a.dtype, a.shape)
+        check(lib.cptc_dev_upload(b._p, a.ctypes.data, a.nbytes), "cptc_dev_upload")
+        return b
+
+    @classmethod
+    def zeros(cls, shape, dtype=np.float64) -> "DevBuf":
+        dt = np.dtype(dtype)
+        n = int(np.prod(shape)) * dt.itemsize
+        b = cls(n, dt, shape)
+        check(lib.cptc_dev_memset(b._p, 0, n), "cptc_dev_memset")
+        return b
+
+    def data_ptr(self) -> int:
+        return int(self._p.value or 0)
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib.cptc_dev_download(out.ctypes.data, self._p, self.nbytes), "cptc_dev_download")
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "_p", None) is not None and self._p.value:
+            lib.cptc_dev_free(self._p)
+            self._p = C.c_void_p()
+
+    def __del__(self):
+        self.free()
 
 
 @dataclass

@@ -78,6 +78,12 @@ SIGNATURES = {
     "cptc_version": (C.c_char_p, []),
     "cptc_last_error": (C.c_char_p, []),
     "cptc_device_count": (_I, []),
+    "cptc_dev_malloc": (_I, [_Z, C.POINTER(_P)]),
+    "cptc_dev_free": (_I, [_P]),
+    "cptc_dev_upload": (_I, [_P, _P, _Z]),
+    "cptc_dev_download": (_I, [_P, _P, _Z]),
+    "cptc_dev_memset": (_I, [_P, _I, _Z]),
+    "cptc_dev_sync": (_I, []),
     "cptc_tns_load3": (_I, [C.c_char_p, C.POINTER(Coo)]),
     "cptc_tns_probe_nmodes": (_I, [C.c_char_p]),
     "cptc_tns_load_generic": (_I, [C.c_char_p, C.POINTER(Coo)]),

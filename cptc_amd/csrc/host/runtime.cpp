@@ -90,3 +90,48 @@ extern "C" int cptc_device_count(void)
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
     return n;
 }
+
+extern "C" int cptc_dev_malloc(size_t bytes, void** d_ptr)
+{
+    CPTC_REQUIRE(d_ptr, CPTC_ERR_ARG, "cptc_dev_malloc: null out pointer");
+    *d_ptr = nullptr;
+    CPTC_HIP(hipMalloc(d_ptr, bytes ? bytes : 1));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dev_free(void* d_ptr)
+{
+    if (d_ptr) CPTC_HIP(hipFree(d_ptr));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dev_upload(void* d_dst, const void* src, size_t bytes)
+{
+    if (bytes == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_dst && src, CPTC_ERR_ARG, "cptc_dev_upload: null pointer");
+    CPTC_HIP(hipMemcpy(d_dst, src, bytes, hipMemcpyHostToDevice));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dev_download(void* dst, const void* d_src, size_t bytes)
+{
+    if (bytes == 0) return CPTC_OK;
+    CPTC_REQUIRE(dst && d_src, CPTC_ERR_ARG, "cptc_dev_download: null pointer");
+    CPTC_HIP(hipMemcpy(dst, d_src, bytes, hipMemcpyDeviceToHost));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dev_memset(void* d_ptr, int value, size_t bytes)
+{
+    if (bytes == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_ptr, CPTC_ERR_ARG, "cptc_dev_memset: null pointer");
+    CPTC_HIP(hipMemset(d_ptr, value, bytes));
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dev_sync(void)
+{
+    CPTC_HIP(hipDeviceSynchronize());
+    CPTC_HIP(hipGetLastError());
+    return CPTC_OK;
+}

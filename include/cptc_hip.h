@@ -62,6 +62,18 @@ const char* cptc_last_error(void);
 /* Number of visible HIP devices (0 on a host without a GPU; never faults). */
 int cptc_device_count(void);
 
+/* Device-memory plumbing for callers without a HIP runtime of their own
+ * (tests, bench, scripting hosts): the library's runtime does the allocation
+ * and copies, so one process never loads two HIP runtimes.  No reference
+ * counterpart (the reference calls cudaMalloc/cudaMemcpy directly). */
+int cptc_dev_malloc(size_t bytes, void** d_ptr);
+int cptc_dev_free(void* d_ptr);
+int cptc_dev_upload(void* d_dst, const void* src, size_t bytes);
+int cptc_dev_download(void* dst, const void* d_src, size_t bytes);
+int cptc_dev_memset(void* d_ptr, int value, size_t bytes);
+/* hipDeviceSynchronize, reporting any pending asynchronous error. */
+int cptc_dev_sync(void);
+
 /* ========================================================================
  * Ingest.
  * ======================================================================== */

@@ -29,12 +29,10 @@ def ca():
 
 @pytest.fixture(scope="session")
 def dev(ca):
-    """torch on cuda:0 for device buffers; the HIP library must see a GPU."""
-    import torch
+    """Device 0 through libcptc's own HIP runtime (device buffers are
+    cptc_amd.DevBuf; no second HIP runtime is loaded into the process)."""
     assert ca.device_count() >= 1, "GPU test run without a visible HIP device"
-    assert torch.cuda.is_available()
-    torch.cuda.set_device(0)
-    return torch
+    return ca
 
 
 def rel_err(got, ref):

@@ -1,4 +1,4 @@
-"""Kernel-level parity through the C ABI (device buffers from torch) against
+"""Kernel-level parity through the C ABI (device buffers from cptc_dev_*) against
 the CPU oracle and numpy closed forms.
 
 Bars: sparse FP64 MTTKRP <= 1e-10 relative; dense-tile FP32-MFMA MTTKRP
@@ -13,12 +13,16 @@ from conftest import rel_err
 pytestmark = pytest.mark.gpu
 
 
-def to_dev(torch, a):
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+def to_dev(ca, a):
+    return ca.DevBuf.from_numpy(a)
 
 
-def stream(torch):
-    return torch.cuda.current_stream().cuda_stream
+def zeros(ca, shape, dtype=np.float64):
+    return ca.DevBuf.zeros(shape, dtype)
+
+
+def stream(_ca):
+    return None   # the null stream
 
 
 def zipf_views(ca, orc, dims, nnz, seed, dup=False):
@@ -33,51 +37,49 @@ def zipf_views(ca, orc, dims, nnz, seed, dup=False):
 
 @pytest.mark.parametrize("R", [1, 3, 8, 16, 31, 32, 64, 100, 128, 200])
 def test_sparse_mttkrp_vs_oracle(ca, orc, dev, R):
-    torch = dev
     dims = (500, 300, 900)
     t, views = zipf_views(ca, orc, dims, 60000, R, dup=True)
     rng = np.random.default_rng(R)
     F = [rng.standard_normal((d, R)) for d in dims]
-    dF = [to_dev(torch, f) for f in F]
+    dF = [to_dev(ca, f) for f in F]
     for mode in range(3):
         v = views[mode]
         ref = orc.mttkrp3_view(views, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
                                dims[mode]).reshape(dims[mode], R)
-        dc, dv = to_dev(torch, v["coords"]), to_dev(torch, v["vals"])
-        br, bs, bc = (to_dev(torch, v[k]) for k in ("blk_row", "blk_start", "blk_cnt"))
-        out = torch.zeros((dims[mode], R), dtype=torch.float64, device="cuda:0")
+        dc, dv = to_dev(ca, v["coords"]), to_dev(ca, v["vals"])
+        br, bs, bc = (to_dev(ca, v[k]) for k in ("blk_row", "blk_start", "blk_cnt"))
+        out = zeros(ca, (dims[mode], R))
         F1 = dF[1] if mode == 0 else dF[0]
         F2 = dF[1] if mode == 2 else dF[2]
         rc = ca.lib.cptc_mttkrp_sparse3(mode, dc.data_ptr(), dv.data_ptr(), br.data_ptr(),
                                         bs.data_ptr(), bc.data_ptr(), len(v["blk_row"]),
                                         F1.data_ptr(), F2.data_ptr(), out.data_ptr(), R,
-                                        stream(torch))
+                                        stream(ca))
         assert rc == 0, ca.lib.cptc_last_error()
-        torch.cuda.synchronize()
-        assert rel_err(out.cpu().numpy(), ref) <= 1e-10, (mode, R)
+        ca.sync()
+        assert rel_err(out.numpy(), ref) <= 1e-10, (mode, R)
 
 
 def test_sparse_mttkrp_misaligned_factor_base(ca, orc, dev):
     """Factor bases that are only 8-byte aligned take the scalar path."""
-    torch = dev
     R, dims = 16, (200, 150, 300)
     t, views = zipf_views(ca, orc, dims, 20000, 4)
     rng = np.random.default_rng(0)
     F = [rng.random((d, R)) for d in dims]
     ref = orc.mttkrp3_view(views, 0, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
                            dims[0]).reshape(dims[0], R)
-    big = to_dev(torch, np.concatenate([[0.0], F[1].ravel(), F[2].ravel()]))
+    big = to_dev(ca, np.concatenate([[0.0], F[1].ravel(), F[2].ravel()]))
     F1p = big.data_ptr() + 8
     F2p = F1p + F[1].size * 8
     v = views[0]
-    dc, dv = to_dev(torch, v["coords"]), to_dev(torch, v["vals"])
-    br, bs, bc = (to_dev(torch, v[k]) for k in ("blk_row", "blk_start", "blk_cnt"))
-    out = torch.zeros((dims[0], R), dtype=torch.float64, device="cuda:0")
+    dc, dv = to_dev(ca, v["coords"]), to_dev(ca, v["vals"])
+    br, bs, bc = (to_dev(ca, v[k]) for k in ("blk_row", "blk_start", "blk_cnt"))
+    out = zeros(ca, (dims[0], R))
     assert ca.lib.cptc_mttkrp_sparse3(0, dc.data_ptr(), dv.data_ptr(), br.data_ptr(),
                                       bs.data_ptr(), bc.data_ptr(), len(v["blk_row"]), F1p, F2p,
-                                      out.data_ptr(), R, stream(torch)) == 0
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), ref) <= 1e-10
+                                      out.data_ptr(), R, stream(ca)) == 0
+    ca.sync()
+    assert rel_err(out.numpy(), ref) <= 1e-10
 
 
 def block_tensor(rng, dims, fill=0.5):
@@ -95,7 +97,6 @@ def block_tensor(rng, dims, fill=0.5):
 
 @pytest.mark.parametrize("R", [8, 16, 20, 32, 128])
 def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R):
-    torch = dev
     rng = np.random.default_rng(50 + R)
     dims = (40, 45, 37)               # boundary tiles in every mode
     idx, val = block_tensor(rng, dims)
@@ -103,95 +104,91 @@ def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R):
     nt = len(p["tiles"])
     assert nt >= 4
     F = [rng.random((d, R)) - 0.3 for d in dims]
-    dF = [to_dev(torch, f) for f in F]
-    tiles = to_dev(torch, p["tiles"].astype(np.int32))
-    off = to_dev(torch, p["pool_off"])
-    lid = to_dev(torch, p["pool_lid"])
-    pv = to_dev(torch, p["pool_val"])
-    tf = torch.empty(nt * 4096, dtype=torch.float32, device="cuda:0")
+    dF = [to_dev(ca, f) for f in F]
+    tiles = to_dev(ca, p["tiles"].astype(np.int32))
+    off = to_dev(ca, p["pool_off"])
+    lid = to_dev(ca, p["pool_lid"])
+    pv = to_dev(ca, p["pool_val"])
+    tf = zeros(ca, (nt * 4096,), np.float32)
     assert ca.lib.cptc_dense_tiles_pack3(lid.data_ptr(), pv.data_ptr(), off.data_ptr(), nt,
-                                         tf.data_ptr(), stream(torch)) == 0
+                                         tf.data_ptr(), stream(ca)) == 0
     for mode in range(3):
         ref = orc.mttkrp3_tiles(p, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
                                 dims).reshape(dims[mode], R)
-        out = torch.zeros((dims[mode], R), dtype=torch.float64, device="cuda:0")
+        out = zeros(ca, (dims[mode], R))
         rc = ca.lib.cptc_mttkrp_dense_tiles3(mode, tiles.data_ptr(), tf.data_ptr(), nt,
                                              dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
-                                             out.data_ptr(), R, *dims, stream(torch))
+                                             out.data_ptr(), R, *dims, stream(ca))
         assert rc == 0, ca.lib.cptc_last_error()
-        torch.cuda.synchronize()
-        assert rel_err(out.cpu().numpy(), ref) <= 1e-5, (mode, R)
+        ca.sync()
+        assert rel_err(out.numpy(), ref) <= 1e-5, (mode, R)
 
 
 def test_dense_tile_pack_last_write_wins(ca, orc, dev):
-    torch = dev
     rng = np.random.default_rng(1)
     cells = np.array(np.meshgrid(*[np.arange(16)] * 3, indexing="ij")).reshape(3, -1)
     idx = np.concatenate([cells, cells[:, :300]], axis=1).astype(np.int32)
     val = rng.standard_normal(idx.shape[1])
     val[5] = 1e300                                   # clamped to FLT_MAX
     p = orc.partition3(idx[0], idx[1], idx[2], val, (16, 16, 16), 0.5)
-    tf = torch.empty(4096, dtype=torch.float32, device="cuda:0")
-    args = [to_dev(torch, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]
+    tf = zeros(ca, (4096,), np.float32)
+    args = [to_dev(ca, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]
     assert ca.lib.cptc_dense_tiles_pack3(*(a.data_ptr() for a in args), 1, tf.data_ptr(),
-                                         stream(torch)) == 0
-    torch.cuda.synchronize()
+                                         stream(ca)) == 0
+    ca.sync()
     X = np.zeros((16, 16, 16))
     X[tuple(idx)] = np.clip(val, -np.finfo(np.float32).max, np.finfo(np.float32).max)
-    assert np.array_equal(tf.cpu().numpy(), X.ravel().astype(np.float32))
+    assert np.array_equal(tf.numpy(), X.ravel().astype(np.float32))
 
 
 @pytest.mark.parametrize("rows,R", [(1, 1), (1000, 7), (28818, 128), (5000, 200), (0, 16)])
 def test_gram(ca, dev, rows, R):
-    torch = dev
     F = np.random.default_rng(rows + R).standard_normal((rows, R))
-    dF = to_dev(torch, F)
-    G = torch.empty((R, R), dtype=torch.float64, device="cuda:0")
-    assert ca.lib.cptc_gram(dF.data_ptr(), rows, R, G.data_ptr(), stream(torch)) == 0
-    torch.cuda.synchronize()
-    assert rel_err(G.cpu().numpy(), F.T @ F) < 1e-13 if rows else np.all(G.cpu().numpy() == 0)
+    dF = to_dev(ca, F)
+    G = zeros(ca, (R, R))
+    assert ca.lib.cptc_gram(dF.data_ptr(), rows, R, G.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    assert rel_err(G.numpy(), F.T @ F) < 1e-13 if rows else np.all(G.numpy() == 0)
 
 
 @pytest.mark.parametrize("R", [1, 5, 16, 32, 128])
 def test_solve_pinv_spd(ca, dev, R):
-    torch = dev
     rng = np.random.default_rng(R)
     Fa, Fb = rng.random((3 * R + 20, R)), rng.random((2 * R + 30, R))
     A = (Fa.T @ Fa) * (Fb.T @ Fb)
     dim = 777
     Y = rng.standard_normal((dim, R))
     lam = rng.random(R) + 0.5
-    dA, dY, dl = to_dev(torch, A), to_dev(torch, Y), to_dev(torch, lam)
-    out = torch.empty((dim, R), dtype=torch.float64, device="cuda:0")
-    path = torch.zeros(1, dtype=torch.int32, device="cuda:0")
-    Ainv = torch.empty((R, R), dtype=torch.float64, device="cuda:0")
+    dA, dY, dl = to_dev(ca, A), to_dev(ca, Y), to_dev(ca, lam)
+    out = zeros(ca, (dim, R))
+    path = zeros(ca, (1,), np.int32)
+    Ainv = zeros(ca, (R, R))
     assert ca.lib.cptc_pinv_sym(dA.data_ptr(), Ainv.data_ptr(), R, path.data_ptr(),
-                                stream(torch)) == 0
+                                stream(ca)) == 0
     assert ca.lib.cptc_solve_pinv(dA.data_ptr(), dY.data_ptr(), out.data_ptr(), dim, R,
-                                  dl.data_ptr(), stream(torch)) == 0
-    torch.cuda.synchronize()
-    assert int(path.item()) == 0                    # Cholesky fast path
+                                  dl.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    assert int(path.numpy()[0]) == 0                    # Cholesky fast path
     inv = np.linalg.inv(A)
-    assert rel_err(Ainv.cpu().numpy(), inv) < 1e-9
-    assert rel_err(out.cpu().numpy(), (Y @ inv) / lam) < 1e-9
+    assert rel_err(Ainv.numpy(), inv) < 1e-9
+    assert rel_err(out.numpy(), (Y @ inv) / lam) < 1e-9
 
 
 def test_pinv_singular_takes_jacobi_path(ca, orc, dev):
-    torch = dev
     rng = np.random.default_rng(3)
     R = 24
     F = rng.random((60, R))
     F[:, 7] = F[:, 3]
     F[:, 11] = 0.0
     A = F.T @ F
-    dA = to_dev(torch, A)
-    Ainv = torch.empty((R, R), dtype=torch.float64, device="cuda:0")
-    path = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    dA = to_dev(ca, A)
+    Ainv = zeros(ca, (R, R))
+    path = zeros(ca, (1,), np.int32)
     assert ca.lib.cptc_pinv_sym(dA.data_ptr(), Ainv.data_ptr(), R, path.data_ptr(),
-                                stream(torch)) == 0
-    torch.cuda.synchronize()
-    assert int(path.item()) == 1
-    P = Ainv.cpu().numpy()
+                                stream(ca)) == 0
+    ca.sync()
+    assert int(path.numpy()[0]) == 1
+    P = Ainv.numpy()
     ref, _ = orc.pinv_sym(A.ravel(), R)
     assert rel_err(P, ref.reshape(R, R)) < 1e-8
     assert rel_err(A @ P @ A, A) < 1e-10
@@ -199,32 +196,31 @@ def test_pinv_singular_takes_jacobi_path(ca, orc, dev):
 
 
 def test_norms_normalize_fit(ca, dev):
-    torch = dev
     rng = np.random.default_rng(8)
     rows, R = 3001, 32
     F = rng.standard_normal((rows, R))
     F[:, 4] = 0.0                                    # zero column: n < 1e-14
     M = rng.standard_normal((rows, R))
     lam = rng.random(R) + 0.1
-    dF, dM, dl = to_dev(torch, F), to_dev(torch, M), to_dev(torch, lam)
-    n = torch.empty(R, dtype=torch.float64, device="cuda:0")
-    assert ca.lib.cptc_colnorms(dF.data_ptr(), rows, R, n.data_ptr(), stream(torch)) == 0
+    dF, dM, dl = to_dev(ca, F), to_dev(ca, M), to_dev(ca, lam)
+    n = zeros(ca, (R,))
+    assert ca.lib.cptc_colnorms(dF.data_ptr(), rows, R, n.data_ptr(), stream(ca)) == 0
     assert ca.lib.cptc_normalize_absorb(dF.data_ptr(), rows, R, n.data_ptr(), dl.data_ptr(),
-                                        stream(torch)) == 0
-    torch.cuda.synchronize()
+                                        stream(ca)) == 0
+    ca.sync()
     nr = np.sqrt(np.sum(F * F, axis=0))
-    assert rel_err(n.cpu().numpy(), nr) < 1e-14
+    assert rel_err(n.numpy(), nr) < 1e-14
     Fn = np.where(nr < 1e-14, 0.0, F / np.where(nr < 1e-14, 1, nr))
-    assert rel_err(dF.cpu().numpy(), Fn) < 1e-14
-    assert rel_err(dl.cpu().numpy(), np.where(nr < 1e-14, 0.0, lam * nr)) < 1e-14
+    assert rel_err(dF.numpy(), Fn) < 1e-14
+    assert rel_err(dl.numpy(), np.where(nr < 1e-14, 0.0, lam * nr)) < 1e-14
     G = [rng.random((R, R)) for _ in range(3)]
-    dG = to_dev(torch, np.concatenate([g.ravel() for g in G]))
-    out = torch.empty(2, dtype=torch.float64, device="cuda:0")
-    lam2 = dl.cpu().numpy()
+    dG = to_dev(ca, np.concatenate([g.ravel() for g in G]))
+    out = zeros(ca, (2,))
+    lam2 = dl.numpy()
     assert ca.lib.cptc_fit_gram(dF.data_ptr(), dM.data_ptr(), rows, dl.data_ptr(), dG.data_ptr(),
-                                3, R, out.data_ptr(), stream(torch)) == 0
-    torch.cuda.synchronize()
+                                3, R, out.data_ptr(), stream(ca)) == 0
+    ca.sync()
     ip = np.sum(lam2 * np.sum(Fn * M, axis=0))
     md = np.sum(np.outer(lam2, lam2) * G[0] * G[1] * G[2])
-    o = out.cpu().numpy()
+    o = out.numpy()
     assert abs(o[0] - ip) < 1e-10 * abs(ip) and abs(o[1] - md) < 1e-12 * abs(md)
