@@ -68,7 +68,11 @@ def main() -> int:
     ap.add_argument("--R", type=int, default=0)
     ap.add_argument("--cpu-iters", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib", action="store_true",
+                    help="run only a streaming kernel of known size (PMC scaling)")
     args = ap.parse_args()
+    if args.calib:
+        return calib()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here "
@@ -176,6 +180,22 @@ def main() -> int:
     }
     h.close()
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def calib() -> int:
+    """A streaming kernel of known size for scaling rocprofv3 FETCH_SIZE /
+    WRITE_SIZE: cptc_hadamard over n doubles reads 16 n and writes 8 n bytes."""
+    import cptc_amd as ca
+
+    n = 1 << 25
+    a, b, c = (ca.DevBuf.zeros((n,)) for _ in range(3))
+    for _ in range(5):
+        ca.check(ca.lib.cptc_hadamard(a.data_ptr(), b.data_ptr(), c.data_ptr(), n, None),
+                 "cptc_hadamard")
+    ca.sync()
+    print(json.dumps({"calib": "hadamard_kernel", "n": n, "read_bytes": 16 * n,
+                      "write_bytes": 8 * n, "launches": 5}), flush=True)
     return 0
 
 

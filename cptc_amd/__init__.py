@@ -13,13 +13,13 @@ from dataclasses import dataclass
 import numpy as np
 
 from ._lib import (CLI_PATH, LIB_PATH, SIGNATURES, Als3Info, Als3Opts, Coo, CptcError, check,
-                   lib)
+                   lib)  # noqa: F401  (check is part of the public surface)
 
 __all__ = [
     "lib", "LIB_PATH", "CLI_PATH", "SIGNATURES", "CptcError", "Tensor", "synth_config",
     "synth_zipf", "synth_lowrank3", "synth_blocks3", "synth_units5", "load_tns3",
     "load_tns_generic", "probe_nmodes", "write_tns", "cadr3", "Als3", "device_count", "ptr",
-    "DevBuf", "sync",
+    "DevBuf", "sync", "check",
 ]
 
 

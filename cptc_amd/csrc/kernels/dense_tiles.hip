@@ -34,7 +34,7 @@ __device__ inline float fold(const double* __restrict__ F, int row, int dim, int
 }
 
 template <int MODE>
-__global__ __launch_bounds__(WAVE* WAVES_PER_WG) void dense_tiles3_kernel(
+__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles3_kernel(
     const int32_t* __restrict__ tiles4, const float* __restrict__ tile_f32, size_t ntiles,
     const double* __restrict__ A, const double* __restrict__ B, const double* __restrict__ C,
     double* __restrict__ FtV, int R, int dimI, int dimJ, int dimK)
@@ -93,20 +93,36 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) void dense_tiles3_kernel(
         float bf[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s) bf[s] = fold(Ff, fb + 4 * s + hi, fdim, r, R);
+        // four groups of four slices: inside a group the four 4-deep MFMA
+        // chains are interleaved (s outer, slice inner); a scheduling
+        // barrier between groups keeps only one group's accumulators live.
+        // A slice beyond the mode holds no cells and gets weight 0.
         double tot[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-        for (int x = 0; x < 16; ++x)
+        for (int xg = 0; xg < 16; xg += 4)
         {
-            if (wb + x >= wdim) continue;   // uniform across the wave
-            floatx4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+            double w[4];
+#pragma unroll
+            for (int xx = 0; xx < 4; ++xx)
+                w[xx] = (r < R && wb + xg + xx < wdim) ? Fw[size_t(wb + xg + xx) * R + r] : 0.0;
+            floatx4 d[4];
+#pragma unroll
+            for (int xx = 0; xx < 4; ++xx) d[xx] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 4; ++s)
-                d = __builtin_amdgcn_mfma_f32_16x16x4f32(cells[s][x], bf[s], d, 0, 0, 0);
-            const double w = (r < R) ? Fw[size_t(wb + x) * R + r] : 0.0;
-            tot[0] += double(d[0]) * w;
-            tot[1] += double(d[1]) * w;
-            tot[2] += double(d[2]) * w;
-            tot[3] += double(d[3]) * w;
+#pragma unroll
+                for (int xx = 0; xx < 4; ++xx)
+                    d[xx] = __builtin_amdgcn_mfma_f32_16x16x4f32(cells[s][xg + xx], bf[s], d[xx],
+                                                                 0, 0, 0);
+#pragma unroll
+            for (int xx = 0; xx < 4; ++xx)
+            {
+                tot[0] += double(d[xx][0]) * w[xx];
+                tot[1] += double(d[xx][1]) * w[xx];
+                tot[2] += double(d[xx][2]) * w[xx];
+                tot[3] += double(d[xx][3]) * w[xx];
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (r < R)
         {

@@ -8,11 +8,10 @@
 // Mapping.  A lane owns VEC consecutive ranks (VEC = 2: one 16-byte load per
 // factor row per lane, so a wave reads a 1 KB R=128 row as 64 x 16 B fully
 // coalesced).  LPE = RT / VEC lanes cover one element's rank tile RT; a wave
-// carries EPW = 64 / LPE elements at a time ("rank-dependent element
-// packing": R=128 -> 1, 64 -> 2, 32 -> 4, 16 -> 8, 8 -> 16 elements per wave).
-// WAVES waves of a workgroup stride over the segment; partial sums meet in
-// registers (xor-shuffles across the EPW slots of a wave) and then in LDS
-// across waves.  R > RT runs RT-wide rank blocks on grid.y.
+// carries EPW = 64 / LPE element slots ("rank-dependent element packing":
+// R=128 -> 1, 64 -> 2, 32 -> 4, 16 -> 8, 8 -> 16 slots per wave).  Partial
+// sums meet in registers (xor-shuffles across the EPW slots of a wave) and
+// then in LDS across waves.  R > RT runs RT-wide rank blocks on grid.y.
 #include <hip/hip_runtime.h>
 
 #include "../host/hip_util.hpp"
@@ -21,6 +20,34 @@ namespace {
 
 constexpr int WAVE = 64;
 
+template <int VEC>
+struct Row;
+template <>
+struct Row<2>
+{
+    double x[2];
+    __device__ void load(const double* __restrict__ p)
+    {
+        const double2 v = *reinterpret_cast<const double2*>(p);
+        x[0] = v.x;
+        x[1] = v.y;
+    }
+};
+template <>
+struct Row<1>
+{
+    double x[1];
+    __device__ void load(const double* __restrict__ p) { x[0] = *p; }
+};
+
+// One workgroup per row segment.  The WAVES * EPW element slots of the
+// workgroup each take a contiguous chunk of the segment and walk it in view
+// order (o1 ascending, then o0), so every run of equal o1 is handled by one
+// slot: t += v * F1[o0] over the run, acc += t * F2[o1] once per run.  The
+// second factor row is gathered once per run instead of once per element
+// (the sum is reassociated: acc_r = sum_runs F2[o1, r] * sum_e v_e F1[o0_e, r]).
+// View coordinates and values are streamed with non-temporal loads so they
+// do not evict factor rows from L2.
 template <int RT, int VEC, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     int mode, const uint64_t* __restrict__ coords, const double* __restrict__ vals,
@@ -29,14 +56,14 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     const double* __restrict__ F2, double* __restrict__ FtV, int R)
 {
     constexpr int LPE = RT / VEC;          // lanes per element
-    constexpr int EPW = WAVE / LPE;        // elements per wave step
-    constexpr int STEP = EPW * WAVES;      // elements per workgroup step
+    constexpr int EPW = WAVE / LPE;        // element slots per wave
+    constexpr int SLOTS = EPW * WAVES;     // element slots per workgroup
     static_assert(WAVE % LPE == 0, "rank tile must divide the wave");
 
     const uint32_t seg = blockIdx.x;
     const uint32_t row = blk_row[seg];
     const uint32_t start = blk_start[seg];
-    const uint32_t end = start + blk_cnt[seg];
+    const uint32_t cnt = blk_cnt[seg];
 
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
@@ -44,78 +71,84 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     const int slot = lane / LPE;
     const int r0 = int(blockIdx.y) * RT + (lane % LPE) * VEC;   // first rank of this lane
     const bool rank_ok = r0 < R;
+    const int rr = rank_ok ? r0 : 0;                            // in-bounds row offset
 
     // per-mode field shifts of the packed (i<<30 | j<<15 | k) coordinate
     const int sh0 = (mode == 0) ? 15 : 30;   // o0 = j (mode 0) or i
     const int sh1 = (mode == 2) ? 15 : 0;    // o1 = k (modes 0,1) or j
 
-    double acc[VEC];
-#pragma unroll
-    for (int q = 0; q < VEC; ++q) acc[q] = 0.0;
+    // this slot's contiguous chunk
+    const uint32_t g = uint32_t(wave * EPW + slot);
+    const uint32_t chunk = (cnt + SLOTS - 1) / SLOTS;
+    uint32_t lo = start + g * chunk;
+    const uint32_t hi = (g * chunk + chunk < cnt) ? lo + chunk : start + cnt;
+    if (lo > hi) lo = hi;
 
-    uint32_t e = start + uint32_t(wave * EPW + slot);
-    for (; e + uint32_t((UNROLL - 1) * STEP) < end; e += uint32_t(UNROLL * STEP))
+    double acc[VEC], t[VEC];
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) acc[q] = t[q] = 0.0;
+    uint32_t cur = 0xFFFFFFFFu;   // o1 of the open run (none yet)
+
+    auto close_run = [&](uint32_t o1) {
+        Row<VEC> f2;
+        f2.load(F2 + size_t(o1) * R + rr);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q)
+        {
+            acc[q] += t[q] * f2.x[q];
+            t[q] = 0.0;
+        }
+    };
+
+    uint32_t e = lo;
+    for (; e + UNROLL <= hi; e += UNROLL)
     {
         uint64_t pc[UNROLL];
         double v[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-            pc[u] = coords[e + u * STEP];
-            v[u] = vals[e + u * STEP];
+            pc[u] = __builtin_nontemporal_load(coords + e + u);
+            v[u] = __builtin_nontemporal_load(vals + e + u);
         }
-        if (rank_ok)
+        uint32_t o0[UNROLL], o1[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
         {
-            double a[UNROLL][VEC], b[UNROLL][VEC];
-#pragma unroll
-            for (int u = 0; u < UNROLL; ++u)
-            {
-                const uint32_t o0 = uint32_t(pc[u] >> sh0) & 0x7FFFu;
-                const uint32_t o1 = uint32_t(pc[u] >> sh1) & 0x7FFFu;
-                const double* p1 = F1 + size_t(o0) * R + r0;
-                const double* p2 = F2 + size_t(o1) * R + r0;
-                if constexpr (VEC == 2)
-                {
-                    const double2 x = *reinterpret_cast<const double2*>(p1);
-                    const double2 y = *reinterpret_cast<const double2*>(p2);
-                    a[u][0] = x.x; a[u][1] = x.y;
-                    b[u][0] = y.x; b[u][1] = y.y;
-                }
-                else
-                {
-                    a[u][0] = *p1;
-                    b[u][0] = *p2;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-                for (int q = 0; q < VEC; ++q)
-                    if (VEC == 1 || r0 + q < R) acc[q] += v[u] * a[u][q] * b[u][q];
+            o0[u] = uint32_t(pc[u] >> sh0) & 0x7FFFu;
+            o1[u] = uint32_t(pc[u] >> sh1) & 0x7FFFu;
         }
+        Row<VEC> f1[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) f1[u].load(F1 + size_t(o0[u]) * R + rr);
+        if (o1[0] != cur && cur != 0xFFFFFFFFu) close_run(cur);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+#pragma unroll
+            for (int q = 0; q < VEC; ++q) t[q] += v[u] * f1[u].x[q];
+            if (u + 1 < UNROLL && o1[u] != o1[u + 1]) close_run(o1[u]);
+        }
+        cur = o1[UNROLL - 1];
     }
-    for (; e < end; e += uint32_t(STEP))
+    for (; e < hi; ++e)
     {
-        const uint64_t pc = coords[e];
-        const double v = vals[e];
-        if (rank_ok)
-        {
-            const uint32_t o0 = uint32_t(pc >> sh0) & 0x7FFFu;
-            const uint32_t o1 = uint32_t(pc >> sh1) & 0x7FFFu;
-            const double* p1 = F1 + size_t(o0) * R + r0;
-            const double* p2 = F2 + size_t(o1) * R + r0;
-            if constexpr (VEC == 2)
-            {
-                const double2 x = *reinterpret_cast<const double2*>(p1);
-                const double2 y = *reinterpret_cast<const double2*>(p2);
-                acc[0] += v * x.x * y.x;
-                if (r0 + 1 < R) acc[1] += v * x.y * y.y;
-            }
-            else
-            {
-                acc[0] += v * *p1 * *p2;
-            }
-        }
+        const uint64_t pc = __builtin_nontemporal_load(coords + e);
+        const double v = __builtin_nontemporal_load(vals + e);
+        const uint32_t o0 = uint32_t(pc >> sh0) & 0x7FFFu;
+        const uint32_t o1 = uint32_t(pc >> sh1) & 0x7FFFu;
+        if (o1 != cur && cur != 0xFFFFFFFFu) close_run(cur);
+        Row<VEC> f1;
+        f1.load(F1 + size_t(o0) * R + rr);
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) t[q] += v * f1.x[q];
+        cur = o1;
+    }
+    if (cur != 0xFFFFFFFFu) close_run(cur);
+    if (!rank_ok)
+    {
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) acc[q] = 0.0;
     }
 
     // reduce the EPW element slots of the wave (lanes l, l^LPE, l^2LPE, ...)
@@ -145,10 +178,10 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
         {
             const int r = int(blockIdx.y) * RT + x;
             if (r >= R) continue;
-            double t = 0.0;
+            double tot = 0.0;
 #pragma unroll
-            for (int w = 0; w < WAVES; ++w) t += red[w][x];
-            if (t != 0.0) atomicAdd(FtV + size_t(row) * R + r, t);
+            for (int w = 0; w < WAVES; ++w) tot += red[w][x];
+            if (tot != 0.0) atomicAdd(FtV + size_t(row) * R + r, tot);
         }
     }
 }
@@ -159,7 +192,7 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
                      const double* F2, double* FtV, int R, hipStream_t s)
 {
     constexpr int WAVES = 4;
-    constexpr int UNROLL = 4;
+    constexpr int UNROLL = 8;
     const unsigned ry = unsigned((R + RT - 1) / RT);
     dim3 grid(unsigned(nblocks), ry);
     hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid, dim3(WAVE * WAVES), 0,

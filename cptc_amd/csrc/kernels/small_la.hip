@@ -95,12 +95,27 @@ __global__ void hadamard_kernel(const double* A, const double* B, double* C, siz
 }
 
 // ---------------------------------------------------------------------------
-// pinv, fast path: Cholesky A = L L^T (right-looking, one workgroup, A in
-// LDS for R <= 128 or in global scratch), then Ainv = L^-T L^-1 column by
-// column.  Any pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1
-// and leaves Ainv to the Jacobi kernel.
+// pinv, fast path, one workgroup, A in LDS for R <= 128 (global scratch
+// otherwise):
+//   1. blocked Cholesky A = L L^T: 16-column panels factored by wave 0
+//      (lanes over rows, no workgroup barrier inside a panel), then the
+//      trailing update by the whole workgroup;
+//   2. X = L^-1 by columns, one 8-lane group per column (the dot products
+//      split over the group and reduced with xor-shuffles), X^T stored in
+//      the free upper triangle;
+//   3. Ainv = X^T X.
+// Any pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1 and
+// leaves Ainv to the Jacobi kernel.
 // ---------------------------------------------------------------------------
 constexpr int PINV_THREADS = 1024;
+constexpr int CHOL_NB = 16;
+constexpr int INV_G = 8;
+
+__device__ inline void wave_sync_lds()
+{
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
 
 __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double* __restrict__ Ain,
                                                                     int R, double* work,
@@ -111,7 +126,10 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
     double* A = use_lds ? lds : work;
     __shared__ int ok;
     __shared__ double tau;
+    __shared__ double xd[512];   // diagonal of X = L^-1 (R <= 512)
     const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
     const int n2 = R * R;
     for (int x = tid; x < n2; x += PINV_THREADS) A[x] = Ain[x];
     if (tid == 0) *fallback = 0;
@@ -124,36 +142,43 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
         ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
     }
     __syncthreads();
-    // `ok` is written only by thread 0 before the first barrier of an
-    // iteration and read by everyone between that barrier and the next, so
-    // every thread leaves the loop at the same k.
-    for (int k = 0; k < R; ++k)
+    // 1. blocked right-looking Cholesky (lower triangle)
+    for (int kb = 0; kb < R; kb += CHOL_NB)
     {
-        if (tid == 0 && ok)
+        const int ke = (kb + CHOL_NB < R) ? kb + CHOL_NB : R;
+        if (wave == 0 && ok)
         {
-            const double d = A[k * R + k];
-            if (!(d > tau) || !isfinite(d))
-                ok = 0;
-            else
-                A[k * R + k] = sqrt(d);
+            for (int k = kb; k < ke; ++k)
+            {
+                const double d = A[k * R + k];
+                if (!(d > tau) || !isfinite(d))
+                {
+                    if (lane == 0) ok = 0;   // every lane read the same d: uniform exit
+                    break;
+                }
+                const double lkk = sqrt(d);
+                for (int i = k + 1 + lane; i < R; i += WAVE) A[i * R + k] /= lkk;
+                wave_sync_lds();
+                if (lane == 0) A[k * R + k] = lkk;
+                for (int j = k + 1; j < ke; ++j)
+                {
+                    const double ajk = A[j * R + k];
+                    for (int i = j + lane; i < R; i += WAVE) A[i * R + j] -= A[i * R + k] * ajk;
+                }
+                wave_sync_lds();
+            }
         }
         __syncthreads();
         if (!ok) break;
-        const double lkk = A[k * R + k];
-        for (int i = k + 1 + tid; i < R; i += PINV_THREADS) A[i * R + k] /= lkk;
-        __syncthreads();
-        // trailing lower triangle: (i, j) with k < j <= i < R
-        const int m = R - k - 1;
-        const int cnt = m * (m + 1) / 2;
-        for (int t = tid; t < cnt; t += PINV_THREADS)
+        const int m = R - ke;
+        for (int idx = tid; idx < m * m; idx += PINV_THREADS)
         {
-            // row-major enumeration of the lower triangle of size m
-            int ii = int((sqrt(8.0 * t + 1.0) - 1.0) * 0.5);
-            while ((ii + 1) * (ii + 2) / 2 <= t) ++ii;
-            while (ii * (ii + 1) / 2 > t) --ii;
-            const int jj = t - ii * (ii + 1) / 2;
-            const int i = k + 1 + ii, j = k + 1 + jj;
-            A[i * R + j] -= A[i * R + k] * A[j * R + k];
+            const int ii = idx / m, jj = idx - ii * m;
+            if (jj > ii) continue;
+            const int i = ke + ii, j = ke + jj;
+            double acc = 0.0;
+            for (int k = kb; k < ke; ++k) acc += A[i * R + k] * A[j * R + k];
+            A[i * R + j] -= acc;
         }
         __syncthreads();
     }
@@ -162,23 +187,33 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
         if (tid == 0) *fallback = 1;
         return;
     }
-    // column c of L^-T L^-1: forward solve L y = e_c, back solve L^T x = y;
-    // the working vector lives in Ainv[:, c]
-    for (int c = tid; c < R; c += PINV_THREADS)
+    // 2. X = L^-1: column c by group c; X[j][c] (j > c) at A[c][j], X[c][c] at xd[c]
+    const int grp = tid / INV_G, gl = tid % INV_G;
+    for (int c = grp; c < R; c += PINV_THREADS / INV_G)
     {
-        for (int j = 0; j < c; ++j) Ainv[j * R + c] = 0.0;
-        for (int j = c; j < R; ++j)
+        const double xc = 1.0 / A[c * R + c];
+        if (gl == 0) xd[c] = xc;
+        for (int j = c + 1; j < R; ++j)
         {
-            double s = (j == c) ? 1.0 : 0.0;
-            for (int q = c; q < j; ++q) s -= A[j * R + q] * Ainv[q * R + c];
-            Ainv[j * R + c] = s / A[j * R + j];
+            double s = (gl == 0) ? A[j * R + c] * xc : 0.0;
+            for (int q = c + 1 + gl; q < j; q += INV_G) s += A[j * R + q] * A[c * R + q];
+            s += __shfl_xor(s, 4, INV_G);
+            s += __shfl_xor(s, 2, INV_G);
+            s += __shfl_xor(s, 1, INV_G);
+            if (gl == 0) A[c * R + j] = -s / A[j * R + j];
+            wave_sync_lds();
         }
-        for (int j = R - 1; j >= 0; --j)
-        {
-            double s = Ainv[j * R + c];
-            for (int q = j + 1; q < R; ++q) s -= A[q * R + j] * Ainv[q * R + c];
-            Ainv[j * R + c] = s / A[j * R + j];
-        }
+    }
+    __syncthreads();
+    // 3. Ainv[r][s] = sum_{j >= max(r, s)} X[j][r] X[j][s]
+    for (int idx = tid; idx < n2; idx += PINV_THREADS)
+    {
+        const int r = idx / R, c = idx - r * R;
+        if (c < r) continue;
+        double acc = xd[c] * (r == c ? xd[r] : A[r * R + c]);
+        for (int j = c + 1; j < R; ++j) acc += A[r * R + j] * A[c * R + j];
+        Ainv[r * R + c] = acc;
+        Ainv[c * R + r] = acc;
     }
 }
 
