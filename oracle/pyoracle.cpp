@@ -7,6 +7,7 @@
 #include <omp.h>
 
 #include "cptc_oracle.hpp"
+#include "cptc_oracle_nd.hpp"
 
 namespace py = pybind11;
 using namespace oracle;
@@ -120,6 +121,103 @@ static View3 view_from_list(const py::list& l)
     return v;
 }
 
+
+static CooN coon_from(arr<uint32_t> coords, arr<double> vals, py::sequence dims)
+{
+    CooN t;
+    t.N = int(py::len(dims));
+    for (int m = 0; m < t.N; ++m) t.dims.push_back(dims[m].cast<size_t>());
+    const size_t nnz = vals.size();
+    t.val = vec(vals);
+    t.c.resize(t.N);
+    for (int m = 0; m < t.N; ++m)
+        t.c[m].assign(coords.data() + size_t(m) * nnz, coords.data() + size_t(m + 1) * nnz);
+    return t;
+}
+
+static arr<uint32_t> coords_np(const CooN& t)
+{
+    const size_t nnz = t.nnz();
+    arr<uint32_t> a(std::vector<ssize_t>{ssize_t(t.N), ssize_t(nnz)});
+    for (int m = 0; m < t.N; ++m)
+        if (nnz) std::memcpy(a.mutable_data() + size_t(m) * nnz, t.c[m].data(), nnz * 4);
+    return a;
+}
+
+static std::vector<std::vector<double>> flist(py::list F)
+{
+    std::vector<std::vector<double>> out;
+    for (auto f : F) out.push_back(vec(f.cast<arr<double>>()));
+    return out;
+}
+
+static py::list flist_np(const std::vector<std::vector<double>>& F)
+{
+    py::list l;
+    for (auto& f : F) l.append(np(f));
+    return l;
+}
+
+static py::dict units_to_dict(const UnitsN& u)
+{
+    py::dict d;
+    d["cutoff"] = u.cutoff;
+    d["unit6"] = np(u.unit6).attr("reshape")(py::make_tuple(-1, 6));
+    d["outer_coords"] = np(u.outer_coords);
+    d["lid"] = np(u.lid);
+    d["val"] = np(u.val);
+    d["is_dense"] = np(u.is_dense);
+    return d;
+}
+
+static UnitsN units_from_dict(const py::dict& d, int N)
+{
+    UnitsN u;
+    u.cutoff = d["cutoff"].cast<int>();
+    for (int m = 3; m < N; ++m) u.outer.push_back(m);
+    u.unit6 = vec(d["unit6"].cast<arr<uint32_t>>());
+    u.outer_coords = vec(d["outer_coords"].cast<arr<uint32_t>>());
+    u.lid = vec(d["lid"].cast<arr<uint32_t>>());
+    u.val = vec(d["val"].cast<arr<double>>());
+    u.is_dense = vec(d["is_dense"].cast<arr<uint8_t>>());
+    return u;
+}
+
+static py::list viewn_to_list(const ViewN& v)
+{
+    py::list l;
+    for (size_t n = 0; n < v.sv.size(); ++n)
+    {
+        py::dict d;
+        d["scoords"] = np(v.sc[n]);
+        d["vals"] = np(v.sv[n]);
+        d["skip"] = np(v.skip[n]);
+        d["row"] = np(v.row[n]);
+        d["start"] = np(v.start[n]);
+        d["cnt"] = np(v.cnt[n]);
+        d["single"] = np(v.single[n]);
+        l.append(d);
+    }
+    return l;
+}
+
+static ViewN viewn_from_list(const py::list& l)
+{
+    ViewN v;
+    for (auto item : l)
+    {
+        py::dict d = item.cast<py::dict>();
+        v.sc.push_back(vec(d["scoords"].cast<arr<uint32_t>>()));
+        v.sv.push_back(vec(d["vals"].cast<arr<double>>()));
+        v.skip.push_back(vec(d["skip"].cast<arr<uint8_t>>()));
+        v.row.push_back(vec(d["row"].cast<arr<uint32_t>>()));
+        v.start.push_back(vec(d["start"].cast<arr<uint32_t>>()));
+        v.cnt.push_back(vec(d["cnt"].cast<arr<uint32_t>>()));
+        v.single.push_back(vec(d["single"].cast<arr<uint8_t>>()));
+    }
+    return v;
+}
+
 struct PyAls3
 {
     View3 residual, dense_view;
@@ -225,6 +323,90 @@ PYBIND11_MODULE(cptc_oracle, m)
         std::vector<double> out(size_t(R) * R);
         const int sweeps = pinv_sym(A.data(), R, out.data());
         return py::make_tuple(np(out), sweeps);
+    });
+
+
+    // ---------------- generic N-order ----------------
+    m.def("reorder_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
+                           const std::string& how, int rounds, size_t sample_budget) {
+        CooN t = coon_from(coords, vals, dims);
+        std::vector<std::vector<uint32_t>> rank;
+        reorder_nd(t, how, rounds, sample_budget, rank);
+        py::list rl;
+        for (auto& r : rank) rl.append(np(r));
+        return py::make_tuple(coords_np(t), rl);
+    });
+    m.def("splitbit_hash", &splitbit_hash);
+    m.def("dense_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, double thr) {
+        CooN t = coon_from(coords, vals, dims);
+        UnitsN u;
+        dense_nd(t, thr, u);
+        return units_to_dict(u);
+    });
+    m.def("views_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
+                         py::object is_dense, bool enabled) {
+        CooN t = coon_from(coords, vals, dims);
+        std::vector<uint8_t> isd;
+        if (!is_dense.is_none()) isd = vec(is_dense.cast<arr<uint8_t>>());
+        ViewN v;
+        views_nd(t, isd, enabled, v);
+        return viewn_to_list(v);
+    });
+    m.def("mttkrp_seg_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
+                              py::list views, int n, bool use_skip, py::list F, int R,
+                              py::object init) {
+        CooN t = coon_from(coords, vals, dims);
+        ViewN v = viewn_from_list(views);
+        std::vector<double> out(t.dims[n] * size_t(R), 0.0);
+        if (!init.is_none()) out = vec(init.cast<arr<double>>());
+        mttkrp_seg_nd(t, v, n, use_skip, flist(F), R, out.data());
+        return np(out);
+    });
+    m.def("mttkrp_units_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
+                                py::dict units, int n, py::list F, int R) {
+        CooN t = coon_from(coords, vals, dims);
+        UnitsN u = units_from_dict(units, t.N);
+        std::vector<double> out(t.dims[n] * size_t(R), 0.0);
+        mttkrp_units_nd(t, u, n, flist(F), R, out.data());
+        return np(out);
+    });
+    m.def("chol_solve_nd", [](arr<double> FtF, arr<double> FtV, int R) {
+        const size_t dim = FtV.size() / size_t(R);
+        std::vector<double> out(dim * size_t(R));
+        chol_solve_nd(FtF.data(), FtV.data(), out.data(), dim, R);
+        return np(out);
+    });
+    m.def("als_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::list rank,
+                       int R, unsigned seed, bool svd, bool dense, double thr, int iters) {
+        CooN t = coon_from(coords, vals, dims);
+        std::vector<std::vector<uint32_t>> rk;
+        for (auto r : rank) rk.push_back(vec(r.cast<arr<uint32_t>>()));
+        AlsNOpts o;
+        o.R = R;
+        o.seed = seed;
+        o.svd = svd;
+        o.dense = dense;
+        o.threshold = thr;
+        AlsNState st;
+        {
+            py::gil_scoped_release rel;
+            als_nd(t, rk, o, iters, st);
+        }
+        return py::make_tuple(np(st.fits), np(st.iprod), np(st.model2), flist_np(st.F),
+                              np(st.lambda));
+    });
+    m.def("residual_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::list F,
+                            arr<double> lam, int R) {
+        CooN t = coon_from(coords, vals, dims);
+        return residual_nd(t, flist(F), vec(lam), R);
+    });
+    m.def("selftest_tensor", []() {
+        CooN t;
+        std::vector<std::vector<double>> F;
+        selftest_tensor(t, F);
+        return py::make_tuple(coords_np(t), np(t.val),
+                              py::make_tuple(t.dims[0], t.dims[1], t.dims[2], t.dims[3]),
+                              flist_np(F));
     });
 
     py::class_<PyAls3>(m, "Als3")
