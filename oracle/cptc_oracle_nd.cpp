@@ -159,20 +159,25 @@ void reorder_nd(CooN& t, const std::string& how, int rounds, size_t sample_budge
 }
 
 // generic.cu:578-725
-void dense_nd(const CooN& t, double threshold, UnitsN& u)
+void dense_nd(const CooN& t, double threshold, const int inner[3], UnitsN& u)
 {
     u = UnitsN{};
     const int N = t.N;
     const size_t nnz = t.nnz();
     u.cutoff = int(4096.0 * threshold);
-    for (int m = 3; m < N; ++m) u.outer.push_back(m);
+    for (int s = 0; s < 3; ++s) u.inner[s] = inner[s];
+    for (int m = 0; m < N; ++m)
+        if (m != inner[0] && m != inner[1] && m != inner[2]) u.outer.push_back(m);
+    const auto& c0 = t.c[inner[0]];
+    const auto& c1 = t.c[inner[1]];
+    const auto& c2 = t.c[inner[2]];
     std::vector<uint64_t> key(nnz);
     std::unordered_map<uint64_t, uint32_t> cnt;
     for (size_t e = 0; e < nnz; ++e)
     {
-        const uint32_t a = t.c[0][e], b = t.c[1][e], c = t.c[2][e];
+        const uint32_t a = c0[e], b = c1[e], c = c2[e];
         uint64_t o = 0;
-        for (int m = 3; m < N; ++m) o = o * 1000003ull + t.c[m][e];
+        for (int m : u.outer) o = o * 1000003ull + t.c[m][e];
         const uint64_t tile =
             (uint64_t(a / 16) << 40) | (uint64_t(b / 16) << 20) | uint64_t(c / 16);
         key[e] = splitbit_hash(tile ^ (o * 0x9E3779B97F4A7C15ull));
@@ -186,9 +191,9 @@ void dense_nd(const CooN& t, double threshold, UnitsN& u)
         if (index.count(key[e])) continue;
         index[key[e]] = uint32_t(nn.size());
         nn.push_back(0);
-        u.unit6.insert(u.unit6.end(), {t.c[0][e] / 16, t.c[1][e] / 16, t.c[2][e] / 16, 0u, 0u,
+        u.unit6.insert(u.unit6.end(), {c0[e] / 16, c1[e] / 16, c2[e] / 16, 0u, 0u,
                                        uint32_t((nn.size() - 1) * size_t(N - 3))});
-        for (int m = 3; m < N; ++m) u.outer_coords.push_back(t.c[m][e]);
+        for (int m : u.outer) u.outer_coords.push_back(t.c[m][e]);
     }
     u.is_dense.assign(nnz, 0);
     if (nn.empty()) return;
@@ -213,7 +218,7 @@ void dense_nd(const CooN& t, double threshold, UnitsN& u)
         auto it = index.find(key[e]);
         if (it == index.end()) continue;
         const uint32_t k = it->second;
-        u.lid[cur[k]] = (t.c[0][e] % 16) * 256 + (t.c[1][e] % 16) * 16 + (t.c[2][e] % 16);
+        u.lid[cur[k]] = (c0[e] % 16) * 256 + (c1[e] % 16) * 16 + (c2[e] % 16);
         u.val[cur[k]] = t.val[e];
         ++cur[k];
         u.is_dense[e] = 1;
@@ -221,7 +226,8 @@ void dense_nd(const CooN& t, double threshold, UnitsN& u)
 }
 
 // generic.cu:1848-1958
-void views_nd(const CooN& t, const std::vector<uint8_t>& is_dense, bool dense_enabled, ViewN& v)
+void views_nd(const CooN& t, const std::vector<uint8_t>& is_dense, unsigned force_accumulate,
+              ViewN& v)
 {
     const int N = t.N;
     const size_t nnz = t.nnz();
@@ -270,7 +276,7 @@ void views_nd(const CooN& t, const std::vector<uint8_t>& is_dense, bool dense_en
                 v.single[n].push_back(nseg == 1 ? 1 : 0);
             }
         }
-        if (dense_enabled && n < 3)
+        if (force_accumulate & (1u << n))
             for (auto& s8 : v.single[n]) s8 = 0;
     }
 }
@@ -316,8 +322,13 @@ void mttkrp_seg_nd(const CooN& t, const ViewN& v, int n, bool use_skip,
 void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
                      const std::vector<std::vector<double>>& F, int R, double* FtV)
 {
-    if (n < 0 || n > 2) throw std::runtime_error("mttkrp_units_nd: inner modes only");
-    const int p = (n + 1) % 3, q = (n + 2) % 3;
+    int sl = -1;
+    for (int x = 0; x < 3; ++x)
+        if (u.inner[x] == n) sl = x;
+    if (sl < 0) throw std::runtime_error("mttkrp_units_nd: inner modes only");
+    // slots: sl = target, p = contracted, q = sliced (generic.cu:500-540)
+    const int p = (sl + 1) % 3, q = (sl + 2) % 3;
+    const int mp = u.inner[p], mq = u.inner[q];
     std::vector<double> T(4096), w(static_cast<size_t>(R)), acc(16 * static_cast<size_t>(R));
     const int N = t.N;
     for (size_t k = 0; k < u.n_units(); ++k)
@@ -329,33 +340,33 @@ void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
         for (int oq = 0; oq < N - 3; ++oq)
         {
             const uint32_t c = u.outer_coords[U[5] + oq];
-            for (int r = 0; r < R; ++r) w[r] *= F[3 + oq][size_t(c) * R + r];
+            for (int r = 0; r < R; ++r) w[r] *= F[u.outer[oq]][size_t(c) * R + r];
         }
         std::fill(acc.begin(), acc.end(), 0.0);
         const int base[3] = {int(U[0]) * 16, int(U[1]) * 16, int(U[2]) * 16};
         for (int lt = 0; lt < 16; ++lt)
             for (int lq = 0; lq < 16; ++lq)
             {
-                if (base[q] + lq >= int(t.dims[q])) continue;
+                if (base[q] + lq >= int(t.dims[mq])) continue;
                 for (int r = 0; r < R; ++r)
                 {
                     double g = 0.0;
                     for (int lp = 0; lp < 16; ++lp)
                     {
-                        if (base[p] + lp >= int(t.dims[p])) continue;
+                        if (base[p] + lp >= int(t.dims[mp])) continue;
                         int loc[3];
-                        loc[n] = lt;
+                        loc[sl] = lt;
                         loc[p] = lp;
                         loc[q] = lq;
                         const double x = T[size_t(loc[0] * 256 + loc[1] * 16 + loc[2])];
-                        if (x != 0.0) g += x * F[p][size_t(base[p] + lp) * R + r];
+                        if (x != 0.0) g += x * F[mp][size_t(base[p] + lp) * R + r];
                     }
-                    acc[size_t(lt) * R + r] += g * F[q][size_t(base[q] + lq) * R + r] * w[r];
+                    acc[size_t(lt) * R + r] += g * F[mq][size_t(base[q] + lq) * R + r] * w[r];
                 }
             }
         for (int lt = 0; lt < 16; ++lt)
         {
-            const int row = base[n] + lt;
+            const int row = base[sl] + lt;
             if (row >= int(t.dims[n])) continue;
             for (int r = 0; r < R; ++r) FtV[size_t(row) * R + r] += acc[size_t(lt) * R + r];
         }
@@ -427,13 +438,15 @@ void als_nd(const CooN& t, const std::vector<std::vector<uint32_t>>& rank, const
     st.lambda.assign(size_t(R), 1.0);
     UnitsN units;
     bool enabled = false;
+    unsigned inner_mask = 0;
+    for (int s = 0; s < 3; ++s) inner_mask |= 1u << o.inner[s];
     if (o.dense && N >= 4 && o.threshold > 0.0)
     {
-        dense_nd(t, o.threshold, units);
+        dense_nd(t, o.threshold, o.inner, units);
         enabled = units.n_units() > 0;
     }
     ViewN v;
-    views_nd(t, enabled ? units.is_dense : std::vector<uint8_t>(), enabled, v);
+    views_nd(t, enabled ? units.is_dense : std::vector<uint8_t>(), enabled ? inner_mask : 0u, v);
     std::vector<std::vector<double>> G(N, std::vector<double>(RR));
     for (int m = 0; m < N; ++m) gram(st.F[m].data(), t.dims[m], R, G[m].data());
     double X2 = 0.0;
@@ -452,7 +465,7 @@ void als_nd(const CooN& t, const std::vector<std::vector<uint32_t>>& rank, const
                     for (size_t x = 0; x < RR; ++x) FtF[x] *= G[m][x];
             const size_t dim = t.dims[n];
             std::fill(FtV.begin(), FtV.begin() + dim * R, 0.0);
-            const bool inner = enabled && n < 3;
+            const bool inner = enabled && (inner_mask & (1u << n));
             if (inner) mttkrp_units_nd(t, units, n, st.F, R, FtV.data());
             mttkrp_seg_nd(t, v, n, inner, st.F, R, FtV.data());
             if (o.svd)

@@ -41,6 +41,7 @@ uint64_t splitbit_hash(uint64_t x);
 struct UnitsN
 {
     int cutoff = 0;
+    int inner[3] = {0, 1, 2};             // modes of tile slots a, b, c
     std::vector<int> outer;               // outer modes, ascending
     // per unit: bi, bj, bk, nnz, start, outer_off
     std::vector<uint32_t> unit6;
@@ -51,8 +52,8 @@ struct UnitsN
     size_t n_units() const { return unit6.size() / 6; }
 };
 
-// generic.cu:564-725 (inner modes 0, 1, 2)
-void dense_nd(const CooN& t, double threshold, UnitsN& u);
+// generic.cu:564-725; `inner` = the three tile-slot modes (default 0, 1, 2)
+void dense_nd(const CooN& t, double threshold, const int inner[3], UnitsN& u);
 
 struct ViewN
 {
@@ -65,8 +66,9 @@ struct ViewN
     std::vector<std::vector<uint8_t>> single;
 };
 
-// generic.cu:1848-1958.  `dense_enabled` forces single = 0 on modes 0..2.
-void views_nd(const CooN& t, const std::vector<uint8_t>& is_dense, bool dense_enabled,
+// generic.cu:1848-1958.  Modes whose bit is set in `force_accumulate` (the
+// inner modes when the dense path is on) get single = 0.
+void views_nd(const CooN& t, const std::vector<uint8_t>& is_dense, unsigned force_accumulate,
               ViewN& v);
 
 // generic.cu:271-343: segment MTTKRP (skip honoured when `use_skip`), FP64;
@@ -75,7 +77,8 @@ void mttkrp_seg_nd(const CooN& t, const ViewN& v, int n, bool use_skip,
                    const std::vector<std::vector<double>>& F, int R, double* FtV);
 
 // generic.cu:429-561 in exact FP64 (duplicates inside a unit summed):
-// contribution of the dense units to the MTTKRP of inner mode n.
+// contribution of the dense units to the MTTKRP of inner mode n (n must be
+// one of u.inner; the factors are indexed by mode, not by slot).
 void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
                      const std::vector<std::vector<double>>& F, int R, double* FtV);
 
@@ -89,6 +92,7 @@ struct AlsNOpts
     bool svd = false;            // GEN_SOLVER=svd
     bool dense = true;           // GEN_DENSE
     double threshold = 0.03;     // GEN_DENSE_THRESHOLD
+    int inner[3] = {0, 1, 2};    // GEN_DENSE_INNER
 };
 
 struct AlsNState

@@ -1,5 +1,7 @@
 // Python bindings of the CPU oracle — TEST INFRASTRUCTURE ONLY.
 // Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+#include <array>
+
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -162,6 +164,7 @@ static py::dict units_to_dict(const UnitsN& u)
 {
     py::dict d;
     d["cutoff"] = u.cutoff;
+    d["inner"] = py::make_tuple(u.inner[0], u.inner[1], u.inner[2]);
     d["unit6"] = np(u.unit6).attr("reshape")(py::make_tuple(-1, 6));
     d["outer_coords"] = np(u.outer_coords);
     d["lid"] = np(u.lid);
@@ -174,7 +177,13 @@ static UnitsN units_from_dict(const py::dict& d, int N)
 {
     UnitsN u;
     u.cutoff = d["cutoff"].cast<int>();
-    for (int m = 3; m < N; ++m) u.outer.push_back(m);
+    if (d.contains("inner"))
+    {
+        const auto in = d["inner"].cast<std::array<int, 3>>();
+        for (int x = 0; x < 3; ++x) u.inner[x] = in[x];
+    }
+    for (int m = 0; m < N; ++m)
+        if (m != u.inner[0] && m != u.inner[1] && m != u.inner[2]) u.outer.push_back(m);
     u.unit6 = vec(d["unit6"].cast<arr<uint32_t>>());
     u.outer_coords = vec(d["outer_coords"].cast<arr<uint32_t>>());
     u.lid = vec(d["lid"].cast<arr<uint32_t>>());
@@ -337,21 +346,33 @@ PYBIND11_MODULE(cptc_oracle, m)
         return py::make_tuple(coords_np(t), rl);
     });
     m.def("splitbit_hash", &splitbit_hash);
-    m.def("dense_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, double thr) {
-        CooN t = coon_from(coords, vals, dims);
-        UnitsN u;
-        dense_nd(t, thr, u);
-        return units_to_dict(u);
-    });
-    m.def("views_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
-                         py::object is_dense, bool enabled) {
-        CooN t = coon_from(coords, vals, dims);
-        std::vector<uint8_t> isd;
-        if (!is_dense.is_none()) isd = vec(is_dense.cast<arr<uint8_t>>());
-        ViewN v;
-        views_nd(t, isd, enabled, v);
-        return viewn_to_list(v);
-    });
+    m.def(
+        "dense_nd",
+        [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, double thr,
+           std::array<int, 3> inner) {
+            CooN t = coon_from(coords, vals, dims);
+            UnitsN u;
+            dense_nd(t, thr, inner.data(), u);
+            return units_to_dict(u);
+        },
+        py::arg("coords"), py::arg("vals"), py::arg("dims"), py::arg("thr"),
+        py::arg("inner") = std::array<int, 3>{0, 1, 2});
+    m.def(
+        "views_nd",
+        [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::object is_dense,
+           bool enabled, std::array<int, 3> inner) {
+            CooN t = coon_from(coords, vals, dims);
+            std::vector<uint8_t> isd;
+            if (!is_dense.is_none()) isd = vec(is_dense.cast<arr<uint8_t>>());
+            unsigned mask = 0;
+            if (enabled)
+                for (int x : inner) mask |= 1u << x;
+            ViewN v;
+            views_nd(t, isd, mask, v);
+            return viewn_to_list(v);
+        },
+        py::arg("coords"), py::arg("vals"), py::arg("dims"), py::arg("is_dense"),
+        py::arg("enabled"), py::arg("inner") = std::array<int, 3>{0, 1, 2});
     m.def("mttkrp_seg_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
                               py::list views, int n, bool use_skip, py::list F, int R,
                               py::object init) {
@@ -377,7 +398,8 @@ PYBIND11_MODULE(cptc_oracle, m)
         return np(out);
     });
     m.def("als_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::list rank,
-                       int R, unsigned seed, bool svd, bool dense, double thr, int iters) {
+                       int R, unsigned seed, bool svd, bool dense, double thr, int iters,
+                       std::array<int, 3> inner) {
         CooN t = coon_from(coords, vals, dims);
         std::vector<std::vector<uint32_t>> rk;
         for (auto r : rank) rk.push_back(vec(r.cast<arr<uint32_t>>()));
@@ -387,6 +409,7 @@ PYBIND11_MODULE(cptc_oracle, m)
         o.svd = svd;
         o.dense = dense;
         o.threshold = thr;
+        for (int x = 0; x < 3; ++x) o.inner[x] = inner[x];
         AlsNState st;
         {
             py::gil_scoped_release rel;
@@ -394,7 +417,9 @@ PYBIND11_MODULE(cptc_oracle, m)
         }
         return py::make_tuple(np(st.fits), np(st.iprod), np(st.model2), flist_np(st.F),
                               np(st.lambda));
-    });
+    }, py::arg("coords"), py::arg("vals"), py::arg("dims"), py::arg("rank"), py::arg("R"),
+       py::arg("seed"), py::arg("svd"), py::arg("dense"), py::arg("thr"), py::arg("iters"),
+       py::arg("inner") = std::array<int, 3>{0, 1, 2});
     m.def("residual_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::list F,
                             arr<double> lam, int R) {
         CooN t = coon_from(coords, vals, dims);

@@ -136,14 +136,15 @@ def test_auto_reorder_follows_probe(orc):
             assert len(rank) == 0 and np.array_equal(new, idx)
 
 
-def np_dense_nd(idx, val, dims, thr):
+def np_dense_nd(idx, val, dims, thr, inner=(0, 1, 2)):
     N = len(dims)
     cutoff = int(4096.0 * thr)
+    outer = [m for m in range(N) if m not in inner]
     keys = []
     for e in range(idx.shape[1]):
-        a, b, c = (int(idx[m, e]) for m in range(3))
+        a, b, c = (int(idx[m, e]) for m in inner)
         o = 0
-        for m in range(3, N):
+        for m in outer:
             o = (o * 1000003 + int(idx[m, e])) & M64
         tile = ((a // 16) << 40) | ((b // 16) << 20) | (c // 16)
         keys.append(py_hash(tile ^ ((o * 0x9E3779B97F4A7C15) & M64)))
@@ -162,31 +163,43 @@ def np_dense_nd(idx, val, dims, thr):
     return order, members
 
 
-@pytest.mark.parametrize("N,thr", [(4, 0.03), (5, 0.01), (4, 0.0001)])
-def test_dense_nd_matches_python(orc, N, thr):
+def clustered(rng, dims, inner, frac, nbg):
+    """A half-filled 16^3 block on the inner modes at outer coordinate 0,
+    plus uniform background."""
+    N = len(dims)
+    lo = [0, 0, 16]
+    cells = np.array(np.meshgrid(*[np.arange(l, l + 16) for l in lo], indexing="ij"))
+    cells = cells.reshape(3, -1)[:, rng.random(4096) < frac]
+    clus = np.zeros((N, cells.shape[1]), np.uint32)
+    for s, m in enumerate(inner):
+        clus[m] = cells[s]
+    bg, _ = rand_nd(rng, dims, nbg)
+    return np.ascontiguousarray(np.concatenate([clus, bg], axis=1))
+
+
+@pytest.mark.parametrize("N,thr,inner", [(4, 0.03, (0, 1, 2)), (5, 0.01, (0, 1, 2)),
+                                         (4, 0.0001, (0, 1, 2)), (4, 0.03, (1, 2, 3)),
+                                         (5, 0.03, (0, 2, 4))])
+def test_dense_nd_matches_python(orc, N, thr, inner):
     rng = np.random.default_rng(N)
-    dims = (40, 35, 48, 3, 2)[:N]
-    # clustered cells so that units exist
-    cells = np.array(np.meshgrid(np.arange(16), np.arange(16), np.arange(16, 32), indexing="ij"))
-    cells = cells.reshape(3, -1)[:, rng.random(4096) < 0.3]
-    outer = [np.zeros(cells.shape[1], np.int64) for _ in range(N - 3)]
-    clus = np.concatenate([cells] + [o[None] for o in outer])
-    bg, _ = rand_nd(rng, dims, 2000)
-    idx = np.ascontiguousarray(np.concatenate([clus.astype(np.uint32), bg], axis=1))
+    dims = (40, 35, 48, 33, 34)[:N]
+    idx = clustered(rng, dims, inner, 0.3, 2000)
     val = rng.random(idx.shape[1])
-    u = orc.dense_nd(idx, val, dims, thr)
-    order, members = np_dense_nd(idx, val, dims, thr)
+    u = orc.dense_nd(idx, val, dims, thr, inner)
+    order, members = np_dense_nd(idx, val, dims, thr, inner)
+    outer = [m for m in range(N) if m not in inner]
     assert len(u["unit6"]) == len(order) and len(order) > 0
     off = 0
     for k, (e0, mem) in enumerate(zip(order, members)):
         row = u["unit6"][k]
-        assert list(row[:3]) == [idx[0, e0] // 16, idx[1, e0] // 16, idx[2, e0] // 16]
+        assert list(row[:3]) == [idx[m, e0] // 16 for m in inner]
         assert row[3] == len(mem) and row[4] == off and row[5] == k * (N - 3)
-        lid = [(idx[0, e] % 16) * 256 + (idx[1, e] % 16) * 16 + idx[2, e] % 16 for e in mem]
+        a, b, c = inner
+        lid = [(idx[a, e] % 16) * 256 + (idx[b, e] % 16) * 16 + idx[c, e] % 16 for e in mem]
         assert u["lid"][off:off + len(mem)].tolist() == lid
         assert u["val"][off:off + len(mem)].tolist() == val[mem].tolist()
         assert u["outer_coords"][k * (N - 3):(k + 1) * (N - 3)].tolist() == \
-            [int(idx[m, e0]) for m in range(3, N)]
+            [int(idx[m, e0]) for m in outer]
         off += len(mem)
     flags = np.zeros(idx.shape[1], np.uint8)
     for mem in members:
@@ -227,32 +240,36 @@ def einsum_mttkrp(X, F, n):
     letters = "abcdefg"[:N]
     spec = letters + "," + ",".join(letters[m] + "r" for m in range(N) if m != n) + \
         "->" + letters[n] + "r"
-    return np.einsum(spec, X, *[F[m] for m in range(N) if m != n])
+    return np.einsum(spec, X, *[F[m] for m in range(N) if m != n], optimize=True)
 
 
-@pytest.mark.parametrize("N,R", [(4, 8), (4, 16), (5, 32), (3, 5)])
-def test_mttkrp_nd_closed_form(orc, N, R):
+@pytest.mark.parametrize("N,R,inner", [(4, 8, (0, 1, 2)), (4, 16, (0, 1, 2)),
+                                       (5, 32, (0, 1, 2)), (3, 5, (0, 1, 2)),
+                                       (4, 8, (1, 2, 3)), (4, 8, (0, 2, 3)),
+                                       (5, 16, (1, 3, 4))])
+def test_mttkrp_nd_closed_form(orc, N, R, inner):
     rng = np.random.default_rng(N * 10 + R)
-    dims = (40, 30, 36, 4, 3)[:N]
-    cells = np.array(np.meshgrid(np.arange(16), np.arange(16, 30), np.arange(0, 16),
-                                 indexing="ij")).reshape(3, -1)
-    cells = cells[:, rng.random(cells.shape[1]) < 0.5]
-    clus = np.concatenate([cells] + [np.full((1, cells.shape[1]), 1)] * (N - 3))
-    bg, _ = rand_nd(rng, dims, 3000, dup=True)
-    idx = np.ascontiguousarray(np.concatenate([clus.astype(np.uint32), bg], axis=1))
+    dims = (40, 30, 36, 33, 34)[:N]
+    idx = clustered(rng, dims, inner, 0.5, 3000)
+    # duplicates: repeat a few elements
+    idx = np.ascontiguousarray(np.concatenate([idx, idx[:, :50]], axis=1))
     val = rng.standard_normal(idx.shape[1])
     F = [rng.random((d, R)) for d in dims]
     X = dense_of(idx, val, dims)
     enabled = N >= 4
-    u = orc.dense_nd(idx, val, dims, 0.03) if enabled else None
+    u = orc.dense_nd(idx, val, dims, 0.03, inner) if enabled else None
+    if enabled:
+        assert len(u["unit6"]) > 0
     isd = u["is_dense"] if enabled else None
-    v = orc.views_nd(idx, val, dims, isd, enabled)
+    v = orc.views_nd(idx, val, dims, isd, enabled, inner)
     for n in range(N):
-        inner = enabled and n < 3
+        is_inner = enabled and n in inner
+        if enabled:
+            assert all(v[n]["single"] == 0) or not is_inner
         out = np.zeros(dims[n] * R)
-        if inner:
+        if is_inner:
             out = orc.mttkrp_units_nd(idx, val, dims, u, n, [f.ravel() for f in F], R)
-        out = orc.mttkrp_seg_nd(idx, val, dims, v, n, inner, [f.ravel() for f in F], R, out)
+        out = orc.mttkrp_seg_nd(idx, val, dims, v, n, is_inner, [f.ravel() for f in F], R, out)
         assert rel_err(out.reshape(dims[n], R), einsum_mttkrp(X, F, n)) < 1e-12, n
 
 
