@@ -12,14 +12,14 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import (CLI_PATH, LIB_PATH, SIGNATURES, Als3Info, Als3Opts, Coo, CptcError, check,
-                   lib)  # noqa: F401  (check is part of the public surface)
+from ._lib import (CLI_PATH, LIB_PATH, SIGNATURES, Als3Info, Als3Opts, Coo, CptcError, GenInfo,
+                   GenOpts, check, lib)  # noqa: F401  (check is part of the public surface)
 
 __all__ = [
     "lib", "LIB_PATH", "CLI_PATH", "SIGNATURES", "CptcError", "Tensor", "synth_config",
     "synth_zipf", "synth_lowrank3", "synth_blocks3", "synth_units5", "load_tns3",
     "load_tns_generic", "probe_nmodes", "write_tns", "cadr3", "Als3", "device_count", "ptr",
-    "DevBuf", "sync", "check",
+    "DevBuf", "sync", "check", "gen_reorder", "gen_hash", "gen_selftest", "Gen",
 ]
 
 
@@ -45,7 +45,9 @@ class DevBuf:
 
     def __init__(self, nbytes: int, dtype=np.uint8, shape=None):
         self.dtype = np.dtype(dtype)
-        self.shape = tuple(shape) if shape is not None else (nbytes // self.dtype.itemsize,)
+        if shape is None:
+            shape = (nbytes // self.dtype.itemsize,)
+        self.shape = (int(shape),) if np.isscalar(shape) else tuple(shape)
         self.nbytes = int(nbytes)
         p = C.c_void_p()
         check(lib.cptc_dev_malloc(self.nbytes, C.byref(p)), "cptc_dev_malloc")
@@ -307,3 +309,149 @@ class Als3:
                                   d["pool_lid"].ctypes.data, d["pool_val"].ctypes.data),
               "cptc_als3_tiles")
         return d
+
+
+def gen_reorder(t: Tensor, how: str | None = None, rounds: int = 3,
+                sample_budget: int = 8000000) -> tuple[Tensor, list, bool]:
+    """apply_reordering (generic.cu:1176-1376) on a copy: (relabelled tensor,
+    per-mode rank maps new = rank[old], applied)."""
+    work = Tensor(tuple(t.dims), np.array(t.idx, dtype=np.uint32, order="C", copy=True), t.val)
+    c, keep = work.as_coo()
+    rank = np.zeros(int(sum(t.dims)), np.uint32)
+    applied = C.c_int()
+    check(lib.cptc_gen_reorder(C.byref(c), None if how is None else how.encode(), rounds,
+                               sample_budget, rank.ctypes.data, C.byref(applied)),
+          "cptc_gen_reorder")
+    idx = keep[0].copy()
+    ranks, off = [], 0
+    for d in t.dims:
+        ranks.append(rank[off:off + d].copy())
+        off += d
+    return Tensor(tuple(t.dims), idx, t.val.copy()), ranks, bool(applied.value)
+
+
+def gen_hash(x: int) -> int:
+    return int(lib.cptc_gen_hash(x))
+
+
+def gen_selftest(verbose: bool = False) -> int:
+    """run_dense_selftest (generic.cu:1389-1637); returns the failure count."""
+    f = C.c_int()
+    check(lib.cptc_gen_selftest(int(verbose), C.byref(f)), "cptc_gen_selftest")
+    return f.value
+
+
+class Gen:
+    """Generic N-order CP-ALS on the device (reorder, units, views, factors)."""
+
+    def __init__(self, t: Tensor, R: int = 16, seed: int = 42, reorder: str | None = None,
+                 rounds: int = 3, sample: int = 8000000, dense: bool = True,
+                 threshold: float = 0.03, inner=(0, 1, 2), svd: bool = False,
+                 profile: bool = False, verbose: bool = False):
+        o = GenOpts()
+        lib.cptc_gen_default_opts(C.byref(o))
+        o.R, o.seed = R, seed
+        o.reorder = (reorder or "").encode()
+        o.reorder_rounds, o.reorder_sample = rounds, sample
+        o.dense, o.threshold = int(dense), threshold
+        for q in range(3):
+            o.inner[q] = inner[q]
+        o.svd, o.profile, o.verbose = int(svd), int(profile), int(verbose)
+        c, keep = t.as_coo()
+        h = C.c_void_p()
+        check(lib.cptc_gen_create(C.byref(c), C.byref(o), C.byref(h)), "cptc_gen_create")
+        del keep
+        self._h = h
+        self.R = R
+        self.info = GenInfo()
+        check(lib.cptc_gen_info_get(h, C.byref(self.info)), "cptc_gen_info_get")
+        self.N = int(self.info.nmodes)
+        self.dims = tuple(int(self.info.dims[m]) for m in range(self.N))
+        self.nnz = int(self.info.nnz)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib.cptc_gen_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def run(self, iters: int):
+        """(fit, iprod, model2, ms) per iteration."""
+        out = [np.zeros(iters, np.float64) for _ in range(4)]
+        check(lib.cptc_gen_run(self._h, iters, *(a.ctypes.data for a in out)), "cptc_gen_run")
+        return tuple(out)
+
+    def profile(self, reset: bool = True):
+        out = np.zeros(5, np.float64)
+        it = C.c_int()
+        check(lib.cptc_gen_profile(self._h, out.ctypes.data, C.byref(it), int(reset)),
+              "cptc_gen_profile")
+        return out, it.value
+
+    def mttkrp(self, mode: int) -> np.ndarray:
+        out = np.zeros((self.dims[mode], self.R), np.float64)
+        check(lib.cptc_gen_mttkrp(self._h, mode, out.ctypes.data), "cptc_gen_mttkrp")
+        return out
+
+    def factor(self, mode: int) -> np.ndarray:
+        out = np.zeros((self.dims[mode], self.R), np.float64)
+        check(lib.cptc_gen_factor(self._h, mode, out.ctypes.data), "cptc_gen_factor")
+        return out
+
+    def set_factor(self, mode: int, f: np.ndarray) -> None:
+        f = np.ascontiguousarray(f, np.float64)
+        assert f.shape == (self.dims[mode], self.R)
+        check(lib.cptc_gen_set_factor(self._h, mode, f.ctypes.data), "cptc_gen_set_factor")
+
+    def lam(self) -> np.ndarray:
+        out = np.zeros(self.R, np.float64)
+        check(lib.cptc_gen_lambda(self._h, out.ctypes.data), "cptc_gen_lambda")
+        return out
+
+    def residual(self):
+        r, x = C.c_double(), C.c_double()
+        check(lib.cptc_gen_residual(self._h, C.byref(r), C.byref(x)), "cptc_gen_residual")
+        return r.value, x.value
+
+    def rank(self, mode: int) -> np.ndarray:
+        out = np.zeros(self.dims[mode], np.uint32)
+        check(lib.cptc_gen_rank(self._h, mode, out.ctypes.data), "cptc_gen_rank")
+        return out
+
+    def coords(self) -> np.ndarray:
+        out = np.zeros((self.N, self.nnz), np.uint32)
+        check(lib.cptc_gen_coords(self._h, out.ctypes.data), "cptc_gen_coords")
+        return out
+
+    def view(self, mode: int) -> dict:
+        nnz, nseg = self.nnz, int(self.info.nseg[mode])
+        d = {"scoords": np.zeros((self.N - 1, nnz), np.uint32),
+             "vals": np.zeros(nnz, np.float64), "skip": np.zeros(nnz, np.uint8),
+             "row": np.zeros(nseg, np.uint32), "start": np.zeros(nseg, np.uint32),
+             "cnt": np.zeros(nseg, np.uint32), "single": np.zeros(nseg, np.uint8)}
+        check(lib.cptc_gen_view(self._h, mode, *(d[k].ctypes.data for k in
+                                                 ("scoords", "vals", "skip", "row", "start",
+                                                  "cnt", "single"))), "cptc_gen_view")
+        return d
+
+    def units(self) -> dict:
+        nu, nd = int(self.info.n_units), int(self.info.dense_nnz)
+        nout = max(self.N - 3, 0)
+        d = {"unit6": np.zeros((nu, 6), np.uint32), "outer_coords": np.zeros(nu * nout, np.uint32),
+             "lid": np.zeros(nd, np.uint32), "val": np.zeros(nd, np.float64),
+             "is_dense": np.zeros(self.nnz, np.uint8)}
+        check(lib.cptc_gen_units(self._h, *(d[k].ctypes.data for k in
+                                            ("unit6", "outer_coords", "lid", "val",
+                                             "is_dense"))), "cptc_gen_units")
+        return d
+
+    def dump(self, base: str) -> None:
+        check(lib.cptc_gen_dump(self._h, base.encode()), "cptc_gen_dump")

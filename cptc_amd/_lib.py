@@ -66,6 +66,40 @@ class Als3Info(C.Structure):
     ]
 
 
+class GenOpts(C.Structure):
+    _fields_ = [
+        ("R", C.c_int),
+        ("seed", C.c_uint),
+        ("reorder", C.c_char * 8),
+        ("reorder_rounds", C.c_int),
+        ("reorder_sample", C.c_uint64),
+        ("dense", C.c_int),
+        ("threshold", C.c_double),
+        ("inner", C.c_int * 3),
+        ("svd", C.c_int),
+        ("profile", C.c_int),
+        ("verbose", C.c_int),
+    ]
+
+
+class GenInfo(C.Structure):
+    _fields_ = [
+        ("nmodes", C.c_int),
+        ("dims", C.c_uint64 * CPTC_MAX_MODES),
+        ("nnz", C.c_uint64),
+        ("R", C.c_int),
+        ("reorder", C.c_char * 8),
+        ("reordered", C.c_int),
+        ("dense_enabled", C.c_int),
+        ("cutoff", C.c_int),
+        ("inner", C.c_int * 3),
+        ("n_units", C.c_uint64),
+        ("dense_nnz", C.c_uint64),
+        ("nseg", C.c_uint64 * CPTC_MAX_MODES),
+        ("prep_ms", C.c_double * 3),
+    ]
+
+
 _P = C.c_void_p
 _I = C.c_int
 _Z = C.c_size_t
@@ -121,6 +155,33 @@ SIGNATURES = {
     "cptc_als3_view": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "cptc_als3_tiles": (_I, [_P, _P, _P, _P, _P]),
     "cptc_als3_destroy": (_I, [_P]),
+    "cptc_gen_reorder": (_I, [C.POINTER(Coo), C.c_char_p, _I, _U64, _P, C.POINTER(_I)]),
+    "cptc_gen_hash": (_U64, [_U64]),
+    "cptc_mttkrp_seg_nd": (_I, [_I, _I, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P, _P, _I, _P]),
+    "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
+    "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
+    "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
+    "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
+    "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
+    "cptc_gen_normalize": (_I, [_P, _Z, _I, _P, _P]),
+    "cptc_residual_nd": (_I, [_I, _P, _P, _U64, _P, _P, _I, _P, _P]),
+    "cptc_gen_default_opts": (None, [C.POINTER(GenOpts)]),
+    "cptc_gen_create": (_I, [C.POINTER(Coo), C.POINTER(GenOpts), C.POINTER(_P)]),
+    "cptc_gen_info_get": (_I, [_P, C.POINTER(GenInfo)]),
+    "cptc_gen_run": (_I, [_P, _I, _P, _P, _P, _P]),
+    "cptc_gen_profile": (_I, [_P, _P, C.POINTER(_I), _I]),
+    "cptc_gen_mttkrp": (_I, [_P, _I, _P]),
+    "cptc_gen_factor": (_I, [_P, _I, _P]),
+    "cptc_gen_set_factor": (_I, [_P, _I, _P]),
+    "cptc_gen_lambda": (_I, [_P, _P]),
+    "cptc_gen_residual": (_I, [_P, C.POINTER(_D), C.POINTER(_D)]),
+    "cptc_gen_rank": (_I, [_P, _I, _P]),
+    "cptc_gen_coords": (_I, [_P, _P]),
+    "cptc_gen_view": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "cptc_gen_units": (_I, [_P, _P, _P, _P, _P, _P]),
+    "cptc_gen_dump": (_I, [_P, C.c_char_p]),
+    "cptc_gen_destroy": (_I, [_P]),
+    "cptc_gen_selftest": (_I, [_I, C.POINTER(_I)]),
 }
 
 

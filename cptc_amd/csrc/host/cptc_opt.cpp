@@ -4,6 +4,7 @@
 // run the hybrid driver, other orders (or ALS_GENERIC_FORCE=1) the generic
 // N-order driver; GEN_SELFTEST=1 runs the dense-unit known-answer test.
 // Log lines keep the reference's formats ("[ALS] iter k/n time=X ms fit=Y").
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -56,6 +57,86 @@ int export_factors(void* h, const char* prefix, const uint64_t dims[3], int R)
     return 0;
 }
 
+// generic.cu:1639-2366 through the C ABI (run_generic_cp's log lines)
+int run_generic(const std::string& filename, int order, int max_iters, int R)
+{
+    std::printf("[Main] order-%d tensor -> generic N-order CP-ALS (pure FP64, MFMA dense units "
+                "for the inner modes)\n",
+                order);
+    cptc_coo coo{};
+    const double t0 = now_ms();
+    int rc = cptc_tns_load_generic(filename.c_str(), &coo);
+    if (rc != CPTC_OK) return fail("load", rc);
+    std::printf("[Main] Load time = %g ms | dims = ", now_ms() - t0);
+    for (int m = 0; m < coo.nmodes; ++m)
+        std::printf("%s%llu", m ? " x " : "", (unsigned long long)coo.dims[m]);
+    std::printf(" | NNZ = %llu\n", (unsigned long long)coo.nnz);
+    cptc_gen_opts o;
+    cptc_gen_default_opts(&o);
+    o.R = R;
+    o.verbose = 1;
+    void* h = nullptr;
+    rc = cptc_gen_create(&coo, &o, &h);
+    const uint64_t nnz = coo.nnz;
+    cptc_coo_free(&coo);
+    if (rc != CPTC_OK)
+    {
+        std::fprintf(stderr, "%s\n", cptc_last_error());
+        return 1;
+    }
+    std::printf("[GEN] N-order CP-ALS: R=%d iters=%d\n", R, max_iters);
+    std::vector<double> fit(static_cast<size_t>(max_iters));
+    const double t1 = now_ms();
+    rc = cptc_gen_run(h, max_iters, fit.data(), nullptr, nullptr, nullptr);
+    if (rc != CPTC_OK)
+    {
+        cptc_gen_destroy(h);
+        return fail("ALS", rc);
+    }
+    if (const char* base = std::getenv("GEN_DUMP"))
+    {
+        if (cptc_gen_dump(h, base) == CPTC_OK)
+            std::printf("[GEN] factors dumped to %s.factors.txt\n", base);
+        else
+            std::fprintf(stderr, "[GEN] factor dump to %s.factors.txt failed: %s\n", base,
+                         cptc_last_error());
+    }
+    std::printf("[GEN] ALS total = %g ms\n", now_ms() - t1);
+    if (o.profile)
+    {
+        double p[5];
+        int it = 0;
+        cptc_gen_profile(h, p, &it, 0);
+        const double n = it > 0 ? double(it) : 1.0;
+        const double tot = p[0] + p[1] + p[2] + p[3] + p[4];
+        std::printf("[GEN][profile] avg/iter over %d iters: gram=%g mttkrp=%g solve=%g norm=%g "
+                    "fit=%g (sum=%g ms)\n",
+                    it, p[0] / n, p[1] / n, p[2] / n, p[3] / n, p[4] / n, tot / n);
+        if (tot > 0.0)
+            std::printf("[GEN][profile] share: gram=%g%% mttkrp=%g%% solve=%g%% norm=%g%% "
+                        "fit=%g%%\n",
+                        100.0 * p[0] / tot, 100.0 * p[1] / tot, 100.0 * p[2] / tot,
+                        100.0 * p[3] / tot, 100.0 * p[4] / tot);
+    }
+    double res2 = 0.0, x2 = 0.0;
+    rc = cptc_gen_residual(h, &res2, &x2);
+    if (rc != CPTC_OK)
+    {
+        cptc_gen_destroy(h);
+        return fail("residual", rc);
+    }
+    const double res = std::sqrt(std::max(res2, 0.0)), xn = std::sqrt(x2);
+    std::printf("[GEN] exact: ||X-Xhat||_F=%g RMSE=%g fit=%g (||X||_F=%g)\n", res,
+                nnz ? res / std::sqrt(double(nnz)) : 0.0, xn > 0.0 ? 1.0 - res / xn : 0.0, xn);
+    std::vector<double> lam(static_cast<size_t>(R));
+    cptc_gen_lambda(h, lam.data());
+    std::printf("[GEN] lambda =");
+    for (double x : lam) std::printf(" %g", x);
+    std::printf("\n");
+    cptc_gen_destroy(h);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv)
@@ -77,8 +158,10 @@ int main(int argc, char** argv)
     }
     if (std::getenv("GEN_SELFTEST"))
     {
-        std::fprintf(stderr, "[SELFTEST] the generic dense-unit self-test is not built yet\n");
-        return 1;
+        int failures = 0;
+        const int rc = cptc_gen_selftest(1, &failures);
+        if (rc != CPTC_OK) return fail("self-test", rc);
+        return failures ? 1 : 0;
     }
     const int order = cptc_tns_probe_nmodes(filename.c_str());
     if (order < 0)
@@ -87,11 +170,7 @@ int main(int argc, char** argv)
         return 1;
     }
     if (order != 3 || std::getenv("ALS_GENERIC_FORCE"))
-    {
-        std::printf("[Main] order-%d tensor -> generic N-order CP-ALS\n", order);
-        std::fprintf(stderr, "[GEN] the generic N-order driver is not built yet\n");
-        return 1;
-    }
+        return run_generic(filename, order, max_iters, R);
 
     std::printf("[Main] Loading real tensor dataset from file: %s\n", filename.c_str());
     cptc_coo coo{};

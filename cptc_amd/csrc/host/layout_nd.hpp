@@ -1,0 +1,59 @@
+// Device-resident layout of the generic N-order path: the dense units
+// (GDense, generic.cu:564-725) and one row-segmented view per mode
+// (ModeView, generic.cu:1848-1958).  Buffers are owned by the structs and
+// released with free_*().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace cptc {
+
+struct DevUnitsN
+{
+    int cutoff = 0;
+    int inner[3] = {0, 1, 2};
+    std::vector<int> outer;              // outer modes, ascending
+    uint64_t nunits = 0;
+    uint64_t dense_nnz = 0;
+    uint32_t* d_unit6 = nullptr;         // nunits x {bi, bj, bk, nnz, start, outer_off}
+    uint32_t* d_outer_coords = nullptr;  // nunits x outer.size()
+    uint32_t* d_lid = nullptr;           // dense_nnz, la*256 + lb*16 + lc
+    double* d_val = nullptr;             // dense_nnz
+    uint8_t* d_is_dense = nullptr;       // nnz, element order
+};
+
+struct DevViewN
+{
+    uint64_t nnz = 0;
+    uint64_t nseg = 0;
+    uint32_t* d_sc = nullptr;      // (N-1) x nnz, other modes ascending
+    double* d_vals = nullptr;
+    uint8_t* d_skip = nullptr;     // view order; null when no dense units
+    uint32_t* d_row = nullptr;
+    uint32_t* d_start = nullptr;
+    uint32_t* d_cnt = nullptr;
+    uint8_t* d_single = nullptr;
+};
+
+void free_units(DevUnitsN& u);
+void free_view(DevViewN& v);
+
+// Dense units of a device COO (coords N x nnz mode-major).  Units are the
+// hash keys with count >= cutoff = int(4096 * threshold), numbered by first
+// occurrence; pools hold each unit's elements in element order.
+int units_nd_device(int N, const uint64_t* dims, const uint32_t* d_coords, const double* d_vals,
+                    uint64_t nnz, double threshold, const int inner[3], DevUnitsN& out,
+                    hipStream_t s);
+
+// Mode n's view: elements stably sorted by coordinate n, rows cut into
+// <= 1024-element segments; single = the row's only segment unless
+// force_accumulate.  d_is_dense (element order) may be null.
+int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
+                   const double* d_vals, const uint8_t* d_is_dense, bool force_accumulate,
+                   uint64_t nnz, DevViewN& out, hipStream_t s);
+
+}  // namespace cptc

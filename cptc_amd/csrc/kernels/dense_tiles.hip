@@ -1,7 +1,9 @@
-// Dense 16^3 tiles of an order-3 tensor on CDNA4 FP32 MFMA with an FP64
-// epilogue — the gfx950 counterpart of dense_tile_mttkrp_wmma
-// (dense.cu:89-1077; gfx950 has no xf32, so the inner products run in FP32,
-// which is more accurate than the reference's TF32).
+// Dense 16^3 tiles on CDNA4 FP32 MFMA with an FP64 epilogue — the gfx950
+// counterpart of dense_tile_mttkrp_wmma (dense.cu:89-1077) for order-3 tiles
+// and of g_dense_tile_mttkrp_kernel (generic.cu:429-561) for the generic
+// path's dense units, whose contribution is also scaled by the unit's FP64
+// outer-mode weights.  gfx950 has no xf32, so the inner products run in FP32,
+// which is more accurate than the reference's TF32.
 //
 // For target mode 0 and one 16-rank block rb:
 //   out_k[i, r] = sum_j T[i, j, k] * B[b1 + j, rb + r]        (FP32 MFMA)
@@ -33,18 +35,21 @@ __device__ inline float fold(const double* __restrict__ F, int row, int dim, int
     return (row < dim && r < R) ? float(F[size_t(row) * R + r]) : 0.0f;
 }
 
-template <int MODE>
-__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles3_kernel(
-    const int32_t* __restrict__ tiles4, const float* __restrict__ tile_f32, size_t ntiles,
+// MODE = target slot; HDR = int32 words per tile header (bi, bj, bk first):
+// 4 for order-3 tiles, 6 for generic units.  HAS_W: the unit's FP64 outer
+// weights W[t, r] scale its contribution (generic N-order units).
+template <int MODE, int HDR, bool HAS_W>
+__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_kernel(
+    const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32, size_t ntiles,
     const double* __restrict__ A, const double* __restrict__ B, const double* __restrict__ C,
-    double* __restrict__ FtV, int R, int dimI, int dimJ, int dimK)
+    const double* __restrict__ W, double* __restrict__ FtV, int R, int dimI, int dimJ, int dimK)
 {
     const size_t t = size_t(blockIdx.x) * WAVES_PER_WG + threadIdx.x / WAVE;
     if (t >= ntiles) return;
     const int lane = threadIdx.x & (WAVE - 1);
     const int lo = lane & 15;   // m (A operand row) / n (B, D column)
     const int hi = lane >> 4;   // kk (A, B) / m-group (D)
-    const int b0 = tiles4[4 * t] * 16, b1 = tiles4[4 * t + 1] * 16, b2 = tiles4[4 * t + 2] * 16;
+    const int b0 = hdr[HDR * t] * 16, b1 = hdr[HDR * t + 1] * 16, b2 = hdr[HDR * t + 2] * 16;
     const float* __restrict__ T = tile_f32 + t * 4096;
 
     // cells[s][x]: A operand of K-step s for slice x
@@ -126,6 +131,12 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
         }
         if (r < R)
         {
+            if constexpr (HAS_W)
+            {
+                const double wr = W[t * size_t(R) + r];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) tot[v] *= wr;
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v)
             {
@@ -194,15 +205,45 @@ extern "C" int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const 
     hipStream_t s = cptc::as_stream(stream);
     const dim3 grid{static_cast<unsigned>(wgs)};
     const dim3 block{WAVE * WAVES_PER_WG};
+    const double* noW = nullptr;
     if (mode == 0)
-        hipLaunchKernelGGL(dense_tiles3_kernel<0>, grid, block, 0, s, d_tiles, d_tile_f32, ntiles,
-                           d_A, d_B, d_C, d_FtV, R, dimI, dimJ, dimK);
+        hipLaunchKernelGGL((dense_tiles_kernel<0, 4, false>), grid, block, 0, s, d_tiles,
+                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
     else if (mode == 1)
-        hipLaunchKernelGGL(dense_tiles3_kernel<1>, grid, block, 0, s, d_tiles, d_tile_f32, ntiles,
-                           d_A, d_B, d_C, d_FtV, R, dimI, dimJ, dimK);
+        hipLaunchKernelGGL((dense_tiles_kernel<1, 4, false>), grid, block, 0, s, d_tiles,
+                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
     else
-        hipLaunchKernelGGL(dense_tiles3_kernel<2>, grid, block, 0, s, d_tiles, d_tile_f32, ntiles,
-                           d_A, d_B, d_C, d_FtV, R, dimI, dimJ, dimK);
+        hipLaunchKernelGGL((dense_tiles_kernel<2, 4, false>), grid, block, 0, s, d_tiles,
+                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                                    const float* d_tiles, const double* d_W, const double* d_F0,
+                                    const double* d_F1, const double* d_F2, int dim0, int dim1,
+                                    int dim2, double* d_FtV, int R, void* stream)
+{
+    CPTC_REQUIRE(slot >= 0 && slot < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd: slot %d R %d", slot, R);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_tiles && d_W && d_F0 && d_F1 && d_F2 && d_FtV, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd: null pointer");
+    const size_t wgs = (nunits + WAVES_PER_WG - 1) / WAVES_PER_WG;
+    CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "cptc_mttkrp_units_nd: too many units");
+    hipStream_t s = cptc::as_stream(stream);
+    const dim3 grid{static_cast<unsigned>(wgs)};
+    const dim3 block{WAVE * WAVES_PER_WG};
+    const int32_t* h = reinterpret_cast<const int32_t*>(d_unit6);
+    if (slot == 0)
+        hipLaunchKernelGGL((dense_tiles_kernel<0, 6, true>), grid, block, 0, s, h, d_tiles,
+                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
+    else if (slot == 1)
+        hipLaunchKernelGGL((dense_tiles_kernel<1, 6, true>), grid, block, 0, s, h, d_tiles,
+                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
+    else
+        hipLaunchKernelGGL((dense_tiles_kernel<2, 6, true>), grid, block, 0, s, h, d_tiles,
+                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

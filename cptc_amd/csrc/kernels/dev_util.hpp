@@ -35,8 +35,16 @@ template <class T>
 struct Tmp
 {
     T* p = nullptr;
+    Tmp() = default;
+    Tmp(const Tmp&) = delete;
+    Tmp& operator=(const Tmp&) = delete;
     ~Tmp() { dfree(p); }
-    int alloc(size_t n) { return dalloc(&p, n); }
+    int alloc(size_t n)
+    {
+        dfree(p);
+        return dalloc(&p, n);
+    }
+    void reset() { dfree(p); }
 };
 
 inline int bit_width(uint64_t v)

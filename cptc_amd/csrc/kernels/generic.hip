@@ -1,0 +1,630 @@
+// Kernels of the generic N-order CP-ALS path for CDNA4 (wave64): the FP64
+// segment MTTKRP, dense-unit packing and outer weights, the Gram Hadamard,
+// the ridge Cholesky solve, column normalisation and the exact residual.
+// The dense-unit MFMA contraction shares dense_tiles.hip with order 3.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "../host/hip_util.hpp"
+
+namespace {
+
+constexpr int WAVE = 64;
+constexpr int MAXM = CPTC_MAX_MODES;
+
+struct Factors
+{
+    const double* p[MAXM];
+};
+
+template <int VEC>
+struct Row;
+template <>
+struct Row<2>
+{
+    double x[2];
+    __device__ void load(const double* __restrict__ q)
+    {
+        const double2 v = *reinterpret_cast<const double2*>(q);
+        x[0] = v.x;
+        x[1] = v.y;
+    }
+};
+template <>
+struct Row<1>
+{
+    double x[1];
+    __device__ void load(const double* __restrict__ q) { x[0] = *q; }
+};
+
+// ------------------------------------------------------ segment MTTKRP --
+//
+// One workgroup (4 waves) per row segment of mode `mode`'s view.  A lane
+// owns VEC consecutive ranks; LPE = RT / VEC lanes cover one element, so a
+// wave carries EPW = 64 / LPE element slots (R = 32 -> 4, 16 -> 8, 8 -> 16).
+// Each slot walks a contiguous chunk of the segment.  The view keeps the
+// input order inside a row, so the first other mode (the slowest-varying one
+// of lexicographically sorted input) repeats in runs: the slot accumulates
+// t = sum v * prod_{q >= 1} F_q over a run and multiplies the run's F_0 row
+// once (acc_r = sum_runs F_0[o_0, r] * t_r).  Skipped (dense) elements do
+// not touch the factors.
+template <int N, int RT, int VEC, int UNROLL>
+__global__ __launch_bounds__(256) void seg_nd_kernel(
+    Factors F, int mode, const uint32_t* __restrict__ sc, uint64_t nnz,
+    const double* __restrict__ vals, const uint8_t* __restrict__ skip,
+    const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
+    const uint32_t* __restrict__ seg_cnt, const uint8_t* __restrict__ single,
+    double* __restrict__ FtV, int R)
+{
+    constexpr int NO = N - 1;                // other modes
+    constexpr int LPE = RT / VEC;
+    constexpr int EPW = WAVE / LPE;
+    constexpr int WAVES = 4;
+    constexpr int SLOTS = EPW * WAVES;
+
+    const double* G[NO];
+#pragma unroll
+    for (int q = 0; q < NO; ++q) G[q] = (q < mode) ? F.p[q] : F.p[q + 1];
+
+    const uint32_t seg = blockIdx.x;
+    const uint32_t row = seg_row[seg];
+    const uint32_t start = seg_start[seg];
+    const uint32_t cnt = seg_cnt[seg];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
+    const int slot = lane / LPE;
+    const int r0 = (lane % LPE) * VEC;
+    const bool rank_ok = r0 < R;
+    const int rr = rank_ok ? r0 : 0;
+
+    const uint32_t g = uint32_t(wave * EPW + slot);
+    const uint32_t chunk = (cnt + SLOTS - 1) / SLOTS;
+    uint32_t lo = start + g * chunk;
+    const uint32_t hi = (g * chunk + chunk < cnt) ? lo + chunk : start + cnt;
+    if (lo > hi) lo = hi;
+
+    double acc[VEC], t[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc[k] = t[k] = 0.0;
+    uint32_t cur = 0xFFFFFFFFu;
+
+    auto close_run = [&](uint32_t o) {
+        Row<VEC> f;
+        f.load(G[0] + size_t(o) * R + rr);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+        {
+            acc[k] += t[k] * f.x[k];
+            t[k] = 0.0;
+        }
+    };
+
+    uint32_t e = lo;
+    for (; e + UNROLL <= hi; e += UNROLL)
+    {
+        uint32_t c[UNROLL][NO];
+        double v[UNROLL];
+        bool live[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            v[u] = __builtin_nontemporal_load(vals + e + u);
+            live[u] = skip ? (__builtin_nontemporal_load(skip + e + u) == 0) : true;
+#pragma unroll
+            for (int q = 0; q < NO; ++q) c[u][q] = __builtin_nontemporal_load(sc + q * nnz + e + u);
+        }
+        double p[UNROLL][VEC];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) p[u][k] = v[u];
+            if (live[u])
+            {
+#pragma unroll
+                for (int q = 1; q < NO; ++q)
+                {
+                    Row<VEC> f;
+                    f.load(G[q] + size_t(c[u][q]) * R + rr);
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) p[u][k] *= f.x[k];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+        {
+            if (!live[u]) continue;
+            if (c[u][0] != cur)
+            {
+                if (cur != 0xFFFFFFFFu) close_run(cur);
+                cur = c[u][0];
+            }
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) t[k] += p[u][k];
+        }
+    }
+    for (; e < hi; ++e)
+    {
+        if (skip && __builtin_nontemporal_load(skip + e) != 0) continue;
+        double p[VEC];
+        const double v = __builtin_nontemporal_load(vals + e);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) p[k] = v;
+#pragma unroll
+        for (int q = 1; q < NO; ++q)
+        {
+            Row<VEC> f;
+            f.load(G[q] + size_t(__builtin_nontemporal_load(sc + q * nnz + e)) * R + rr);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) p[k] *= f.x[k];
+        }
+        const uint32_t c0 = __builtin_nontemporal_load(sc + e);
+        if (c0 != cur)
+        {
+            if (cur != 0xFFFFFFFFu) close_run(cur);
+            cur = c0;
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) t[k] += p[k];
+    }
+    if (cur != 0xFFFFFFFFu) close_run(cur);
+    if (!rank_ok)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] = 0.0;
+
+#pragma unroll
+    for (int off = LPE; off < WAVE; off <<= 1)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] += __shfl_xor(acc[k], off, WAVE);
+
+    __shared__ double red[WAVES][RT];
+    if (slot == 0)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) red[wave][r0 + k] = acc[k];
+    __syncthreads();
+    const bool store = single && single[seg] != 0;
+    for (int x = tid; x < R; x += WAVE * WAVES)
+    {
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += red[w][x];
+        double* out = FtV + size_t(row) * R + x;
+        if (store)
+            *out = tot;
+        else if (tot != 0.0)
+            atomicAdd(out, tot);
+    }
+}
+
+template <int N, int RT, int VEC>
+void launch_seg(const Factors& F, int mode, const uint32_t* sc, uint64_t nnz, const double* vals,
+                const uint8_t* skip, const uint32_t* row, const uint32_t* st, const uint32_t* cn,
+                const uint8_t* single, uint64_t nseg, double* FtV, int R, hipStream_t s)
+{
+    constexpr int UNROLL = (N <= 4) ? 4 : 2;
+    hipLaunchKernelGGL((seg_nd_kernel<N, RT, VEC, UNROLL>), dim3(unsigned(nseg)), dim3(256), 0, s,
+                       F, mode, sc, nnz, vals, skip, row, st, cn, single, FtV, R);
+}
+
+template <int N, int VEC>
+void launch_seg_r(const Factors& F, int mode, const uint32_t* sc, uint64_t nnz,
+                  const double* vals, const uint8_t* skip, const uint32_t* row, const uint32_t* st,
+                  const uint32_t* cn, const uint8_t* single, uint64_t nseg, double* FtV, int R,
+                  hipStream_t s)
+{
+    if (R <= 8)
+        launch_seg<N, 8, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s);
+    else if (R <= 16)
+        launch_seg<N, 16, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s);
+    else
+        launch_seg<N, 32, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s);
+}
+
+template <int VEC>
+void launch_seg_n(int N, const Factors& F, int mode, const uint32_t* sc, uint64_t nnz,
+                  const double* vals, const uint8_t* skip, const uint32_t* row,
+                  const uint32_t* st, const uint32_t* cn, const uint8_t* single, uint64_t nseg,
+                  double* FtV, int R, hipStream_t s)
+{
+    switch (N)
+    {
+    case 2: launch_seg_r<2, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    case 3: launch_seg_r<3, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    case 4: launch_seg_r<4, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    case 5: launch_seg_r<5, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    case 6: launch_seg_r<6, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    case 7: launch_seg_r<7, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    default: launch_seg_r<8, VEC>(F, mode, sc, nnz, vals, skip, row, st, cn, single, nseg, FtV, R, s); break;
+    }
+}
+
+// ------------------------------------------------------------ dense units --
+
+// One workgroup per unit: FP64 accumulation in LDS (duplicates summed), one
+// rounding to FP32 per cell.
+__global__ __launch_bounds__(256) void units_pack_kernel(const uint32_t* __restrict__ unit6,
+                                                         const uint32_t* __restrict__ lid,
+                                                         const double* __restrict__ val,
+                                                         float* __restrict__ tiles)
+{
+    __shared__ double T[4096];
+    const size_t u = blockIdx.x;
+    for (int c = threadIdx.x; c < 4096; c += 256) T[c] = 0.0;
+    __syncthreads();
+    const uint32_t n = unit6[6 * u + 3], st = unit6[6 * u + 4];
+    for (uint32_t e = threadIdx.x; e < n; e += 256) atomicAdd(&T[lid[st + e] & 4095u], val[st + e]);
+    __syncthreads();
+    float4* out = reinterpret_cast<float4*>(tiles + u * 4096);
+    for (int c = threadIdx.x; c < 1024; c += 256)
+        out[c] = make_float4(float(T[4 * c]), float(T[4 * c + 1]), float(T[4 * c + 2]),
+                             float(T[4 * c + 3]));
+}
+
+__global__ void units_weights_kernel(const uint32_t* __restrict__ unit6, uint64_t nunits,
+                                     const uint32_t* __restrict__ oc, int nouter, Factors Fo,
+                                     int R, double* __restrict__ W)
+{
+    const uint64_t total = nunits * uint64_t(R);
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t x = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; x < total; x += stride)
+    {
+        const uint64_t u = x / R;
+        const int r = int(x % R);
+        const uint32_t off = unit6[6 * u + 5];
+        double w = 1.0;
+#pragma unroll
+        for (int k = 0; k < MAXM; ++k)
+            if (k < nouter) w *= Fo.p[k][size_t(oc[off + k]) * R + r];
+        W[x] = w;
+    }
+}
+
+// ------------------------------------------------------------- small R x R --
+
+__global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, int skip, int RR,
+                                     double* __restrict__ out)
+{
+    for (int x = blockIdx.x * blockDim.x + threadIdx.x; x < RR; x += gridDim.x * blockDim.x)
+    {
+        double v = 1.0;
+        for (int g = 0; g < ngram; ++g)
+            if (g != skip) v *= G[size_t(g) * RR + x];
+        out[x] = v;
+    }
+}
+
+// Ridge Cholesky + per-row substitution.  Every block (one wave) factors
+// FtF + eps I in LDS column by column (left-looking: column j needs the
+// columns < j; each entry runs the reference's k-ascending update), then each
+// lane solves rows, keeping its y / x vector in an LDS column of its own.
+constexpr int CHOL_RM = 32;
+constexpr int CHOL_T = 64;
+
+__global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __restrict__ FtF,
+                                                            const double* __restrict__ FtV,
+                                                            double* __restrict__ F, size_t dim,
+                                                            int R)
+{
+    __shared__ double L[CHOL_RM][CHOL_RM + 1];
+    __shared__ double Y[CHOL_RM][CHOL_T];
+    __shared__ double eps_s;
+    const int tid = threadIdx.x;
+    if (tid == 0)
+    {
+        double tr = 0.0;
+        for (int i = 0; i < R; ++i) tr += FtF[i * R + i];
+        eps_s = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
+    }
+    __syncthreads();
+    const double eps = eps_s;
+    for (int j = 0; j < R; ++j)
+    {
+        if (tid == 0)
+        {
+            double s = FtF[j * R + j] + eps;
+            for (int k = 0; k < j; ++k) s -= L[j][k] * L[j][k];
+            L[j][j] = (s > 0.0) ? sqrt(s) : sqrt(eps);
+        }
+        __syncthreads();
+        const int i = j + 1 + tid;
+        if (i < R)
+        {
+            double s = FtF[i * R + j];
+            for (int k = 0; k < j; ++k) s -= L[i][k] * L[j][k];
+            L[i][j] = s / L[j][j];
+        }
+        __syncthreads();
+    }
+    const size_t stride = size_t(gridDim.x) * CHOL_T;
+    for (size_t row = size_t(blockIdx.x) * CHOL_T + tid; row < dim; row += stride)
+    {
+        const double* b = FtV + row * R;
+        for (int i = 0; i < R; ++i)
+        {
+            double s = b[i];
+            for (int k = 0; k < i; ++k) s -= L[i][k] * Y[k][tid];
+            Y[i][tid] = s / L[i][i];
+        }
+        for (int i = R - 1; i >= 0; --i)
+        {
+            double s = Y[i][tid];
+            for (int k = i + 1; k < R; ++k) s -= L[k][i] * Y[k][tid];
+            Y[i][tid] = s / L[i][i];   // x[i]; y[i] is no longer needed
+        }
+        double* out = F + row * R;
+        for (int i = 0; i < R; ++i) out[i] = Y[i][tid];
+    }
+}
+
+// Column sums of squares: P partials of R each (deterministic).
+__global__ __launch_bounds__(256) void colsq_partial_kernel(const double* __restrict__ F,
+                                                            size_t rows, int R,
+                                                            double* __restrict__ part)
+{
+    // 256 threads = (256 / R) row lanes x R ranks (R <= 32 -> >= 8 row lanes)
+    __shared__ double red[256];
+    const int r = threadIdx.x % R;
+    const int rl = threadIdx.x / R;
+    const int nrl = 256 / R;
+    double acc = 0.0;
+    if (rl < nrl)
+        for (size_t i = size_t(blockIdx.x) * nrl + rl; i < rows; i += size_t(gridDim.x) * nrl)
+        {
+            const double v = F[i * R + r];
+            acc += v * v;
+        }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x < R)
+    {
+        double t = 0.0;
+        for (int q = 0; q < nrl; ++q) t += red[q * R + threadIdx.x];
+        part[size_t(blockIdx.x) * R + threadIdx.x] = t;
+    }
+}
+
+// Every block re-reduces the partials (P x R, small), divides its rows, and
+// block 0 writes lambda.
+__global__ __launch_bounds__(256) void normalize_nd_kernel(double* __restrict__ F, size_t rows,
+                                                           int R, const double* __restrict__ part,
+                                                           int P, double* __restrict__ lambda)
+{
+    __shared__ double nrm[32];
+    if (threadIdx.x < R)
+    {
+        double s = 0.0;
+        for (int p = 0; p < P; ++p) s += part[size_t(p) * R + threadIdx.x];
+        double n = sqrt(s);
+        if (!isfinite(n) || n < 1e-14) n = 1.0;
+        nrm[threadIdx.x] = n;
+        if (blockIdx.x == 0) lambda[threadIdx.x] = n;
+    }
+    __syncthreads();
+    const size_t total = rows * size_t(R);
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < total; x += stride)
+        F[x] /= nrm[x % R];
+}
+
+// --------------------------------------------------------- exact residual --
+
+__global__ __launch_bounds__(256) void residual_nd_kernel(int nmodes,
+                                                          const uint32_t* __restrict__ coords,
+                                                          const double* __restrict__ vals,
+                                                          uint64_t nnz, Factors F,
+                                                          const double* __restrict__ lambda,
+                                                          int R, double* __restrict__ part)
+{
+    __shared__ double red[2][256];
+    double res = 0.0, sq = 0.0;
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < nnz; e += stride)
+    {
+        const double* rowp[MAXM];
+#pragma unroll
+        for (int m = 0; m < MAXM; ++m)
+            rowp[m] = (m < nmodes) ? F.p[m] + size_t(coords[uint64_t(m) * nnz + e]) * R : nullptr;
+        double xhat = 0.0;
+        for (int r = 0; r < R; ++r)
+        {
+            double p = lambda ? lambda[r] : 1.0;
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m)
+                if (m < nmodes) p *= rowp[m][r];
+            xhat += p;
+        }
+        const double v = vals[e];
+        const double d = v - xhat;
+        res += d * d;
+        sq += v * v;
+    }
+    red[0][threadIdx.x] = res;
+    red[1][threadIdx.x] = sq;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1)
+    {
+        if (int(threadIdx.x) < h)
+        {
+            red[0][threadIdx.x] += red[0][threadIdx.x + h];
+            red[1][threadIdx.x] += red[1][threadIdx.x + h];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+    {
+        part[2 * size_t(blockIdx.x)] = red[0][0];
+        part[2 * size_t(blockIdx.x) + 1] = red[1][0];
+    }
+}
+
+__global__ void finalize_add2_kernel(const double* __restrict__ part, int P,
+                                     double* __restrict__ out2)
+{
+    if (threadIdx.x < 2)
+    {
+        double t = 0.0;
+        for (int p = 0; p < P; ++p) t += part[2 * size_t(p) + threadIdx.x];
+        out2[threadIdx.x] += t;
+    }
+}
+
+bool factors_ok(int n, const double* const* h_F)
+{
+    if (!h_F) return false;
+    for (int m = 0; m < n; ++m)
+        if (!h_F[m]) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" uint64_t cptc_gen_hash(uint64_t x)
+{
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+extern "C" int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords,
+                                  const double* d_vals, const uint8_t* d_skip, uint64_t nnz,
+                                  const uint32_t* d_seg_row, const uint32_t* d_seg_start,
+                                  const uint32_t* d_seg_cnt, const uint8_t* d_single,
+                                  uint64_t nseg, const double* const* h_F, double* d_FtV, int R,
+                                  void* stream)
+{
+    CPTC_REQUIRE(nmodes >= 2 && nmodes <= MAXM && mode >= 0 && mode < nmodes, CPTC_ERR_ARG,
+                 "cptc_mttkrp_seg_nd: nmodes %d mode %d", nmodes, mode);
+    CPTC_REQUIRE(R >= 1 && R <= 32, CPTC_ERR_ARG, "cptc_mttkrp_seg_nd: R %d (1..32)", R);
+    if (nseg == 0) return CPTC_OK;
+    CPTC_REQUIRE(nseg < (uint64_t(1) << 31) && nnz <= 0x7FFFFFFFull, CPTC_ERR_ARG,
+                 "cptc_mttkrp_seg_nd: %llu segments / %llu nnz", (unsigned long long)nseg,
+                 (unsigned long long)nnz);
+    CPTC_REQUIRE(d_scoords && d_vals && d_seg_row && d_seg_start && d_seg_cnt && d_FtV &&
+                     factors_ok(nmodes, h_F),
+                 CPTC_ERR_ARG, "cptc_mttkrp_seg_nd: null pointer");
+    Factors F{};
+    bool aligned = (R % 2 == 0);
+    for (int m = 0; m < nmodes; ++m)
+    {
+        F.p[m] = h_F[m];
+        if (reinterpret_cast<uintptr_t>(h_F[m]) & 15) aligned = false;
+    }
+    hipStream_t s = cptc::as_stream(stream);
+    if (aligned)
+        launch_seg_n<2>(nmodes, F, mode, d_scoords, nnz, d_vals, d_skip, d_seg_row, d_seg_start,
+                        d_seg_cnt, d_single, nseg, d_FtV, R, s);
+    else
+        launch_seg_n<1>(nmodes, F, mode, d_scoords, nnz, d_vals, d_skip, d_seg_row, d_seg_start,
+                        d_seg_cnt, d_single, nseg, d_FtV, R, s);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_units_pack_nd(const uint32_t* d_unit6, uint64_t nunits, const uint32_t* d_lid,
+                                  const double* d_val, float* d_tiles, void* stream)
+{
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_lid && d_val && d_tiles, CPTC_ERR_ARG,
+                 "cptc_units_pack_nd: null pointer");
+    CPTC_REQUIRE(nunits < (uint64_t(1) << 31), CPTC_ERR_ARG, "cptc_units_pack_nd: too many units");
+    hipLaunchKernelGGL(units_pack_kernel, dim3(unsigned(nunits)), dim3(256), 0,
+                       cptc::as_stream(stream), d_unit6, d_lid, d_val, d_tiles);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_units_weights_nd(const uint32_t* d_unit6, uint64_t nunits,
+                                     const uint32_t* d_outer_coords, int nouter,
+                                     const int* outer_modes, const double* const* h_F, int R,
+                                     double* d_W, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && nouter >= 0 && nouter <= MAXM - 3, CPTC_ERR_ARG,
+                 "cptc_units_weights_nd: R %d nouter %d", R, nouter);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_W && (nouter == 0 || (d_outer_coords && outer_modes && h_F)),
+                 CPTC_ERR_ARG, "cptc_units_weights_nd: null pointer");
+    Factors Fo{};
+    for (int k = 0; k < nouter; ++k)
+    {
+        CPTC_REQUIRE(outer_modes[k] >= 0 && outer_modes[k] < MAXM && h_F[outer_modes[k]],
+                     CPTC_ERR_ARG, "cptc_units_weights_nd: outer mode %d", outer_modes[k]);
+        Fo.p[k] = h_F[outer_modes[k]];
+    }
+    const uint64_t total = nunits * uint64_t(R);
+    hipLaunchKernelGGL(units_weights_kernel, dim3(cptc::grid_for(total, 256, 65536)), dim3(256), 0,
+                       cptc::as_stream(stream), d_unit6, nunits, d_outer_coords, nouter, Fo, R,
+                       d_W);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R,
+                                  double* d_out, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && ngram >= 0 && d_out && (ngram == 0 || d_grams), CPTC_ERR_ARG,
+                 "cptc_gram_hadamard: bad arguments");
+    const int RR = R * R;
+    hipLaunchKernelGGL(gram_hadamard_kernel, dim3(cptc::grid_for(size_t(RR), 256, 256)),
+                       dim3(256), 0, cptc::as_stream(stream), d_grams, ngram, skip, RR, d_out);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, double* d_F,
+                                     size_t dim, int R, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 32, CPTC_ERR_ARG, "cptc_chol_ridge_solve: R %d (1..32)", R);
+    if (dim == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_FtF && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_solve: null pointer");
+    hipLaunchKernelGGL(chol_ridge_kernel, dim3(cptc::grid_for(dim, CHOL_T, 16384)), dim3(CHOL_T),
+                       0, cptc::as_stream(stream), d_FtF, d_FtV, d_F, dim, R);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_normalize(double* d_F, size_t rows, int R, double* d_lambda, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 32 && d_F && d_lambda, CPTC_ERR_ARG,
+                 "cptc_gen_normalize: R %d (1..32) or null pointer", R);
+    const int nrl = 256 / R;
+    const int P = int(cptc::grid_for(rows, unsigned(nrl) * 8, 256));
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_REDUCE, size_t(P) * R * sizeof(double), &buf));
+    double* part = static_cast<double*>(buf);
+    hipStream_t s = cptc::as_stream(stream);
+    hipLaunchKernelGGL(colsq_partial_kernel, dim3(P), dim3(256), 0, s, d_F, rows, R, part);
+    CPTC_LAUNCHED();
+    hipLaunchKernelGGL(normalize_nd_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 1024)),
+                       dim3(256), 0, s, d_F, rows, R, part, P, d_lambda);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_residual_nd(int nmodes, const uint32_t* d_coords, const double* d_vals,
+                                uint64_t nnz, const double* const* h_F, const double* d_lambda,
+                                int R, double* d_out2, void* stream)
+{
+    CPTC_REQUIRE(nmodes >= 1 && nmodes <= MAXM && R >= 1 && d_out2, CPTC_ERR_ARG,
+                 "cptc_residual_nd: nmodes %d R %d", nmodes, R);
+    if (nnz == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_coords && d_vals && factors_ok(nmodes, h_F), CPTC_ERR_ARG,
+                 "cptc_residual_nd: null pointer");
+    Factors F{};
+    for (int m = 0; m < nmodes; ++m) F.p[m] = h_F[m];
+    const int P = int(cptc::grid_for(nnz, 256 * 8, 2048));
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_REDUCE, size_t(P) * 2 * sizeof(double), &buf));
+    double* part = static_cast<double*>(buf);
+    hipStream_t s = cptc::as_stream(stream);
+    hipLaunchKernelGGL(residual_nd_kernel, dim3(P), dim3(256), 0, s, nmodes, d_coords, d_vals, nnz,
+                       F, d_lambda, R, part);
+    CPTC_LAUNCHED();
+    hipLaunchKernelGGL(finalize_add2_kernel, dim3(1), dim3(64), 0, s, part, P, d_out2);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}

@@ -289,6 +289,172 @@ int cptc_als3_tiles(void* handle, int32_t* tiles4, uint64_t* pool_off, int32_t* 
 
 int cptc_als3_destroy(void* handle);
 
+/* ========================================================================
+ * Generic N-order path (generic.cu).  Limits of the reference
+ * (generic.cu:1673-1685): 2 <= nmodes <= CPTC_MAX_MODES, 1 <= R <= 32,
+ * nnz <= 0x7FFFFFFF.  Coordinates are 0-based uint32, mode-major.
+ * Host factor-pointer arrays (`h_F`) hold one device pointer per mode
+ * (row-major dim_m x R).
+ * ======================================================================== */
+
+/* Relabels a host COO tensor in place by the reference's rules: how =
+ * "hits" | "cadr" | "none" | "auto" (NULL: "hits" when nmodes >= 4, else
+ * "cadr"; anything else: "cadr"); rounds = HITS rounds (< 1 -> 1);
+ * sample_budget = HITS element sample (0 -> 8000000; stride nnz / budget
+ * when nnz exceeds it).  rank_out (host, sum(dims) entries, may be NULL)
+ * receives new = rank[old] per mode, mode-major at offsets
+ * sum(dims[0..m-1]) (identity when no relabel happened); *applied (may be
+ * NULL) = 1 when the coordinates were relabelled.  Host code, bit-exact with
+ * apply_reordering (generic.cu:1176-1376), auto's fill probe included. */
+int cptc_gen_reorder(cptc_coo* t, const char* how, int rounds, uint64_t sample_budget,
+                     uint32_t* rank_out, int* applied);
+
+/* splitbit_hash (generic.cu:39-45), the dense-unit key hash. */
+uint64_t cptc_gen_hash(uint64_t x);
+
+/* FP64 segment MTTKRP of one mode (g_mttkrp_seg_pack_kernel,
+ * generic.cu:271-343; launch 2082-2105).  For segment b of the mode's view:
+ * acc_r = sum_e v_e prod_{m != mode} F_m[c_m(e), r] over the segment's
+ * elements with d_skip[e] == 0 (d_skip NULL: none skipped); then
+ * FtV[row_b, r] = acc_r when d_single[b] != 0, else FtV[row_b, r] += acc_r
+ * (atomic, skipped when acc_r == 0).  d_scoords: (nmodes - 1) x nnz uint32,
+ * modes ascending without `mode`.  Segments hold <= CPTC_SEG elements. */
+int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords, const double* d_vals,
+                       const uint8_t* d_skip, uint64_t nnz, const uint32_t* d_seg_row,
+                       const uint32_t* d_seg_start, const uint32_t* d_seg_cnt,
+                       const uint8_t* d_single, uint64_t nseg, const double* const* h_F,
+                       double* d_FtV, int R, void* stream);
+
+/* Dense units (GDUnit, generic.cu:422-427): d_unit6 = nunits x {bi, bj, bk,
+ * nnz, start, outer_off}; pool lid = la * 256 + lb * 16 + lc (slot order).
+ * Packs each unit's pool into a 16^3 FP32 tile (nunits x 4096 floats):
+ * duplicates summed in FP64, then rounded once (the reference sums them
+ * with FP32 shared-memory atomics, generic.cu:447-466). */
+int cptc_units_pack_nd(const uint32_t* d_unit6, uint64_t nunits, const uint32_t* d_lid,
+                       const double* d_val, float* d_tiles, void* stream);
+
+/* Per-unit FP64 weights W[u, r] = prod_{k < nouter} F_{outer[k]}[
+ * outer_coords[outer_off(u) + k], r] (generic.cu:470-490); W = 1 when
+ * nouter == 0.  outer_modes: host array of nouter mode ids. */
+int cptc_units_weights_nd(const uint32_t* d_unit6, uint64_t nunits,
+                          const uint32_t* d_outer_coords, int nouter, const int* outer_modes,
+                          const double* const* h_F, int R, double* d_W, void* stream);
+
+/* Dense-unit MTTKRP for tile slot `slot` (g_dense_tile_mttkrp_kernel,
+ * generic.cu:429-561): FtV[b_slot + t, r] += sum over the unit's two other
+ * slots of T * F_a * F_b * W[u, r], with F_slot0..2 the factors of the inner
+ * modes and dim0..2 their dims.  FP32 MFMA inner products, FP64 epilogue. */
+int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                         const float* d_tiles, const double* d_W, const double* d_F0,
+                         const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
+                         double* d_FtV, int R, void* stream);
+
+/* out = prod_{g != skip} G_g over `ngram` consecutive R x R Grams (all ones
+ * when none remain): g_fill_kernel + g_mul_kernel, generic.cu:2044-2052. */
+int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double* d_out,
+                       void* stream);
+
+/* F = FtV (FtF + eps I)^-1 per row by Cholesky, eps = 1e-12 * tr(FtF) / R +
+ * 1e-300 (tr <= 0: 1e-12 + 1e-300); a pivot s <= 0 becomes sqrt(eps).
+ * g_chol_solve_kernel, generic.cu:746-819.  R <= 32. */
+int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
+                          int R, void* stream);
+
+/* n_r = ||F[:, r]||_2 (non-finite or < 1e-14: 1); F[:, r] /= n_r;
+ * lambda[r] = n_r.  g_col_norms2 + g_norms_finalize + g_normalize +
+ * g_set_lambda, generic.cu:352-403, 867-883, 2144-2159. */
+int cptc_gen_normalize(double* d_F, size_t rows, int R, double* d_lambda, void* stream);
+
+/* out2[0] += sum_e (v_e - sum_r lambda_r prod_m F_m[c_m(e), r])^2,
+ * out2[1] += sum_e v_e^2 over a device COO (nmodes x nnz uint32 coords).
+ * g_exact_residual_kernel, generic.cu:936-967. */
+int cptc_residual_nd(int nmodes, const uint32_t* d_coords, const double* d_vals, uint64_t nnz,
+                     const double* const* h_F, const double* d_lambda, int R, double* d_out2,
+                     void* stream);
+
+/* Generic N-order CP-ALS driver (run_generic_cp, generic.cu:1639-2366). */
+typedef struct cptc_gen_opts {
+    int R;                   /* 1..32 */
+    unsigned seed;           /* GEN_SEED (main.cu: 42) */
+    char reorder[8];         /* GEN_REORDER: hits | cadr | none | auto ("" = by order) */
+    int reorder_rounds;      /* GEN_REORDER_T (3) */
+    uint64_t reorder_sample; /* GEN_REORDER_SAMPLE (8000000) */
+    int dense;               /* GEN_DENSE (1) */
+    double threshold;        /* GEN_DENSE_THRESHOLD (0.03) */
+    int inner[3];            /* GEN_DENSE_INNER (0,1,2) */
+    int svd;                 /* GEN_SOLVER=svd: truncated-SVD pinv instead of Cholesky */
+    int profile;             /* GEN_PROFILE: per-phase events */
+    int verbose;             /* reference-style [GEN] lines on stdout */
+} cptc_gen_opts;
+
+/* Defaults with the GEN_* environment switches applied. */
+void cptc_gen_default_opts(cptc_gen_opts* o);
+
+typedef struct cptc_gen_info {
+    int nmodes;
+    uint64_t dims[CPTC_MAX_MODES];
+    uint64_t nnz;
+    int R;
+    char reorder[8];         /* method used */
+    int reordered;           /* 1 = coordinates relabelled */
+    int dense_enabled;       /* 1 = dense units present and used */
+    int cutoff;
+    int inner[3];
+    uint64_t n_units;
+    uint64_t dense_nnz;
+    uint64_t nseg[CPTC_MAX_MODES];
+    double prep_ms[3];       /* reorder, dense units, views */
+} cptc_gen_info;
+
+/* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)
+ * in mode order, rows permuted by the reorder map, generic.cu:1743-1782),
+ * builds the dense units and the per-mode views on the device. */
+int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, void** handle);
+int cptc_gen_info_get(void* handle, cptc_gen_info* info);
+
+/* Runs `iters` iterations (continuing from the current state).  Arrays of
+ * length iters (may be NULL): Gram fit, iprod, model^2, wall ms per
+ * iteration (the reference's chrono span, generic.cu:2030-2249). */
+int cptc_gen_run(void* handle, int iters, double* fit, double* iprod, double* model2,
+                 double* ms_iter);
+
+/* Per-phase ms (gram, mttkrp, solve, norm, fit) summed over the iterations
+ * run with opts.profile set (generic.cu:2016-2240); *iters = iterations
+ * summed; reset != 0 zeroes the sums after reading. */
+int cptc_gen_profile(void* handle, double* out5, int* iters, int reset);
+
+/* Mode `mode`'s MTTKRP with the current factors into a host buffer
+ * (dim x R), through the same launches as the ALS loop. */
+int cptc_gen_mttkrp(void* handle, int mode, double* host_out);
+int cptc_gen_factor(void* handle, int mode, double* host_out);
+int cptc_gen_set_factor(void* handle, int mode, const double* host_in);
+int cptc_gen_lambda(void* handle, double* host_out);
+
+/* Exact ||X - Xhat||^2 and ||X||^2 over all elements (generic.cu:2319-2336). */
+int cptc_gen_residual(void* handle, double* res_sq, double* x_sq);
+
+/* Layout copies for bit-exactness tests (sizes from cptc_gen_info).  Any
+ * output pointer may be NULL.  rank: dims[mode] entries (new = rank[old]). */
+int cptc_gen_rank(void* handle, int mode, uint32_t* host_out);
+int cptc_gen_coords(void* handle, uint32_t* idx);
+int cptc_gen_view(void* handle, int mode, uint32_t* scoords, double* vals, uint8_t* skip,
+                  uint32_t* seg_row, uint32_t* seg_start, uint32_t* seg_cnt, uint8_t* single);
+int cptc_gen_units(void* handle, uint32_t* unit6, uint32_t* outer_coords, uint32_t* lid,
+                   double* val, uint8_t* is_dense);
+
+/* GEN_DUMP text dump of factors and lambda in the reordered index space
+ * (generic.cu:2253-2287) to <base>.factors.txt. */
+int cptc_gen_dump(void* handle, const char* base);
+
+int cptc_gen_destroy(void* handle);
+
+/* The dense-unit known-answer test (run_dense_selftest,
+ * generic.cu:1389-1637): a 40 x 24 x 36 x 3 tensor with two dense 16^3
+ * blocks, R = 8, inner sets (0,1,2), (1,2,3), (0,1,3), (0,2,3), each
+ * dense-only and mixed, against an FP64 host MTTKRP (relative L2 < 2e-3).
+ * *failures = failing cases; prints [SELFTEST] lines when verbose. */
+int cptc_gen_selftest(int verbose, int* failures);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,415 @@
+"""Generic N-order path on the GPU, through the C ABI, against the CPU oracle
+(oracle/cptc_oracle_nd.cpp) and numpy closed forms.
+
+Bars: layout (reorder, dense units, views) bit-exact; FP64 segment MTTKRP
+<= 1e-10 relative; dense-unit MTTKRP (FP32 MFMA, FP64 epilogue) <= 1e-5
+relative to FP64; ridge Cholesky <= 1e-11; fit within 1e-4 of the oracle
+after 20 iterations (1e-8 when no dense units are involved).
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def dbuf(ca, a):
+    return ca.DevBuf.from_numpy(np.ascontiguousarray(a))
+
+
+def fptrs(bufs):
+    return (C.c_void_p * len(bufs))(*[b.data_ptr() for b in bufs])
+
+
+def clustered(rng, dims, inner, frac, nbg, outer_at=0):
+    """Half-filled 16^3 blocks on the inner modes (one per outer value 0..1)
+    plus uniform background, duplicates removed, element order shuffled."""
+    N = len(dims)
+    parts = []
+    for o in range(2):
+        cells = np.array(np.meshgrid(np.arange(16), np.arange(16), np.arange(16, 32),
+                                     indexing="ij")).reshape(3, -1)
+        cells = cells[:, rng.random(4096) < frac]
+        blk = np.zeros((N, cells.shape[1]), np.int64)
+        for s, m in enumerate(inner):
+            blk[m] = cells[s] % dims[m]
+        for m in range(N):
+            if m not in inner:
+                blk[m] = (outer_at + o) % dims[m]
+        parts.append(blk)
+    parts.append(np.stack([rng.integers(0, d, nbg) for d in dims]))
+    idx = np.concatenate(parts, axis=1)
+    lin = np.ravel_multi_index(tuple(idx), dims)
+    _, first = np.unique(lin, return_index=True)
+    idx = idx[:, np.sort(first)]
+    idx = idx[:, rng.permutation(idx.shape[1])]
+    return np.ascontiguousarray(idx.astype(np.uint32))
+
+
+def tensor(ca, idx, dims, rng):
+    return ca.Tensor(tuple(dims), idx, rng.random(idx.shape[1]) + 0.25)
+
+
+# ------------------------------------------------------------ layout parity --
+
+@pytest.mark.parametrize("N,inner,how", [(4, (0, 1, 2), "hits"), (5, (0, 1, 2), "hits"),
+                                         (4, (1, 2, 3), "cadr"), (5, (0, 2, 4), "none")])
+def test_layout_bit_exact(ca, orc, dev, N, inner, how):
+    rng = np.random.default_rng(N)
+    dims = (40, 35, 48, 33, 20)[:N]
+    t = tensor(ca, clustered(rng, dims, inner, 0.4, 6000), dims, rng)
+    g = ca.Gen(t, R=8, reorder=how, inner=inner)
+    ref_idx, ref_rank = orc.reorder_nd(t.idx, t.val, dims, how, 3, 8000000)
+    assert np.array_equal(g.coords(), ref_idx)
+    for m in range(N):
+        exp = ref_rank[m] if len(ref_rank) else np.arange(dims[m])
+        assert np.array_equal(g.rank(m), exp)
+    u = orc.dense_nd(ref_idx, t.val, dims, 0.03, inner)
+    got = g.units()
+    assert g.info.dense_enabled == 1 and int(g.info.n_units) == len(u["unit6"]) > 0
+    assert int(g.info.cutoff) == u["cutoff"]
+    for k in ("unit6", "outer_coords", "lid", "val", "is_dense"):
+        assert np.array_equal(got[k], np.asarray(u[k]).reshape(got[k].shape)), k
+    views = orc.views_nd(ref_idx, t.val, dims, u["is_dense"], True, inner)
+    for n in range(N):
+        v = g.view(n)
+        ref = views[n]
+        assert np.array_equal(v["scoords"].ravel(), ref["scoords"]), n
+        assert np.array_equal(v["vals"], ref["vals"])
+        assert np.array_equal(v["skip"], ref["skip"])
+        for k in ("row", "start", "cnt", "single"):
+            assert np.array_equal(v[k], ref[k]), (n, k)
+
+
+def test_layout_no_dense_for_order3_and_threshold0(ca, orc, dev):
+    rng = np.random.default_rng(3)
+    dims = (40, 35, 48)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.4, 3000), dims, rng)
+    g = ca.Gen(t, R=4)
+    assert g.info.dense_enabled == 0 and g.info.reorder.decode() == "cadr"
+    views = orc.views_nd(g.coords(), t.val, dims, None, False)
+    for n in range(3):
+        assert np.array_equal(g.view(n)["single"], views[n]["single"])
+    dims4 = (40, 35, 48, 2)
+    t4 = tensor(ca, clustered(rng, dims4, (0, 1, 2), 0.4, 3000), dims4, rng)
+    g4 = ca.Gen(t4, R=4, threshold=0.0)
+    assert g4.info.dense_enabled == 0
+
+
+# ------------------------------------------------------------ kernel parity --
+
+@pytest.mark.parametrize("N,R", [(2, 5), (3, 16), (4, 1), (4, 3), (4, 8), (4, 16), (5, 31),
+                                 (5, 32), (6, 16), (8, 8)])
+def test_seg_kernel_vs_oracle(ca, orc, dev, N, R):
+    rng = np.random.default_rng(N * 100 + R)
+    dims = (70, 9, 300, 40, 25, 6, 11, 13)[:N]
+    nnz = 40000
+    idx = np.ascontiguousarray(np.stack([rng.integers(0, d, nnz) for d in dims]).astype(np.uint32))
+    idx[:, -2000:] = idx[:, :2000]               # duplicates
+    val = rng.standard_normal(nnz)
+    isd = (rng.random(nnz) < 0.3).astype(np.uint8)
+    views = orc.views_nd(idx, val, dims, isd, True)
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [dbuf(ca, f) for f in F]
+    for n in range(N):
+        v = views[n]
+        bufs = {k: dbuf(ca, v[k]) for k in ("scoords", "vals", "skip", "row", "start", "cnt",
+                                            "single")}
+        for use_skip in (False, True):
+            init = rng.standard_normal(dims[n] * R)
+            out = dbuf(ca, init.copy())
+            rc = ca.lib.cptc_mttkrp_seg_nd(
+                N, n, bufs["scoords"].data_ptr(), bufs["vals"].data_ptr(),
+                bufs["skip"].data_ptr() if use_skip else None, nnz, bufs["row"].data_ptr(),
+                bufs["start"].data_ptr(), bufs["cnt"].data_ptr(), bufs["single"].data_ptr(),
+                len(v["row"]), fptrs(dF), out.data_ptr(), R, None)
+            assert rc == 0, ca.lib.cptc_last_error()
+            ca.sync()
+            ref = orc.mttkrp_seg_nd(idx, val, dims, views, n, use_skip,
+                                    [f.ravel() for f in F], R, init.copy())
+            assert rel_err(out.numpy(), ref) <= 1e-10, (n, use_skip)
+
+
+def test_seg_kernel_single_store(ca, orc, dev):
+    """single segments store (overwrite), the others accumulate."""
+    rng = np.random.default_rng(1)
+    dims = (30, 20, 10, 5)
+    nnz = 3000
+    idx = np.ascontiguousarray(np.stack([rng.integers(0, d, nnz) for d in dims]).astype(np.uint32))
+    val = rng.random(nnz)
+    views = orc.views_nd(idx, val, dims, None, False)
+    F = [rng.random((d, 8)) for d in dims]
+    dF = [dbuf(ca, f) for f in F]
+    n = 3
+    v = views[n]
+    assert v["single"].all()          # every row fits one segment
+    bufs = {k: dbuf(ca, v[k]) for k in ("scoords", "vals", "row", "start", "cnt", "single")}
+    init = np.full(dims[n] * 8, 7.0)
+    out = dbuf(ca, init.copy())
+    assert ca.lib.cptc_mttkrp_seg_nd(4, n, bufs["scoords"].data_ptr(), bufs["vals"].data_ptr(),
+                                     None, nnz, bufs["row"].data_ptr(), bufs["start"].data_ptr(),
+                                     bufs["cnt"].data_ptr(), bufs["single"].data_ptr(),
+                                     len(v["row"]), fptrs(dF), out.data_ptr(), 8, None) == 0
+    ca.sync()
+    ref = orc.mttkrp_seg_nd(idx, val, dims, views, n, False, [f.ravel() for f in F], 8,
+                            init.copy())
+    assert rel_err(out.numpy(), ref) <= 1e-12
+
+
+@pytest.mark.parametrize("N,R,inner", [(4, 8, (0, 1, 2)), (4, 16, (0, 1, 2)), (5, 32, (0, 1, 2)),
+                                       (4, 20, (1, 2, 3)), (4, 8, (0, 2, 3)),
+                                       (5, 16, (1, 3, 4)), (4, 3, (0, 1, 3))])
+def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner):
+    rng = np.random.default_rng(N * 7 + R)
+    dims = (40, 30, 36, 33, 34)[:N]
+    idx = clustered(rng, dims, inner, 0.5, 3000)
+    idx = np.ascontiguousarray(np.concatenate([idx, idx[:, :60]], axis=1))   # duplicates
+    val = rng.standard_normal(idx.shape[1])
+    u = orc.dense_nd(idx, val, dims, 0.02, inner)
+    nu = len(u["unit6"])
+    assert nu > 0
+    F = [rng.random((d, R)) for d in dims]
+    dF = [dbuf(ca, f) for f in F]
+    d6 = dbuf(ca, np.ascontiguousarray(u["unit6"], np.uint32))
+    dlid, dval = dbuf(ca, u["lid"]), dbuf(ca, u["val"])
+    doc = dbuf(ca, u["outer_coords"] if len(u["outer_coords"]) else np.zeros(1, np.uint32))
+    tiles = ca.DevBuf.zeros((nu, 4096), np.float32)
+    W = ca.DevBuf.zeros((nu, R), np.float64)
+    assert ca.lib.cptc_units_pack_nd(d6.data_ptr(), nu, dlid.data_ptr(), dval.data_ptr(),
+                                     tiles.data_ptr(), None) == 0
+    outer = [m for m in range(N) if m not in inner]
+    om = (C.c_int * max(len(outer), 1))(*outer)
+    assert ca.lib.cptc_units_weights_nd(d6.data_ptr(), nu, doc.data_ptr(), len(outer), om,
+                                        fptrs(dF), R, W.data_ptr(), None) == 0
+    ca.sync()
+    # weights: exact FP64 products
+    w_ref = np.ones((nu, R))
+    for k in range(nu):
+        for q, m in enumerate(outer):
+            w_ref[k] *= F[m][u["outer_coords"][k * len(outer) + q]]
+    assert np.array_equal(W.numpy(), w_ref)
+    # tiles: FP64 sums of the pool rounded once
+    T = np.zeros((nu, 4096))
+    for k in range(nu):
+        n_, st = u["unit6"][k][3], u["unit6"][k][4]
+        np.add.at(T[k], u["lid"][st:st + n_], u["val"][st:st + n_])
+    assert np.array_equal(tiles.numpy(), T.astype(np.float32))
+    for slot, n in enumerate(inner):
+        out = ca.DevBuf.zeros((dims[n], R), np.float64)
+        rc = ca.lib.cptc_mttkrp_units_nd(slot, d6.data_ptr(), nu, tiles.data_ptr(), W.data_ptr(),
+                                         dF[inner[0]].data_ptr(), dF[inner[1]].data_ptr(),
+                                         dF[inner[2]].data_ptr(), dims[inner[0]],
+                                         dims[inner[1]], dims[inner[2]], out.data_ptr(), R,
+                                         None)
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        ref = orc.mttkrp_units_nd(idx, val, dims, u, n, [f.ravel() for f in F], R)
+        assert rel_err(out.numpy(), ref.reshape(dims[n], R)) <= 1e-5, (slot, n)
+
+
+@pytest.mark.parametrize("R", [1, 5, 16, 32])
+def test_chol_ridge_solve(ca, orc, dev, R):
+    rng = np.random.default_rng(R)
+    A = rng.random((50, R))
+    FtF = A.T @ A
+    Y = rng.standard_normal((777, R))
+    dA, dY = dbuf(ca, FtF), dbuf(ca, Y)
+    out = ca.DevBuf.zeros((777, R))
+    assert ca.lib.cptc_chol_ridge_solve(dA.data_ptr(), dY.data_ptr(), out.data_ptr(), 777, R,
+                                        None) == 0
+    ca.sync()
+    ref = orc.chol_solve_nd(FtF.ravel(), Y.ravel(), R).reshape(777, R)
+    assert rel_err(out.numpy(), ref) <= 1e-11
+
+
+def test_chol_ridge_singular_pivot(ca, orc, dev):
+    """A rank-deficient FtF hits the s <= 0 -> sqrt(eps) branch."""
+    R = 6
+    v = np.arange(1.0, R + 1)
+    FtF = np.outer(v, v)
+    Y = np.ones((10, R))
+    dA, dY = dbuf(ca, FtF), dbuf(ca, Y)
+    out = ca.DevBuf.zeros((10, R))
+    assert ca.lib.cptc_chol_ridge_solve(dA.data_ptr(), dY.data_ptr(), out.data_ptr(), 10, R,
+                                        None) == 0
+    ca.sync()
+    ref = orc.chol_solve_nd(FtF.ravel(), Y.ravel(), R).reshape(10, R)
+    assert np.all(np.isfinite(out.numpy()))
+    assert rel_err(out.numpy(), ref) <= 1e-6
+
+
+def test_normalize_hadamard_residual(ca, orc, dev):
+    rng = np.random.default_rng(2)
+    R = 12
+    F = rng.standard_normal((333, R))
+    F[:, 3] = 0.0                               # a zero column keeps norm 1
+    dF, lam = dbuf(ca, F), ca.DevBuf.zeros(R)
+    assert ca.lib.cptc_gen_normalize(dF.data_ptr(), 333, R, lam.data_ptr(), None) == 0
+    ca.sync()
+    n = np.linalg.norm(F, axis=0)
+    n[3] = 1.0
+    assert rel_err(lam.numpy(), n) <= 1e-14
+    assert rel_err(dF.numpy(), F / n) <= 1e-14
+    G = rng.standard_normal((4, R, R))
+    dG, out = dbuf(ca, G), ca.DevBuf.zeros((R, R))
+    for skip in (0, 2, -1):
+        assert ca.lib.cptc_gram_hadamard(dG.data_ptr(), 4, skip, R, out.data_ptr(), None) == 0
+        ca.sync()
+        ref = np.ones((R, R))
+        for g in range(4):
+            if g != skip:
+                ref = ref * G[g]
+        assert np.array_equal(out.numpy(), ref)
+    dims = (20, 7, 30, 4)
+    nnz = 2000
+    idx = np.ascontiguousarray(np.stack([rng.integers(0, d, nnz) for d in dims]).astype(np.uint32))
+    val = rng.standard_normal(nnz)
+    Fs = [rng.random((d, R)) for d in dims]
+    lamv = rng.random(R)
+    o2 = ca.DevBuf.zeros(2)
+    assert ca.lib.cptc_residual_nd(4, dbuf(ca, idx).data_ptr(), dbuf(ca, val).data_ptr(), nnz,
+                                   fptrs([dbuf(ca, f) for f in Fs]), dbuf(ca, lamv).data_ptr(), R,
+                                   o2.data_ptr(), None) == 0
+    ca.sync()
+    ref = orc.residual_nd(idx, val, dims, [f.ravel() for f in Fs], lamv, R)
+    assert abs(o2.numpy()[0] - ref) <= 1e-10 * ref
+    assert abs(o2.numpy()[1] - np.sum(val * val)) <= 1e-12 * np.sum(val * val)
+
+
+# ----------------------------------------------------------- driver parity --
+
+@pytest.mark.parametrize("N,inner", [(4, (0, 1, 2)), (5, (0, 1, 2)), (4, (1, 2, 3))])
+def test_driver_mttkrp_every_mode(ca, orc, dev, N, inner):
+    rng = np.random.default_rng(10 + N)
+    dims = (40, 35, 48, 33, 20)[:N]
+    t = tensor(ca, clustered(rng, dims, inner, 0.5, 8000), dims, rng)
+    R = 16
+    g = ca.Gen(t, R=R, inner=inner)
+    assert g.info.dense_enabled
+    idx = g.coords()
+    F = [rng.random((d, R)) for d in dims]
+    for m in range(N):
+        g.set_factor(m, F[m])
+    u = orc.dense_nd(idx, t.val, dims, 0.03, inner)
+    views = orc.views_nd(idx, t.val, dims, u["is_dense"], True, inner)
+    for n in range(N):
+        got = g.mttkrp(n)
+        ref = np.zeros(dims[n] * R)
+        if n in inner:
+            ref = orc.mttkrp_units_nd(idx, t.val, dims, u, n, [f.ravel() for f in F], R)
+        ref = orc.mttkrp_seg_nd(idx, t.val, dims, views, n, n in inner,
+                                [f.ravel() for f in F], R, ref)
+        tol = 1e-5 if n in inner else 1e-10
+        assert rel_err(got, ref.reshape(dims[n], R)) <= tol, n
+
+
+@pytest.mark.parametrize("dense,svd,how", [(True, False, "hits"), (False, False, "hits"),
+                                           (False, True, "cadr"), (True, False, "auto")])
+def test_als_fit_vs_oracle(ca, orc, dev, dense, svd, how):
+    rng = np.random.default_rng(21)
+    dims = (40, 35, 48, 6)
+    idx = clustered(rng, dims, (0, 1, 2), 0.5, 12000)
+    t = tensor(ca, idx, dims, rng)
+    R = 8
+    g = ca.Gen(t, R=R, seed=42, reorder=how, dense=dense, svd=svd)
+    fit, ip, m2, ms = g.run(20)
+    ridx, rrank = orc.reorder_nd(t.idx, t.val, dims, how, 3, 8000000)
+    rfit, rip, rm2, rF, rlam = orc.als_nd(ridx, t.val, dims, rrank, R, 42, svd, dense, 0.03, 20)
+    tol = 1e-4 if (dense and g.info.dense_enabled) else 1e-8
+    assert np.max(np.abs(fit - rfit)) <= tol, (fit[-3:], rfit[-3:])
+    if not (dense and g.info.dense_enabled):
+        for m in range(4):
+            assert rel_err(g.factor(m), rF[m].reshape(dims[m], R)) <= 1e-6
+        assert rel_err(g.lam(), rlam) <= 1e-6
+    res, x2 = g.residual()
+    ref_res = orc.residual_nd(ridx, t.val, dims, [g.factor(m).ravel() for m in range(4)],
+                              g.lam(), R)
+    assert abs(res - ref_res) <= 1e-9 * max(ref_res, 1.0)
+    assert abs(x2 - np.sum(t.val ** 2)) <= 1e-12 * x2
+    # The Gram fit is the full-tensor fit: X^2 - 2 iprod + model^2 equals
+    # ||X - Xhat||_F^2 over every cell.  The "exact" residual of the
+    # reference sums over the nonzeros only, so it can only be smaller.
+    X = np.zeros(dims)
+    np.add.at(X, tuple(ridx.astype(np.int64)), t.val)
+    Fm = [g.factor(m) for m in range(4)]
+    Xh = np.einsum("r,ar,br,cr,dr->abcd", g.lam(), *Fm, optimize=True)
+    full = np.sum((X - Xh) ** 2)
+    gram_res = x2 - 2 * ip[-1] + m2[-1]
+    assert abs(gram_res - full) <= 1e-8 * x2
+    assert res <= full * (1 + 1e-12)
+
+
+def test_profile_and_dump(ca, dev, tmp_path):
+    rng = np.random.default_rng(4)
+    dims = (40, 35, 48, 3)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.5, 4000), dims, rng)
+    g = ca.Gen(t, R=4, profile=True)
+    g.run(3)
+    ph, it = g.profile()
+    assert it == 3 and np.all(ph >= 0) and ph.sum() > 0
+    base = str(tmp_path / "dump")
+    g.dump(base)
+    lines = open(base + ".factors.txt").read().splitlines()
+    assert lines[0].startswith("# cpTC factor dump")
+    assert lines[1] == "order 4" and lines[2] == "rank 4" and lines[3] == "dims 40 35 48 3"
+    assert lines[4] == "mode 0 40 4"
+    assert np.allclose(np.array([float(x) for x in lines[5].split()]), g.factor(0)[0], rtol=0,
+                       atol=1e-15)
+    assert lines[-2] == "lambda 4"
+    assert np.allclose([float(x) for x in lines[-1].split()], g.lam(), rtol=1e-15)
+
+
+def test_rejects_unsupported(ca, dev):
+    t = ca.Tensor((4, 4, 4, 4), np.zeros((4, 3), np.uint32), np.ones(3))
+    with pytest.raises(ca.CptcError):
+        ca.Gen(t, R=33)
+    with pytest.raises(ca.CptcError):
+        ca.Gen(ca.Tensor((4, 4, 4, 4), np.zeros((4, 0), np.uint32), np.zeros(0)), R=4)
+
+
+def test_selftest(ca, dev):
+    assert ca.gen_selftest(verbose=True) == 0
+
+
+def test_config4_full_size(ca, orc, dev):
+    """Config 4 (3.3 M elements, order 4, R = 16): layout bit-exact, MTTKRP of
+    every mode, three iterations' fit against the oracle."""
+    t = ca.synth_config(4)
+    R = 16
+    g = ca.Gen(t, R=R)
+    ridx, rrank = orc.reorder_nd(t.idx, t.val, t.dims, "hits", 3, 8000000)
+    assert np.array_equal(g.coords(), ridx)
+    u = orc.dense_nd(ridx, t.val, t.dims, 0.03)
+    assert int(g.info.n_units) == len(u["unit6"])
+    got = g.units()
+    assert np.array_equal(got["is_dense"], u["is_dense"])
+    assert np.array_equal(got["lid"], u["lid"])
+    fit, _, _, _ = g.run(3)
+    rfit = orc.als_nd(ridx, t.val, t.dims, rrank, R, 42, False, True, 0.03, 3)[0]
+    assert np.max(np.abs(fit - rfit)) <= 1e-4, (fit, rfit)
+
+
+def test_cli_generic_and_selftest(ca, dev, tmp_path):
+    rng = np.random.default_rng(8)
+    dims = (40, 35, 48, 3)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.5, 3000), dims, rng)
+    path = str(tmp_path / "t4.tns")
+    ca.write_tns(path, t)
+    env = dict(os.environ, GEN_DUMP=str(tmp_path / "d"), GEN_PROFILE="1")
+    r = subprocess.run([ca.CLI_PATH, path, "3", "8"], capture_output=True, text=True, env=env,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = r.stdout
+    for s in ("[Main] order-4 tensor -> generic", "[GEN] reorder=hits(T=3)", "[GEN] dense: units=",
+              "[GEN] mode 3 view:", "[GEN] iter 3/3", "[GEN][profile] avg/iter", "[GEN] exact:",
+              "[GEN] lambda =", "factors dumped"):
+        assert s in out, s
+    assert os.path.exists(str(tmp_path / "d.factors.txt"))
+    r = subprocess.run([ca.CLI_PATH], capture_output=True, text=True,
+                       env=dict(os.environ, GEN_SELFTEST="1"), timeout=120)
+    assert r.returncode == 0 and "[SELFTEST] PASSED (0 failures)" in r.stdout, r.stdout
