@@ -157,7 +157,8 @@ SIGNATURES = {
     "cptc_als3_destroy": (_I, [_P]),
     "cptc_gen_reorder": (_I, [C.POINTER(Coo), C.c_char_p, _I, _U64, _P, C.POINTER(_I)]),
     "cptc_gen_hash": (_U64, [_U64]),
-    "cptc_mttkrp_seg_nd": (_I, [_I, _I, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P, _P, _I, _P]),
+    "cptc_mttkrp_seg_nd": (_I, [_I, _I, _P, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P, _P, _I,
+                                _P]),
     "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _I, _P]),

@@ -340,7 +340,8 @@ struct Gen
     float* d_tiles = nullptr;
     double* d_W = nullptr;
     bool w_dirty = true;
-    std::vector<cptc::DevViewN> views;
+    std::vector<cptc::DevViewN> views;   // kernel views (dense elements dropped, rows sorted)
+    std::vector<uint64_t> ref_nseg;      // segments of the reference-layout views
 
     // GEN_PROFILE: gram, mttkrp, solve, norm, fit
     std::vector<hipEvent_t> ev;
@@ -396,8 +397,9 @@ struct Gen
                                           int(dims[in3[2]]), d_FtV, R, s));
         }
         const cptc::DevViewN& v = views[n];
-        CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.d_vals, in ? v.d_skip : nullptr, nnz, v.d_row,
-                                    v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV, R, s));
+        CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals, nullptr, v.nnz,
+                                    v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV,
+                                    R, s));
         return CPTC_OK;
     }
 
@@ -681,18 +683,27 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
         for (int q = 0; q < 3; ++q) g->units.inner[q] = in[q];
     }
 
-    // views
+    // views: the kernel's (dense elements of the inner modes dropped, rows
+    // sorted over the other modes) and the reference layout's segment counts
     t0 = Clock::now();
     g->views.resize(N);
+    g->ref_nseg.assign(N, 0);
     for (int n = 0; n < N; ++n)
     {
-        const bool acc = g->dense && (g->inner_mask & (1u << n));
-        GEN_TRY(cptc::view_nd_device(N, g->dims.data(), n, g->d_coords, g->d_vals,
-                                     g->dense ? g->units.d_is_dense : nullptr, acc, g->nnz,
-                                     g->views[n], s));
+        const bool in = g->dense && (g->inner_mask & (1u << n));
+        GEN_TRY(cptc::work_view_nd_device(N, g->dims.data(), n, g->d_coords, g->d_vals,
+                                          in ? g->units.d_is_dense : nullptr, in, g->nnz,
+                                          g->views[n], s));
+        std::vector<uint64_t> deg(g->dims[n], 0);
+        const uint32_t* cn = h.c(n);
+        for (uint64_t e = 0; e < g->nnz; ++e) ++deg[cn[e]];
+        for (uint64_t d : deg) g->ref_nseg[n] += (d + CPTC_SEG - 1) / CPTC_SEG;
         if (verbose)
-            std::printf("[GEN] mode %d view: %llu segments (%llu nnz)\n", n,
-                        (unsigned long long)g->views[n].nseg, (unsigned long long)g->nnz);
+            std::printf("[GEN] mode %d view: %llu segments (%llu nnz; kernel view %llu nnz in "
+                        "%llu segments)\n",
+                        n, (unsigned long long)g->ref_nseg[n], (unsigned long long)g->nnz,
+                        (unsigned long long)g->views[n].nnz,
+                        (unsigned long long)g->views[n].nseg);
     }
     g->prep_ms[2] = ms_since(t0);
 
@@ -718,7 +729,7 @@ extern "C" int cptc_gen_info_get(void* handle, cptc_gen_info* info)
     for (int m = 0; m < g->N; ++m)
     {
         info->dims[m] = g->dims[m];
-        info->nseg[m] = g->views[m].nseg;
+        info->nseg[m] = g->ref_nseg[m];
     }
     info->nnz = g->nnz;
     info->R = g->R;
@@ -859,8 +870,20 @@ extern "C" int cptc_gen_view(void* handle, int mode, uint32_t* scoords, double* 
     CPTC_REQUIRE(handle, CPTC_ERR_ARG, "cptc_gen_view: null handle");
     Gen* g = as_gen(handle);
     CPTC_REQUIRE(mode >= 0 && mode < g->N, CPTC_ERR_ARG, "cptc_gen_view: mode %d", mode);
-    const cptc::DevViewN& v = g->views[mode];
     hipStream_t s = g->s;
+    // the reference layout, built for this copy (the kernel keeps its own views)
+    const bool in = g->dense && (g->inner_mask & (1u << mode));
+    cptc::DevViewN v;
+    struct VFree
+    {
+        cptc::DevViewN* v;
+        ~VFree() { cptc::free_view(*v); }
+    } vfree{&v};
+    CPTC_TRY(cptc::view_nd_device(g->N, g->dims.data(), mode, g->d_coords, g->d_vals,
+                                  g->dense ? g->units.d_is_dense : nullptr, in, g->nnz, v, s));
+    CPTC_REQUIRE(v.nseg == g->ref_nseg[mode], CPTC_ERR_STATE,
+                 "cptc_gen_view: %llu segments, expected %llu", (unsigned long long)v.nseg,
+                 (unsigned long long)g->ref_nseg[mode]);
     auto get = [&](void* dst, const void* src, size_t bytes) -> int {
         if (!dst || bytes == 0) return CPTC_OK;
         if (!src)
@@ -1121,11 +1144,11 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
                         cptc::DevViewN* v;
                         ~VFree() { cptc::free_view(*v); }
                     } vfree{&v};
-                    CPTC_TRY(cptc::view_nd_device(N, dims64, n, d_co, d_va, u.d_is_dense, true,
-                                                  nnz, v, s));
-                    CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.d_vals, v.d_skip, nnz, v.d_row,
-                                                v.d_start, v.d_cnt, v.d_single, v.nseg,
-                                                dF.data(), d_FtV, R, s));
+                    CPTC_TRY(cptc::work_view_nd_device(N, dims64, n, d_co, d_va, u.d_is_dense,
+                                                       true, nnz, v, s));
+                    CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals,
+                                                nullptr, v.nnz, v.d_row, v.d_start, v.d_cnt,
+                                                v.d_single, v.nseg, dF.data(), d_FtV, R, s));
                     CPTC_HIP(hipStreamSynchronize(s));
                 }
                 std::vector<double> got(size_t(R) * T.dims[n]);

@@ -30,7 +30,8 @@ struct DevViewN
 {
     uint64_t nnz = 0;
     uint64_t nseg = 0;
-    uint32_t* d_sc = nullptr;      // (N-1) x nnz, other modes ascending
+    std::vector<int> level_modes;  // mode of each d_sc row (reference views: ascending)
+    uint32_t* d_sc = nullptr;      // (N-1) x nnz
     double* d_vals = nullptr;
     uint8_t* d_skip = nullptr;     // view order; null when no dense units
     uint32_t* d_row = nullptr;
@@ -55,5 +56,15 @@ int units_nd_device(int N, const uint64_t* dims, const uint32_t* d_coords, const
 int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
                    const double* d_vals, const uint8_t* d_is_dense, bool force_accumulate,
                    uint64_t nnz, DevViewN& out, hipStream_t s);
+
+// The view the MTTKRP kernel runs on.  Dense elements (d_is_dense, may be
+// null) are dropped; each row is sorted lexicographically over the other
+// modes, smallest dimension first (level_modes), so equal coordinate
+// prefixes form runs whose factor rows the kernel gathers once per run.
+// Every segment accumulates when force_accumulate, else a row's only segment
+// stores.
+int work_view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
+                        const double* d_vals, const uint8_t* d_is_dense, bool force_accumulate,
+                        uint64_t nnz, DevViewN& out, hipStream_t s);
 
 }  // namespace cptc

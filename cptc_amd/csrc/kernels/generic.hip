@@ -40,32 +40,34 @@ struct Row<1>
 
 // ------------------------------------------------------ segment MTTKRP --
 //
-// One workgroup (4 waves) per row segment of mode `mode`'s view.  A lane
-// owns VEC consecutive ranks; LPE = RT / VEC lanes cover one element, so a
-// wave carries EPW = 64 / LPE element slots (R = 32 -> 4, 16 -> 8, 8 -> 16).
-// Each slot walks a contiguous chunk of the segment.  The view keeps the
-// input order inside a row, so the first other mode (the slowest-varying one
-// of lexicographically sorted input) repeats in runs: the slot accumulates
-// t = sum v * prod_{q >= 1} F_q over a run and multiplies the run's F_0 row
-// once (acc_r = sum_runs F_0[o_0, r] * t_r).  Skipped (dense) elements do
-// not touch the factors.
+// One workgroup (4 waves) per row segment.  A lane owns VEC consecutive
+// ranks; LPE = RT / VEC lanes cover one element, so a wave carries
+// EPW = 64 / LPE element slots (R = 32 -> 4, 16 -> 8, 8 -> 16).  Each slot
+// walks a contiguous chunk of the segment.
+//
+// The segment's other coordinates come in NO = N - 1 levels (the view's row
+// order, G[q] = factor of level q).  The slot evaluates the sum as a tree
+// over equal coordinate prefixes (the CSF form of the MTTKRP):
+//   acc = sum_{o0} G0[o0] * sum_{o1} G1[o1] * ... * sum_{o_last} v * G_last[o_last]
+// t[k] holds the open partial sum under the current prefix o0..ok; when
+// o_k changes, levels deeper than k-1 are closed (t[k] * G_k[cur_k] is
+// added one level up).  Each factor row is therefore gathered once per run
+// of its prefix; in a view without runs this is one gather per level per
+// element, the plain product.  Skipped (dense) elements touch nothing.
 template <int N, int RT, int VEC, int UNROLL>
 __global__ __launch_bounds__(256) void seg_nd_kernel(
-    Factors F, int mode, const uint32_t* __restrict__ sc, uint64_t nnz,
+    Factors F, const uint32_t* __restrict__ sc, uint64_t nnz,
     const double* __restrict__ vals, const uint8_t* __restrict__ skip,
     const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
     const uint32_t* __restrict__ seg_cnt, const uint8_t* __restrict__ single,
     double* __restrict__ FtV, int R)
 {
-    constexpr int NO = N - 1;                // other modes
+    constexpr int NO = N - 1;                // levels
+    constexpr int NL = (NO > 1) ? NO - 1 : 1; // run levels (0 .. NO-2)
     constexpr int LPE = RT / VEC;
     constexpr int EPW = WAVE / LPE;
     constexpr int WAVES = 4;
     constexpr int SLOTS = EPW * WAVES;
-
-    const double* G[NO];
-#pragma unroll
-    for (int q = 0; q < NO; ++q) G[q] = (q < mode) ? F.p[q] : F.p[q + 1];
 
     const uint32_t seg = blockIdx.x;
     const uint32_t row = seg_row[seg];
@@ -86,19 +88,68 @@ __global__ __launch_bounds__(256) void seg_nd_kernel(
     const uint32_t hi = (g * chunk + chunk < cnt) ? lo + chunk : start + cnt;
     if (lo > hi) lo = hi;
 
-    double acc[VEC], t[VEC];
+    double acc[VEC];
+    double t[NL][VEC];
+    uint32_t cur[NL];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] = t[k] = 0.0;
-    uint32_t cur = 0xFFFFFFFFu;
+    for (int k = 0; k < VEC; ++k) acc[k] = 0.0;
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+    {
+        cur[l] = 0;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) t[l][k] = 0.0;
+    }
+    bool open = false;
 
-    auto close_run = [&](uint32_t o) {
-        Row<VEC> f;
-        f.load(G[0] + size_t(o) * R + rr);
+    // close run levels from NO-2 down to `to` (all of them when to == 0)
+    auto close_levels = [&](int to) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k)
+        for (int l = NL - 1; l >= 0; --l)
         {
-            acc[k] += t[k] * f.x[k];
-            t[k] = 0.0;
+            if (l < to) break;
+            Row<VEC> f;
+            f.load(F.p[l] + size_t(cur[l]) * R + rr);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k)
+            {
+                const double x = t[l][k] * f.x[k];
+                if (l == 0)
+                    acc[k] += x;
+                else
+                    t[l - 1][k] += x;
+                t[l][k] = 0.0;
+            }
+        }
+    };
+
+    // one live element: coordinates o[0..NO-1], value-weighted last-level row p
+    auto consume = [&](const uint32_t* o, const double* p) {
+        if constexpr (NO == 1)
+        {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) acc[k] += p[k];
+        }
+        else
+        {
+            int L = NL;
+            if (!open)
+            {
+                L = 0;
+                open = true;
+            }
+            else
+            {
+#pragma unroll
+                for (int l = NL - 1; l >= 0; --l)
+                    if (o[l] != cur[l]) L = l;
+                if (L < NL) close_levels(L);
+            }
+#pragma unroll
+            for (int l = 0; l < NL; ++l)
+                if (l >= L) cur[l] = o[l];
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) t[NL - 1][k] += p[k];
         }
     };
 
@@ -120,58 +171,32 @@ __global__ __launch_bounds__(256) void seg_nd_kernel(
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
         {
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) p[u][k] = v[u];
+            Row<VEC> f;
             if (live[u])
-            {
+                f.load(F.p[NO - 1] + size_t(c[u][NO - 1]) * R + rr);
 #pragma unroll
-                for (int q = 1; q < NO; ++q)
-                {
-                    Row<VEC> f;
-                    f.load(G[q] + size_t(c[u][q]) * R + rr);
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) p[u][k] *= f.x[k];
-                }
-            }
+            for (int k = 0; k < VEC; ++k) p[u][k] = live[u] ? v[u] * f.x[k] : 0.0;
         }
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u)
-        {
-            if (!live[u]) continue;
-            if (c[u][0] != cur)
-            {
-                if (cur != 0xFFFFFFFFu) close_run(cur);
-                cur = c[u][0];
-            }
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) t[k] += p[u][k];
-        }
+            if (live[u]) consume(c[u], p[u]);
     }
     for (; e < hi; ++e)
     {
         if (skip && __builtin_nontemporal_load(skip + e) != 0) continue;
-        double p[VEC];
+        uint32_t c[NO];
+#pragma unroll
+        for (int q = 0; q < NO; ++q) c[q] = __builtin_nontemporal_load(sc + q * nnz + e);
         const double v = __builtin_nontemporal_load(vals + e);
+        Row<VEC> f;
+        f.load(F.p[NO - 1] + size_t(c[NO - 1]) * R + rr);
+        double p[VEC];
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) p[k] = v;
-#pragma unroll
-        for (int q = 1; q < NO; ++q)
-        {
-            Row<VEC> f;
-            f.load(G[q] + size_t(__builtin_nontemporal_load(sc + q * nnz + e)) * R + rr);
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) p[k] *= f.x[k];
-        }
-        const uint32_t c0 = __builtin_nontemporal_load(sc + e);
-        if (c0 != cur)
-        {
-            if (cur != 0xFFFFFFFFu) close_run(cur);
-            cur = c0;
-        }
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) t[k] += p[k];
+        for (int k = 0; k < VEC; ++k) p[k] = v * f.x[k];
+        consume(c, p);
     }
-    if (cur != 0xFFFFFFFFu) close_run(cur);
+    if constexpr (NO > 1)
+        if (open) close_levels(0);
     if (!rank_ok)
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc[k] = 0.0;
@@ -205,9 +230,10 @@ void launch_seg(const Factors& F, int mode, const uint32_t* sc, uint64_t nnz, co
                 const uint8_t* skip, const uint32_t* row, const uint32_t* st, const uint32_t* cn,
                 const uint8_t* single, uint64_t nseg, double* FtV, int R, hipStream_t s)
 {
+    (void)mode;
     constexpr int UNROLL = (N <= 4) ? 4 : 2;
     hipLaunchKernelGGL((seg_nd_kernel<N, RT, VEC, UNROLL>), dim3(unsigned(nseg)), dim3(256), 0, s,
-                       F, mode, sc, nnz, vals, skip, row, st, cn, single, FtV, R);
+                       F, sc, nnz, vals, skip, row, st, cn, single, FtV, R);
 }
 
 template <int N, int VEC>
@@ -491,11 +517,11 @@ extern "C" uint64_t cptc_gen_hash(uint64_t x)
 }
 
 extern "C" int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords,
-                                  const double* d_vals, const uint8_t* d_skip, uint64_t nnz,
-                                  const uint32_t* d_seg_row, const uint32_t* d_seg_start,
-                                  const uint32_t* d_seg_cnt, const uint8_t* d_single,
-                                  uint64_t nseg, const double* const* h_F, double* d_FtV, int R,
-                                  void* stream)
+                                  const int* level_modes, const double* d_vals,
+                                  const uint8_t* d_skip, uint64_t nnz, const uint32_t* d_seg_row,
+                                  const uint32_t* d_seg_start, const uint32_t* d_seg_cnt,
+                                  const uint8_t* d_single, uint64_t nseg,
+                                  const double* const* h_F, double* d_FtV, int R, void* stream)
 {
     CPTC_REQUIRE(nmodes >= 2 && nmodes <= MAXM && mode >= 0 && mode < nmodes, CPTC_ERR_ARG,
                  "cptc_mttkrp_seg_nd: nmodes %d mode %d", nmodes, mode);
@@ -507,11 +533,17 @@ extern "C" int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoord
     CPTC_REQUIRE(d_scoords && d_vals && d_seg_row && d_seg_start && d_seg_cnt && d_FtV &&
                      factors_ok(nmodes, h_F),
                  CPTC_ERR_ARG, "cptc_mttkrp_seg_nd: null pointer");
+    // factors in level order (the d_scoords rows)
     Factors F{};
     bool aligned = (R % 2 == 0);
-    for (int m = 0; m < nmodes; ++m)
+    unsigned seen = 1u << mode;
+    for (int q = 0; q < nmodes - 1; ++q)
     {
-        F.p[m] = h_F[m];
+        const int m = level_modes ? level_modes[q] : (q < mode ? q : q + 1);
+        CPTC_REQUIRE(m >= 0 && m < nmodes && !(seen & (1u << m)), CPTC_ERR_ARG,
+                     "cptc_mttkrp_seg_nd: level_modes is not a permutation of the other modes");
+        seen |= 1u << m;
+        F.p[q] = h_F[m];
         if (reinterpret_cast<uintptr_t>(h_F[m]) & 15) aligned = false;
     }
     hipStream_t s = cptc::as_stream(stream);

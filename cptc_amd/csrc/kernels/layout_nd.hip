@@ -11,8 +11,12 @@
 //
 // Views (generic.cu:1848-1958).  A stable radix sort by coordinate n is the
 // counting sort of the reference; segments are cut on the host from the row
-// run lengths.
+// run lengths.  The kernel's own views ("work views") drop the dense
+// elements and sort each row over the other modes with successive stable
+// sorts (least significant level first).
 #include "dev_util.hpp"
+
+#include <rocprim/device/device_select.hpp>
 
 #include <algorithm>
 #include <vector>
@@ -169,6 +173,45 @@ __global__ void view_gather_kernel(const uint32_t* __restrict__ order,
     }
 }
 
+__global__ void keep_flags_kernel(const uint8_t* __restrict__ isd, uint64_t n,
+                                  uint8_t* __restrict__ keep)
+{
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        keep[i] = isd[i] ? 0 : 1;
+}
+
+__global__ void gather_keys_kernel(const uint32_t* __restrict__ col,
+                                   const uint32_t* __restrict__ perm, uint64_t n,
+                                   uint32_t* __restrict__ key)
+{
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        key[i] = col[perm[i]];
+}
+
+struct Levels
+{
+    int m[CPTC_MAX_MODES];
+};
+
+__global__ void work_gather_kernel(const uint32_t* __restrict__ order,
+                                   const uint32_t* __restrict__ co,
+                                   const double* __restrict__ vals, uint64_t nnz, uint64_t M,
+                                   int nlev, Levels lv, uint32_t* __restrict__ sc,
+                                   double* __restrict__ sv)
+{
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < M; i += stride)
+    {
+        const uint64_t e = order[i];
+        sv[i] = vals[e];
+#pragma unroll
+        for (int q = 0; q < CPTC_MAX_MODES; ++q)
+            if (q < nlev) sc[uint64_t(q) * M + i] = co[uint64_t(lv.m[q]) * nnz + e];
+    }
+}
+
 template <class T>
 int upload(T** d, const std::vector<T>& h, hipStream_t s)
 {
@@ -200,6 +243,7 @@ void free_view(DevViewN& v)
     dfree(v.d_cnt);
     dfree(v.d_single);
     v.nnz = v.nseg = 0;
+    v.level_modes.clear();
 }
 
 // generic.cu:578-725
@@ -299,6 +343,9 @@ int units_nd_device(int N, const uint64_t* dims, const uint32_t* d_coords, const
     return CPTC_OK;
 }
 
+int build_segments(const uint32_t* d_sorted_rows, uint64_t nnz, bool force_accumulate,
+                   DevViewN& out, hipStream_t s);
+
 // generic.cu:1848-1958
 int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
                    const double* d_vals, const uint8_t* d_is_dense, bool force_accumulate,
@@ -306,6 +353,8 @@ int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
 {
     free_view(out);
     out.nnz = nnz;
+    for (int m = 0; m < N; ++m)
+        if (m != n) out.level_modes.push_back(m);
     if (nnz == 0) return CPTC_OK;
     CPTC_REQUIRE(nnz <= 0x7FFFFFFFull, CPTC_ERR_UNSUPPORTED, "views: nnz %llu > 0x7FFFFFFF",
                  (unsigned long long)nnz);
@@ -326,12 +375,21 @@ int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
     hipLaunchKernelGGL(view_gather_kernel, dim3(g), dim3(256), 0, s, order.p, d_coords, d_vals,
                        d_is_dense, nnz, N, n, out.d_sc, out.d_vals, out.d_skip);
     CPTC_LAUNCHED();
-    // row run lengths -> segments on the host
+    CPTC_TRY(build_segments(skey.p, nnz, force_accumulate, out, s));
+    CPTC_HIP(hipStreamSynchronize(s));
+    return CPTC_OK;
+}
+
+// Row run lengths of the sorted target coordinates -> <= 1024-element
+// segments in ascending row order (host), uploaded into `out`.
+int build_segments(const uint32_t* d_sorted_rows, uint64_t nnz, bool force_accumulate,
+                   DevViewN& out, hipStream_t s)
+{
     Tmp<uint32_t> urow, counts, nruns_d;
     CPTC_TRY(urow.alloc(nnz));
     CPTC_TRY(counts.alloc(nnz));
     CPTC_TRY(nruns_d.alloc(1));
-    CPTC_TRY(run_length(skey.p, nnz, urow.p, counts.p, nruns_d.p, s));
+    CPTC_TRY(run_length(d_sorted_rows, nnz, urow.p, counts.p, nruns_d.p, s));
     uint32_t nruns = 0;
     CPTC_TRY(d2h_one(&nruns, nruns_d.p, s));
     std::vector<uint32_t> hrow(nruns), hcnt(nruns);
@@ -359,6 +417,76 @@ int view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
     CPTC_TRY(upload(&out.d_start, start, s));
     CPTC_TRY(upload(&out.d_cnt, cnt, s));
     CPTC_TRY(upload(&out.d_single, single, s));
+    return CPTC_OK;
+}
+
+int work_view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_coords,
+                        const double* d_vals, const uint8_t* d_is_dense, bool force_accumulate,
+                        uint64_t nnz, DevViewN& out, hipStream_t s)
+{
+    free_view(out);
+    // levels: the other modes by dimension, smallest first (ties: mode order)
+    out.level_modes.clear();
+    for (int m = 0; m < N; ++m)
+        if (m != n) out.level_modes.push_back(m);
+    std::stable_sort(out.level_modes.begin(), out.level_modes.end(),
+                     [&](int a, int b) { return dims[a] < dims[b]; });
+    if (nnz == 0) return CPTC_OK;
+    CPTC_REQUIRE(nnz <= 0x7FFFFFFFull, CPTC_ERR_UNSUPPORTED, "views: nnz %llu > 0x7FFFFFFF",
+                 (unsigned long long)nnz);
+    const unsigned g = grid_for(nnz, 256, 8192);
+    Tmp<uint32_t> perm, perm2, key, key2;
+    CPTC_TRY(perm.alloc(nnz));
+    CPTC_TRY(perm2.alloc(nnz));
+    CPTC_TRY(key.alloc(nnz));
+    CPTC_TRY(key2.alloc(nnz));
+    uint64_t M = nnz;
+    hipLaunchKernelGGL(iota_kernel, dim3(g), dim3(256), 0, s, perm2.p, nnz);
+    CPTC_LAUNCHED();
+    if (d_is_dense)
+    {
+        Tmp<uint8_t> keep;
+        Tmp<uint64_t> cnt_d;
+        CPTC_TRY(keep.alloc(nnz));
+        CPTC_TRY(cnt_d.alloc(1));
+        hipLaunchKernelGGL(keep_flags_kernel, dim3(g), dim3(256), 0, s, d_is_dense, nnz, keep.p);
+        CPTC_LAUNCHED();
+        size_t bytes = 0;
+        CPTC_HIP(rocprim::select(nullptr, bytes, perm2.p, keep.p, perm.p, cnt_d.p, nnz, s));
+        Tmp<char> tmp;
+        CPTC_TRY(tmp.alloc(bytes ? bytes : 1));
+        CPTC_HIP(rocprim::select(tmp.p, bytes, perm2.p, keep.p, perm.p, cnt_d.p, nnz, s));
+        CPTC_TRY(d2h_one(&M, cnt_d.p, s));
+    }
+    else
+    {
+        std::swap(perm.p, perm2.p);
+    }
+    out.nnz = M;
+    if (M == 0) return CPTC_OK;
+    const unsigned gm = grid_for(M, 256, 8192);
+    // least significant level first, the target coordinate last
+    std::vector<int> passes(out.level_modes.rbegin(), out.level_modes.rend());
+    passes.push_back(n);
+    for (int m : passes)
+    {
+        hipLaunchKernelGGL(gather_keys_kernel, dim3(gm), dim3(256), 0, s,
+                           d_coords + uint64_t(m) * nnz, perm.p, M, key.p);
+        CPTC_LAUNCHED();
+        CPTC_TRY(sort_pairs(key.p, key2.p, perm.p, perm2.p, M,
+                            bit_width(dims[m] > 0 ? dims[m] - 1 : 0), s));
+        std::swap(perm.p, perm2.p);
+    }
+    // perm = final order, key2 = its sorted target rows
+    Levels lv{};
+    const int nlev = N - 1;
+    for (int q = 0; q < nlev; ++q) lv.m[q] = out.level_modes[q];
+    CPTC_TRY(dalloc(&out.d_sc, size_t(nlev) * M));
+    CPTC_TRY(dalloc(&out.d_vals, M));
+    hipLaunchKernelGGL(work_gather_kernel, dim3(gm), dim3(256), 0, s, perm.p, d_coords, d_vals,
+                       nnz, M, nlev, lv, out.d_sc, out.d_vals);
+    CPTC_LAUNCHED();
+    CPTC_TRY(build_segments(key2.p, M, force_accumulate, out, s));
     CPTC_HIP(hipStreamSynchronize(s));
     return CPTC_OK;
 }

@@ -317,13 +317,17 @@ uint64_t cptc_gen_hash(uint64_t x);
  * acc_r = sum_e v_e prod_{m != mode} F_m[c_m(e), r] over the segment's
  * elements with d_skip[e] == 0 (d_skip NULL: none skipped); then
  * FtV[row_b, r] = acc_r when d_single[b] != 0, else FtV[row_b, r] += acc_r
- * (atomic, skipped when acc_r == 0).  d_scoords: (nmodes - 1) x nnz uint32,
- * modes ascending without `mode`.  Segments hold <= CPTC_SEG elements. */
-int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords, const double* d_vals,
-                       const uint8_t* d_skip, uint64_t nnz, const uint32_t* d_seg_row,
-                       const uint32_t* d_seg_start, const uint32_t* d_seg_cnt,
-                       const uint8_t* d_single, uint64_t nseg, const double* const* h_F,
-                       double* d_FtV, int R, void* stream);
+ * (atomic, skipped when acc_r == 0).  d_scoords: (nmodes - 1) x nnz uint32;
+ * row q holds the coordinates of mode level_modes[q] (host array; NULL =
+ * the other modes ascending, the reference's layout).  Any element order
+ * is valid; runs of equal leading coordinates inside a segment are summed
+ * before their factor rows are applied.  Segments hold <= CPTC_SEG
+ * elements. */
+int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords, const int* level_modes,
+                       const double* d_vals, const uint8_t* d_skip, uint64_t nnz,
+                       const uint32_t* d_seg_row, const uint32_t* d_seg_start,
+                       const uint32_t* d_seg_cnt, const uint8_t* d_single, uint64_t nseg,
+                       const double* const* h_F, double* d_FtV, int R, void* stream);
 
 /* Dense units (GDUnit, generic.cu:422-427): d_unit6 = nunits x {bi, bj, bk,
  * nnz, start, outer_off}; pool lid = la * 256 + lb * 16 + lc (slot order).

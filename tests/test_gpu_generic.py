@@ -124,7 +124,7 @@ def test_seg_kernel_vs_oracle(ca, orc, dev, N, R):
             init = rng.standard_normal(dims[n] * R)
             out = dbuf(ca, init.copy())
             rc = ca.lib.cptc_mttkrp_seg_nd(
-                N, n, bufs["scoords"].data_ptr(), bufs["vals"].data_ptr(),
+                N, n, bufs["scoords"].data_ptr(), None, bufs["vals"].data_ptr(),
                 bufs["skip"].data_ptr() if use_skip else None, nnz, bufs["row"].data_ptr(),
                 bufs["start"].data_ptr(), bufs["cnt"].data_ptr(), bufs["single"].data_ptr(),
                 len(v["row"]), fptrs(dF), out.data_ptr(), R, None)
@@ -151,8 +151,8 @@ def test_seg_kernel_single_store(ca, orc, dev):
     bufs = {k: dbuf(ca, v[k]) for k in ("scoords", "vals", "row", "start", "cnt", "single")}
     init = np.full(dims[n] * 8, 7.0)
     out = dbuf(ca, init.copy())
-    assert ca.lib.cptc_mttkrp_seg_nd(4, n, bufs["scoords"].data_ptr(), bufs["vals"].data_ptr(),
-                                     None, nnz, bufs["row"].data_ptr(), bufs["start"].data_ptr(),
+    assert ca.lib.cptc_mttkrp_seg_nd(4, n, bufs["scoords"].data_ptr(), None,
+                                     bufs["vals"].data_ptr(), None, nnz, bufs["row"].data_ptr(), bufs["start"].data_ptr(),
                                      bufs["cnt"].data_ptr(), bufs["single"].data_ptr(),
                                      len(v["row"]), fptrs(dF), out.data_ptr(), 8, None) == 0
     ca.sync()
