@@ -138,6 +138,7 @@ SIGNATURES = {
     "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),
     "cptc_colnorms": (_I, [_P, _Z, _I, _P, _P]),
     "cptc_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P]),
+    "cptc_clamp": (_I, [_P, _Z, _D, _D, _P]),
     "cptc_fit_gram": (_I, [_P, _P, _Z, _P, _P, _I, _I, _P, _P]),
     "cptc_residual3_view": (_I, [_P, _P, _Z, _P, _P, _P, _P, _I, _P, _P]),
     "cptc_residual3_tiles": (_I, [_P, _P, _P, _P, _Z, _P, _P, _P, _P, _I, _P, _P]),

@@ -144,6 +144,8 @@ void destroy(Als3* h)
     delete h;
 }
 
+int alloc_buffers(Als3& h);
+
 int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
 {
     cptc_als3_opts o;
@@ -282,7 +284,21 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
         }
     }
 
-    // 6. ALS buffers (als.cu:389-430)
+    CPTC_TRY(alloc_buffers(*h));
+    if (o.verbose)
+        std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
+                    "-> %s\n",
+                    (unsigned long long)h->dense_nnz_total, h->part.sparse_nnz,
+                    (long long)h->tiles_total, h->avg_fill, h->fill_min,
+                    h->use_mfma ? "MFMA tiles + FP64 residual" : "FP64 only");
+    return CPTC_OK;
+}
+
+// ALS buffers (als.cu:389-430) and ||X||^2 (als.cu:439-450)
+int alloc_buffers(Als3& hr)
+{
+    Als3* h = &hr;
+    const int R = h->R;
     const size_t RR = size_t(R) * R;
     const uint64_t maxdim = std::max({h->dims[0], h->dims[1], h->dims[2]});
     CPTC_HIP(hipMalloc(&h->d_lambda, size_t(R) * sizeof(double)));
@@ -302,12 +318,6 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     CPTC_HIP(hipMemcpyAsync(r2, h->d_scal + 2, 2 * sizeof(double), hipMemcpyDeviceToHost, h->s));
     CPTC_HIP(hipStreamSynchronize(h->s));
     h->x_sq = r2[1];
-    if (o.verbose)
-        std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
-                    "-> %s\n",
-                    (unsigned long long)h->dense_nnz_total, h->part.sparse_nnz,
-                    (long long)h->tiles_total, h->avg_fill, h->fill_min,
-                    h->use_mfma ? "MFMA tiles + FP64 residual" : "FP64 only");
     return CPTC_OK;
 }
 
@@ -386,6 +396,62 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
 Als3* as_h(void* p) { return static_cast<Als3*>(p); }
 
 }  // namespace
+
+// The iteration on a caller-owned layout and caller-owned factors (the
+// contract of execute_als_decomposition, als.cu:362-821).  The layout and
+// the factor buffers are borrowed: they are detached before the driver's
+// own buffers are released.
+int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevViews3& views,
+                 const DevViews3& dviews, float* tile_f32, bool use_mfma, double* A, double* B,
+                 double* C, double* lambda_out, int R, int iters, bool verbose, double* fit_last)
+{
+    CPTC_REQUIRE(A && B && C && lambda_out && R >= 1 && R <= 512 && iters >= 0, CPTC_ERR_ARG,
+                 "als3_execute: bad arguments");
+    Als3* h = new Als3();
+    cptc_als3_default_opts(&h->o);
+    h->o.R = R;
+    h->o.verbose = verbose ? 1 : 0;
+    h->R = R;
+    for (int m = 0; m < 3; ++m) h->dims[m] = dims[m];
+    h->part = part;
+    h->views = views;
+    h->dviews = dviews;
+    h->d_tile_f32 = tile_f32;
+    h->use_mfma = use_mfma && part.ntiles > 0 && tile_f32 != nullptr;
+    h->skip_dense = env_flag("ALS_NO_DENSE") != 0;
+    h->skip_sparse = env_flag("ALS_NO_SPARSE") != 0;
+    h->nnz = views.nnz + part.dense_nnz;
+    h->F[0] = A;
+    h->F[1] = B;
+    h->F[2] = C;
+    int rc = CPTC_OK;
+    auto step = [&](int r) {
+        if (rc == CPTC_OK) rc = r;
+    };
+    step(hipStreamCreateWithFlags(&h->s, hipStreamNonBlocking) == hipSuccess ? CPTC_OK
+                                                                              : CPTC_ERR_HIP);
+    for (auto& e : h->ev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
+    for (auto& e : h->kev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
+    if (rc == CPTC_OK) step(alloc_buffers(*h));
+    std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
+    if (rc == CPTC_OK) step(run(*h, iters, fits.data(), nullptr, nullptr));
+    if (rc == CPTC_OK)
+    {
+        step(hipMemcpyAsync(lambda_out, h->d_lambda, size_t(R) * sizeof(double),
+                            hipMemcpyDeviceToDevice, h->s) == hipSuccess
+                 ? CPTC_OK
+                 : CPTC_ERR_HIP);
+        step(hipStreamSynchronize(h->s) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
+        if (fit_last && iters > 0) *fit_last = fits[size_t(iters) - 1];
+    }
+    h->part = DevPartition3{};
+    h->views = DevViews3{};
+    h->dviews = DevViews3{};
+    h->d_tile_f32 = nullptr;
+    destroy(h);
+    return rc;
+}
+
 }  // namespace cptc
 
 using cptc::Als3;

@@ -78,4 +78,11 @@ int views3_device(const uint32_t* d_i, const uint32_t* d_j, const uint32_t* d_k,
 int dense_views3_device(const DevPartition3& p, const uint64_t dims[3], DevViews3& out,
                         hipStream_t s);
 
+// The order-3 ALS iteration on a borrowed layout and caller-owned factors
+// (execute_als_decomposition, als.cu:362-821); writes lambda_out (device, R)
+// and the last Gram fit.  tile_f32 = packed FP32 tiles (MFMA path) or null.
+int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevViews3& views,
+                 const DevViews3& dviews, float* tile_f32, bool use_mfma, double* A, double* B,
+                 double* C, double* lambda_out, int R, int iters, bool verbose, double* fit_last);
+
 }  // namespace cptc

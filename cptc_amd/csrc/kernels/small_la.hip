@@ -703,3 +703,24 @@ extern "C" int cptc_fit_gram(const double* d_F, const double* d_M, size_t rows,
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
+
+namespace {
+
+__global__ void clamp_kernel(double* __restrict__ x, size_t n, double lo, double hi)
+{
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        x[i] = x[i] < lo ? lo : (x[i] > hi ? hi : x[i]);
+}
+
+}  // namespace
+
+extern "C" int cptc_clamp(double* d_x, size_t n, double lo, double hi, void* stream)
+{
+    if (n == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_x && lo <= hi, CPTC_ERR_ARG, "cptc_clamp: null pointer or lo > hi");
+    hipLaunchKernelGGL(clamp_kernel, dim3(cptc::grid_for(n, 256, 4096)), dim3(256), 0,
+                       cptc::as_stream(stream), d_x, n, lo, hi);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}

@@ -191,6 +191,10 @@ int cptc_colnorms(const double* d_F, size_t rows, int R, double* d_norms, void* 
 int cptc_normalize_absorb(double* d_F, size_t rows, int R, const double* d_norms,
                           double* d_lambda, void* stream);
 
+/* x[i] = min(max(x[i], lo), hi) over n doubles.  Backs clamp_factor_thrust
+ * (common.cu:160-190). */
+int cptc_clamp(double* d_x, size_t n, double lo, double hi, void* stream);
+
 /* Gram fit scalars: out[0] = iprod = sum_r lambda_r <F[:, r], M[:, r]>,
  * out[1] = model^2 = sum_{r,s} lambda_r lambda_s prod_m G_m[r, s]
  * over the `ngram` Grams in d_grams (consecutive R x R blocks).

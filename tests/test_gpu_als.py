@@ -146,3 +146,36 @@ def test_cli_runs_and_exports(ca, dev, tmp_path):
     assert len([x for x in lines[3:] if x]) == t.dims[0] * 8
     lam = open(str(tmp_path / "f.lambda.out")).read().split("\n")
     assert lam[:3] == ["vector", "1", "8"]
+
+
+@pytest.mark.parametrize("env_path,path", [({}, -1), ({"ALS_FORCE_CUDA": "1"}, 2),
+                                           ({"ALS_FORCE_WMMA": "1"}, 1)])
+def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
+    """The CLI runs main.cu's flow on the C++ interface (load_tns_file,
+    compute/apply_cadr_reordering, init_factors_random, create_hybrid_format,
+    build_mttkrp_views, build_dense_mttkrp_views, execute_als_decomposition,
+    unpermute_factor_matrices).  It must reproduce the C-ABI driver, which
+    runs the same CADR, initial factors, layout and kernels."""
+    t = clustered(ca, 3)
+    fpath = str(tmp_path / "t.tns")
+    ca.write_tns(fpath, t)
+    env = dict(os.environ, **env_path)
+    for k in ("ALS_FORCE_CUDA", "ALS_FORCE_WMMA"):
+        if k not in env_path:
+            env.pop(k, None)
+    out = subprocess.run([ca.CLI_PATH, fpath, "6", "16"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.splitlines()
+    fits = np.array([float(l.split("fit=")[1]) for l in lines if l.startswith("[ALS] iter ")])
+    assert len(fits) == 6
+    for s in ("[CADR] Total reordering time", "[Main] density check:", "[Fit Report] final R=16",
+              "[ALS] Final RMSE=", "[Main] Final CP weights:", "Unpermutation!"):
+        assert any(s in l for l in lines), s
+    t2 = ca.load_tns3(fpath)
+    with ca.Als3(t2, R=16, path=path) as h:
+        ref, _, _ = h.run(6)
+        lam = h.lam()
+    assert np.max(np.abs(fits - ref)) <= 1e-9, (fits, ref)
+    cli_lam = [l for l in lines if l.startswith("[Main] Final CP weights:")][0].split(":")[1]
+    assert np.allclose(np.array([float(x) for x in cli_lam.split()]), lam, rtol=1e-5)
