@@ -11,6 +11,10 @@ resident in HBM.  Prints ONE JSON line on stdout; progress goes to stderr.
 The CPU baseline runs the CPU oracle's OpenMP ALS (the reference's semantics)
 on the same row-sorted views, copied from the device, for --cpu-iters
 iterations on the full tensor.
+
+--config 4 / 5 run the generic N-order path on BASELINE configs 4 and 5
+instead (secondary measurements; same JSON shape, the segment MTTKRP as the
+roofline kernel and the dense-unit MFMA kernel beside it).
 """
 from __future__ import annotations
 
@@ -25,6 +29,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+BASELINE_METRIC = "ms per ALS iteration + sparse MTTKRP HBM GB/s (% of peak), order-3 R=128"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor figure
 
@@ -33,6 +38,10 @@ CONFIG_SPEC = {
     2: dict(R=32, thr=0.03, name="cfg2: order-3 512^3, 2000 16^3 blocks + 2e-4 background"),
     3: dict(R=128, thr=0.03,
             name="cfg3: order-3 12092x9184x28818, 76.9M nnz, Zipf(1.1), log-normal values"),
+    4: dict(R=16, thr=0.03,
+            name="cfg4: order-4 183x24x1140x1717, 3.3M nnz, HITS(T=3), dense units (0,1,2)"),
+    5: dict(R=32, thr=0.03,
+            name="cfg5: order-5 64x64x64x32x16, 20M nnz, 4000 dense units + background"),
 }
 
 
@@ -87,6 +96,8 @@ def main() -> int:
     spec = CONFIG_SPEC[args.config]
     R = args.R or spec["R"]
     thr = spec["thr"]
+    if args.config in (4, 5):
+        return bench_generic(ca, args, spec, R)
 
     t0 = time.perf_counter()
     t = ca.synth_config(args.config, 42)
@@ -135,13 +146,16 @@ def main() -> int:
     achieved = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
     workload = f"cfg{args.config}-R{R}"
     traffic = load_traffic(workload)
+    traffic_gbs = (traffic / (sum(launch_ms) / 3 * 1e-3) / 1e9) if (traffic and snnz) else None
+    # compulsory traffic per launch: the view stream + every factor row once + output rows
+    compulsory = [snnz * 20 + sum(dims) * R * 8 + dims[m] * R * 8 for m in range(3)]
 
     cpu = None
     if not args.no_cpu and args.cpu_iters > 0:
         cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma)
 
     line = {
-        "metric": "ms per ALS iteration + sparse MTTKRP HBM GB/s (% of peak), order-3 R=128",
+        "metric": BASELINE_METRIC,
         "value": round(ms_per_step, 4),
         "unit": "ms/iteration",
         "n_gpus": 1,
@@ -173,12 +187,87 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_GBs": round(traffic_gbs, 1) if traffic_gbs else None,
+            "traffic_frac": round(traffic_gbs / HBM_PEAK_GBS, 4) if traffic_gbs else None,
             "launch_ms": [round(x, 4) for x in launch_ms],
             "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
+            "compulsory_bytes_per_launch": [int(b) for b in compulsory],
+            "note": "achieved = no-reuse gather model (every factor row read per nonzero) over "
+                    "the measured launch time; L2 and MALL serve most gathers, so it exceeds "
+                    "the HBM peak. traffic = rocprofv3 FETCH_SIZE*2.0 + WRITE_SIZE per launch "
+                    "(L2-miss bytes), traffic_GBs = traffic over the same launch time.",
         },
         "cpu_baseline": cpu,
     }
     h.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_generic(ca, args, spec, R) -> int:
+    """Configs 4 and 5 through the generic N-order driver (cptc_gen_*)."""
+    t0 = time.perf_counter()
+    t = ca.synth_config(args.config, 42)
+    log(f"generated config {args.config}: dims {t.dims} nnz {t.nnz} in "
+        f"{time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    g = ca.Gen(t, R=R, reorder="hits", rounds=3, threshold=spec["thr"])
+    info = g.info
+    N = g.N
+    knnz = [int(info.kernel_nnz[m]) for m in range(N)]
+    log(f"setup {time.perf_counter() - t0:.2f} s: reorder {info.reorder.decode()} units "
+        f"{info.n_units} dense_nnz {info.dense_nnz} kernel-view nnz {knnz}")
+    if args.warmup:
+        g.run(args.warmup)
+    g.kernel_times(reset=True)
+    ca.sync()
+    t0 = time.perf_counter()
+    fits, _, _, ms_iter = g.run(args.steps)
+    ca.sync()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    seg_ms, unit_ms, kit = g.kernel_times(reset=True)
+    assert kit == args.steps
+    dims = t.dims
+    b_seg = [gather_bytes(knnz[m], dims[m], R, N) for m in range(N)]
+    seg_launch = [float(seg_ms[m]) / kit for m in range(N)]
+    achieved = sum(b_seg) / (sum(seg_launch) * 1e-3) / 1e9
+    inner = [m for m in range(N) if info.dense_enabled and m in tuple(info.inner)]
+    unit_launch = [float(unit_ms[m]) / kit for m in inner]
+    flops = 8192.0 * R * int(info.n_units)
+    tflops = (flops * len(inner) / (sum(unit_launch) * 1e-3) / 1e12) if unit_launch else 0.0
+    log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter; seg launch ms "
+        f"{[round(x, 4) for x in seg_launch]}; unit launch ms {[round(x, 4) for x in unit_launch]}")
+    line = {
+        "metric": BASELINE_METRIC,
+        "value": round(ms_per_step, 4),
+        "unit": "ms/iteration",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f64 (dense units: fp32 MFMA, f64 epilogue)",
+        "data": "synthetic (deterministic generator, seed 42)",
+        "config": {"workload": spec["name"] if R == spec["R"] else f"{spec['name']} (R={R})",
+                   "R": R, "nnz": t.nnz, "dims": list(dims), "dense_units": int(info.n_units),
+                   "dense_nnz": int(info.dense_nnz), "kernel_view_nnz": knnz,
+                   "path": "generic N-order", "parallelism": "single GPU"},
+        "fit_last": float(fits[-1]),
+        "roofline": {
+            "kernel": "seg_nd_kernel (FP64 segment MTTKRP), per launch = one mode",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "launch_ms": [round(x, 4) for x in seg_launch],
+            "algorithmic_bytes_per_launch": [int(b) for b in b_seg],
+        },
+        "roofline_units": {
+            "kernel": "dense_tiles_kernel<slot,6,true> (dense units, FP32 MFMA), per inner mode",
+            "bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "flops_per_launch": flops, "launch_ms": [round(x, 4) for x in unit_launch],
+        },
+        "cpu_baseline": None,
+    }
+    g.close()
     print(json.dumps(line), flush=True)
     return 0
 

@@ -396,6 +396,14 @@ class Gen:
               "cptc_gen_profile")
         return out, it.value
 
+    def kernel_times(self, reset: bool = True):
+        """(segment-kernel ms per mode, unit-kernel ms per mode, iterations)."""
+        out = np.zeros(16, np.float64)
+        it = C.c_int()
+        check(lib.cptc_gen_kernel_times(self._h, out.ctypes.data, C.byref(it), int(reset)),
+              "cptc_gen_kernel_times")
+        return out[:self.N], out[8:8 + self.N], it.value
+
     def mttkrp(self, mode: int) -> np.ndarray:
         out = np.zeros((self.dims[mode], self.R), np.float64)
         check(lib.cptc_gen_mttkrp(self._h, mode, out.ctypes.data), "cptc_gen_mttkrp")

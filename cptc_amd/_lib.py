@@ -97,6 +97,7 @@ class GenInfo(C.Structure):
         ("dense_nnz", C.c_uint64),
         ("nseg", C.c_uint64 * CPTC_MAX_MODES),
         ("prep_ms", C.c_double * 3),
+        ("kernel_nnz", C.c_uint64 * CPTC_MAX_MODES),
     ]
 
 
@@ -172,6 +173,7 @@ SIGNATURES = {
     "cptc_gen_info_get": (_I, [_P, C.POINTER(GenInfo)]),
     "cptc_gen_run": (_I, [_P, _I, _P, _P, _P, _P]),
     "cptc_gen_profile": (_I, [_P, _P, C.POINTER(_I), _I]),
+    "cptc_gen_kernel_times": (_I, [_P, _P, C.POINTER(_I), _I]),
     "cptc_gen_mttkrp": (_I, [_P, _I, _P]),
     "cptc_gen_factor": (_I, [_P, _I, _P]),
     "cptc_gen_set_factor": (_I, [_P, _I, _P]),

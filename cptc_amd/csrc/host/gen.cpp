@@ -343,6 +343,12 @@ struct Gen
     std::vector<cptc::DevViewN> views;   // kernel views (dense elements dropped, rows sorted)
     std::vector<uint64_t> ref_nseg;      // segments of the reference-layout views
 
+    // per-kernel timing: seg / unit kernel of each mode, summed over iterations
+    hipEvent_t kev[4 * CPTC_MAX_MODES] = {};
+    bool timing = false;
+    double k_seg[CPTC_MAX_MODES] = {}, k_unit[CPTC_MAX_MODES] = {};
+    int k_iters = 0;
+
     // GEN_PROFILE: gram, mttkrp, solve, norm, fit
     std::vector<hipEvent_t> ev;
     double prof[5] = {0, 0, 0, 0, 0};
@@ -364,6 +370,8 @@ struct Gen
         cptc::free_units(units);
         for (auto& v : views) cptc::free_view(v);
         for (auto& e : ev) (void)hipEventDestroy(e);
+        for (auto& e : kev)
+            if (e) (void)hipEventDestroy(e);
         if (s) (void)hipStreamDestroy(s);
     }
 
@@ -376,11 +384,14 @@ struct Gen
 
     const double* const* F() const { return d_F.data(); }
 
-    // FtV = MTTKRP of mode n (zeroed first).
+    // FtV = MTTKRP of mode n (zeroed first).  With `timing`, events bracket
+    // the unit kernel (kev 0-1) and the segment kernel (kev 2-3).
     int mttkrp(int n)
     {
         CPTC_HIP(hipMemsetAsync(d_FtV, 0, dims[n] * size_t(R) * sizeof(double), s));
         const bool in = dense && (inner_mask & (1u << n));
+        hipEvent_t* ke = kev + 4 * n;
+        if (timing) CPTC_HIP(hipEventRecord(ke[0], s));
         if (in)
         {
             if (w_dirty)
@@ -396,10 +407,31 @@ struct Gen
                                           int(dims[in3[0]]), int(dims[in3[1]]),
                                           int(dims[in3[2]]), d_FtV, R, s));
         }
+        if (timing)
+        {
+            CPTC_HIP(hipEventRecord(ke[1], s));
+            CPTC_HIP(hipEventRecord(ke[2], s));
+        }
         const cptc::DevViewN& v = views[n];
         CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals, nullptr, v.nnz,
                                     v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV,
                                     R, s));
+        if (timing) CPTC_HIP(hipEventRecord(ke[3], s));
+        return CPTC_OK;
+    }
+
+    // accumulate every mode's kernel events (after the iteration's sync)
+    int collect_kernel_times()
+    {
+        for (int n = 0; n < N; ++n)
+        {
+            float a = 0.0f, b = 0.0f;
+            CPTC_HIP(hipEventElapsedTime(&a, kev[4 * n], kev[4 * n + 1]));
+            CPTC_HIP(hipEventElapsedTime(&b, kev[4 * n + 2], kev[4 * n + 3]));
+            k_unit[n] += a;
+            k_seg[n] += b;
+        }
+        ++k_iters;
         return CPTC_OK;
     }
 
@@ -434,6 +466,7 @@ struct Gen
         CPTC_HIP(hipMemcpyAsync(h, d_out2, sizeof(h), hipMemcpyDeviceToHost, s));
         CPTC_HIP(hipStreamSynchronize(s));
         mark(mk++);
+        if (timing) CPTC_TRY(collect_kernel_times());
         const double res = std::max(x2 - 2.0 * h[0] + h[1], 0.0);
         const double xn = std::sqrt(x2);
         if (fit) *fit = (xn > 0.0) ? 1.0 - std::sqrt(res) / xn : 0.0;
@@ -713,6 +746,7 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
         g->ev.resize(size_t(2 + 4 * N));
         for (auto& e : g->ev) GEN_HIP(hipEventCreate(&e));
     }
+    for (auto& e : g->kev) GEN_HIP(hipEventCreate(&e));
     GEN_HIP(hipStreamSynchronize(s));
 #undef GEN_TRY
 #undef GEN_HIP
@@ -740,6 +774,7 @@ extern "C" int cptc_gen_info_get(void* handle, cptc_gen_info* info)
     for (int q = 0; q < 3; ++q) info->inner[q] = g->units.inner[q];
     info->n_units = g->units.nunits;
     info->dense_nnz = g->units.dense_nnz;
+    for (int m = 0; m < g->N; ++m) info->kernel_nnz[m] = g->views[m].nnz;
     for (int q = 0; q < 3; ++q) info->prep_ms[q] = g->prep_ms[q];
     return CPTC_OK;
 }
@@ -749,6 +784,12 @@ extern "C" int cptc_gen_run(void* handle, int iters, double* fit, double* iprod,
 {
     CPTC_REQUIRE(handle && iters >= 0, CPTC_ERR_ARG, "cptc_gen_run: bad arguments");
     Gen* g = as_gen(handle);
+    struct Timing
+    {
+        Gen* g;
+        ~Timing() { g->timing = false; }
+    } timing_guard{g};
+    g->timing = true;
     for (int it = 0; it < iters; ++it)
     {
         const auto t0 = Clock::now();
@@ -776,6 +817,24 @@ extern "C" int cptc_gen_profile(void* handle, double* out5, int* iters, int rese
     {
         for (double& x : g->prof) x = 0.0;
         g->prof_iters = 0;
+    }
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_kernel_times(void* handle, double* out16, int* iters, int reset)
+{
+    CPTC_REQUIRE(handle && out16, CPTC_ERR_ARG, "cptc_gen_kernel_times: null argument");
+    Gen* g = as_gen(handle);
+    for (int m = 0; m < CPTC_MAX_MODES; ++m)
+    {
+        out16[m] = g->k_seg[m];
+        out16[CPTC_MAX_MODES + m] = g->k_unit[m];
+    }
+    if (iters) *iters = g->k_iters;
+    if (reset)
+    {
+        for (int m = 0; m < CPTC_MAX_MODES; ++m) g->k_seg[m] = g->k_unit[m] = 0.0;
+        g->k_iters = 0;
     }
     return CPTC_OK;
 }

@@ -412,6 +412,8 @@ typedef struct cptc_gen_info {
     uint64_t dense_nnz;
     uint64_t nseg[CPTC_MAX_MODES];
     double prep_ms[3];       /* reorder, dense units, views */
+    uint64_t kernel_nnz[CPTC_MAX_MODES];   /* elements of the MTTKRP kernel's view per mode
+                                              (the inner modes' dense elements dropped) */
 } cptc_gen_info;
 
 /* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)
@@ -430,6 +432,14 @@ int cptc_gen_run(void* handle, int iters, double* fit, double* iprod, double* mo
  * run with opts.profile set (generic.cu:2016-2240); *iters = iterations
  * summed; reset != 0 zeroes the sums after reading. */
 int cptc_gen_profile(void* handle, double* out5, int* iters, int reset);
+
+/* Kernel times summed over cptc_gen_run iterations (hipEvents on the
+ * driver's stream): out[m] = ms of mode m's segment MTTKRP kernel,
+ * out[CPTC_MAX_MODES + m] = ms of its dense-unit kernel (0 when none);
+ * *iters = iterations summed; reset != 0 zeroes the sums.  Measurement
+ * plumbing (GEN_PROFILE's phase events, generic.cu:2016-2240, are the
+ * closest counterpart). */
+int cptc_gen_kernel_times(void* handle, double* out16, int* iters, int reset);
 
 /* Mode `mode`'s MTTKRP with the current factors into a host buffer
  * (dim x R), through the same launches as the ALS loop. */
