@@ -131,7 +131,9 @@ SIGNATURES = {
     "cptc_cadr3": (_I, [_P, _P, _P, _Z, _P, _P, _P, _P, _I]),
     "cptc_unpermute_factor": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_mttkrp_sparse3": (_I, [_I, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _P]),
-    "cptc_mttkrp_dense_tiles3": (_I, [_I, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "cptc_mttkrp_dense_tiles3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
+                                      _I, _P]),
+    "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),
     "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
     "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
@@ -163,7 +165,8 @@ SIGNATURES = {
                                 _P]),
     "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
-    "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
+    "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,
+                                  _I, _P]),
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_gen_normalize": (_I, [_P, _Z, _I, _P, _P]),

@@ -50,6 +50,10 @@ struct Als3
     DevPartition3 part;
     DevViews3 views, dviews;
     float* d_tile_f32 = nullptr;
+    // per-mode tile groups (one target row block each) for the grouped MFMA launch
+    uint32_t* d_order[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_goff[3] = {nullptr, nullptr, nullptr};
+    size_t ngroups[3] = {0, 0, 0};
     bool use_mfma = false;
     double fill_min = 0.08, avg_fill = 0.0;
     int64_t tiles_total = 0;
@@ -86,7 +90,8 @@ int mttkrp_launch(Als3& h, int mode)
     const double* C = h.F[2];
     if (h.use_mfma && !h.skip_dense && h.part.ntiles > 0)
         CPTC_TRY(cptc_mttkrp_dense_tiles3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
-                                          A, B, C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
+                                          h.d_order[mode], h.d_goff[mode], h.ngroups[mode], A, B,
+                                          C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
                                           int(h.dims[2]), h.s));
     if (!h.skip_sparse)
     {
@@ -133,6 +138,9 @@ void destroy(Als3* h)
     free_views(h->dviews);
     for (auto& p : h->d_perm)
         if (p) (void)hipFree(p);
+    for (int m = 0; m < 3; ++m)
+        for (void* p : {(void*)h->d_order[m], (void*)h->d_goff[m]})
+            if (p) (void)hipFree(p);
     for (void* p : {(void*)h->d_tile_f32, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
                     (void*)h->d_FtF, (void*)h->d_FtV, (void*)h->d_norms, (void*)h->d_scal})
         if (p) (void)hipFree(p);
@@ -145,6 +153,33 @@ void destroy(Als3* h)
 }
 
 int alloc_buffers(Als3& h);
+
+// Tiles of each mode grouped by target row block (at most TILE_GROUP per
+// wave); only for the MFMA path at R <= 128 (the grouped kernel's LDS limit).
+constexpr int TILE_GROUP = 8;
+
+int build_groups(Als3& h)
+{
+    if (!h.use_mfma || h.part.ntiles <= 0 || h.R > 128) return CPTC_OK;
+    const size_t nt = size_t(h.part.ntiles);
+    CPTC_REQUIRE(h.part.h_tiles4.size() == 4 * nt, CPTC_ERR_STATE, "tile groups: no host headers");
+    std::vector<uint32_t> order(nt), goff(nt + 1);
+    for (int m = 0; m < 3; ++m)
+    {
+        size_t ng = 0;
+        CPTC_TRY(cptc_dense_groups(h.part.h_tiles4.data(), 4, nt, m, TILE_GROUP, order.data(),
+                                   goff.data(), &ng));
+        CPTC_HIP(hipMalloc(&h.d_order[m], nt * sizeof(uint32_t)));
+        CPTC_HIP(hipMalloc(&h.d_goff[m], (ng + 1) * sizeof(uint32_t)));
+        CPTC_HIP(hipMemcpyAsync(h.d_order[m], order.data(), nt * sizeof(uint32_t),
+                                hipMemcpyHostToDevice, h.s));
+        CPTC_HIP(hipMemcpyAsync(h.d_goff[m], goff.data(), (ng + 1) * sizeof(uint32_t),
+                                hipMemcpyHostToDevice, h.s));
+        CPTC_HIP(hipStreamSynchronize(h.s));
+        h.ngroups[m] = ng;
+    }
+    return CPTC_OK;
+}
 
 int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
 {
@@ -284,6 +319,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
         }
     }
 
+    CPTC_TRY(build_groups(*h));
     CPTC_TRY(alloc_buffers(*h));
     if (o.verbose)
         std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
@@ -432,6 +468,7 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
                                                                               : CPTC_ERR_HIP);
     for (auto& e : h->ev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
     for (auto& e : h->kev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
+    if (rc == CPTC_OK) step(build_groups(*h));
     if (rc == CPTC_OK) step(alloc_buffers(*h));
     std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
     if (rc == CPTC_OK) step(run(*h, iters, fits.data(), nullptr, nullptr));

@@ -405,7 +405,8 @@ void compute_dense_mttkrp_async(const HybridCOOTensor& hybrid, int mode, double*
     if (hybrid.num_dense_tiles <= 0) return;
     const float* t = tiles_f32(hybrid, stream);
     API_TRY("compute_dense_mttkrp_async",
-            cptc_mttkrp_dense_tiles3(mode, hybrid.d_tiles4, t, size_t(hybrid.num_dense_tiles), d_A,
+            cptc_mttkrp_dense_tiles3(mode, hybrid.d_tiles4, t, size_t(hybrid.num_dense_tiles),
+                                     nullptr, nullptr, 0, d_A,
                                      d_B, d_C, d_FtV, R, int(hybrid.dims[0]), int(hybrid.dims[1]),
                                      int(hybrid.dims[2]), stream));
 }

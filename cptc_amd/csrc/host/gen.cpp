@@ -339,6 +339,10 @@ struct Gen
     cptc::DevUnitsN units;
     float* d_tiles = nullptr;
     double* d_W = nullptr;
+    // per-slot unit groups (one target row block each) for the grouped MFMA launch
+    uint32_t* d_uorder[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_ugoff[3] = {nullptr, nullptr, nullptr};
+    size_t ungroups[3] = {0, 0, 0};
     bool w_dirty = true;
     std::vector<cptc::DevViewN> views;   // kernel views (dense elements dropped, rows sorted)
     std::vector<uint64_t> ref_nseg;      // segments of the reference-layout views
@@ -367,6 +371,11 @@ struct Gen
         dfree(d_out2);
         dfree(d_tiles);
         dfree(d_W);
+        for (int q = 0; q < 3; ++q)
+        {
+            dfree(d_uorder[q]);
+            dfree(d_ugoff[q]);
+        }
         cptc::free_units(units);
         for (auto& v : views) cptc::free_view(v);
         for (auto& e : ev) (void)hipEventDestroy(e);
@@ -402,7 +411,9 @@ struct Gen
                 w_dirty = false;
             }
             const int* in3 = units.inner;
-            CPTC_TRY(cptc_mttkrp_units_nd(slot_of(n), units.d_unit6, units.nunits, d_tiles, d_W,
+            const int sl = slot_of(n);
+            CPTC_TRY(cptc_mttkrp_units_nd(sl, units.d_unit6, units.nunits, d_tiles, d_W,
+                                          d_uorder[sl], d_ugoff[sl], ungroups[sl],
                                           d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
                                           int(dims[in3[0]]), int(dims[in3[1]]),
                                           int(dims[in3[2]]), d_FtV, R, s));
@@ -495,6 +506,39 @@ struct Gen
 };
 
 Gen* as_gen(void* h) { return static_cast<Gen*>(h); }
+
+// Units of each slot grouped by target row block for the grouped MFMA
+// launch (UNIT_GROUP units per wave at most).  Device arrays are allocated
+// here; the caller frees them.
+constexpr int UNIT_GROUP = 16;
+
+int build_unit_groups(const cptc::DevUnitsN& u, hipStream_t s, uint32_t* order[3],
+                      uint32_t* goff[3], size_t ng[3])
+{
+    for (int q = 0; q < 3; ++q)
+    {
+        order[q] = goff[q] = nullptr;
+        ng[q] = 0;
+    }
+    const size_t nu = u.nunits;
+    if (nu == 0) return CPTC_OK;
+    std::vector<int32_t> hdr(nu * 6);
+    CPTC_HIP(hipMemcpyAsync(hdr.data(), u.d_unit6, hdr.size() * sizeof(int32_t),
+                            hipMemcpyDeviceToHost, s));
+    CPTC_HIP(hipStreamSynchronize(s));
+    std::vector<uint32_t> ord(nu), off(nu + 1);
+    for (int q = 0; q < 3; ++q)
+    {
+        CPTC_TRY(cptc_dense_groups(hdr.data(), 6, nu, q, UNIT_GROUP, ord.data(), off.data(), &ng[q]));
+        CPTC_HIP(hipMalloc(&order[q], nu * sizeof(uint32_t)));
+        CPTC_HIP(hipMalloc(&goff[q], (ng[q] + 1) * sizeof(uint32_t)));
+        CPTC_HIP(hipMemcpyAsync(order[q], ord.data(), nu * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+        CPTC_HIP(hipMemcpyAsync(goff[q], off.data(), (ng[q] + 1) * sizeof(uint32_t),
+                                hipMemcpyHostToDevice, s));
+        CPTC_HIP(hipStreamSynchronize(s));
+    }
+    return CPTC_OK;
+}
 
 bool env_set(const char* k) { return std::getenv(k) != nullptr; }
 
@@ -701,6 +745,7 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
             GEN_TRY(dmalloc(&g->d_W, g->units.nunits * R));
             GEN_TRY(cptc_units_pack_nd(g->units.d_unit6, g->units.nunits, g->units.d_lid,
                                        g->units.d_val, g->d_tiles, s));
+            GEN_TRY(build_unit_groups(g->units, s, g->d_uorder, g->d_ugoff, g->ungroups));
         }
         g->prep_ms[1] = ms_since(t0);
         if (verbose)
@@ -1177,11 +1222,21 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
                             100.0 * double(u.dense_nnz) / double(nnz));
             float* d_tiles = nullptr;
             double* d_W = nullptr;
+            uint32_t* gorder[3] = {nullptr, nullptr, nullptr};
+            uint32_t* ggoff[3] = {nullptr, nullptr, nullptr};
+            size_t gn[3] = {0, 0, 0};
             if (u.nunits)
             {
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_tiles), u.nunits * 4096 * sizeof(float)));
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_W), u.nunits * R * sizeof(double)));
                 CPTC_TRY(cptc_units_pack_nd(u.d_unit6, u.nunits, u.d_lid, u.d_val, d_tiles, s));
+                const int rcg = build_unit_groups(u, s, gorder, ggoff, gn);
+                for (int q = 0; q < 3; ++q)
+                {
+                    own.p.push_back(gorder[q]);
+                    own.p.push_back(ggoff[q]);
+                }
+                CPTC_TRY(rcg);
                 const int om = u.outer.empty() ? 0 : u.outer[0];
                 CPTC_TRY(cptc_units_weights_nd(u.d_unit6, u.nunits, u.d_outer_coords,
                                                int(u.outer.size()), &om, dF.data(), R, d_W, s));
@@ -1192,6 +1247,7 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
                 CPTC_HIP(hipMemsetAsync(d_FtV, 0, size_t(maxd) * R * sizeof(double), s));
                 if (u.nunits)
                     CPTC_TRY(cptc_mttkrp_units_nd(ii, u.d_unit6, u.nunits, d_tiles, d_W,
+                                                  gorder[ii], ggoff[ii], gn[ii],
                                                   dF[inner[0]], dF[inner[1]], dF[inner[2]],
                                                   T.dims[inner[0]], T.dims[inner[1]],
                                                   T.dims[inner[2]], d_FtV, R, s));

@@ -19,7 +19,9 @@
 // registers (the tile is read from HBM once per launch).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
+#include <vector>
 
 #include "../host/hip_util.hpp"
 
@@ -38,17 +40,45 @@ __device__ inline float fold(const double* __restrict__ F, int row, int dim, int
 // MODE = target slot; HDR = int32 words per tile header (bi, bj, bk first):
 // 4 for order-3 tiles, 6 for generic units.  HAS_W: the unit's FP64 outer
 // weights W[t, r] scale its contribution (generic N-order units).
-template <int MODE, int HDR, bool HAS_W>
+// GROUPED: a wave takes a group of tiles that share the target row block
+// (order[goff[g] .. goff[g+1]]) and sums their (row, rank) results in its own
+// LDS block (16 x Rp doubles; each lane owns its entries, so no barrier),
+// then flushes one atomic per (row, rank) per group instead of per tile.
+template <int MODE, int HDR, bool HAS_W, bool GROUPED>
 __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_kernel(
     const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32, size_t ntiles,
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ goff, size_t ngroups,
     const double* __restrict__ A, const double* __restrict__ B, const double* __restrict__ C,
-    const double* __restrict__ W, double* __restrict__ FtV, int R, int dimI, int dimJ, int dimK)
+    const double* __restrict__ W, double* __restrict__ FtV, int R, int Rp, int dimI, int dimJ,
+    int dimK)
 {
-    const size_t t = size_t(blockIdx.x) * WAVES_PER_WG + threadIdx.x / WAVE;
-    if (t >= ntiles) return;
+    extern __shared__ double gacc_lds[];
+    const size_t wid = size_t(blockIdx.x) * WAVES_PER_WG + threadIdx.x / WAVE;
+    size_t it0, it1;
+    if constexpr (GROUPED)
+    {
+        if (wid >= ngroups) return;
+        it0 = goff[wid];
+        it1 = goff[wid + 1];
+    }
+    else
+    {
+        if (wid >= ntiles) return;
+        it0 = wid;
+        it1 = wid + 1;
+    }
     const int lane = threadIdx.x & (WAVE - 1);
     const int lo = lane & 15;   // m (A operand row) / n (B, D column)
     const int hi = lane >> 4;   // kk (A, B) / m-group (D)
+    double* gacc = gacc_lds + size_t(threadIdx.x / WAVE) * 16 * Rp;
+    if constexpr (GROUPED)
+        for (int rb = 0; rb < R; rb += 16)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) gacc[(4 * hi + v) * Rp + rb + lo] = 0.0;
+    int ob = 0, odim = 0;
+    for (size_t it = it0; it < it1; ++it)
+    {
+    const size_t t = GROUPED ? size_t(order[it]) : it;
     const int b0 = hdr[HDR * t] * 16, b1 = hdr[HDR * t + 1] * 16, b2 = hdr[HDR * t + 2] * 16;
     const float* __restrict__ T = tile_f32 + t * 4096;
 
@@ -89,8 +119,8 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     const int wb = (MODE == 2) ? b1 : b2;
     const int wdim = (MODE == 2) ? dimJ : dimK;
     // output rows
-    const int ob = (MODE == 0) ? b0 : (MODE == 1) ? b1 : b2;
-    const int odim = (MODE == 0) ? dimI : (MODE == 1) ? dimJ : dimK;
+    ob = (MODE == 0) ? b0 : (MODE == 1) ? b1 : b2;
+    odim = (MODE == 0) ? dimI : (MODE == 1) ? dimJ : dimK;
 
     for (int rb = 0; rb < R; rb += 16)
     {
@@ -137,11 +167,36 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
 #pragma unroll
                 for (int v = 0; v < 4; ++v) tot[v] *= wr;
             }
+            if constexpr (GROUPED)
+            {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) gacc[(4 * hi + v) * Rp + r] += tot[v];
+            }
+            else
+            {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                {
+                    const int row = ob + 4 * hi + v;
+                    if (row < odim && tot[v] != 0.0) atomicAdd(FtV + size_t(row) * R + r, tot[v]);
+                }
+            }
+        }
+    }
+    }
+    if constexpr (GROUPED)
+    {
+        // every tile of the group has target block ob
+        for (int rb = 0; rb < R; rb += 16)
+        {
+            const int r = rb + lo;
+            if (r >= R) continue;
 #pragma unroll
             for (int v = 0; v < 4; ++v)
             {
                 const int row = ob + 4 * hi + v;
-                if (row < odim && tot[v] != 0.0) atomicAdd(FtV + size_t(row) * R + r, tot[v]);
+                const double x = gacc[(4 * hi + v) * Rp + r];
+                if (row < odim && x != 0.0) atomicAdd(FtV + size_t(row) * R + r, x);
             }
         }
     }
@@ -190,60 +245,122 @@ extern "C" int cptc_dense_tiles_pack3(const int32_t* d_pool_lid, const double* d
     return CPTC_OK;
 }
 
+namespace {
+
+constexpr int GROUP_LDS_MAX_R = 128;   // 4 waves x 16 rows x 128 ranks x 8 B = 64 KB
+
+template <int MODE, int HDR, bool HAS_W>
+int launch_tiles(const int32_t* hdr, const float* tiles, size_t ntiles, const uint32_t* order,
+                 const uint32_t* goff, size_t ngroups, const double* A, const double* B,
+                 const double* C, const double* W, double* FtV, int R, int dI, int dJ, int dK,
+                 hipStream_t s)
+{
+    const dim3 block{WAVE * WAVES_PER_WG};
+    const bool grouped = order && goff && ngroups > 0 && R <= GROUP_LDS_MAX_R;
+    if (grouped)
+    {
+        const int Rp = (R + 15) / 16 * 16;
+        const size_t wgs = (ngroups + WAVES_PER_WG - 1) / WAVES_PER_WG;
+        CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many groups");
+        const size_t lds = size_t(WAVES_PER_WG) * 16 * Rp * sizeof(double);
+        hipLaunchKernelGGL((dense_tiles_kernel<MODE, HDR, HAS_W, true>),
+                           dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles, ntiles,
+                           order, goff, ngroups, A, B, C, W, FtV, R, Rp, dI, dJ, dK);
+    }
+    else
+    {
+        const size_t wgs = (ntiles + WAVES_PER_WG - 1) / WAVES_PER_WG;
+        CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many tiles");
+        hipLaunchKernelGGL((dense_tiles_kernel<MODE, HDR, HAS_W, false>),
+                           dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ntiles,
+                           nullptr, nullptr, size_t(0), A, B, C, W, FtV, R, R, dI, dJ, dK);
+    }
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+template <int HDR, bool HAS_W>
+int launch_slot(int slot, const int32_t* hdr, const float* tiles, size_t ntiles,
+                const uint32_t* order, const uint32_t* goff, size_t ngroups, const double* A,
+                const double* B, const double* C, const double* W, double* FtV, int R, int dI,
+                int dJ, int dK, hipStream_t s)
+{
+    if (slot == 0)
+        return launch_tiles<0, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, A, B, C, W,
+                                           FtV, R, dI, dJ, dK, s);
+    if (slot == 1)
+        return launch_tiles<1, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, A, B, C, W,
+                                           FtV, R, dI, dJ, dK, s);
+    return launch_tiles<2, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, A, B, C, W, FtV,
+                                       R, dI, dJ, dK, s);
+}
+
+}  // namespace
+
 extern "C" int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const float* d_tile_f32,
-                                        size_t ntiles, const double* d_A, const double* d_B,
-                                        const double* d_C, double* d_FtV, int R, int dimI,
-                                        int dimJ, int dimK, void* stream)
+                                        size_t ntiles, const uint32_t* d_order,
+                                        const uint32_t* d_group_off, size_t ngroups,
+                                        const double* d_A, const double* d_B, const double* d_C,
+                                        double* d_FtV, int R, int dimI, int dimJ, int dimK,
+                                        void* stream)
 {
     CPTC_REQUIRE(mode >= 0 && mode < 3 && R >= 1, CPTC_ERR_ARG,
                  "cptc_mttkrp_dense_tiles3: mode %d R %d", mode, R);
     if (ntiles == 0) return CPTC_OK;
     CPTC_REQUIRE(d_tiles && d_tile_f32 && d_A && d_B && d_C && d_FtV, CPTC_ERR_ARG,
                  "cptc_mttkrp_dense_tiles3: null pointer");
-    const size_t wgs = (ntiles + WAVES_PER_WG - 1) / WAVES_PER_WG;
-    CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "cptc_mttkrp_dense_tiles3: too many tiles");
-    hipStream_t s = cptc::as_stream(stream);
-    const dim3 grid{static_cast<unsigned>(wgs)};
-    const dim3 block{WAVE * WAVES_PER_WG};
-    const double* noW = nullptr;
-    if (mode == 0)
-        hipLaunchKernelGGL((dense_tiles_kernel<0, 4, false>), grid, block, 0, s, d_tiles,
-                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
-    else if (mode == 1)
-        hipLaunchKernelGGL((dense_tiles_kernel<1, 4, false>), grid, block, 0, s, d_tiles,
-                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
-    else
-        hipLaunchKernelGGL((dense_tiles_kernel<2, 4, false>), grid, block, 0, s, d_tiles,
-                           d_tile_f32, ntiles, d_A, d_B, d_C, noW, d_FtV, R, dimI, dimJ, dimK);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    return launch_slot<4, false>(mode, d_tiles, d_tile_f32, ntiles, d_order, d_group_off, ngroups,
+                                 d_A, d_B, d_C, nullptr, d_FtV, R, dimI, dimJ, dimK,
+                                 cptc::as_stream(stream));
 }
 
 extern "C" int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
-                                    const float* d_tiles, const double* d_W, const double* d_F0,
-                                    const double* d_F1, const double* d_F2, int dim0, int dim1,
-                                    int dim2, double* d_FtV, int R, void* stream)
+                                    const float* d_tiles, const double* d_W,
+                                    const uint32_t* d_order, const uint32_t* d_group_off,
+                                    size_t ngroups, const double* d_F0, const double* d_F1,
+                                    const double* d_F2, int dim0, int dim1, int dim2,
+                                    double* d_FtV, int R, void* stream)
 {
     CPTC_REQUIRE(slot >= 0 && slot < 3 && R >= 1, CPTC_ERR_ARG,
                  "cptc_mttkrp_units_nd: slot %d R %d", slot, R);
     if (nunits == 0) return CPTC_OK;
     CPTC_REQUIRE(d_unit6 && d_tiles && d_W && d_F0 && d_F1 && d_F2 && d_FtV, CPTC_ERR_ARG,
                  "cptc_mttkrp_units_nd: null pointer");
-    const size_t wgs = (nunits + WAVES_PER_WG - 1) / WAVES_PER_WG;
-    CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "cptc_mttkrp_units_nd: too many units");
-    hipStream_t s = cptc::as_stream(stream);
-    const dim3 grid{static_cast<unsigned>(wgs)};
-    const dim3 block{WAVE * WAVES_PER_WG};
-    const int32_t* h = reinterpret_cast<const int32_t*>(d_unit6);
-    if (slot == 0)
-        hipLaunchKernelGGL((dense_tiles_kernel<0, 6, true>), grid, block, 0, s, h, d_tiles,
-                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
-    else if (slot == 1)
-        hipLaunchKernelGGL((dense_tiles_kernel<1, 6, true>), grid, block, 0, s, h, d_tiles,
-                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
-    else
-        hipLaunchKernelGGL((dense_tiles_kernel<2, 6, true>), grid, block, 0, s, h, d_tiles,
-                           size_t(nunits), d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2);
-    CPTC_LAUNCHED();
+    return launch_slot<6, true>(slot, reinterpret_cast<const int32_t*>(d_unit6), d_tiles,
+                                size_t(nunits), d_order, d_group_off, ngroups, d_F0, d_F1, d_F2,
+                                d_W, d_FtV, R, dim0, dim1, dim2, cptc::as_stream(stream));
+}
+
+// Host: tiles in (target block, other blocks) order, cut into runs of at
+// most max_group tiles with one target block.
+extern "C" int cptc_dense_groups(const int32_t* hdr, int hdr_words, size_t ntiles, int slot,
+                                 int max_group, uint32_t* order_out, uint32_t* group_off_out,
+                                 size_t* ngroups_out)
+{
+    CPTC_REQUIRE(hdr_words >= 3 && slot >= 0 && slot < 3 && max_group >= 1 &&
+                     (ntiles == 0 || (hdr && order_out && group_off_out)) && ngroups_out,
+                 CPTC_ERR_ARG, "cptc_dense_groups: bad arguments");
+    CPTC_REQUIRE(ntiles < (size_t(1) << 32), CPTC_ERR_ARG, "cptc_dense_groups: too many tiles");
+    const int p = (slot + 1) % 3, q = (slot + 2) % 3;
+    std::vector<uint32_t> ord(ntiles);
+    for (size_t t = 0; t < ntiles; ++t) ord[t] = uint32_t(t);
+    auto key = [&](uint32_t t, int c) { return hdr[size_t(hdr_words) * t + c]; };
+    std::stable_sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+        if (key(a, slot) != key(b, slot)) return key(a, slot) < key(b, slot);
+        if (key(a, p) != key(b, p)) return key(a, p) < key(b, p);
+        return key(a, q) < key(b, q);
+    });
+    size_t ng = 0;
+    group_off_out[0] = 0;
+    for (size_t i = 0; i < ntiles;)
+    {
+        size_t j = i + 1;
+        while (j < ntiles && j - i < size_t(max_group) && key(ord[j], slot) == key(ord[i], slot))
+            ++j;
+        group_off_out[++ng] = uint32_t(j);
+        i = j;
+    }
+    for (size_t t = 0; t < ntiles; ++t) order_out[t] = ord[t];
+    *ngroups_out = ng;
     return CPTC_OK;
 }

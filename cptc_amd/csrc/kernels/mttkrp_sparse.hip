@@ -40,14 +40,19 @@ struct Row<1>
     __device__ void load(const double* __restrict__ p) { x[0] = *p; }
 };
 
-// One workgroup per row segment.  The WAVES * EPW element slots of the
-// workgroup each take a contiguous chunk of the segment and walk it in view
-// order (o1 ascending, then o0), so every run of equal o1 is handled by one
-// slot: t += v * F1[o0] over the run, acc += t * F2[o1] once per run.  The
-// second factor row is gathered once per run instead of once per element
-// (the sum is reassociated: acc_r = sum_runs F2[o1, r] * sum_e v_e F1[o0_e, r]).
-// View coordinates and values are streamed with non-temporal loads so they
-// do not evict factor rows from L2.
+// One workgroup per row segment; each wave takes a contiguous quarter of it.
+// A wave streams its range in windows of 64 elements: lane L loads element
+// base + L (one coalesced load for the coordinates, one for the values), and
+// the next window is requested before the current one is consumed, so the
+// HBM latency of the view stream overlaps the factor gathers.  Inside a
+// window the EPW element slots of the wave each take LPE consecutive
+// elements (their coordinates and values are broadcast from the loading
+// lanes) and walk them in view order (o1 ascending, then o0): t += v * F1[o0]
+// over a run of equal o1, acc += t * F2[o1] once per run — the second factor
+// row is gathered once per run (acc_r = sum_runs F2[o1, r] * sum_e v_e
+// F1[o0_e, r], the reference's sum reassociated).  UNROLL gathers of a slot
+// are in flight together.  View data uses non-temporal loads so it does not
+// evict factor rows from L2.
 template <int RT, int VEC, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     int mode, const uint64_t* __restrict__ coords, const double* __restrict__ vals,
@@ -55,9 +60,8 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     const uint32_t* __restrict__ blk_cnt, const double* __restrict__ F1,
     const double* __restrict__ F2, double* __restrict__ FtV, int R)
 {
-    constexpr int LPE = RT / VEC;          // lanes per element
-    constexpr int EPW = WAVE / LPE;        // element slots per wave
-    constexpr int SLOTS = EPW * WAVES;     // element slots per workgroup
+    constexpr int LPE = RT / VEC;          // lanes per element = elements per slot per window
+    constexpr int U = (UNROLL < LPE) ? UNROLL : LPE;
     static_assert(WAVE % LPE == 0, "rank tile must divide the wave");
 
     const uint32_t seg = blockIdx.x;
@@ -77,12 +81,10 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     const int sh0 = (mode == 0) ? 15 : 30;   // o0 = j (mode 0) or i
     const int sh1 = (mode == 2) ? 15 : 0;    // o1 = k (modes 0,1) or j
 
-    // this slot's contiguous chunk
-    const uint32_t g = uint32_t(wave * EPW + slot);
-    const uint32_t chunk = (cnt + SLOTS - 1) / SLOTS;
-    uint32_t lo = start + g * chunk;
-    const uint32_t hi = (g * chunk + chunk < cnt) ? lo + chunk : start + cnt;
-    if (lo > hi) lo = hi;
+    // this wave's contiguous range of the segment
+    const uint32_t wchunk = (cnt + WAVES - 1) / WAVES;
+    const uint32_t lo = start + min(cnt, uint32_t(wave) * wchunk);
+    const uint32_t hi = start + min(cnt, uint32_t(wave + 1) * wchunk);
 
     double acc[VEC], t[VEC];
 #pragma unroll
@@ -100,49 +102,73 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
         }
     };
 
-    uint32_t e = lo;
-    for (; e + UNROLL <= hi; e += UNROLL)
+    uint64_t pc = 0;
+    double v = 0.0;
+    if (lo + uint32_t(lane) < hi)
     {
-        uint64_t pc[UNROLL];
-        double v[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-        {
-            pc[u] = __builtin_nontemporal_load(coords + e + u);
-            v[u] = __builtin_nontemporal_load(vals + e + u);
-        }
-        uint32_t o0[UNROLL], o1[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-        {
-            o0[u] = uint32_t(pc[u] >> sh0) & 0x7FFFu;
-            o1[u] = uint32_t(pc[u] >> sh1) & 0x7FFFu;
-        }
-        Row<VEC> f1[UNROLL];
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u) f1[u].load(F1 + size_t(o0[u]) * R + rr);
-        if (o1[0] != cur && cur != 0xFFFFFFFFu) close_run(cur);
-#pragma unroll
-        for (int u = 0; u < UNROLL; ++u)
-        {
-#pragma unroll
-            for (int q = 0; q < VEC; ++q) t[q] += v[u] * f1[u].x[q];
-            if (u + 1 < UNROLL && o1[u] != o1[u + 1]) close_run(o1[u]);
-        }
-        cur = o1[UNROLL - 1];
+        pc = __builtin_nontemporal_load(coords + lo + lane);
+        v = __builtin_nontemporal_load(vals + lo + lane);
     }
-    for (; e < hi; ++e)
+    for (uint32_t base = lo; base < hi; base += WAVE)
     {
-        const uint64_t pc = __builtin_nontemporal_load(coords + e);
-        const double v = __builtin_nontemporal_load(vals + e);
-        const uint32_t o0 = uint32_t(pc >> sh0) & 0x7FFFu;
-        const uint32_t o1 = uint32_t(pc >> sh1) & 0x7FFFu;
-        if (o1 != cur && cur != 0xFFFFFFFFu) close_run(cur);
-        Row<VEC> f1;
-        f1.load(F1 + size_t(o0) * R + rr);
+        // request the next window before consuming this one
+        uint64_t pcn = 0;
+        double vn = 0.0;
+        if (base + WAVE + uint32_t(lane) < hi)
+        {
+            pcn = __builtin_nontemporal_load(coords + base + WAVE + lane);
+            vn = __builtin_nontemporal_load(vals + base + WAVE + lane);
+        }
+        // this slot's elements: window positions [slot*LPE, slot*LPE + n)
+        const int j0 = slot * LPE;
+        const int left = int(hi - base) - j0;
+        const int n = left < 0 ? 0 : (left > LPE ? LPE : left);
+        for (int i = 0; i < n; i += U)
+        {
+            uint32_t o0[U], o1[U];
+            double ev[U];
+            Row<VEC> f1[U];
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) t[q] += v * f1.x[q];
-        cur = o1;
+            for (int u = 0; u < U; ++u)
+            {
+                const int j = j0 + i + u;
+                const uint64_t pj = __shfl(pc, j, WAVE);
+                ev[u] = __shfl(v, j, WAVE);
+                o0[u] = uint32_t(pj >> sh0) & 0x7FFFu;
+                o1[u] = uint32_t(pj >> sh1) & 0x7FFFu;
+            }
+            // the F2 row a run boundary at position u closes: the previous o1
+            // (known now), requested together with the F1 rows
+            Row<VEC> f2[U];
+            bool closes[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                const uint32_t prev = (u == 0) ? cur : o1[u - 1];
+                closes[u] = (i + u < n) && o1[u] != prev && prev != 0xFFFFFFFFu;
+                if (i + u < n) f1[u].load(F1 + size_t(o0[u]) * R + rr);
+                if (closes[u]) f2[u].load(F2 + size_t(prev) * R + rr);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                if (i + u >= n) break;
+                if (closes[u])
+                {
+#pragma unroll
+                    for (int q = 0; q < VEC; ++q)
+                    {
+                        acc[q] += t[q] * f2[u].x[q];
+                        t[q] = 0.0;
+                    }
+                }
+                cur = o1[u];
+#pragma unroll
+                for (int q = 0; q < VEC; ++q) t[q] += ev[u] * f1[u].x[q];
+            }
+        }
+        pc = pcn;
+        v = vn;
     }
     if (cur != 0xFFFFFFFFu) close_run(cur);
     if (!rank_ok)

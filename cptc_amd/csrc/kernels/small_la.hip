@@ -205,15 +205,52 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
         }
     }
     __syncthreads();
-    // 3. Ainv[r][s] = sum_{j >= max(r, s)} X[j][r] X[j][s]
+    // 3. X row-major lower triangular in place (L is no longer needed): each
+    //    lower entry is written from its transposed upper entry by one thread
     for (int idx = tid; idx < n2; idx += PINV_THREADS)
     {
         const int r = idx / R, c = idx - r * R;
-        if (c < r) continue;
-        double acc = xd[c] * (r == c ? xd[r] : A[r * R + c]);
-        for (int j = c + 1; j < R; ++j) acc += A[r * R + j] * A[c * R + j];
-        Ainv[r * R + c] = acc;
-        Ainv[c * R + r] = acc;
+        if (c < r) A[r * R + c] = A[c * R + r];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < n2; idx += PINV_THREADS)
+    {
+        const int r = idx / R, c = idx - r * R;
+        if (c > r) A[r * R + c] = 0.0;
+        if (c == r) A[r * R + r] = xd[r];
+    }
+    __syncthreads();
+    // 4. Ainv = X^T X in 4 x 4 register blocks: Ainv[r][c] = sum_j X[j][r] X[j][c]
+    //    (X[j][r] = 0 for j < r, so j starts at the block's smaller index)
+    const int nb = (R + 3) / 4;
+    for (int b = tid; b < nb * nb; b += PINV_THREADS)
+    {
+        const int r0 = 4 * (b / nb), c0 = 4 * (b % nb);
+        double acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[i][k] = 0.0;
+        for (int j = (r0 < c0 ? r0 : c0); j < R; ++j)
+        {
+            const double* xj = A + size_t(j) * R;
+            double xr[4], xc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+            {
+                xr[i] = (r0 + i < R) ? xj[r0 + i] : 0.0;
+                xc[i] = (c0 + i < R) ? xj[c0 + i] : 0.0;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[i][k] += xr[i] * xc[k];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (r0 + i < R && c0 + k < R) Ainv[(r0 + i) * R + c0 + k] = acc[i][k];
     }
 }
 

@@ -146,9 +146,23 @@ int cptc_mttkrp_sparse3(int mode, const uint64_t* d_coords, const double* d_vals
  * Replaces compute_dense_mttkrp_async -> dense_mttkrp_wmma_kernel ->
  * dense_tile_mttkrp_wmma (dense.cu:89-1077, 1569-1621, 2072-2246). */
 int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const float* d_tile_f32,
-                             size_t ntiles, const double* d_A, const double* d_B,
+                             size_t ntiles, const uint32_t* d_order, const uint32_t* d_group_off,
+                             size_t ngroups, const double* d_A, const double* d_B,
                              const double* d_C, double* d_FtV, int R, int dimI, int dimJ,
                              int dimK, void* stream);
+
+/* Tile groups for the grouped MFMA launches (no reference counterpart; the
+ * reference issues one atomic per (row, rank, tile)).  hdr: ntiles x
+ * hdr_words int32 on the host ({bi, bj, bk, ...}: 4 words for order-3 tiles,
+ * 6 for generic units).  order_out (ntiles) = tile indices sorted by (block
+ * of `slot`, then the other two blocks); group_off_out (ntiles + 1) cuts
+ * them into runs of <= max_group tiles with one target block; *ngroups_out
+ * = number of runs.  Passing d_order / d_group_off / ngroups (device copies)
+ * to cptc_mttkrp_dense_tiles3 or cptc_mttkrp_units_nd makes one wave sum
+ * a group in LDS and issue one atomic per (row, rank) per group (R <= 128;
+ * NULL / larger R: one atomic per tile).  Host code. */
+int cptc_dense_groups(const int32_t* hdr, int hdr_words, size_t ntiles, int slot, int max_group,
+                      uint32_t* order_out, uint32_t* group_off_out, size_t* ngroups_out);
 
 /* Materialises dense tiles: cell (lid) of tile t holds the value of the last
  * pool entry with that lid (pool order), clamped to +-FLT_MAX, as fp32;
@@ -353,7 +367,8 @@ int cptc_units_weights_nd(const uint32_t* d_unit6, uint64_t nunits,
  * slots of T * F_a * F_b * W[u, r], with F_slot0..2 the factors of the inner
  * modes and dim0..2 their dims.  FP32 MFMA inner products, FP64 epilogue. */
 int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
-                         const float* d_tiles, const double* d_W, const double* d_F0,
+                         const float* d_tiles, const double* d_W, const uint32_t* d_order,
+                         const uint32_t* d_group_off, size_t ngroups, const double* d_F0,
                          const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
                          double* d_FtV, int R, void* stream);
 

@@ -39,8 +39,12 @@ def test_version_and_no_device_here(ca):
     lambda l: l.cptc_mttkrp_sparse3(3, 0, 0, 0, 0, 0, 10, 0, 0, 0, 32, None),
     lambda l: l.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 10, 0, 0, 0, 0, None),
     lambda l: l.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 10, 0, 0, 0, 32, None),
-    lambda l: l.cptc_mttkrp_dense_tiles3(5, 0, 0, 1, 0, 0, 0, 0, 16, 1, 1, 1, None),
-    lambda l: l.cptc_mttkrp_dense_tiles3(0, 0, 0, 1, 0, 0, 0, 0, 16, 1, 1, 1, None),
+    lambda l: l.cptc_mttkrp_dense_tiles3(5, 0, 0, 1, None, None, 0, 0, 0, 0, 0, 16, 1, 1, 1,
+                                         None),
+    lambda l: l.cptc_mttkrp_dense_tiles3(0, 0, 0, 1, None, None, 0, 0, 0, 0, 0, 16, 1, 1, 1,
+                                         None),
+    lambda l: l.cptc_dense_groups(None, 4, 3, 0, 8, None, None, None),
+    lambda l: l.cptc_mttkrp_units_nd(3, 0, 1, 0, 0, None, None, 0, 0, 0, 0, 1, 1, 1, 0, 8, None),
     lambda l: l.cptc_gram(0, 10, 8, 0, None),
     lambda l: l.cptc_hadamard(0, 0, 0, 10, None),
     lambda l: l.cptc_solve_pinv(0, 0, 0, 10, 8, 0, None),
@@ -63,7 +67,8 @@ def test_bad_arguments_rejected(ca, call):
 def test_empty_work_is_ok(ca):
     # zero segments / tiles: nothing to launch, success
     assert ca.lib.cptc_mttkrp_sparse3(0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 32, None) == 0
-    assert ca.lib.cptc_mttkrp_dense_tiles3(0, 0, 0, 0, 0, 0, 0, 0, 16, 1, 1, 1, None) == 0
+    assert ca.lib.cptc_mttkrp_dense_tiles3(0, 0, 0, 0, None, None, 0, 0, 0, 0, 0, 16, 1, 1, 1,
+                                           None) == 0
     assert ca.lib.cptc_hadamard(1, 1, 1, 0, None) == 0
 
 
@@ -83,3 +88,33 @@ def test_cadr3_rejects_out_of_range_index(ca):
     t = ca.Tensor((4, 4, 4), np.array([[0, 1], [1, 9], [2, 2]], np.uint32), np.ones(2))
     with pytest.raises(ca.CptcError, match="index"):
         ca.cadr3(t)
+
+
+@pytest.mark.parametrize("hdr_words,slot,G", [(4, 0, 8), (4, 1, 8), (4, 2, 3), (6, 1, 16)])
+def test_dense_groups(ca, hdr_words, slot, G):
+    """Host group builder: a permutation sorted by (target block, others),
+    runs of <= G tiles with one target block covering every tile."""
+    import ctypes as C
+    rng = np.random.default_rng(slot + G)
+    n = 500
+    hdr = rng.integers(0, 6, (n, hdr_words)).astype(np.int32)
+    order = np.zeros(n, np.uint32)
+    off = np.zeros(n + 1, np.uint32)
+    ng = C.c_size_t()
+    assert ca.lib.cptc_dense_groups(hdr.ctypes.data, hdr_words, n, slot, G, order.ctypes.data,
+                                    off.ctypes.data, C.byref(ng)) == 0
+    ng = ng.value
+    assert np.array_equal(np.sort(order), np.arange(n))
+    p, q = (slot + 1) % 3, (slot + 2) % 3
+    keys = [tuple(hdr[t, [slot, p, q]]) for t in order]
+    assert keys == sorted(keys)
+    assert off[0] == 0 and off[ng] == n
+    for g in range(ng):
+        a, b = off[g], off[g + 1]
+        assert 1 <= b - a <= G
+        assert len(set(hdr[order[a:b], slot])) == 1
+    # maximal runs: a new group starts only at a block change or a full group
+    for g in range(1, ng):
+        a = off[g]
+        if hdr[order[a], slot] == hdr[order[a - 1], slot]:
+            assert off[g] - off[g - 1] == G

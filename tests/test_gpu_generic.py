@@ -161,10 +161,11 @@ def test_seg_kernel_single_store(ca, orc, dev):
     assert rel_err(out.numpy(), ref) <= 1e-12
 
 
-@pytest.mark.parametrize("N,R,inner", [(4, 8, (0, 1, 2)), (4, 16, (0, 1, 2)), (5, 32, (0, 1, 2)),
-                                       (4, 20, (1, 2, 3)), (4, 8, (0, 2, 3)),
-                                       (5, 16, (1, 3, 4)), (4, 3, (0, 1, 3))])
-def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner):
+@pytest.mark.parametrize("N,R,inner,G", [(4, 8, (0, 1, 2), 0), (4, 16, (0, 1, 2), 4),
+                                         (5, 32, (0, 1, 2), 16), (4, 20, (1, 2, 3), 0),
+                                         (4, 8, (0, 2, 3), 2), (5, 16, (1, 3, 4), 16),
+                                         (4, 3, (0, 1, 3), 0)])
+def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G):
     rng = np.random.default_rng(N * 7 + R)
     dims = (40, 30, 36, 33, 34)[:N]
     idx = clustered(rng, dims, inner, 0.5, 3000)
@@ -201,7 +202,18 @@ def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner):
     assert np.array_equal(tiles.numpy(), T.astype(np.float32))
     for slot, n in enumerate(inner):
         out = ca.DevBuf.zeros((dims[n], R), np.float64)
+        grp = (None, None, 0)
+        if G:
+            order = np.zeros(nu, np.uint32)
+            off = np.zeros(nu + 1, np.uint32)
+            ng = C.c_size_t()
+            hdr = np.ascontiguousarray(u["unit6"], np.uint32).view(np.int32)
+            assert ca.lib.cptc_dense_groups(hdr.ctypes.data, 6, nu, slot, G, order.ctypes.data,
+                                            off.ctypes.data, C.byref(ng)) == 0
+            gbufs = (dbuf(ca, order), dbuf(ca, off[:ng.value + 1].copy()))
+            grp = (gbufs[0].data_ptr(), gbufs[1].data_ptr(), ng.value)
         rc = ca.lib.cptc_mttkrp_units_nd(slot, d6.data_ptr(), nu, tiles.data_ptr(), W.data_ptr(),
+                                         *grp,
                                          dF[inner[0]].data_ptr(), dF[inner[1]].data_ptr(),
                                          dF[inner[2]].data_ptr(), dims[inner[0]],
                                          dims[inner[1]], dims[inner[2]], out.data_ptr(), R,

@@ -95,8 +95,21 @@ def block_tensor(rng, dims, fill=0.5):
     return idx, rng.standard_normal(idx.shape[1])
 
 
-@pytest.mark.parametrize("R", [8, 16, 20, 32, 128])
-def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R):
+def tile_groups(ca, hdr, words, slot, G):
+    import ctypes as C
+    n = hdr.shape[0]
+    order = np.zeros(n, np.uint32)
+    off = np.zeros(n + 1, np.uint32)
+    ng = C.c_size_t()
+    assert ca.lib.cptc_dense_groups(np.ascontiguousarray(hdr, np.int32).ctypes.data, words, n,
+                                    slot, G, order.ctypes.data, off.ctypes.data,
+                                    C.byref(ng)) == 0
+    return to_dev(ca, order), to_dev(ca, off[:ng.value + 1].copy()), ng.value
+
+
+@pytest.mark.parametrize("R,G", [(8, 0), (16, 0), (20, 0), (32, 0), (128, 0), (8, 3), (32, 8),
+                                 (128, 8), (200, 8)])
+def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G):
     rng = np.random.default_rng(50 + R)
     dims = (40, 45, 37)               # boundary tiles in every mode
     idx, val = block_tensor(rng, dims)
@@ -116,7 +129,11 @@ def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R):
         ref = orc.mttkrp3_tiles(p, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
                                 dims).reshape(dims[mode], R)
         out = zeros(ca, (dims[mode], R))
-        rc = ca.lib.cptc_mttkrp_dense_tiles3(mode, tiles.data_ptr(), tf.data_ptr(), nt,
+        grp = (None, None, 0)
+        if G:
+            go, gf, ng = tile_groups(ca, p["tiles"], 4, mode, G)
+            grp = (go.data_ptr(), gf.data_ptr(), ng)
+        rc = ca.lib.cptc_mttkrp_dense_tiles3(mode, tiles.data_ptr(), tf.data_ptr(), nt, *grp,
                                              dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
                                              out.data_ptr(), R, *dims, stream(ca))
         assert rc == 0, ca.lib.cptc_last_error()
