@@ -10,7 +10,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libcptc.so")
+# CPTC_LIB_PATH overrides the library location (e.g. an alternative build)
+LIB_PATH = os.environ.get("CPTC_LIB_PATH") or os.path.join(_HERE, "lib", "libcptc.so")
 CLI_PATH = os.path.join(_HERE, "bin", "cptc_opt")
 
 CPTC_MAX_MODES = 8

@@ -16,6 +16,10 @@
 
 #include "../host/hip_util.hpp"
 
+#ifndef CPTC_SPARSE3_UNROLL
+#define CPTC_SPARSE3_UNROLL 8   // gathers in flight per element slot
+#endif
+
 namespace {
 
 constexpr int WAVE = 64;
@@ -218,7 +222,7 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
                      const double* F2, double* FtV, int R, hipStream_t s)
 {
     constexpr int WAVES = 4;
-    constexpr int UNROLL = 8;
+    constexpr int UNROLL = CPTC_SPARSE3_UNROLL;
     const unsigned ry = unsigned((R + RT - 1) / RT);
     dim3 grid(unsigned(nblocks), ry);
     hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid, dim3(WAVE * WAVES), 0,
