@@ -4,9 +4,14 @@
 // Follows main.cu:136-672 (setup and selection) and als.cu:362-821 (the
 // iteration).  MI355X-native differences, none of which changes a result
 // beyond floating-point reassociation:
-//   * one HIP stream per driver; MTTKRP launches (MFMA tiles, FP64 residual,
-//     FP64 dense view) are queued back to back with no host synchronisation
-//     inside an iteration; the host waits once per iteration for the fit;
+//   * one main HIP stream per driver plus two side streams (all at the
+//     default priority): within a mode the MFMA dense tiles and the
+//     pseudoinverse of FtF run on the side streams while the FP64 residual
+//     runs on the main one (both MTTKRP halves add into FtV atomically, the
+//     pseudoinverse only reads FtF), and the main stream joins them before
+//     the factor update.  No host synchronisation inside an iteration; the
+//     host waits once per iteration for the fit.  ALS_SERIAL=1 queues
+//     everything on the main stream;
 //   * Grams are cached per mode and refreshed right after that mode's update
 //     (the reference recomputes the same matrices from the same factors);
 //   * the solve is an on-device pseudoinverse (Cholesky inverse with an exact
@@ -43,6 +48,9 @@ struct Als3
     uint64_t dims[3] = {0, 0, 0};
     size_t nnz = 0;
     hipStream_t s = nullptr;
+    hipStream_t s_pinv = nullptr, s_dense = nullptr;  // side streams, joined per mode
+    hipEvent_t e_fork = nullptr, e_pinv = nullptr, e_dense = nullptr;
+    bool overlap = true;
     int num_cus = 0;
 
     std::vector<int32_t> perm[3];
@@ -66,6 +74,7 @@ struct Als3
     double* d_G = nullptr;  // 3 x R x R
     bool gram_ok[3] = {false, false, false};
     double* d_FtF = nullptr;
+    double* d_Ainv = nullptr;  // pinv(FtF) of the mode being updated
     double* d_FtV = nullptr;
     double* d_norms = nullptr;
     double* d_scal = nullptr;  // fit iprod/model2 (2) + residual (2)
@@ -80,7 +89,10 @@ struct Als3
     double* G(int m) const { return d_G + size_t(m) * R * R; }
 };
 
-int mttkrp_launch(Als3& h, int mode)
+// FtV = MTTKRP of `mode`; with_pinv also writes pinv(FtF) to d_Ainv (FtF
+// must already hold the mode's Hadamard product).  Everything is ordered
+// on the main stream when this returns.
+int mttkrp_launch(Als3& h, int mode, bool with_pinv)
 {
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
@@ -88,11 +100,26 @@ int mttkrp_launch(Als3& h, int mode)
     const double* A = h.F[0];
     const double* B = h.F[1];
     const double* C = h.F[2];
-    if (h.use_mfma && !h.skip_dense && h.part.ntiles > 0)
+    const bool dense = h.use_mfma && !h.skip_dense && h.part.ntiles > 0;
+    const bool fork = h.overlap && (dense || with_pinv);
+    if (fork) CPTC_HIP(hipEventRecord(h.e_fork, h.s));
+    if (with_pinv)
+    {
+        hipStream_t ps = h.overlap ? h.s_pinv : h.s;
+        if (h.overlap) CPTC_HIP(hipStreamWaitEvent(ps, h.e_fork, 0));
+        CPTC_TRY(cptc_pinv_sym(h.d_FtF, h.d_Ainv, R, nullptr, ps));
+        if (h.overlap) CPTC_HIP(hipEventRecord(h.e_pinv, ps));
+    }
+    if (dense)
+    {
+        hipStream_t ds = h.overlap ? h.s_dense : h.s;
+        if (h.overlap) CPTC_HIP(hipStreamWaitEvent(ds, h.e_fork, 0));
         CPTC_TRY(cptc_mttkrp_dense_tiles3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
                                           h.d_order[mode], h.d_goff[mode], h.ngroups[mode], A, B,
                                           C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
-                                          int(h.dims[2]), h.s));
+                                          int(h.dims[2]), ds));
+        if (h.overlap) CPTC_HIP(hipEventRecord(h.e_dense, ds));
+    }
     if (!h.skip_sparse)
     {
         const double* F1 = mode == 0 ? B : A;
@@ -109,6 +136,21 @@ int mttkrp_launch(Als3& h, int mode)
             if (timed) CPTC_HIP(hipEventRecord(h.kev[2 * mode + 1], h.s));
         }
     }
+    if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
+    if (h.overlap && dense) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
+    return CPTC_OK;
+}
+
+// The main stream, the two side streams and the driver's events.
+int init_streams(Als3& h)
+{
+    h.overlap = env_flag("ALS_SERIAL") == 0;
+    for (hipStream_t* p : {&h.s, &h.s_pinv, &h.s_dense})
+        CPTC_HIP(hipStreamCreateWithFlags(p, hipStreamNonBlocking));
+    for (auto& e : h.ev) CPTC_HIP(hipEventCreate(&e));
+    for (auto& e : h.kev) CPTC_HIP(hipEventCreate(&e));
+    for (hipEvent_t* p : {&h.e_fork, &h.e_pinv, &h.e_dense})
+        CPTC_HIP(hipEventCreateWithFlags(p, hipEventDisableTiming));
     return CPTC_OK;
 }
 
@@ -132,7 +174,8 @@ int residual_launch(Als3& h, bool with_lambda)
 void destroy(Als3* h)
 {
     if (!h) return;
-    if (h->s) (void)hipStreamSynchronize(h->s);
+    for (hipStream_t st : {h->s, h->s_pinv, h->s_dense})
+        if (st) (void)hipStreamSynchronize(st);
     free_partition(h->part);
     free_views(h->views);
     free_views(h->dviews);
@@ -142,13 +185,17 @@ void destroy(Als3* h)
         for (void* p : {(void*)h->d_order[m], (void*)h->d_goff[m]})
             if (p) (void)hipFree(p);
     for (void* p : {(void*)h->d_tile_f32, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
-                    (void*)h->d_FtF, (void*)h->d_FtV, (void*)h->d_norms, (void*)h->d_scal})
+                    (void*)h->d_FtF, (void*)h->d_Ainv, (void*)h->d_FtV, (void*)h->d_norms,
+                    (void*)h->d_scal})
         if (p) (void)hipFree(p);
     for (auto& e : h->ev)
         if (e) (void)hipEventDestroy(e);
     for (auto& e : h->kev)
         if (e) (void)hipEventDestroy(e);
-    if (h->s) (void)hipStreamDestroy(h->s);
+    for (hipEvent_t e : {h->e_fork, h->e_pinv, h->e_dense})
+        if (e) (void)hipEventDestroy(e);
+    for (hipStream_t st : {h->s, h->s_pinv, h->s_dense})
+        if (st) (void)hipStreamDestroy(st);
     delete h;
 }
 
@@ -210,9 +257,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
                      "cptc_als3_create: mode %d index %llu >= dim %llu", m,
                      (unsigned long long)mx, (unsigned long long)h->dims[m]);
     }
-    CPTC_HIP(hipStreamCreateWithFlags(&h->s, hipStreamNonBlocking));
-    for (auto& e : h->ev) CPTC_HIP(hipEventCreate(&e));
-    for (auto& e : h->kev) CPTC_HIP(hipEventCreate(&e));
+    CPTC_TRY(init_streams(*h));
     int dev = 0;
     CPTC_HIP(hipGetDevice(&dev));
     hipDeviceProp_t prop{};
@@ -340,6 +385,7 @@ int alloc_buffers(Als3& hr)
     CPTC_HIP(hipMalloc(&h->d_lambda, size_t(R) * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_G, 3 * RR * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_FtF, RR * sizeof(double)));
+    CPTC_HIP(hipMalloc(&h->d_Ainv, RR * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_FtV, maxdim * size_t(R) * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_norms, size_t(R) * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_scal, 4 * sizeof(double)));
@@ -361,9 +407,10 @@ int update_mode(Als3& h, int mode)
 {
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
-    // solve (pinv) and divide by lambda, column norms, normalise + absorb,
-    // then refresh this mode's Gram (als.cu:480-517)
-    CPTC_TRY(cptc_solve_pinv(h.d_FtF, h.d_FtV, h.F[mode], dim, R, h.d_lambda, h.s));
+    // F = FtV * pinv(FtF) (pinv computed beside the MTTKRP) and divide by
+    // lambda, column norms, normalise + absorb, then refresh this mode's
+    // Gram (als.cu:480-517)
+    CPTC_TRY(cptc_apply_pinv(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.d_lambda, h.s));
     CPTC_TRY(cptc_colnorms(h.F[mode], dim, R, h.d_norms, h.s));
     CPTC_TRY(cptc_normalize_absorb(h.F[mode], dim, R, h.d_norms, h.d_lambda, h.s));
     CPTC_TRY(cptc_gram(h.F[mode], dim, R, h.G(mode), h.s));
@@ -391,7 +438,7 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
                 }
             CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
             CPTC_HIP(hipEventRecord(h.ev[1 + 2 * mode], h.s));
-            CPTC_TRY(mttkrp_launch(h, mode));
+            CPTC_TRY(mttkrp_launch(h, mode, true));
             CPTC_HIP(hipEventRecord(h.ev[2 + 2 * mode], h.s));
             CPTC_TRY(update_mode(h, mode));
         }
@@ -464,10 +511,7 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
     auto step = [&](int r) {
         if (rc == CPTC_OK) rc = r;
     };
-    step(hipStreamCreateWithFlags(&h->s, hipStreamNonBlocking) == hipSuccess ? CPTC_OK
-                                                                              : CPTC_ERR_HIP);
-    for (auto& e : h->ev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
-    for (auto& e : h->kev) step(hipEventCreate(&e) == hipSuccess ? CPTC_OK : CPTC_ERR_HIP);
+    step(init_streams(*h));
     if (rc == CPTC_OK) step(build_groups(*h));
     if (rc == CPTC_OK) step(alloc_buffers(*h));
     std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
@@ -583,7 +627,7 @@ extern "C" int cptc_als3_mttkrp(void* handle, int mode, double* host_out)
     CPTC_REQUIRE(h && host_out && mode >= 0 && mode < 3, CPTC_ERR_ARG,
                  "cptc_als3_mttkrp: bad arguments");
     h->timing_kernels = false;
-    CPTC_TRY(cptc::mttkrp_launch(*h, mode));
+    CPTC_TRY(cptc::mttkrp_launch(*h, mode, false));
     CPTC_HIP(hipMemcpyAsync(host_out, h->d_FtV, h->dims[mode] * size_t(h->R) * sizeof(double),
                             hipMemcpyDeviceToHost, h->s));
     CPTC_HIP(hipStreamSynchronize(h->s));

@@ -684,6 +684,19 @@ extern "C" int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double*
     return CPTC_OK;
 }
 
+extern "C" int cptc_apply_pinv(const double* d_FtV, const double* d_Ainv, double* d_F,
+                               size_t dim, int R, const double* d_div, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 512 && d_FtV && d_Ainv && d_F, CPTC_ERR_ARG,
+                 "cptc_apply_pinv: bad arguments (R %d, supported 1..512)", R);
+    if (dim == 0) return CPTC_OK;
+    dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
+    hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, cptc::as_stream(stream), d_FtV, d_Ainv,
+                       d_F, dim, R, d_div);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
 namespace {
 int col_reduce(const double* F, const double* M, size_t rows, int R, hipStream_t s, double** part,
                int* P_out)

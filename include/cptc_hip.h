@@ -197,6 +197,14 @@ int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_
  * *d_path (device int, may be NULL) receives 0 = Cholesky, 1 = Jacobi. */
 int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path, void* stream);
 
+/* F = FtV * Ainv (row-major dim x R), then F[:, r] /= div[r] when d_div !=
+ * NULL: the second half of cptc_solve_pinv, for callers that compute
+ * pinv(FtF) with cptc_pinv_sym on another stream while FtV is still being
+ * accumulated.  Same split of the reference's solve + lambda divide
+ * (the factor gemm at solver.cu:985-997; als.cu:345-360). */
+int cptc_apply_pinv(const double* d_FtV, const double* d_Ainv, double* d_F, size_t dim, int R,
+                    const double* d_div, void* stream);
+
 /* norms[r] = ||F[:, r]||_2.  Replaces column_norms_kernel2 (als.cu:258-303). */
 int cptc_colnorms(const double* d_F, size_t rows, int R, double* d_norms, void* stream);
 
