@@ -165,6 +165,10 @@ SIGNATURES = {
     "cptc_gen_hash": (_U64, [_U64]),
     "cptc_mttkrp_seg_nd": (_I, [_I, _I, _P, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P, _P, _I,
                                 _P]),
+    "cptc_level_key_bytes": (_I, [_I, _P]),
+    "cptc_pack_level_keys": (_I, [_I, _P, _U64, _P, _P, _I, _P]),
+    "cptc_mttkrp_seg_nd_keys": (_I, [_I, _I, _P, _I, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P,
+                                     _P, _I, _P]),
     "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,

@@ -424,9 +424,15 @@ struct Gen
             CPTC_HIP(hipEventRecord(ke[2], s));
         }
         const cptc::DevViewN& v = views[n];
-        CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals, nullptr, v.nnz,
-                                    v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV,
-                                    R, s));
+        if (v.key_bytes > 0 && R % 2 == 0)
+            CPTC_TRY(cptc_mttkrp_seg_nd_keys(N, n, v.d_key, v.key_bytes, v.level_modes.data(),
+                                             v.level_bits.data(), v.d_vals, v.nnz, v.d_row,
+                                             v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV,
+                                             R, s));
+        else
+            CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals, nullptr,
+                                        v.nnz, v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg,
+                                        F(), d_FtV, R, s));
         if (timing) CPTC_HIP(hipEventRecord(ke[3], s));
         return CPTC_OK;
     }

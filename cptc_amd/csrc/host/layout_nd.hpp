@@ -38,6 +38,11 @@ struct DevViewN
     uint32_t* d_start = nullptr;
     uint32_t* d_cnt = nullptr;
     uint8_t* d_single = nullptr;
+    // kernel views: the level coordinates packed into one key per element
+    // (level 0 in the top bits); key_bytes 0 when they need more than 64 bits
+    void* d_key = nullptr;
+    int key_bytes = 0;
+    std::vector<int> level_bits;
 };
 
 void free_units(DevUnitsN& u);

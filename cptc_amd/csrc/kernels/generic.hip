@@ -323,10 +323,12 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
     }
 }
 
-// Ridge Cholesky + per-row substitution.  Every block (one wave) factors
-// FtF + eps I in LDS column by column (left-looking: column j needs the
-// columns < j; each entry runs the reference's k-ascending update), then each
-// lane solves rows, keeping its y / x vector in an LDS column of its own.
+// Ridge Cholesky + per-row substitution.  Every block (one wave) stages FtF
+// in LDS with one coalesced pass and factors FtF + eps I there in place,
+// column by column (left-looking: column j needs the columns < j; each entry
+// runs the reference's k-ascending update; the strict upper triangle keeps
+// FtF and is never read again), then each lane solves rows, keeping its
+// y / x vector in an LDS column of its own.
 constexpr int CHOL_RM = 32;
 constexpr int CHOL_T = 64;
 
@@ -339,10 +341,12 @@ __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __rest
     __shared__ double Y[CHOL_RM][CHOL_T];
     __shared__ double eps_s;
     const int tid = threadIdx.x;
+    for (int x = tid; x < R * R; x += CHOL_T) L[x / R][x % R] = FtF[x];
+    __syncthreads();
     if (tid == 0)
     {
         double tr = 0.0;
-        for (int i = 0; i < R; ++i) tr += FtF[i * R + i];
+        for (int i = 0; i < R; ++i) tr += L[i][i];
         eps_s = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
     }
     __syncthreads();
@@ -351,7 +355,7 @@ __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __rest
     {
         if (tid == 0)
         {
-            double s = FtF[j * R + j] + eps;
+            double s = L[j][j] + eps;
             for (int k = 0; k < j; ++k) s -= L[j][k] * L[j][k];
             L[j][j] = (s > 0.0) ? sqrt(s) : sqrt(eps);
         }
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __rest
         const int i = j + 1 + tid;
         if (i < R)
         {
-            double s = FtF[i * R + j];
+            double s = L[i][j];
             for (int k = 0; k < j; ++k) s -= L[i][k] * L[j][k];
             L[i][j] = s / L[j][j];
         }

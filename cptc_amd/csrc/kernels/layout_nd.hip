@@ -242,6 +242,10 @@ void free_view(DevViewN& v)
     dfree(v.d_start);
     dfree(v.d_cnt);
     dfree(v.d_single);
+    if (v.d_key) (void)hipFree(v.d_key);
+    v.d_key = nullptr;
+    v.key_bytes = 0;
+    v.level_bits.clear();
     v.nnz = v.nseg = 0;
     v.level_modes.clear();
 }
@@ -486,6 +490,19 @@ int work_view_nd_device(int N, const uint64_t* dims, int n, const uint32_t* d_co
     hipLaunchKernelGGL(work_gather_kernel, dim3(gm), dim3(256), 0, s, perm.p, d_coords, d_vals,
                        nnz, M, nlev, lv, out.d_sc, out.d_vals);
     CPTC_LAUNCHED();
+    // packed level keys for the MTTKRP kernel (when the widths fit 64 bits)
+    for (int q = 0; q < nlev; ++q)
+    {
+        const uint64_t d = dims[out.level_modes[q]];
+        out.level_bits.push_back(std::max(1, bit_width(d > 0 ? d - 1 : 0)));
+    }
+    out.key_bytes = cptc_level_key_bytes(nlev, out.level_bits.data());
+    if (out.key_bytes > 0)
+    {
+        CPTC_HIP(hipMalloc(&out.d_key, size_t(M) * size_t(out.key_bytes)));
+        CPTC_TRY(cptc_pack_level_keys(nlev, out.d_sc, M, out.level_bits.data(), out.d_key,
+                                      out.key_bytes, s));
+    }
     CPTC_TRY(build_segments(key2.p, M, force_accumulate, out, s));
     CPTC_HIP(hipStreamSynchronize(s));
     return CPTC_OK;

@@ -355,6 +355,28 @@ int cptc_mttkrp_seg_nd(int nmodes, int mode, const uint32_t* d_scoords, const in
                        const uint32_t* d_seg_cnt, const uint8_t* d_single, uint64_t nseg,
                        const double* const* h_F, double* d_FtV, int R, void* stream);
 
+/* Packed level keys for the segment MTTKRP (no reference counterpart: the
+ * reference's kernel reads the SoA d_scoords, generic.cu:271-343).
+ * level_bits[q] (1..32) is the width of level q's field; level 0 takes the
+ * top bits: key = sum_q c_q << (bits of levels q+1 .. nlev-1).
+ * cptc_level_key_bytes returns 4 (sum <= 32), 8 (sum <= 64) or 0 (no key).
+ * cptc_pack_level_keys writes d_keys[e] from d_scoords (nlev x nnz uint32,
+ * row q = level q). */
+int cptc_level_key_bytes(int nlev, const int* level_bits);
+int cptc_pack_level_keys(int nlev, const uint32_t* d_scoords, uint64_t nnz, const int* level_bits,
+                         void* d_keys, int key_bytes, void* stream);
+
+/* cptc_mttkrp_seg_nd over packed level keys (same result and the same
+ * single-store / atomic rule; no skip flags).  level_modes[q] (host array)
+ * is the mode of level q, level_bits its field width as packed; R even in
+ * 2..32; factors 16-byte aligned.  The keys kernel streams one key and one
+ * value per element and evaluates runs of equal level prefixes once. */
+int cptc_mttkrp_seg_nd_keys(int nmodes, int mode, const void* d_keys, int key_bytes,
+                            const int* level_modes, const int* level_bits, const double* d_vals,
+                            uint64_t nnz, const uint32_t* d_seg_row, const uint32_t* d_seg_start,
+                            const uint32_t* d_seg_cnt, const uint8_t* d_single, uint64_t nseg,
+                            const double* const* h_F, double* d_FtV, int R, void* stream);
+
 /* Dense units (GDUnit, generic.cu:422-427): d_unit6 = nunits x {bi, bj, bk,
  * nnz, start, outer_off}; pool lid = la * 256 + lb * 16 + lc (slot order).
  * Packs each unit's pool into a 16^3 FP32 tile (nunits x 4096 floats):

@@ -58,6 +58,14 @@ def test_version_and_no_device_here(ca):
     lambda l: l.cptc_dense_tiles_pack3(0, 0, 0, 4, 0, None),
     lambda l: l.cptc_als3_run(None, 1, None, None, None),
     lambda l: l.cptc_als3_info_get(None, None),
+    # odd R, 4-byte keys for 40 bits, a level wider than 32 bits
+    lambda l: l.cptc_mttkrp_seg_nd_keys(3, 0, 1, 4, (C.c_int * 2)(1, 2), (C.c_int * 2)(4, 4), 1,
+                                        10, 1, 1, 1, None, 1, (C.c_void_p * 3)(16, 16, 16), 1,
+                                        7, None),
+    lambda l: l.cptc_mttkrp_seg_nd_keys(3, 0, 1, 4, (C.c_int * 2)(1, 2), (C.c_int * 2)(20, 20),
+                                        1, 10, 1, 1, 1, None, 1, (C.c_void_p * 3)(16, 16, 16), 1,
+                                        8, None),
+    lambda l: l.cptc_pack_level_keys(2, 1, 10, (C.c_int * 2)(33, 1), 1, 8, None),
 ])
 def test_bad_arguments_rejected(ca, call):
     assert call(ca.lib) == -1
@@ -118,3 +126,12 @@ def test_dense_groups(ca, hdr_words, slot, G):
         a = off[g]
         if hdr[order[a], slot] == hdr[order[a - 1], slot]:
             assert off[g] - off[g - 1] == G
+
+
+@pytest.mark.parametrize("bits,nbytes", [((6, 6, 6, 4), 4), ((16, 16), 4), ((17, 16), 8),
+                                         ((1,), 4), ((32, 32), 8), ((32, 32, 1), 0),
+                                         ((0, 5), 0), ((33,), 0)])
+def test_level_key_bytes(ca, bits, nbytes):
+    """Packed level keys: 4 bytes up to 32 bits, 8 up to 64, none beyond or
+    for a field outside 1..32 bits."""
+    assert ca.lib.cptc_level_key_bytes(len(bits), (C.c_int * len(bits))(*bits)) == nbytes

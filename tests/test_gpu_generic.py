@@ -161,6 +161,75 @@ def test_seg_kernel_single_store(ca, orc, dev):
     assert rel_err(out.numpy(), ref) <= 1e-12
 
 
+def seg_table(rows, limit=1024):
+    """Row segments of a row-sorted view (<= limit elements; single when the
+    row has one segment), as the view builders make them."""
+    urow, start, cnt = np.unique(rows, return_index=True, return_counts=True)
+    seg = [(r, s + o, min(limit, c - o), c <= limit)
+           for r, s, c in zip(urow, start, cnt) for o in range(0, c, limit)]
+    return [np.array([x[k] for x in seg], dt) for k, dt in
+            ((0, np.uint32), (1, np.uint32), (2, np.uint32), (3, np.uint8))]
+
+
+@pytest.mark.parametrize("N,R,dims,order", [
+    (2, 8, (300, 5000), "runs"), (3, 32, (70, 9, 300), "runs"), (3, 16, (70, 9, 300), "shuffled"),
+    (4, 2, (40, 3, 300, 2), "runs"), (4, 16, (183, 24, 1140, 1717), "runs"),
+    (5, 32, (64, 64, 64, 32, 16), "runs"), (5, 32, (64, 64, 64, 32, 16), "shuffled"),
+    (5, 30, (5000, 70000, 9, 300, 40), "runs"), (6, 8, (70, 9, 300, 40, 25, 6), "runs"),
+    (8, 16, (70, 9, 30, 40, 25, 6, 11, 13), "runs")])
+def test_seg_keys_kernel_vs_closed_form(ca, dev, N, R, dims, order):
+    """The packed-key segment kernel against sum_e v_e prod F (numpy), on
+    views sorted by row then levels (runs) and with rows in random element
+    order; 4- and 8-byte keys; levels by dimension, not mode order."""
+    rng = np.random.default_rng(N * 1000 + R)
+    nnz = 60000
+    # skewed coordinates so that rows exceed one segment and runs repeat
+    idx = np.stack([np.minimum((rng.pareto(1.2, nnz) * d / 8).astype(np.int64), d - 1)
+                    for d in dims]).astype(np.uint32)
+    idx[:, -3000:] = idx[:, :3000]               # duplicates
+    val = rng.standard_normal(nnz)
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [dbuf(ca, f) for f in F]
+    kinds = set()
+    for n in range(N):
+        lev = sorted([m for m in range(N) if m != n], key=lambda m: dims[m])
+        bits = [max(1, int(dims[m] - 1).bit_length()) for m in lev]
+        kb = ca.lib.cptc_level_key_bytes(len(lev), (C.c_int * len(lev))(*bits))
+        assert kb == (4 if sum(bits) <= 32 else 8)
+        if order == "runs":
+            perm = np.lexsort(tuple(idx[m] for m in reversed(lev)) + (idx[n],))
+        else:
+            perm = np.argsort(idx[n], kind="stable")
+        rows = idx[n][perm]
+        sc = np.ascontiguousarray(np.stack([idx[m][perm] for m in lev]))
+        srow, sst, scnt, ssingle = seg_table(rows)
+        b = {k: dbuf(ca, a) for k, a in (("sc", sc), ("val", val[perm]), ("row", srow),
+                                         ("st", sst), ("cnt", scnt), ("single", ssingle))}
+        keys = ca.DevBuf.zeros(nnz * kb // 8 + 1)
+        lb = (C.c_int * len(lev))(*bits)
+        assert ca.lib.cptc_pack_level_keys(len(lev), b["sc"].data_ptr(), nnz, lb,
+                                           keys.data_ptr(), kb, None) == 0
+        init = rng.standard_normal((dims[n], R))
+        out = dbuf(ca, init.copy())
+        rc = ca.lib.cptc_mttkrp_seg_nd_keys(
+            N, n, keys.data_ptr(), kb, (C.c_int * len(lev))(*lev), lb, b["val"].data_ptr(), nnz,
+            b["row"].data_ptr(), b["st"].data_ptr(), b["cnt"].data_ptr(), b["single"].data_ptr(),
+            len(srow), fptrs(dF), out.data_ptr(), R, None)
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        contrib = val[:, None] * np.prod([F[m][idx[m]] for m in range(N) if m != n], axis=0)
+        M = np.zeros((dims[n], R))
+        np.add.at(M, idx[n], contrib)
+        exp = init.copy()
+        for r, single in zip(srow, ssingle):
+            exp[r] = M[r] if single else init[r]
+        multi = np.unique(srow[ssingle == 0])
+        exp[multi] += M[multi]
+        kinds |= set(ssingle.tolist())
+        assert rel_err(out.numpy().reshape(dims[n], R), exp) <= 1e-10, (n, order)
+    assert kinds == {0, 1}, "both store and atomic rows exercised"
+
+
 @pytest.mark.parametrize("N,R,inner,G", [(4, 8, (0, 1, 2), 0), (4, 16, (0, 1, 2), 4),
                                          (5, 32, (0, 1, 2), 16), (4, 20, (1, 2, 3), 0),
                                          (4, 8, (0, 2, 3), 2), (5, 16, (1, 3, 4), 16),
