@@ -661,24 +661,6 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
     const int N = g->N;
     const bool verbose = opts->verbose != 0;
 
-    // reorder (host)
-    auto t0 = Clock::now();
-    HostCoo h = host_copy(coo);
-    std::string how = opts->reorder[0] ? std::string(opts->reorder, strnlen(opts->reorder, 8))
-                                       : (N >= 4 ? "hits" : "cadr");
-    g->method = reorder(h, how, opts->reorder_rounds, opts->reorder_sample, g->rank, verbose);
-    g->prep_ms[0] = ms_since(t0);
-    if (verbose)
-    {
-        std::printf("[GEN] reorder=%s", g->method.c_str());
-        if (g->method == "hits") std::printf("(T=%d)", std::max(opts->reorder_rounds, 1));
-        std::printf(" prep=%g ms\n", g->prep_ms[0]);
-        std::printf("[GEN] N-order CP-ALS: order=%d R=%d nnz=%llu\n[GEN] dims = ", N, R,
-                    (unsigned long long)g->nnz);
-        for (int m = 0; m < N; ++m)
-            std::printf("%s%llu", m ? " x " : "", (unsigned long long)g->dims[m]);
-        std::printf("\n");
-    }
     for (uint64_t e = 0; e < g->nnz; ++e) g->x2 += coo->val[e] * coo->val[e];
 
     int rc;
@@ -703,11 +685,33 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
     GEN_HIP(hipStreamCreateWithFlags(&g->s, hipStreamNonBlocking));
     hipStream_t s = g->s;
     const size_t RR = size_t(R) * R;
-    GEN_TRY(dmalloc(&g->d_coords, h.idx.size()));
+    const uint64_t ncoords = uint64_t(N) * g->nnz;
+    GEN_TRY(dmalloc(&g->d_coords, ncoords));
     GEN_TRY(dmalloc(&g->d_vals, g->nnz));
-    GEN_HIP(hipMemcpyAsync(g->d_coords, h.idx.data(), h.idx.size() * sizeof(uint32_t),
+    GEN_HIP(hipMemcpyAsync(g->d_coords, coo->idx, ncoords * sizeof(uint32_t),
                            hipMemcpyHostToDevice, s));
     GEN_HIP(hipMemcpyAsync(g->d_vals, coo->val, g->nnz * sizeof(double), hipMemcpyHostToDevice, s));
+
+    // reorder on the device (relabels d_coords; ranks come back for the factors)
+    auto t0 = Clock::now();
+    std::string how = opts->reorder[0] ? std::string(opts->reorder, strnlen(opts->reorder, 8))
+                                       : (N >= 4 ? "hits" : "cadr");
+    GEN_TRY(cptc::reorder_nd_device(N, g->dims.data(), g->d_coords, g->nnz, how,
+                                    opts->reorder_rounds, opts->reorder_sample, g->rank,
+                                    g->method, verbose, s));
+    GEN_HIP(hipStreamSynchronize(s));
+    g->prep_ms[0] = ms_since(t0);
+    if (verbose)
+    {
+        std::printf("[GEN] reorder=%s", g->method.c_str());
+        if (g->method == "hits") std::printf("(T=%d)", std::max(opts->reorder_rounds, 1));
+        std::printf(" prep=%g ms (device)\n", g->prep_ms[0]);
+        std::printf("[GEN] N-order CP-ALS: order=%d R=%d nnz=%llu\n[GEN] dims = ", N, R,
+                    (unsigned long long)g->nnz);
+        for (int m = 0; m < N; ++m)
+            std::printf("%s%llu", m ? " x " : "", (unsigned long long)g->dims[m]);
+        std::printf("\n");
+    }
 
     std::vector<std::vector<double>> F0;
     init_factors(g->dims, R, opts->seed, g->rank, F0);
@@ -779,7 +783,8 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
                                           in ? g->units.d_is_dense : nullptr, in, g->nnz,
                                           g->views[n], s));
         std::vector<uint64_t> deg(g->dims[n], 0);
-        const uint32_t* cn = h.c(n);
+        // the degree multiset does not change under relabelling
+        const uint32_t* cn = coo->idx + uint64_t(n) * g->nnz;
         for (uint64_t e = 0; e < g->nnz; ++e) ++deg[cn[e]];
         for (uint64_t d : deg) g->ref_nseg[n] += (d + CPTC_SEG - 1) / CPTC_SEG;
         if (verbose)

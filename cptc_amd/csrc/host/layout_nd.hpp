@@ -8,6 +8,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <string>
 #include <vector>
 
 namespace cptc {
@@ -44,6 +45,16 @@ struct DevViewN
     int key_bytes = 0;
     std::vector<int> level_bits;
 };
+
+// The reference's generic reordering (hits / cadr / auto / none,
+// generic.cu:1176-1376) on the device: relabels d_coords (N x nnz,
+// mode-major) in place and returns the per-mode ranks on the host (empty
+// when nothing was applied) and the method applied in `used`.  Bit-exact
+// with the reference's host code.
+int reorder_nd_device(int N, const uint64_t* dims, uint32_t* d_coords, uint64_t nnz,
+                      std::string how, int rounds, uint64_t budget,
+                      std::vector<std::vector<uint32_t>>& rank, std::string& used, bool verbose,
+                      hipStream_t s);
 
 void free_units(DevUnitsN& u);
 void free_view(DevViewN& v);

@@ -101,6 +101,65 @@ def test_layout_no_dense_for_order3_and_threshold0(ca, orc, dev):
     assert g4.info.dense_enabled == 0
 
 
+def zipf_tensor(ca, rng, dims, nnz, zipf):
+    cols = []
+    for m, d in enumerate(dims):
+        if zipf[m]:
+            p = 1.0 / np.arange(1, d + 1) ** zipf[m]
+            cols.append(rng.choice(d, nnz, p=p / p.sum()))
+        else:
+            cols.append(rng.integers(0, d, nnz))
+    return ca.Tensor(tuple(dims), np.ascontiguousarray(np.stack(cols).astype(np.uint32)),
+                     rng.random(nnz) + 0.5)
+
+
+@pytest.mark.parametrize("how,rounds,budget", [("hits", 3, 8000000), ("hits", 1, 8000000),
+                                               ("hits", 3, 777), ("cadr", 3, 8000000),
+                                               ("none", 3, 8000000), ("bogus", 3, 8000000),
+                                               (None, 3, 8000000)])
+def test_device_reorder_matches_oracle(ca, orc, dev, how, rounds, budget):
+    """The driver's device reordering (sampled HITS, CADR, none, unknown ->
+    cadr, default by order) against the oracle, bit for bit."""
+    rng = np.random.default_rng(11)
+    t = zipf_tensor(ca, rng, (60, 20, 300, 45), 20000, (1.1, 0, 1.2, 1.0))
+    g = ca.Gen(t, R=4, reorder=how, rounds=rounds, sample=budget, dense=False)
+    ohow = {"bogus": "cadr", None: "hits"}.get(how, how)
+    ref_idx, ref_rank = orc.reorder_nd(t.idx, t.val, t.dims, ohow, rounds, budget)
+    assert g.info.reorder.decode() == ohow
+    assert np.array_equal(g.coords(), ref_idx)
+    for m in range(4):
+        exp = ref_rank[m] if len(ref_rank) else np.arange(t.dims[m])
+        assert np.array_equal(g.rank(m), exp), m
+
+
+def test_device_reorder_auto_both_branches(ca, orc, dev):
+    rng = np.random.default_rng(5)
+    dense = zipf_tensor(ca, rng, (32, 32, 32, 2), 30000, (0, 0, 0, 0))
+    sparse = zipf_tensor(ca, rng, (5000, 5000, 5000, 2), 3000, (0, 0, 0, 0))
+    outcomes = set()
+    for t in (dense, sparse):
+        g = ca.Gen(t, R=4, reorder="auto", dense=False)
+        ref_idx, ref_rank = orc.reorder_nd(t.idx, t.val, t.dims, "auto", 3, 8000000)
+        assert np.array_equal(g.coords(), ref_idx)
+        applied = g.info.reorder.decode() == "hits"
+        assert applied == (len(ref_rank) > 0)
+        if applied:
+            assert all(np.array_equal(g.rank(m), ref_rank[m]) for m in range(4))
+        outcomes.add(applied)
+    assert outcomes == {True, False}
+
+
+def test_device_reorder_config5_sampled(ca, orc, dev):
+    """Config 5 (20 M elements): HITS over every second element (stride 2),
+    rows of up to ~1.3 M terms summed in element order."""
+    t = ca.synth_config(5)
+    g = ca.Gen(t, R=2, dense=False)
+    ref_idx, ref_rank = orc.reorder_nd(t.idx, t.val, t.dims, "hits", 3, 8000000)
+    for m in range(5):
+        assert np.array_equal(g.rank(m), ref_rank[m]), m
+    assert np.array_equal(g.coords(), ref_idx)
+
+
 # ------------------------------------------------------------ kernel parity --
 
 @pytest.mark.parametrize("N,R", [(2, 5), (3, 16), (4, 1), (4, 3), (4, 8), (4, 16), (5, 31),
@@ -465,6 +524,8 @@ def test_config4_full_size(ca, orc, dev):
     g = ca.Gen(t, R=R)
     ridx, rrank = orc.reorder_nd(t.idx, t.val, t.dims, "hits", 3, 8000000)
     assert np.array_equal(g.coords(), ridx)
+    for m in range(4):
+        assert np.array_equal(g.rank(m), rrank[m]), m
     u = orc.dense_nd(ridx, t.val, t.dims, 0.03)
     assert int(g.info.n_units) == len(u["unit6"])
     got = g.units()
