@@ -8,8 +8,9 @@
 // The reference adds each row's terms one after another in element order, so
 // the sums here keep that order: a stable sort of the sample by c_m gives
 // each row its elements in element order, the products are formed in
-// parallel (the same multiplication order), and one wave per row adds them
-// in sequence (lane 0, fed through LDS by the whole wave).  Ranks sort by
+// parallel (the same multiplication order), and one wave per (mode, row)
+// adds them in sequence (lane 0, fed through LDS by the whole wave).  Ranks
+// sort by
 // score descending, ties by index ascending: a stable descending radix sort
 // of the scores over indices in ascending order.
 // CADR (generic.cu:1342-1357): degree descending, index ascending (same
@@ -47,13 +48,6 @@ struct ModeCoords
     const uint32_t* c[MAXM];
 };
 
-__device__ __forceinline__ void wave_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 __device__ inline uint64_t splitbit_hash(uint64_t x)
 {
     x += 0x9E3779B97F4A7C15ull;
@@ -76,12 +70,51 @@ __global__ void fill_kernel(double* __restrict__ a, uint64_t n, double v)
         a[i] = v;
 }
 
-__global__ void degree_kernel(const uint32_t* __restrict__ c, uint64_t nnz, uint64_t stride,
-                              uint64_t S, uint32_t* __restrict__ deg)
+// deg[x] += #{e : c[e] = x}: per-block LDS counts (dim <= DEG_LDS_MAX), then
+// one global add per bin and block; larger dims count in global memory,
+// where the many bins keep contention low.
+constexpr uint64_t DEG_LDS_MAX = 16384;
+
+__global__ void degree_lds_kernel(const uint32_t* __restrict__ c, uint64_t nnz, uint32_t dim,
+                                  uint32_t* __restrict__ deg)
+{
+    extern __shared__ uint32_t h[];
+    for (uint32_t x = threadIdx.x; x < dim; x += blockDim.x) h[x] = 0;
+    __syncthreads();
+    const uint64_t step = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < nnz; e += step)
+        atomicAdd(&h[c[e]], 1u);
+    __syncthreads();
+    for (uint32_t x = threadIdx.x; x < dim; x += blockDim.x)
+        if (h[x]) atomicAdd(&deg[x], h[x]);
+}
+
+__global__ void degree_global_kernel(const uint32_t* __restrict__ c, uint64_t nnz,
+                                     uint32_t* __restrict__ deg)
 {
     const uint64_t step = uint64_t(gridDim.x) * blockDim.x;
-    for (uint64_t k = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; k < S; k += step)
-        atomicAdd(&deg[c[k * stride]], 1u);
+    for (uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < nnz; e += step)
+        atomicAdd(&deg[c[e]], 1u);
+}
+
+// off[x] = first position of a key >= x in the sorted keys (x = 0..dim)
+__global__ void row_offsets_kernel(const uint32_t* __restrict__ skey, uint64_t S, uint64_t dim,
+                                   uint64_t* __restrict__ off)
+{
+    const uint64_t step = uint64_t(gridDim.x) * blockDim.x;
+    for (uint64_t x = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; x <= dim; x += step)
+    {
+        uint64_t lo = 0, hi = S;
+        while (lo < hi)
+        {
+            const uint64_t mid = (lo + hi) / 2;
+            if (uint64_t(skey[mid]) < x)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        off[x] = lo;
+    }
 }
 
 __global__ void scatter_rank_kernel(const uint32_t* __restrict__ ord, uint64_t n,
@@ -133,21 +166,41 @@ __global__ void hits_products_kernel(Scores sc, int N, int m, const uint32_t* __
     }
 }
 
-// out[x] = ((0 + p[off[x]]) + p[off[x] + 1]) + ... : one wave per row, the
-// terms summed one after another by lane 0 from LDS windows of 256 that the
-// whole wave loads (the next one while lane 0 adds).
+// ns_m[x] = ((0 + p_m[off_m[x]]) + p_m[off_m[x] + 1]) + ... for every mode:
+// one wave per (mode, row).  The wave stages windows of SUM_WIN terms in LDS
+// (coalesced loads, the next window prefetched into registers) and lane 0
+// adds them in order; a full window is unrolled so its LDS reads run ahead
+// of the add chain.
 constexpr int SUM_WIN = 256;
 
-__global__ __launch_bounds__(64) void row_sequential_sum_kernel(const double* __restrict__ p,
-                                                                const uint64_t* __restrict__ off,
-                                                                uint64_t dim,
-                                                                double* __restrict__ out)
+struct RowSums
+{
+    const double* p[MAXM];
+    const uint64_t* off[MAXM];
+    double* ns[MAXM];
+    uint64_t first[MAXM + 1];   // first task of each mode: sum of the dims before it
+    int N;
+};
+
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(64) void row_sequential_sum_kernel(RowSums rs)
 {
     __shared__ double buf[SUM_WIN];
     const int lane = threadIdx.x;
-    for (uint64_t x = blockIdx.x; x < dim; x += gridDim.x)
+    const uint64_t ntask = rs.first[rs.N];
+    for (uint64_t t = blockIdx.x; t < ntask; t += gridDim.x)
     {
-        const uint64_t b = off[x], e = off[x + 1];
+        int m = 0;
+        while (m + 1 < rs.N && t >= rs.first[m + 1]) ++m;
+        const uint64_t x = t - rs.first[m];
+        const double* __restrict__ p = rs.p[m];
+        const uint64_t b = rs.off[m][x], e = rs.off[m][x + 1];
         double acc = 0.0;
         double nxt[SUM_WIN / 64];
         auto load = [&](uint64_t c0) {
@@ -168,12 +221,19 @@ __global__ __launch_bounds__(64) void row_sequential_sum_kernel(const double* __
             if (c0 + SUM_WIN < e) load(c0 + SUM_WIN);
             if (lane == 0)
             {
-                const int cnt = int(std::min<uint64_t>(SUM_WIN, e - c0));
-#pragma unroll 8
-                for (int i = 0; i < cnt; ++i) acc += buf[i];
+                if (e - c0 >= uint64_t(SUM_WIN))
+                {
+#pragma unroll
+                    for (int i = 0; i < SUM_WIN; ++i) acc += buf[i];
+                }
+                else
+                {
+                    const int cnt = int(e - c0);
+                    for (int i = 0; i < cnt; ++i) acc += buf[i];
+                }
             }
         }
-        if (lane == 0) out[x] = acc;
+        if (lane == 0) rs.ns[m][x] = acc;
         wave_sync();
     }
 }
@@ -296,8 +356,26 @@ int cadr_device(int N, const uint64_t* dims, const uint32_t* d_coords, uint64_t 
         Tmp<uint32_t> deg;
         CPTC_TRY(deg.alloc(dims[m]));
         CPTC_HIP(hipMemsetAsync(deg.p, 0, dims[m] * sizeof(uint32_t), s));
-        hipLaunchKernelGGL(degree_kernel, dim3(grid1(nnz)), dim3(256), 0, s,
-                           d_coords + uint64_t(m) * nnz, nnz, uint64_t(1), nnz, deg.p);
+        const uint32_t* c = d_coords + uint64_t(m) * nnz;
+        if (dims[m] <= DEG_LDS_MAX)
+        {
+            static bool attr = false;
+            if (!attr)
+            {
+                CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(degree_lds_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(DEG_LDS_MAX * sizeof(uint32_t))));
+                attr = true;
+            }
+            // one block per CU: each flushes at most dims[m] counts
+            hipLaunchKernelGGL(degree_lds_kernel, dim3(std::min(grid1(nnz), 256u)), dim3(256),
+                               dims[m] * sizeof(uint32_t), s, c, nnz, uint32_t(dims[m]), deg.p);
+        }
+        else
+        {
+            hipLaunchKernelGGL(degree_global_kernel, dim3(grid1(nnz)), dim3(256), 0, s, c, nnz,
+                               deg.p);
+        }
         CPTC_LAUNCHED();
         CPTC_TRY(dalloc(&rk.r[m], dims[m]));
         CPTC_TRY(rank_desc(deg.p, dims[m], 32, rk.r[m], s));
@@ -316,7 +394,7 @@ int hits_device(int N, const uint64_t* dims, const uint32_t* d_coords, uint64_t 
     std::vector<Tmp<uint64_t>> off(N);
     std::vector<Tmp<uint32_t>> co(N);
     {
-        Tmp<uint32_t> key, val, skey, el, cnt;
+        Tmp<uint32_t> key, val, skey, el;
         CPTC_TRY(key.alloc(S));
         CPTC_TRY(val.alloc(S));
         CPTC_TRY(skey.alloc(S));
@@ -328,23 +406,26 @@ int hits_device(int N, const uint64_t* dims, const uint32_t* d_coords, uint64_t 
             CPTC_LAUNCHED();
             CPTC_TRY(sort_pairs(key.p, skey.p, val.p, el.p, S,
                                 bit_width(dims[m] > 0 ? dims[m] - 1 : 0), s));
-            CPTC_TRY(cnt.alloc(dims[m] + 1));
-            CPTC_HIP(hipMemsetAsync(cnt.p, 0, (dims[m] + 1) * sizeof(uint32_t), s));
-            hipLaunchKernelGGL(degree_kernel, dim3(grid1(S)), dim3(256), 0, s, mc.c[m], nnz,
-                               stride, S, cnt.p);
-            CPTC_LAUNCHED();
             CPTC_TRY(off[m].alloc(dims[m] + 1));
-            CPTC_TRY(exclusive_sum(cnt.p, off[m].p, dims[m] + 1, s));
+            hipLaunchKernelGGL(row_offsets_kernel, dim3(grid1(dims[m] + 1)), dim3(256), 0, s,
+                               skey.p, S, dims[m], off[m].p);
+            CPTC_LAUNCHED();
             CPTC_TRY(co[m].alloc(uint64_t(N - 1) * S));
             hipLaunchKernelGGL(gather_others_kernel, dim3(grid1(S)), dim3(256), 0, s, mc, N, m,
                                el.p, stride, S, co[m].p);
             CPTC_LAUNCHED();
         }
     }
-    std::vector<Tmp<double>> sc(N), ns(N);
-    Tmp<double> p, mx;
-    CPTC_TRY(p.alloc(S));
+    std::vector<Tmp<double>> sc(N), ns(N), p(N);
+    Tmp<double> mx;
     CPTC_TRY(mx.alloc(N));
+    RowSums rs{};
+    rs.N = N;
+    for (int m = 0; m < N; ++m)
+    {
+        CPTC_TRY(p[m].alloc(S));
+        rs.first[m + 1] = rs.first[m] + dims[m];
+    }
     for (int m = 0; m < N; ++m)
     {
         CPTC_TRY(sc[m].alloc(dims[m]));
@@ -360,13 +441,15 @@ int hits_device(int N, const uint64_t* dims, const uint32_t* d_coords, uint64_t 
         for (int m = 0; m < N; ++m)
         {
             hipLaunchKernelGGL(hits_products_kernel, dim3(grid1(S)), dim3(256), 0, s, cur, N, m,
-                               co[m].p, S, p.p);
+                               co[m].p, S, p[m].p);
             CPTC_LAUNCHED();
-            const unsigned rows = unsigned(std::min<uint64_t>(dims[m], 65536));
-            hipLaunchKernelGGL(row_sequential_sum_kernel, dim3(rows), dim3(64), 0, s, p.p,
-                               off[m].p, dims[m], ns[m].p);
-            CPTC_LAUNCHED();
+            rs.p[m] = p[m].p;
+            rs.off[m] = off[m].p;
+            rs.ns[m] = ns[m].p;
         }
+        const unsigned tasks = unsigned(std::min<uint64_t>(rs.first[N], 1u << 20));
+        hipLaunchKernelGGL(row_sequential_sum_kernel, dim3(tasks), dim3(64), 0, s, rs);
+        CPTC_LAUNCHED();
         for (int m = 0; m < N; ++m)
         {
             hipLaunchKernelGGL(max_kernel, dim3(1), dim3(1024), 0, s, ns[m].p, dims[m], mx.p + m);
