@@ -1,22 +1,26 @@
-// Dense 16^3 tiles on CDNA4 FP32 MFMA with an FP64 epilogue — the gfx950
-// counterpart of dense_tile_mttkrp_wmma (dense.cu:89-1077) for order-3 tiles
-// and of g_dense_tile_mttkrp_kernel (generic.cu:429-561) for the generic
-// path's dense units, whose contribution is also scaled by the unit's FP64
-// outer-mode weights.  gfx950 has no xf32, so the inner products run in FP32,
-// which is more accurate than the reference's TF32.
+// Dense 16^3 tiles on CDNA4 FP32 MFMA with FP64 output accumulation — the
+// gfx950 counterpart of dense_tile_mttkrp_wmma (dense.cu:89-1077) for
+// order-3 tiles and of g_dense_tile_mttkrp_kernel (generic.cu:429-561) for
+// the generic path's dense units, whose contribution is also scaled by the
+// unit's FP64 outer-mode weights.  gfx950 has no xf32, so the inner products
+// run in FP32, which is more accurate than the reference's TF32.
 //
-// For target mode 0 and one 16-rank block rb:
-//   out_k[i, r] = sum_j T[i, j, k] * B[b1 + j, rb + r]        (FP32 MFMA)
-//   acc[i, r]  += out_k[i, r] * C[b2 + k, rb + r]              (FP64)
-//   FtV[b0 + i, rb + r] += acc[i, r]                          (one atomic)
-// Mode 1 contracts i against A and weights by C[b2 + k]; mode 2 contracts i
-// against A per j-slice and weights by B[b1 + j] (dense.cu:~560-1060).
+// For target mode 0, one tile and one 16-rank block rb:
+//   out[i, r] = sum_{j,k} T[i, j, k] * (B[b1 + j, rb + r] * C[b2 + k, rb + r])
+//   FtV[b0 + i, rb + r] += out[i, r]                 (FP64, one atomic)
+// i.e. a 16 x 256 x 16 product of the tile with the Khatri-Rao block of the
+// other two factors.  The reference contracts one factor per k-slice on the
+// tensor cores and weights each slice by the third factor in FP64
+// (dense.cu:406-549); the same sum in one MFMA chain per rank block needs
+// no per-slice epilogue.  Mode 1 contracts (i, k) against A and C, mode 2
+// (i, j) against A and B.
 //
-// One wave64 owns one tile.  v_mfma_f32_16x16x4f32 lane layout (CDNA3/4):
+// One wave64 owns one tile (or a group of tiles with the same target block).
+// v_mfma_f32_16x16x4f32 lane layout (CDNA3/4):
 //   A[m][kk]: lane = m + 16*kk;  B[kk][n]: lane = n + 16*kk;
 //   D[m][n]:  lane = n + 16*(m/4), element m%4.
-// The lane's 64 tile cells for all four K-steps and 16 slices are held in
-// registers (the tile is read from HBM once per launch).
+// The lane's 64 tile cells for all 64 K-steps are held in registers (the
+// tile is read from HBM once per launch).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -32,11 +36,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int WAVE = 64;
 constexpr int WAVES_PER_WG = 4;
 
-__device__ inline float fold(const double* __restrict__ F, int row, int dim, int r, int R)
-{
-    return (row < dim && r < R) ? float(F[size_t(row) * R + r]) : 0.0f;
-}
-
 // MODE = target slot; HDR = int32 words per tile header (bi, bj, bk first):
 // 4 for order-3 tiles, 6 for generic units.  HAS_W: the unit's FP64 outer
 // weights W[t, r] scale its contribution (generic N-order units).
@@ -44,6 +43,16 @@ __device__ inline float fold(const double* __restrict__ F, int row, int dim, int
 // (order[goff[g] .. goff[g+1]]) and sums their (row, rank) results in its own
 // LDS block (16 x Rp doubles; each lane owns its entries, so no barrier),
 // then flushes one atomic per (row, rank) per group instead of per tile.
+//
+// The contraction takes the Khatri-Rao block as the MFMA B operand:
+//   out[i, r] = sum_{j,k} T[i, j, k] * (B[b1 + j, r] * C[b2 + k, r])   (mode 0)
+// i.e. one 16 x 256 x 16 product per 16-rank block, accumulated in FP32
+// over the tile's 256 (j, k) pairs and added to the FP64 output once per
+// (row, rank, tile) or group.  K-step (x, s) covers slice x and contracted
+// rows 4s..4s+3: the A operand is the lane's tile cells and the B operand is
+// bf[s] * wf[x] formed in FP32.  Two interleaved accumulator
+// chains; the next item's factor values (and, modes 0 and 1, the next
+// tile's cells) load while the current item's MFMAs run.
 template <int MODE, int HDR, bool HAS_W, bool GROUPED>
 __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_kernel(
     const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32, size_t ntiles,
@@ -53,7 +62,10 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     int dimK)
 {
     extern __shared__ double gacc_lds[];
-    const size_t wid = size_t(blockIdx.x) * WAVES_PER_WG + threadIdx.x / WAVE;
+    // the wave index is uniform across the wave: say so, so that the tile
+    // loop, header loads and row pointers live in scalar registers
+    const size_t wid = size_t(blockIdx.x) * WAVES_PER_WG +
+                       size_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / WAVE)));
     size_t it0, it1;
     if constexpr (GROUPED)
     {
@@ -68,99 +80,128 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
         it1 = wid + 1;
     }
     const int lane = threadIdx.x & (WAVE - 1);
-    const int lo = lane & 15;   // m (A operand row) / n (B, D column)
-    const int hi = lane >> 4;   // kk (A, B) / m-group (D)
+    const int lo = lane & 15;
+    const int hi = lane >> 4;
     double* gacc = gacc_lds + size_t(threadIdx.x / WAVE) * 16 * Rp;
     if constexpr (GROUPED)
         for (int rb = 0; rb < R; rb += 16)
 #pragma unroll
             for (int v = 0; v < 4; ++v) gacc[(4 * hi + v) * Rp + rb + lo] = 0.0;
-    int ob = 0, odim = 0;
-    for (size_t it = it0; it < it1; ++it)
-    {
-    const size_t t = GROUPED ? size_t(order[it]) : it;
-    const int b0 = hdr[HDR * t] * 16, b1 = hdr[HDR * t + 1] * 16, b2 = hdr[HDR * t + 2] * 16;
-    const float* __restrict__ T = tile_f32 + t * 4096;
 
-    // cells[s][x]: A operand of K-step s for slice x
-    //   mode 0: T[lo][4s+hi][x]    mode 1: T[4s+hi][lo][x]    mode 2: T[4s+hi][x][lo]
-    float cells[4][16];
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-    {
-        if (MODE == 0 || MODE == 1)
+    const double* __restrict__ Ff = (MODE == 0) ? B : A;   // contracted factor
+    const double* __restrict__ Fw = (MODE == 2) ? B : C;   // slice factor
+    const int fdim = (MODE == 0) ? dimJ : dimI;
+    const int wdim = (MODE == 2) ? dimJ : dimK;
+    const int odim = (MODE == 0) ? dimI : (MODE == 1) ? dimJ : dimK;
+
+    auto tile_of = [&](size_t it) -> size_t { return GROUPED ? size_t(order[it]) : it; };
+    // lane offset of a contracted row (fb + 4q + hi) from the wave-uniform
+    // row pointer Ff + (fb + 4q) R + rb
+    const int boff = hi * R + lo;
+    double bn[4], wn[16];
+    auto load_factors = [&](size_t t, int rb) {
+        const int b0 = hdr[HDR * t] * 16, b1 = hdr[HDR * t + 1] * 16, b2 = hdr[HDR * t + 2] * 16;
+        const int fb = (MODE == 0) ? b1 : b0;
+        const int wb = (MODE == 2) ? b1 : b2;
+        if (fb + 16 <= fdim && wb + 16 <= wdim && rb + 16 <= R)
         {
-            const int i = (MODE == 0) ? lo : 4 * s + hi;
-            const int j = (MODE == 0) ? 4 * s + hi : lo;
-            const float4* p = reinterpret_cast<const float4*>(T + (i * 16 + j) * 16);
+            // interior tile, full rank block: unconditional loads from uniform
+            // row pointers (scalar base + per-lane offset)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-            {
-                const float4 v = p[q];
-                cells[s][4 * q + 0] = v.x;
-                cells[s][4 * q + 1] = v.y;
-                cells[s][4 * q + 2] = v.z;
-                cells[s][4 * q + 3] = v.w;
-            }
+            for (int q = 0; q < 4; ++q) bn[q] = (Ff + size_t(fb + 4 * q) * R + rb)[boff];
+#pragma unroll
+            for (int x = 0; x < 16; ++x) wn[x] = (Fw + size_t(wb + x) * R + rb)[lo];
         }
         else
         {
+            const int r = rb + lo;
 #pragma unroll
-            for (int x = 0; x < 16; ++x) cells[s][x] = T[((4 * s + hi) * 16 + x) * 16 + lo];
+            for (int q = 0; q < 4; ++q)
+                bn[q] = (r < R && fb + 4 * q + hi < fdim) ? Ff[size_t(fb + 4 * q + hi) * R + r]
+                                                          : 0.0;
+#pragma unroll
+            for (int x = 0; x < 16; ++x)
+                wn[x] = (r < R && wb + x < wdim) ? Fw[size_t(wb + x) * R + r] : 0.0;
         }
-    }
-
-    // the contracted factor (B for mode 0, A otherwise) and its tile origin
-    const double* __restrict__ Ff = (MODE == 0) ? B : A;
-    const int fb = (MODE == 0) ? b1 : b0;
-    const int fdim = (MODE == 0) ? dimJ : dimI;
-    // the slice-weight factor (C for modes 0/1, B for mode 2)
-    const double* __restrict__ Fw = (MODE == 2) ? B : C;
-    const int wb = (MODE == 2) ? b1 : b2;
-    const int wdim = (MODE == 2) ? dimJ : dimK;
-    // output rows
-    ob = (MODE == 0) ? b0 : (MODE == 1) ? b1 : b2;
-    odim = (MODE == 0) ? dimI : (MODE == 1) ? dimJ : dimK;
-
-    for (int rb = 0; rb < R; rb += 16)
-    {
-        const int r = rb + lo;
-        float bf[4];
+    };
+    float cells[4][16], ncells[4][16];
+    auto load_cells = [&](size_t t, float (&c)[4][16]) {
+        const float* __restrict__ T = tile_f32 + t * 4096;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) bf[s] = fold(Ff, fb + 4 * s + hi, fdim, r, R);
-        // four groups of four slices: inside a group the four 4-deep MFMA
-        // chains are interleaved (s outer, slice inner); a scheduling
-        // barrier between groups keeps only one group's accumulators live.
-        // A slice beyond the mode holds no cells and gets weight 0.
-        double tot[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-        for (int xg = 0; xg < 16; xg += 4)
+        for (int q = 0; q < 4; ++q)
         {
-            double w[4];
-#pragma unroll
-            for (int xx = 0; xx < 4; ++xx)
-                w[xx] = (r < R && wb + xg + xx < wdim) ? Fw[size_t(wb + xg + xx) * R + r] : 0.0;
-            floatx4 d[4];
-#pragma unroll
-            for (int xx = 0; xx < 4; ++xx) d[xx] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int xx = 0; xx < 4; ++xx)
-                    d[xx] = __builtin_amdgcn_mfma_f32_16x16x4f32(cells[s][xg + xx], bf[s], d[xx],
-                                                                 0, 0, 0);
-#pragma unroll
-            for (int xx = 0; xx < 4; ++xx)
+            if (MODE == 0 || MODE == 1)
             {
-                tot[0] += double(d[xx][0]) * w[xx];
-                tot[1] += double(d[xx][1]) * w[xx];
-                tot[2] += double(d[xx][2]) * w[xx];
-                tot[3] += double(d[xx][3]) * w[xx];
+                const int i = (MODE == 0) ? lo : 4 * q + hi;
+                const int j = (MODE == 0) ? 4 * q + hi : lo;
+                const float4* pp = reinterpret_cast<const float4*>(T + (i * 16 + j) * 16);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                {
+                    const float4 v = pp[u];
+                    c[q][4 * u + 0] = v.x;
+                    c[q][4 * u + 1] = v.y;
+                    c[q][4 * u + 2] = v.z;
+                    c[q][4 * u + 3] = v.w;
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);
+            else
+            {
+#pragma unroll
+                for (int x = 0; x < 16; ++x) c[q][x] = T[((4 * q + hi) * 16 + x) * 16 + lo];
+            }
+        }
+    };
+
+    size_t it = it0;
+    int rb = 0;
+    size_t t = tile_of(it);
+    load_cells(t, cells);
+    load_factors(t, 0);
+    int ob = 0;
+    while (true)
+    {
+        float bf[4], wf[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bf[q] = float(bn[q]);
+#pragma unroll
+        for (int x = 0; x < 16; ++x) wf[x] = float(wn[x]);
+        ob = hdr[HDR * t + MODE] * 16;
+        const int r = rb + lo;
+        size_t itn = it;
+        int rbn = rb + 16;
+        if (rbn >= R)
+        {
+            rbn = 0;
+            ++itn;
+        }
+        const bool more = itn < it1;
+        const size_t tn = more ? tile_of(itn) : t;
+        if (more) load_factors(tn, rbn);
+        // next tile's cells in registers (modes 0 / 1: mode 2's strided cell
+        // loads leave no room for a second set)
+        constexpr bool PF = GROUPED && MODE != 2;
+        const bool next_tile = PF && rb == 0 && it + 1 < it1;
+        if (next_tile) load_cells(tile_of(it + 1), ncells);
+
+        floatx4 a0 = floatx4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+#pragma unroll
+        for (int x = 0; x < 16; x += 2)
+        {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cells[q][x], bf[q] * wf[x], a0, 0, 0,
+                                                          0);
+                a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cells[q][x + 1], bf[q] * wf[x + 1], a1,
+                                                          0, 0, 0);
+            }
         }
         if (r < R)
         {
+            double tot[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) tot[v] = double(a0[v]) + double(a1[v]);
             if constexpr (HAS_W)
             {
                 const double wr = W[t * size_t(R) + r];
@@ -182,14 +223,30 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
                 }
             }
         }
-    }
+        if (!more) break;
+        if (itn != it)
+        {
+            if constexpr (PF)
+            {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) cells[q][x] = ncells[q][x];
+            }
+            else
+            {
+                load_cells(tn, cells);
+            }
+        }
+        it = itn;
+        rb = rbn;
+        t = tn;
     }
     if constexpr (GROUPED)
     {
-        // every tile of the group has target block ob
-        for (int rb = 0; rb < R; rb += 16)
+        for (int rb2 = 0; rb2 < R; rb2 += 16)
         {
-            const int r = rb + lo;
+            const int r = rb2 + lo;
             if (r >= R) continue;
 #pragma unroll
             for (int v = 0; v < 4; ++v)

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
-    const int wave = tid / WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);   // uniform per wave
     const int slot = lane / LPE;
     const int j = lane % LPE;
     const int r0 = j * VEC;
