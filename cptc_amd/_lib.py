@@ -137,6 +137,7 @@ SIGNATURES = {
     "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),
     "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
     "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),
+    "cptc_gram_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),

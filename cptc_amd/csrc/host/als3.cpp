@@ -408,12 +408,11 @@ int update_mode(Als3& h, int mode)
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
     // F = FtV * pinv(FtF) (pinv computed beside the MTTKRP) and divide by
-    // lambda, column norms, normalise + absorb, then refresh this mode's
-    // Gram (als.cu:480-517)
+    // lambda; column norms, normalise + absorb and this mode's Gram refresh
+    // from one Gram of the unnormalised factor (als.cu:480-517)
     CPTC_TRY(cptc_apply_pinv(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.d_lambda, h.s));
-    CPTC_TRY(cptc_colnorms(h.F[mode], dim, R, h.d_norms, h.s));
-    CPTC_TRY(cptc_normalize_absorb(h.F[mode], dim, R, h.d_norms, h.d_lambda, h.s));
-    CPTC_TRY(cptc_gram(h.F[mode], dim, R, h.G(mode), h.s));
+    CPTC_TRY(cptc_gram_normalize_absorb(h.F[mode], dim, R, h.G(mode), h.d_norms, h.d_lambda,
+                                        h.s));
     h.gram_ok[mode] = true;
     return CPTC_OK;
 }

@@ -75,16 +75,28 @@ __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restr
         }
 }
 
+// sum over p of part[p * n + x], in a fixed order: eight interleaved
+// accumulators (partials p = k mod 8), combined pairwise, so the loads of
+// eight partials are in flight at once and the result is the same on every
+// run.
+__device__ inline double ordered_sum(const double* __restrict__ part, int P, size_t stride,
+                                     size_t x)
+{
+    double a[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    int p = 0;
+    for (; p + 8 <= P; p += 8)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] += part[size_t(p + k) * stride + x];
+    for (int k = 0; p < P; ++p, ++k) a[k] += part[size_t(p) * stride + x];
+    return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
 __global__ void sum_partials_kernel(const double* __restrict__ part, int P, size_t n,
                                     double* __restrict__ out)
 {
     for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
          x += size_t(gridDim.x) * blockDim.x)
-    {
-        double s = 0.0;
-        for (int p = 0; p < P; ++p) s += part[size_t(p) * n + x];
-        out[x] = s;
-    }
+        out[x] = ordered_sum(part, P, n, x);
 }
 
 __global__ void hadamard_kernel(const double* A, const double* B, double* C, size_t n)
@@ -472,14 +484,27 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const double* __restri
     for (int rb = 0; rb < R; rb += lanes)
     {
         const int r = rb + rl;
-        double s = 0.0;
+        // four independent chains over rows i = r_lo + sub + k * rows_per_pass
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
         if (sub < rows_per_pass && r < R)
-            for (size_t i = r_lo + sub; i < r_hi; i += rows_per_pass)
+        {
+            size_t i = r_lo + sub;
+            const size_t step = size_t(rows_per_pass);
+            for (; i + 3 * step < r_hi; i += 4 * step)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                {
+                    const size_t ii = i + size_t(k) * step;
+                    const double f = F[ii * R + r];
+                    s4[k] += M ? f * M[ii * R + r] : f * f;
+                }
+            for (int k = 0; i < r_hi; i += step, ++k)
             {
                 const double f = F[i * R + r];
-                s += M ? f * M[i * R + r] : f * f;
+                s4[k] += M ? f * M[i * R + r] : f * f;
             }
-        red[threadIdx.x] = s;
+        }
+        red[threadIdx.x] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
         __syncthreads();
         if (threadIdx.x < lanes && rb + threadIdx.x < R)
         {
@@ -494,12 +519,7 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const double* __restri
 __global__ void norms_finalize_kernel(const double* __restrict__ part, int P, int R,
                                       double* __restrict__ norms)
 {
-    for (int r = threadIdx.x; r < R; r += blockDim.x)
-    {
-        double s = 0.0;
-        for (int p = 0; p < P; ++p) s += part[size_t(p) * R + r];
-        norms[r] = sqrt(s);
-    }
+    for (int r = threadIdx.x; r < R; r += blockDim.x) norms[r] = sqrt(ordered_sum(part, P, R, r));
 }
 
 // als.cu:308-342
@@ -523,44 +543,99 @@ __global__ void normalize_absorb_kernel(double* __restrict__ F, size_t rows, int
         }
 }
 
-// iprod and model^2 of the Gram fit (als.cu:659-715)
-__global__ void fit_finalize_kernel(const double* __restrict__ part, int P, int R,
-                                    const double* __restrict__ lambda,
-                                    const double* __restrict__ grams, int ngram,
-                                    double* __restrict__ out2)
+// iprod and model^2 of the Gram fit (als.cu:659-715), one 1024-thread block
+// (R <= 1024): iprod_r = lambda_r * sum_p part[p][r] with the partials split
+// over 1024 / R thread chunks, model^2 = sum lambda lambda^T o G_1 o ... o
+// G_ngram; fixed-order tree reductions.
+constexpr int FIT_T = 1024;
+
+__device__ inline double block_sum(double v, double* red)
 {
-    __shared__ double red[256];
-    double ip = 0.0;
-    for (int r = threadIdx.x; r < R; r += blockDim.x)
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int w = FIT_T / 2; w > 0; w >>= 1)
     {
-        double d = 0.0;
-        for (int p = 0; p < P; ++p) d += part[size_t(p) * R + r];
-        ip += lambda[r] * d;
+        if (int(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
     }
+    const double t = red[0];
+    __syncthreads();
+    return t;
+}
+
+__global__ __launch_bounds__(FIT_T) void fit_finalize_kernel(const double* __restrict__ part,
+                                                             int P, int R,
+                                                             const double* __restrict__ lambda,
+                                                             const double* __restrict__ grams,
+                                                             int ngram, double* __restrict__ out2)
+{
+    __shared__ double red[FIT_T];
+    const int tid = threadIdx.x;
+    const int C = FIT_T / R;   // chunks of partials per rank
+    const int r = tid % R, c = tid / R;
+    double d = 0.0;
+    if (c < C)
+        for (int p = c; p < P; p += C) d += part[size_t(p) * R + r];
+    red[tid] = (c < C) ? d : 0.0;
+    __syncthreads();
+    double ip = 0.0;
+    if (tid < R)
+    {
+        double t = 0.0;
+        for (int q = 0; q < C; ++q) t += red[q * R + tid];
+        ip = lambda[tid] * t;
+    }
+    __syncthreads();
+    const double iprod = block_sum(ip, red);
     double md = 0.0;
     const int RR = R * R;
-    for (int x = threadIdx.x; x < RR; x += blockDim.x)
+    for (int x = tid; x < RR; x += FIT_T)
     {
         double v = lambda[x / R] * lambda[x % R];
         for (int g = 0; g < ngram; ++g) v *= grams[size_t(g) * RR + x];
         md += v;
     }
-    red[threadIdx.x] = ip;
-    __syncthreads();
-    if (threadIdx.x == 0)
+    const double model2 = block_sum(md, red);
+    if (tid == 0)
     {
-        double t = 0.0;
-        for (int q = 0; q < int(blockDim.x); ++q) t += red[q];
-        out2[0] = t;
+        out2[0] = iprod;
+        out2[1] = model2;
+    }
+}
+
+// The Gram of the normalised factor from the Gram of the unnormalised one
+// (als.cu:308-342 with the Gram refresh after it): n_r = sqrt(G_rr);
+// lambda_r *= n_r and G_rs /= n_r n_s, with a column of norm < 1e-14 set to
+// zero (its lambda and its Gram row / column too).  One block.
+__global__ __launch_bounds__(FIT_T) void gram_norms_absorb_kernel(double* __restrict__ G, int R,
+                                                                  double* __restrict__ norms,
+                                                                  double* __restrict__ lambda)
+{
+    for (int r = threadIdx.x; r < R; r += FIT_T)
+    {
+        const double n = sqrt(G[size_t(r) * R + r]);
+        norms[r] = n;
+        lambda[r] = (n < 1e-14) ? 0.0 : lambda[r] * n;
     }
     __syncthreads();
-    red[threadIdx.x] = md;
-    __syncthreads();
-    if (threadIdx.x == 0)
+    const int RR = R * R;
+    for (int x = threadIdx.x; x < RR; x += FIT_T)
     {
-        double t = 0.0;
-        for (int q = 0; q < int(blockDim.x); ++q) t += red[q];
-        out2[1] = t;
+        const double ni = norms[x / R], nj = norms[x % R];
+        G[x] = (ni < 1e-14 || nj < 1e-14) ? 0.0 : G[x] / (ni * nj);
+    }
+}
+
+// F[:, r] /= n_r (0 when n_r < 1e-14)
+__global__ void scale_columns_kernel(double* __restrict__ F, size_t rows, int R,
+                                     const double* __restrict__ norms)
+{
+    const size_t total = rows * size_t(R);
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < total;
+         x += size_t(gridDim.x) * blockDim.x)
+    {
+        const double n = norms[x % size_t(R)];
+        F[x] = (n < 1e-14) ? 0.0 : F[x] / n;
     }
 }
 
@@ -613,6 +688,23 @@ extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, voi
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(sum_partials_kernel, dim3(cptc::grid_for(RR, 256, 1024)), dim3(256), 0, s,
                        pd, P, RR, d_G);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G,
+                                          double* d_norms, double* d_lambda, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= FIT_T && d_F && d_G && d_norms && d_lambda, CPTC_ERR_ARG,
+                 "cptc_gram_normalize_absorb: bad arguments");
+    hipStream_t s = cptc::as_stream(stream);
+    CPTC_TRY(cptc_gram(d_F, rows, R, d_G, s));
+    hipLaunchKernelGGL(gram_norms_absorb_kernel, dim3(1), dim3(FIT_T), 0, s, d_G, R, d_norms,
+                       d_lambda);
+    CPTC_LAUNCHED();
+    if (rows == 0) return CPTC_OK;
+    hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
+                       dim3(256), 0, s, d_F, rows, R, d_norms);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
@@ -747,8 +839,9 @@ extern "C" int cptc_fit_gram(const double* d_F, const double* d_M, size_t rows,
     hipStream_t s = cptc::as_stream(stream);
     double* part = nullptr;
     int P = 0;
+    CPTC_REQUIRE(R <= FIT_T, CPTC_ERR_ARG, "cptc_fit_gram: R %d > %d", R, FIT_T);
     CPTC_TRY(col_reduce(d_F, d_M, rows, R, s, &part, &P));
-    hipLaunchKernelGGL(fit_finalize_kernel, dim3(1), dim3(256), 0, s, part, P, R, d_lambda,
+    hipLaunchKernelGGL(fit_finalize_kernel, dim3(1), dim3(FIT_T), 0, s, part, P, R, d_lambda,
                        d_grams, ngram, d_out2);
     CPTC_LAUNCHED();
     return CPTC_OK;

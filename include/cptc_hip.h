@@ -178,6 +178,17 @@ int cptc_dense_tiles_pack3(const int32_t* d_pool_lid, const double* d_pool_val,
  * (generic.cu:203-258). */
 int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, void* stream);
 
+/* The update tail of one mode in one pass over the Gram: G = F^T F of the
+ * unnormalised factor, n_r = sqrt(G_rr) (= the column norms, into d_norms),
+ * F[:, r] /= n_r and lambda_r *= n_r (both 0 when n_r < 1e-14), and G scaled
+ * to the Gram of the normalised factor (G_rs / (n_r n_s), 0 for a zero
+ * column).  Same results as cptc_colnorms + cptc_normalize_absorb + cptc_gram
+ * (column_norms_kernel2, normalize_absorb_lambda and compute_gram_matrix,
+ * als.cu:480-517, 616-641) up to rounding, with one pass over F fewer.
+ * R <= 1024. */
+int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G, double* d_norms,
+                               double* d_lambda, void* stream);
+
 /* C = A o B elementwise over n doubles (C may alias A or B).
  * Replaces elementwise_mult_kernel (als.cu:101-106) and g_mul_kernel
  * (generic.cu:50-88). */

@@ -241,3 +241,33 @@ def test_norms_normalize_fit(ca, dev):
     md = np.sum(np.outer(lam2, lam2) * G[0] * G[1] * G[2])
     o = out.numpy()
     assert abs(o[0] - ip) < 1e-10 * abs(ip) and abs(o[1] - md) < 1e-12 * abs(md)
+
+
+@pytest.mark.parametrize("R", [8, 128, 200])
+def test_gram_normalize_absorb_matches_steps(ca, dev, R):
+    """The fused Gram + normalise + absorb equals colnorms, normalize_absorb
+    and gram run one after another (zero column included)."""
+    rng = np.random.default_rng(R)
+    rows = 2003
+    F = rng.standard_normal((rows, R))
+    F[:, 3] = 0.0
+    lam = rng.random(R) + 0.1
+    a_F, a_l = to_dev(ca, F), to_dev(ca, lam)
+    n1, G1 = zeros(ca, (R,)), zeros(ca, (R, R))
+    assert ca.lib.cptc_colnorms(a_F.data_ptr(), rows, R, n1.data_ptr(), stream(ca)) == 0
+    assert ca.lib.cptc_normalize_absorb(a_F.data_ptr(), rows, R, n1.data_ptr(), a_l.data_ptr(),
+                                        stream(ca)) == 0
+    assert ca.lib.cptc_gram(a_F.data_ptr(), rows, R, G1.data_ptr(), stream(ca)) == 0
+    b_F, b_l = to_dev(ca, F), to_dev(ca, lam)
+    n2, G2 = zeros(ca, (R,)), zeros(ca, (R, R))
+    assert ca.lib.cptc_gram_normalize_absorb(b_F.data_ptr(), rows, R, G2.data_ptr(),
+                                             n2.data_ptr(), b_l.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    nr = np.sqrt(np.sum(F * F, axis=0))
+    assert rel_err(n2.numpy(), nr) < 1e-14
+    assert rel_err(b_F.numpy(), a_F.numpy()) < 1e-14
+    assert rel_err(b_l.numpy(), a_l.numpy()) < 1e-14
+    assert rel_err(G2.numpy(), G1.numpy()) < 1e-13
+    Fn = b_F.numpy()
+    assert rel_err(G2.numpy(), Fn.T @ Fn) < 1e-13
+    assert np.all(G2.numpy()[3] == 0.0) and np.all(G2.numpy()[:, 3] == 0.0)
