@@ -82,6 +82,13 @@ struct Als3
     hipEvent_t ev[8] = {};
     // around the FP64 residual-view kernel of each mode, accumulated
     hipEvent_t kev[6] = {};
+    // the event blocks of the iteration being queued (ev / kev, or a block of
+    // the pool in a queued run), the pool and the per-iteration fit scalars
+    hipEvent_t* ev_cur = ev;
+    hipEvent_t* kev_cur = kev;
+    std::vector<hipEvent_t> ev_pool;
+    double* d_fit_hist = nullptr;
+    size_t fit_hist_cap = 0;
     double k_sparse_ms[3] = {0, 0, 0}, k_mttkrp_ms[3] = {0, 0, 0};
     int k_iters = 0;
     bool timing_kernels = false;
@@ -128,12 +135,12 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
         {
             if (!v->ready) continue;
             const bool timed = h.timing_kernels && v == &h.views;
-            if (timed) CPTC_HIP(hipEventRecord(h.kev[2 * mode], h.s));
+            if (timed) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode], h.s));
             CPTC_TRY(cptc_mttkrp_sparse3(mode, v->d_coords[mode], v->d_vals[mode],
                                          v->d_blk_row[mode], v->d_blk_start[mode],
                                          v->d_blk_cnt[mode], v->nseg[mode], F1, F2, h.d_FtV, R,
                                          h.s));
-            if (timed) CPTC_HIP(hipEventRecord(h.kev[2 * mode + 1], h.s));
+            if (timed) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode + 1], h.s));
         }
     }
     if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
@@ -186,7 +193,7 @@ void destroy(Als3* h)
             if (p) (void)hipFree(p);
     for (void* p : {(void*)h->d_tile_f32, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
                     (void*)h->d_FtF, (void*)h->d_Ainv, (void*)h->d_FtV, (void*)h->d_norms,
-                    (void*)h->d_scal})
+                    (void*)h->d_scal, (void*)h->d_fit_hist})
         if (p) (void)hipFree(p);
     for (auto& e : h->ev)
         if (e) (void)hipEventDestroy(e);
@@ -194,6 +201,7 @@ void destroy(Als3* h)
         if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : {h->e_fork, h->e_pinv, h->e_dense})
         if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : h->ev_pool) (void)hipEventDestroy(e);
     for (hipStream_t st : {h->s, h->s_pinv, h->s_dense})
         if (st) (void)hipStreamDestroy(st);
     delete h;
@@ -417,60 +425,123 @@ int update_mode(Als3& h, int mode)
     return CPTC_OK;
 }
 
-int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
+// One iteration's updates and the Gram fit scalars into d_out, recording the
+// events of h.ev_cur / h.kev_cur; no host wait.
+int enqueue_iteration(Als3& h, double* d_out)
 {
     const int R = h.R;
     const size_t RR = size_t(R) * R;
+    CPTC_HIP(hipEventRecord(h.ev_cur[0], h.s));
+    for (int mode = 0; mode < 3; ++mode)
+    {
+        const int p = mode == 0 ? 1 : 0, q = mode == 2 ? 1 : 2;
+        for (int g : {p, q})
+            if (!h.gram_ok[g])
+            {
+                CPTC_TRY(cptc_gram(h.F[g], h.dims[g], R, h.G(g), h.s));
+                h.gram_ok[g] = true;
+            }
+        CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+        CPTC_HIP(hipEventRecord(h.ev_cur[1 + 2 * mode], h.s));
+        CPTC_TRY(mttkrp_launch(h, mode, true));
+        CPTC_HIP(hipEventRecord(h.ev_cur[2 + 2 * mode], h.s));
+        CPTC_TRY(update_mode(h, mode));
+    }
+    // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP
+    CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, d_out, h.s));
+    CPTC_HIP(hipEventRecord(h.ev_cur[7], h.s));
+    return CPTC_OK;
+}
+
+// Fit and timings of a finished iteration (its events in h.ev_cur / h.kev_cur).
+int collect_iteration(Als3& h, int it, int iters, const double sc[2], double* fit_out,
+                      float* ms_out, float* mtt_out)
+{
     const double Xn = std::sqrt(h.x_sq);
+    const double res = std::max(h.x_sq - 2.0 * sc[0] + sc[1], 0.0);
+    const double fit = Xn > 0.0 ? 1.0 - std::sqrt(res) / Xn : 0.0;
+    float ms = 0.0f, mt = 0.0f;
+    CPTC_HIP(hipEventElapsedTime(&ms, h.ev_cur[0], h.ev_cur[7]));
+    for (int m = 0; m < 3; ++m)
+    {
+        float x = 0.0f;
+        CPTC_HIP(hipEventElapsedTime(&x, h.ev_cur[1 + 2 * m], h.ev_cur[2 + 2 * m]));
+        mt += x;
+        h.k_mttkrp_ms[m] += x;
+        if (h.timing_kernels)
+        {
+            float k = 0.0f;
+            CPTC_HIP(hipEventElapsedTime(&k, h.kev_cur[2 * m], h.kev_cur[2 * m + 1]));
+            h.k_sparse_ms[m] += k;
+        }
+    }
+    h.k_iters++;
+    if (fit_out) fit_out[it] = fit;
+    if (ms_out) ms_out[it] = ms;
+    if (mtt_out) mtt_out[it] = mt;
+    if (h.o.verbose) std::printf("[ALS] iter %d/%d time=%g ms fit=%.10g\n", it + 1, iters, ms, fit);
+    if (h.o.verbose && std::getenv("ALS_PROFILE"))
+        std::printf("[ALS][profile] iter %d mttkrp=%g (iter=%g)\n", it + 1, mt, ms);
+    return CPTC_OK;
+}
+
+// Verbose runs wait after every iteration and print the reference's line
+// (als.cu:722-735); quiet runs queue every iteration and wait once.
+int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
+{
     h.timing_kernels = h.views.ready;
+    if (iters <= 0) return CPTC_OK;
+    struct Reset
+    {
+        Als3& h;
+        ~Reset()
+        {
+            h.ev_cur = h.ev;
+            h.kev_cur = h.kev;
+        }
+    } reset{h};
+    if (h.o.verbose)
+    {
+        for (int it = 0; it < iters; ++it)
+        {
+            CPTC_TRY(enqueue_iteration(h, h.d_scal));
+            double sc[2] = {0, 0};
+            CPTC_HIP(hipMemcpyAsync(sc, h.d_scal, 2 * sizeof(double), hipMemcpyDeviceToHost,
+                                    h.s));
+            CPTC_HIP(hipStreamSynchronize(h.s));
+            CPTC_TRY(collect_iteration(h, it, iters, sc, fit_out, ms_out, mtt_out));
+        }
+        return CPTC_OK;
+    }
+    constexpr size_t PER = 14;   // ev (8) + kev (6) per iteration
+    while (h.ev_pool.size() < PER * size_t(iters))
+    {
+        hipEvent_t e = nullptr;
+        CPTC_HIP(hipEventCreate(&e));
+        h.ev_pool.push_back(e);
+    }
+    if (h.fit_hist_cap < size_t(iters))
+    {
+        if (h.d_fit_hist) CPTC_HIP(hipFree(h.d_fit_hist));
+        h.d_fit_hist = nullptr;
+        CPTC_HIP(hipMalloc(&h.d_fit_hist, size_t(2) * iters * sizeof(double)));
+        h.fit_hist_cap = size_t(iters);
+    }
     for (int it = 0; it < iters; ++it)
     {
-        CPTC_HIP(hipEventRecord(h.ev[0], h.s));
-        for (int mode = 0; mode < 3; ++mode)
-        {
-            const int p = mode == 0 ? 1 : 0, q = mode == 2 ? 1 : 2;
-            for (int g : {p, q})
-                if (!h.gram_ok[g])
-                {
-                    CPTC_TRY(cptc_gram(h.F[g], h.dims[g], R, h.G(g), h.s));
-                    h.gram_ok[g] = true;
-                }
-            CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
-            CPTC_HIP(hipEventRecord(h.ev[1 + 2 * mode], h.s));
-            CPTC_TRY(mttkrp_launch(h, mode, true));
-            CPTC_HIP(hipEventRecord(h.ev[2 + 2 * mode], h.s));
-            CPTC_TRY(update_mode(h, mode));
-        }
-        // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP
-        CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, h.d_scal, h.s));
-        CPTC_HIP(hipEventRecord(h.ev[7], h.s));
-        double sc[2] = {0, 0};
-        CPTC_HIP(hipMemcpyAsync(sc, h.d_scal, 2 * sizeof(double), hipMemcpyDeviceToHost, h.s));
-        CPTC_HIP(hipStreamSynchronize(h.s));
-        const double res = std::max(h.x_sq - 2.0 * sc[0] + sc[1], 0.0);
-        const double fit = Xn > 0.0 ? 1.0 - std::sqrt(res) / Xn : 0.0;
-        float ms = 0.0f, mt = 0.0f;
-        CPTC_HIP(hipEventElapsedTime(&ms, h.ev[0], h.ev[7]));
-        for (int m = 0; m < 3; ++m)
-        {
-            float x = 0.0f;
-            CPTC_HIP(hipEventElapsedTime(&x, h.ev[1 + 2 * m], h.ev[2 + 2 * m]));
-            mt += x;
-            h.k_mttkrp_ms[m] += x;
-            if (h.timing_kernels)
-            {
-                float k = 0.0f;
-                CPTC_HIP(hipEventElapsedTime(&k, h.kev[2 * m], h.kev[2 * m + 1]));
-                h.k_sparse_ms[m] += k;
-            }
-        }
-        h.k_iters++;
-        if (fit_out) fit_out[it] = fit;
-        if (ms_out) ms_out[it] = ms;
-        if (mtt_out) mtt_out[it] = mt;
-        if (h.o.verbose) std::printf("[ALS] iter %d/%d time=%g ms fit=%.10g\n", it + 1, iters, ms, fit);
-        if (h.o.verbose && std::getenv("ALS_PROFILE"))
-            std::printf("[ALS][profile] iter %d mttkrp=%g (iter=%g)\n", it + 1, mt, ms);
+        h.ev_cur = h.ev_pool.data() + PER * size_t(it);
+        h.kev_cur = h.ev_cur + 8;
+        CPTC_TRY(enqueue_iteration(h, h.d_fit_hist + 2 * it));
+    }
+    std::vector<double> sc(size_t(2) * iters);
+    CPTC_HIP(hipMemcpyAsync(sc.data(), h.d_fit_hist, sc.size() * sizeof(double),
+                            hipMemcpyDeviceToHost, h.s));
+    CPTC_HIP(hipStreamSynchronize(h.s));
+    for (int it = 0; it < iters; ++it)
+    {
+        h.ev_cur = h.ev_pool.data() + PER * size_t(it);
+        h.kev_cur = h.ev_cur + 8;
+        CPTC_TRY(collect_iteration(h, it, iters, sc.data() + 2 * it, fit_out, ms_out, mtt_out));
     }
     return CPTC_OK;
 }

@@ -292,7 +292,10 @@ int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
 /* Runs `iters` ALS iterations (continuing from the current state).  Arrays
  * of length iters (may be NULL): fit, ms per iteration (hipEvent span of
- * als.cu:613, 722-726), ms of MTTKRP per iteration (sum over modes). */
+ * als.cu:613, 722-726), ms of MTTKRP per iteration (sum over modes).  With
+ * opts.verbose the host waits after every iteration and prints the
+ * reference's "[ALS] iter" line; otherwise every iteration is queued and the
+ * host waits once at the end. */
 int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter, float* ms_mttkrp);
 
 /* Kernel times accumulated over cptc_als3_run iterations (hipEvents on the
@@ -479,8 +482,12 @@ int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, void** handl
 int cptc_gen_info_get(void* handle, cptc_gen_info* info);
 
 /* Runs `iters` iterations (continuing from the current state).  Arrays of
- * length iters (may be NULL): Gram fit, iprod, model^2, wall ms per
- * iteration (the reference's chrono span, generic.cu:2030-2249). */
+ * length iters (may be NULL): Gram fit, iprod, model^2, ms per iteration.
+ * With opts.verbose or opts.profile the host waits after every iteration
+ * and prints the reference's "[GEN] iter" line (generic.cu:2030-2249);
+ * ms_iter is then the host wall time of the iteration.  Otherwise all
+ * iterations are queued and the host waits once; ms_iter is the GPU time
+ * between consecutive iteration ends (hipEvents). */
 int cptc_gen_run(void* handle, int iters, double* fit, double* iprod, double* model2,
                  double* ms_iter);
 
