@@ -75,9 +75,6 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
-    // Left as a per-lane value on purpose: marking it uniform saves six
-    // VGPRs (4 waves per SIMD instead of 3), which runs no faster alone and
-    // slower beside the MFMA tile kernel it shares the CUs with.
     const int wave = tid / WAVE;
     const int slot = lane / LPE;
     const int r0 = int(blockIdx.y) * RT + (lane % LPE) * VEC;   // first rank of this lane
@@ -219,6 +216,145 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
     }
 }
 
+// R in (64, 128] with 16-byte rows: one element per wave (LPE = 64), so the
+// window position, the element's coordinates and value, the run state and
+// the factor-row addresses are the same for every lane.  This variant keeps
+// them wave-uniform: the wave's range comes from readfirstlane, each element
+// is broadcast with readlane into scalar registers, its coordinates are
+// decoded with scalar shifts, and the row loads use a scalar row base plus
+// the lane's fixed rank offset (about a third of the per-element vector
+// instructions of the general kernel).  Same sum and order as
+// mttkrp3_seg_kernel.  The waves-per-EU bound keeps the register allocation
+// free to hold UNROLL gathers in flight; config 3 ran fastest at UNROLL = 8
+// (98 VGPRs) beside the MFMA tile kernel: 12.2 ms per iteration against
+// 13.0 at UNROLL = 16 (159 VGPRs) and 12.6 for the general kernel.
+#ifndef CPTC_SPARSE3_WAVE_UNROLL
+#define CPTC_SPARSE3_WAVE_UNROLL 8   // gathers in flight per wave
+#endif
+template <int WAVES, int UNROLL>
+__global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 3))) void mttkrp3_seg_wave_kernel(
+    int mode, const uint64_t* __restrict__ coords, const double* __restrict__ vals,
+    const uint32_t* __restrict__ blk_row, const uint32_t* __restrict__ blk_start,
+    const uint32_t* __restrict__ blk_cnt, const double* __restrict__ F1,
+    const double* __restrict__ F2, double* __restrict__ FtV, int R)
+{
+    constexpr int RT = 128;
+    constexpr int U = UNROLL;
+    constexpr uint32_t NONE = 0xFFFFFFFFu;
+    const uint32_t seg = blockIdx.x;
+    const uint32_t row = blk_row[seg];
+    const uint32_t start = blk_start[seg];
+    const uint32_t cnt = blk_cnt[seg];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int r0 = int(blockIdx.y) * RT + lane * 2;
+    const bool rank_ok = r0 < R;
+    const int rr = rank_ok ? r0 : 0;
+    const int sh0 = (mode == 0) ? 15 : 30;
+    const int sh1 = (mode == 2) ? 15 : 0;
+
+    const uint32_t wchunk = (cnt + WAVES - 1) / WAVES;
+    const uint32_t lo = start + min(cnt, uint32_t(wave) * wchunk);
+    const uint32_t hi = start + min(cnt, uint32_t(wave + 1) * wchunk);
+
+    double acc0 = 0.0, acc1 = 0.0, t0 = 0.0, t1 = 0.0;
+    uint32_t cur = NONE;
+
+    uint64_t pc = 0;
+    double v = 0.0;
+    if (lo + uint32_t(lane) < hi)
+    {
+        pc = __builtin_nontemporal_load(coords + lo + lane);
+        v = __builtin_nontemporal_load(vals + lo + lane);
+    }
+    for (uint32_t base = lo; base < hi; base += WAVE)
+    {
+        uint64_t pcn = 0;
+        double vn = 0.0;
+        if (base + WAVE + uint32_t(lane) < hi)
+        {
+            pcn = __builtin_nontemporal_load(coords + base + WAVE + lane);
+            vn = __builtin_nontemporal_load(vals + base + WAVE + lane);
+        }
+        const int n = int(min(uint32_t(WAVE), hi - base));
+        const uint32_t pc_lo = uint32_t(pc), pc_hi = uint32_t(pc >> 32);
+        const uint64_t vb = uint64_t(__double_as_longlong(v));
+        const uint32_t v_lo = uint32_t(vb), v_hi = uint32_t(vb >> 32);
+        for (int i = 0; i < n; i += U)
+        {
+            uint32_t o0[U], o1[U];
+            double ev[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                const int j = i + u;   // < 64: i <= 56 when U = 8
+                const uint64_t pj =
+                    (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(pc_hi), j))) << 32) |
+                    uint32_t(__builtin_amdgcn_readlane(int(pc_lo), j));
+                const uint64_t vj =
+                    (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(v_hi), j))) << 32) |
+                    uint32_t(__builtin_amdgcn_readlane(int(v_lo), j));
+                ev[u] = __longlong_as_double((long long)vj);
+                o0[u] = uint32_t(pj >> sh0) & 0x7FFFu;
+                o1[u] = uint32_t(pj >> sh1) & 0x7FFFu;
+            }
+            double2 f1[U], f2[U];
+            bool closes[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                const uint32_t prev = (u == 0) ? cur : o1[u - 1];
+                closes[u] = (i + u < n) && o1[u] != prev && prev != NONE;
+                if (i + u < n)
+                    f1[u] = *reinterpret_cast<const double2*>(F1 + size_t(o0[u]) * R + rr);
+                if (closes[u])
+                    f2[u] = *reinterpret_cast<const double2*>(F2 + size_t(prev) * R + rr);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+            {
+                if (i + u < n)
+                {
+                    if (closes[u])
+                    {
+                        acc0 += t0 * f2[u].x;
+                        acc1 += t1 * f2[u].y;
+                        t0 = t1 = 0.0;
+                    }
+                    cur = o1[u];
+                    t0 += ev[u] * f1[u].x;
+                    t1 += ev[u] * f1[u].y;
+                }
+            }
+        }
+        pc = pcn;
+        v = vn;
+    }
+    if (cur != NONE)
+    {
+        const double2 f2 = *reinterpret_cast<const double2*>(F2 + size_t(cur) * R + rr);
+        acc0 += t0 * f2.x;
+        acc1 += t1 * f2.y;
+    }
+    if (!rank_ok) acc0 = acc1 = 0.0;
+
+    __shared__ double red[WAVES][RT];
+    red[wave][lane * 2] = acc0;
+    red[wave][lane * 2 + 1] = acc1;
+    __syncthreads();
+    for (int x = tid; x < RT; x += WAVE * WAVES)
+    {
+        const int r = int(blockIdx.y) * RT + x;
+        if (r >= R) continue;
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += red[w][x];
+        if (tot != 0.0) atomicAdd(FtV + size_t(row) * R + r, tot);
+    }
+}
+
 template <int RT, int VEC>
 hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const uint32_t* br,
                      const uint32_t* bs, const uint32_t* bc, size_t nblocks, const double* F1,
@@ -228,8 +364,14 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
     constexpr int UNROLL = CPTC_SPARSE3_UNROLL;
     const unsigned ry = unsigned((R + RT - 1) / RT);
     dim3 grid(unsigned(nblocks), ry);
-    hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid, dim3(WAVE * WAVES), 0,
-                       s, mode, coords, vals, br, bs, bc, F1, F2, FtV, R);
+    if constexpr (RT == 128 && VEC == 2)
+        hipLaunchKernelGGL((mttkrp3_seg_wave_kernel<WAVES, CPTC_SPARSE3_WAVE_UNROLL>), grid,
+                           dim3(WAVE * WAVES), 0,
+                           s, mode, coords, vals, br, bs, bc, F1, F2, FtV, R);
+    else
+        hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid,
+                           dim3(WAVE * WAVES), 0, s, mode, coords, vals, br, bs, bc, F1, F2, FtV,
+                           R);
     return hipGetLastError();
 }
 
