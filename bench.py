@@ -180,7 +180,7 @@ def main() -> int:
         "mttkrp_frac_of_hbm_peak": round(mtt_gbs / HBM_PEAK_GBS, 4),
         "fit_last": float(fits[-1]),
         "roofline": {
-            "kernel": "mttkrp3_seg_kernel (FP64 residual view), per launch = one mode",
+            "kernel": "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128]), per launch = one mode",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
