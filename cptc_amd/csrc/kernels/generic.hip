@@ -323,70 +323,110 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
     }
 }
 
-// Ridge Cholesky + per-row substitution.  Every block (one wave) stages FtF
-// in LDS with one coalesced pass and factors FtF + eps I there in place,
-// column by column (left-looking: column j needs the columns < j; each entry
-// runs the reference's k-ascending update; the strict upper triangle keeps
-// FtF and is never read again), then each lane solves rows, keeping its
-// y / x vector in an LDS column of its own.
+// Ridge Cholesky + per-row substitution (generic.cu:746-819).  Every block
+// (one wave) factors FtF + eps I in registers: lane i holds row i, and step j
+// takes the pivot of lane j (readlane), scales column j and subtracts
+// L[i][j] L[k][j] from the trailing entries.  Each entry therefore receives
+// exactly the reference's sequence: (FtF + eps) minus the products for
+// k = 0, 1, ... in ascending order, then the division by the pivot.  L goes
+// to LDS; then each lane solves one row with its y / x vector in registers
+// (RT >= R, loops unrolled to RT with the ranks >= R switched off) while L is
+// read from LDS as a broadcast: the same k-ascending forward and backward
+// substitutions.  The grid covers the rows (every block factors FtF itself:
+// O(R^3 / 3) flops).
 constexpr int CHOL_RM = 32;
 constexpr int CHOL_T = 64;
 
+__device__ __forceinline__ double lane_double(double v, int l)
+{
+    const uint64_t b = uint64_t(__double_as_longlong(v));
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l));
+    return __longlong_as_double((long long)((uint64_t(hi) << 32) | lo));
+}
+
+template <int RT>
 __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __restrict__ FtF,
                                                             const double* __restrict__ FtV,
                                                             double* __restrict__ F, size_t dim,
                                                             int R)
 {
-    __shared__ double L[CHOL_RM][CHOL_RM + 1];
-    __shared__ double Y[CHOL_RM][CHOL_T];
-    __shared__ double eps_s;
+    __shared__ double L[RT][RT + 1];
     const int tid = threadIdx.x;
-    for (int x = tid; x < R * R; x += CHOL_T) L[x / R][x % R] = FtF[x];
-    __syncthreads();
-    if (tid == 0)
+    const bool mine = tid < R;   // this lane holds row tid
+    double a[RT];
+#pragma unroll
+    for (int k = 0; k < RT; ++k) a[k] = (mine && k < R) ? FtF[size_t(tid) * R + k] : 0.0;
+    // eps from the trace, summed in row order (the diagonal of row i is lane i's a[i])
+    double tr = 0.0;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+        if (i < R) tr += lane_double(a[i], i);
+    const double eps = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+        if (tid == i) a[i] += eps;
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
     {
-        double tr = 0.0;
-        for (int i = 0; i < R; ++i) tr += L[i][i];
-        eps_s = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
+        if (j < R)
+        {
+            const double s = lane_double(a[j], j);
+            const double d = (s > 0.0) ? sqrt(s) : sqrt(eps);
+            if (tid == j) a[j] = d;
+            if (mine && tid > j) a[j] = a[j] / d;   // L[tid][j]
+#pragma unroll
+            for (int k = j + 1; k < RT; ++k)
+            {
+                if (k < R)
+                {
+                    const double lkj = lane_double(a[j], k);   // L[k][j]
+                    if (mine && tid >= k) a[k] -= a[j] * lkj;
+                }
+            }
+        }
     }
+    if (mine)
+#pragma unroll
+        for (int k = 0; k < RT; ++k)
+            if (k <= tid) L[tid][k] = a[k];
     __syncthreads();
-    const double eps = eps_s;
-    for (int j = 0; j < R; ++j)
-    {
-        if (tid == 0)
-        {
-            double s = L[j][j] + eps;
-            for (int k = 0; k < j; ++k) s -= L[j][k] * L[j][k];
-            L[j][j] = (s > 0.0) ? sqrt(s) : sqrt(eps);
-        }
-        __syncthreads();
-        const int i = j + 1 + tid;
-        if (i < R)
-        {
-            double s = L[i][j];
-            for (int k = 0; k < j; ++k) s -= L[i][k] * L[j][k];
-            L[i][j] = s / L[j][j];
-        }
-        __syncthreads();
-    }
-    const size_t stride = size_t(gridDim.x) * CHOL_T;
-    for (size_t row = size_t(blockIdx.x) * CHOL_T + tid; row < dim; row += stride)
+    // one row per lane (a row loop would let the compiler hoist all of L
+    // into registers)
+    const size_t row = size_t(blockIdx.x) * CHOL_T + tid;
+    if (row < dim)
     {
         const double* b = FtV + row * R;
-        for (int i = 0; i < R; ++i)
+        double y[RT];
+#pragma unroll
+        for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
         {
-            double s = b[i];
-            for (int k = 0; k < i; ++k) s -= L[i][k] * Y[k][tid];
-            Y[i][tid] = s / L[i][i];
+            if (i < R)
+            {
+                double s = y[i];
+#pragma unroll
+                for (int k = 0; k < i; ++k) s -= L[i][k] * y[k];
+                y[i] = s / L[i][i];
+            }
         }
-        for (int i = R - 1; i >= 0; --i)
+#pragma unroll
+        for (int i = RT - 1; i >= 0; --i)
         {
-            double s = Y[i][tid];
-            for (int k = i + 1; k < R; ++k) s -= L[k][i] * Y[k][tid];
-            Y[i][tid] = s / L[i][i];   // x[i]; y[i] is no longer needed
+            if (i < R)
+            {
+                double s = y[i];
+#pragma unroll
+                for (int k = i + 1; k < RT; ++k)
+                    if (k < R) s -= L[k][i] * y[k];
+                y[i] = s / L[i][i];   // x[i]
+            }
         }
         double* out = F + row * R;
-        for (int i = 0; i < R; ++i) out[i] = Y[i][tid];
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+            if (i < R) out[i] = y[i];
     }
 }
 
@@ -617,8 +657,19 @@ extern "C" int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, d
     CPTC_REQUIRE(R >= 1 && R <= 32, CPTC_ERR_ARG, "cptc_chol_ridge_solve: R %d (1..32)", R);
     if (dim == 0) return CPTC_OK;
     CPTC_REQUIRE(d_FtF && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_solve: null pointer");
-    hipLaunchKernelGGL(chol_ridge_kernel, dim3(cptc::grid_for(dim, CHOL_T, 16384)), dim3(CHOL_T),
-                       0, cptc::as_stream(stream), d_FtF, d_FtV, d_F, dim, R);
+    CPTC_REQUIRE(dim / CHOL_T < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_chol_ridge_solve: %zu rows", dim);
+    const dim3 grid(unsigned((dim + CHOL_T - 1) / CHOL_T));
+    hipStream_t s = cptc::as_stream(stream);
+    if (R <= 8)
+        hipLaunchKernelGGL(chol_ridge_kernel<8>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F, dim,
+                           R);
+    else if (R <= 16)
+        hipLaunchKernelGGL(chol_ridge_kernel<16>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F,
+                           dim, R);
+    else
+        hipLaunchKernelGGL(chol_ridge_kernel<CHOL_RM>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F,
+                           dim, R);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
