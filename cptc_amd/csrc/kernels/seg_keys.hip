@@ -54,12 +54,19 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ double2 row2(const double* __restrict__ base, uint64_t idx, int R, int r)
+// The two ranks r, r + 1 of row idx.  OFF32: the element offset idx R + r
+// fits 28 bits for every level (checked at launch), so it is formed in 32-bit
+// arithmetic from the wave-uniform factor base.
+template <bool OFF32>
+__device__ __forceinline__ double2 row2(const double* __restrict__ base, uint32_t idx, int R, int r)
 {
-    return *reinterpret_cast<const double2*>(base + idx * uint64_t(R) + r);
+    if constexpr (OFF32)
+        return *reinterpret_cast<const double2*>(base + (idx * uint32_t(R) + uint32_t(r)));
+    else
+        return *reinterpret_cast<const double2*>(base + uint64_t(idx) * uint64_t(R) + r);
 }
 
-template <int NO, int RT, typename KEY, int U>
+template <int NO, int RT, typename KEY, int U, bool OFF32>
 __global__ __launch_bounds__(256) void seg_keys_kernel(
     KeyLevels lv, const KEY* __restrict__ keys, const double* __restrict__ vals,
     const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
@@ -101,8 +108,9 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
 
     const double* __restrict__ Fleaf = lv.F[NO - 1];
     const uint32_t sh_leaf = lv.shift[NO - 1];
-    const uint64_t mk_leaf = lv.mask[NO - 1];
-    auto level = [&](KEY k, int l) -> uint64_t { return (uint64_t(k) >> lv.shift[l]) & lv.mask[l]; };
+    const KEY mk_leaf = KEY(lv.mask[NO - 1]);
+    // field of level l (in the key's own width: 32-bit operations for u32 keys)
+    auto level = [&](KEY k, int l) -> uint32_t { return uint32_t((k >> lv.shift[l]) & KEY(lv.mask[l])); };
     // a change above the last level closes at least the deepest run level
     const uint32_t sh_deep = lv.shift[NO > 1 ? NO - 2 : 0];
 
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
         for (int l = NL - 1; l >= 0; --l)
         {
             if (l < to) break;
-            const double2 f = (l == NL - 1) ? fdeep : row2(lv.F[l], level(cur, l), R, rr);
+            const double2 f = (l == NL - 1) ? fdeep : row2<OFF32>(lv.F[l], level(cur, l), R, rr);
             const double x0 = t0[l] * f.x, x1 = t1[l] * f.y;
             if (l == 0)
             {
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
             {
                 gl[u] = make_double2(0.0, 0.0);
                 if (i0 + u < nvalid)
-                    gl[u] = row2(Fleaf, (uint64_t(kk[u]) >> sh_leaf) & mk_leaf, R, rr);
+                    gl[u] = row2<OFF32>(Fleaf, uint32_t((kk[u] >> sh_leaf) & mk_leaf), R, rr);
             }
             if constexpr (NO > 1)
             {
@@ -193,7 +201,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
                     const KEY prev = (u == 0) ? cur : kk[u - 1];
                     const bool has_prev = (u == 0) ? open : true;
                     if (i0 + u < nvalid && has_prev && ((kk[u] ^ prev) >> sh_deep) != 0)
-                        cl[u] = row2(lv.F[NL - 1], level(prev, NL - 1), R, rr);
+                        cl[u] = row2<OFF32>(lv.F[NL - 1], level(prev, NL - 1), R, rr);
                 }
             }
 #pragma unroll
@@ -220,7 +228,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
                             int L = NL - 1;
 #pragma unroll
                             for (int l = NL - 2; l >= 0; --l)
-                                if ((uint64_t(d) >> lv.shift[l]) != 0) L = l;
+                                if ((d >> lv.shift[l]) != 0) L = l;
                             close_from(L, cl[u]);
                             cur = kk[u];
                         }
@@ -232,7 +240,7 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
         }
     }
     if constexpr (NO > 1)
-        if (open) close_from(0, row2(lv.F[NL - 1], level(cur, NL - 1), R, rr));
+        if (open) close_from(0, row2<OFF32>(lv.F[NL - 1], level(cur, NL - 1), R, rr));
     if (!rank_ok) acc0 = acc1 = 0.0;
 
 #pragma unroll
@@ -267,8 +275,18 @@ void launch_rt(const KeyLevels& lv, const void* keys, const double* vals, const 
                double* FtV, int R, hipStream_t s)
 {
     constexpr int U = (NO <= 2) ? 8 : 4;
-    hipLaunchKernelGGL((seg_keys_kernel<NO, RT, KEY, U>), dim3(unsigned(nseg)), dim3(256), 0, s,
-                       lv, static_cast<const KEY*>(keys), vals, row, st, cn, single, FtV, R);
+    // 32-bit row offsets when every level's (field range x R) stays below 2^28
+    bool off32 = true;
+    for (int l = 0; l < NO; ++l)
+        if ((lv.mask[l] + 1) * uint64_t(R) >= (uint64_t(1) << 28)) off32 = false;
+    if (off32)
+        hipLaunchKernelGGL((seg_keys_kernel<NO, RT, KEY, U, true>), dim3(unsigned(nseg)),
+                           dim3(256), 0, s, lv, static_cast<const KEY*>(keys), vals, row, st, cn,
+                           single, FtV, R);
+    else
+        hipLaunchKernelGGL((seg_keys_kernel<NO, RT, KEY, U, false>), dim3(unsigned(nseg)),
+                           dim3(256), 0, s, lv, static_cast<const KEY*>(keys), vals, row, st, cn,
+                           single, FtV, R);
 }
 
 template <int NO, typename KEY>
