@@ -14,6 +14,8 @@
 // then in LDS across waves.  R > RT runs RT-wide rank blocks on grid.y.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "../host/hip_util.hpp"
 
 #ifndef CPTC_SPARSE3_UNROLL
@@ -219,27 +221,36 @@ __global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_kernel(
 // R in (64, 128] with 16-byte rows: one element per wave (LPE = 64), so the
 // window position, the element's coordinates and value, the run state and
 // the factor-row addresses are the same for every lane.  This variant keeps
-// them wave-uniform: the wave's range comes from readfirstlane, each element
-// is broadcast with readlane into scalar registers, its coordinates are
-// decoded with scalar shifts, and the row loads use a scalar row base plus
-// the lane's fixed rank offset (about a third of the per-element vector
-// instructions of the general kernel).  Same sum and order as
-// mttkrp3_seg_kernel.  The waves-per-EU bound keeps the register allocation
-// free to hold UNROLL gathers in flight; config 3 ran fastest at UNROLL = 8
-// (98 VGPRs) beside the MFMA tile kernel: 12.2 ms per iteration against
-// 13.0 at UNROLL = 16 (159 VGPRs) and 12.6 for the general kernel.
+// them wave-uniform and spends as few issue slots per element as it can,
+// because the kernel shares its CUs with the MFMA tile kernel and every
+// slot it frees goes to that kernel:
+//   * the mode is a template parameter (constant field shifts);
+//   * per 64-element window each lane decodes its own element once into the
+//     byte offsets of its F1 and F2 rows; per element two v_readlane move
+//     them to scalar registers, and the row loads are buffer loads with that
+//     offset in soffset and the lane's fixed rank offset in voffset (no
+//     per-element address arithmetic);
+//   * the window's values are broadcast from a per-wave LDS slot (LDS pipe)
+//     instead of by v_readlane;
+//   * full windows run without per-element bound checks.
+// Same sum and order as mttkrp3_seg_kernel.  The waves-per-EU bound keeps
+// the register allocation free to hold UNROLL gathers in flight; UNROLL = 8
+// ran fastest beside the MFMA tile kernel (config 3: 12.2 ms per iteration
+// against 13.0 at UNROLL = 16 and 12.6 for the general kernel, before the
+// issue-slot changes above took it to 11.7).
 #ifndef CPTC_SPARSE3_WAVE_UNROLL
 #define CPTC_SPARSE3_WAVE_UNROLL 8   // gathers in flight per wave
 #endif
-template <int WAVES, int UNROLL>
+template <int MODE, int WAVES, int UNROLL>
 __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 3))) void mttkrp3_seg_wave_kernel(
-    int mode, const uint64_t* __restrict__ coords, const double* __restrict__ vals,
+    const uint64_t* __restrict__ coords, const double* __restrict__ vals,
     const uint32_t* __restrict__ blk_row, const uint32_t* __restrict__ blk_start,
     const uint32_t* __restrict__ blk_cnt, const double* __restrict__ F1,
     const double* __restrict__ F2, double* __restrict__ FtV, int R)
 {
     constexpr int RT = 128;
     constexpr int U = UNROLL;
+    // run state "no open run"; row offsets are < 2^31, so never equal to it
     constexpr uint32_t NONE = 0xFFFFFFFFu;
     const uint32_t seg = blockIdx.x;
     const uint32_t row = blk_row[seg];
@@ -252,8 +263,23 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 
     const int r0 = int(blockIdx.y) * RT + lane * 2;
     const bool rank_ok = r0 < R;
     const int rr = rank_ok ? r0 : 0;
-    const int sh0 = (mode == 0) ? 15 : 30;
-    const int sh1 = (mode == 2) ? 15 : 0;
+    constexpr int sh0 = (MODE == 0) ? 15 : 30;
+    constexpr int sh1 = (MODE == 2) ? 15 : 0;
+    // factor rows by buffer loads: the row offset o*R*8 in soffset (scalar),
+    // the lane's rank offset in voffset (fixed), no per-element vector
+    // address arithmetic
+    const __amdgpu_buffer_rsrc_t rs1 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(F1), short(0), 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs2 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(F2), short(0), 0x7FFFFFF0, 0x00020000);
+    const uint32_t voff = uint32_t(rr) * 8u;
+    const uint32_t rowb = uint32_t(R) * 8u;
+    auto row_load = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, off, 0);
+        return make_double2(
+            __longlong_as_double((long long)((uint64_t(uint32_t(w[1])) << 32) | uint32_t(w[0]))),
+            __longlong_as_double((long long)((uint64_t(uint32_t(w[3])) << 32) | uint32_t(w[2]))));
+    };
 
     const uint32_t wchunk = (cnt + WAVES - 1) / WAVES;
     const uint32_t lo = start + min(cnt, uint32_t(wave) * wchunk);
@@ -269,6 +295,54 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 
         pc = __builtin_nontemporal_load(coords + lo + lane);
         v = __builtin_nontemporal_load(vals + lo + lane);
     }
+    // each window's values are broadcast from a per-wave LDS slot (LDS
+    // pipe) instead of by v_readlane (VALU); a wave's LDS operations are
+    // processed in order, so its own writes are visible to its later reads
+    __shared__ double vbuf[WAVES][WAVE];
+    double* const vw = vbuf[wave];
+    // one batch of U elements starting at window position i; FULL: all U
+    // elements exist (full 64-element window, no per-element guards)
+    auto batch = [&](auto full, int i, int n, uint32_t off1_l, uint32_t off2_l) {
+        constexpr bool FULL = decltype(full)::value;
+        uint32_t o0[U], o1[U];
+        double ev[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const int j = i + u;   // < 64: i <= 56 when U = 8
+            o0[u] = uint32_t(__builtin_amdgcn_readlane(int(off1_l), j));
+            o1[u] = uint32_t(__builtin_amdgcn_readlane(int(off2_l), j));
+            ev[u] = vw[j];
+        }
+        double2 f1[U], f2[U];
+        bool closes[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const bool live = FULL || i + u < n;
+            const uint32_t prev = (u == 0) ? cur : o1[u - 1];
+            // within a batch prev is an element's offset, never NONE
+            closes[u] = live && o1[u] != prev && (u > 0 || prev != NONE);
+            if (live) f1[u] = row_load(rs1, o0[u]);
+            if (closes[u]) f2[u] = row_load(rs2, prev);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            if (FULL || i + u < n)
+            {
+                if (closes[u])
+                {
+                    acc0 += t0 * f2[u].x;
+                    acc1 += t1 * f2[u].y;
+                    t0 = t1 = 0.0;
+                }
+                cur = o1[u];
+                t0 += ev[u] * f1[u].x;
+                t1 += ev[u] * f1[u].y;
+            }
+        }
+    };
     for (uint32_t base = lo; base < hi; base += WAVE)
     {
         uint64_t pcn = 0;
@@ -279,62 +353,29 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 
             vn = __builtin_nontemporal_load(vals + base + WAVE + lane);
         }
         const int n = int(min(uint32_t(WAVE), hi - base));
-        const uint32_t pc_lo = uint32_t(pc), pc_hi = uint32_t(pc >> 32);
-        const uint64_t vb = uint64_t(__double_as_longlong(v));
-        const uint32_t v_lo = uint32_t(vb), v_hi = uint32_t(vb >> 32);
-        for (int i = 0; i < n; i += U)
+        // each lane decodes its element once: byte offsets of its F1 and F2
+        // rows (o * R * 8 < 2^31), broadcast per element by v_readlane
+        const uint32_t off1_l = (uint32_t(pc >> sh0) & 0x7FFFu) * rowb;
+        const uint32_t off2_l = (uint32_t(pc >> sh1) & 0x7FFFu) * rowb;
+        asm volatile("" ::: "memory");   // the previous window's reads come first
+        vw[lane] = v;
+        asm volatile("" ::: "memory");
+        if (n == WAVE)
         {
-            uint32_t o0[U], o1[U];
-            double ev[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-            {
-                const int j = i + u;   // < 64: i <= 56 when U = 8
-                const uint64_t pj =
-                    (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(pc_hi), j))) << 32) |
-                    uint32_t(__builtin_amdgcn_readlane(int(pc_lo), j));
-                const uint64_t vj =
-                    (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(v_hi), j))) << 32) |
-                    uint32_t(__builtin_amdgcn_readlane(int(v_lo), j));
-                ev[u] = __longlong_as_double((long long)vj);
-                o0[u] = uint32_t(pj >> sh0) & 0x7FFFu;
-                o1[u] = uint32_t(pj >> sh1) & 0x7FFFu;
-            }
-            double2 f1[U], f2[U];
-            bool closes[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-            {
-                const uint32_t prev = (u == 0) ? cur : o1[u - 1];
-                closes[u] = (i + u < n) && o1[u] != prev && prev != NONE;
-                if (i + u < n)
-                    f1[u] = *reinterpret_cast<const double2*>(F1 + size_t(o0[u]) * R + rr);
-                if (closes[u])
-                    f2[u] = *reinterpret_cast<const double2*>(F2 + size_t(prev) * R + rr);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-            {
-                if (i + u < n)
-                {
-                    if (closes[u])
-                    {
-                        acc0 += t0 * f2[u].x;
-                        acc1 += t1 * f2[u].y;
-                        t0 = t1 = 0.0;
-                    }
-                    cur = o1[u];
-                    t0 += ev[u] * f1[u].x;
-                    t1 += ev[u] * f1[u].y;
-                }
-            }
+#pragma nounroll
+            for (int i = 0; i < WAVE; i += U) batch(std::true_type{}, i, n, off1_l, off2_l);
+        }
+        else
+        {
+#pragma nounroll
+            for (int i = 0; i < n; i += U) batch(std::false_type{}, i, n, off1_l, off2_l);
         }
         pc = pcn;
         v = vn;
     }
     if (cur != NONE)
     {
-        const double2 f2 = *reinterpret_cast<const double2*>(F2 + size_t(cur) * R + rr);
+        const double2 f2 = row_load(rs2, cur);
         acc0 += t0 * f2.x;
         acc1 += t1 * f2.y;
     }
@@ -364,10 +405,21 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
     constexpr int UNROLL = CPTC_SPARSE3_UNROLL;
     const unsigned ry = unsigned((R + RT - 1) / RT);
     dim3 grid(unsigned(nblocks), ry);
-    if constexpr (RT == 128 && VEC == 2)
-        hipLaunchKernelGGL((mttkrp3_seg_wave_kernel<WAVES, CPTC_SPARSE3_WAVE_UNROLL>), grid,
-                           dim3(WAVE * WAVES), 0,
-                           s, mode, coords, vals, br, bs, bc, F1, F2, FtV, R);
+    // the wave-uniform kernel addresses rows by 32-bit byte offsets o * R * 8
+    // (o < 2^15), so it needs R * 8 * 2^15 < 2^31
+    if (RT == 128 && VEC == 2 && R <= 8000)
+    {
+        const dim3 block(WAVE * WAVES);
+        if (mode == 0)
+            hipLaunchKernelGGL((mttkrp3_seg_wave_kernel<0, WAVES, CPTC_SPARSE3_WAVE_UNROLL>), grid,
+                               block, 0, s, coords, vals, br, bs, bc, F1, F2, FtV, R);
+        else if (mode == 1)
+            hipLaunchKernelGGL((mttkrp3_seg_wave_kernel<1, WAVES, CPTC_SPARSE3_WAVE_UNROLL>), grid,
+                               block, 0, s, coords, vals, br, bs, bc, F1, F2, FtV, R);
+        else
+            hipLaunchKernelGGL((mttkrp3_seg_wave_kernel<2, WAVES, CPTC_SPARSE3_WAVE_UNROLL>), grid,
+                               block, 0, s, coords, vals, br, bs, bc, F1, F2, FtV, R);
+    }
     else
         hipLaunchKernelGGL((mttkrp3_seg_kernel<RT, VEC, WAVES, UNROLL>), grid,
                            dim3(WAVE * WAVES), 0, s, mode, coords, vals, br, bs, bc, F1, F2, FtV,
