@@ -99,18 +99,33 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     // row pointer Ff + (fb + 4q) R + rb
     const int boff = hi * R + lo;
     double bn[4], wn[16];
+    // interior tiles load factor values by buffer loads: the row block's
+    // byte offset in soffset (32-bit scalar arithmetic), the lane's offset
+    // in voffset; needs every row offset of both factors below 2^31
+    const bool buf = uint64_t(fdim) * uint64_t(R) * 8u < (uint64_t(1) << 31) &&
+                     uint64_t(wdim) * uint64_t(R) * 8u < (uint64_t(1) << 31);
+    const __amdgpu_buffer_rsrc_t rsf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(Ff), short(0), 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(Fw), short(0), 0x7FFFFFF0, 0x00020000);
+    const uint32_t vbo = uint32_t(boff) * 8u, vwo = uint32_t(lo) * 8u;
+    const uint32_t rowb = uint32_t(R) * 8u;
+    auto ld = [](const __amdgpu_buffer_rsrc_t& rs, uint32_t voff, uint32_t soff) {
+        return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0));
+    };
     auto load_factors = [&](size_t t, int rb) {
         const int b0 = hdr[HDR * t] * 16, b1 = hdr[HDR * t + 1] * 16, b2 = hdr[HDR * t + 2] * 16;
         const int fb = (MODE == 0) ? b1 : b0;
         const int wb = (MODE == 2) ? b1 : b2;
-        if (fb + 16 <= fdim && wb + 16 <= wdim && rb + 16 <= R)
+        if (buf && fb + 16 <= fdim && wb + 16 <= wdim && rb + 16 <= R)
         {
-            // interior tile, full rank block: unconditional loads from uniform
-            // row pointers (scalar base + per-lane offset)
+            // interior tile, full rank block: unconditional loads
+            const uint32_t so = (uint32_t(fb) * uint32_t(R) + uint32_t(rb)) * 8u;
+            const uint32_t sw = (uint32_t(wb) * uint32_t(R) + uint32_t(rb)) * 8u;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) bn[q] = (Ff + size_t(fb + 4 * q) * R + rb)[boff];
+            for (int q = 0; q < 4; ++q) bn[q] = ld(rsf, vbo, so + uint32_t(4 * q) * rowb);
 #pragma unroll
-            for (int x = 0; x < 16; ++x) wn[x] = (Fw + size_t(wb + x) * R + rb)[lo];
+            for (int x = 0; x < 16; ++x) wn[x] = ld(rsw, vwo, sw + uint32_t(x) * rowb);
         }
         else
         {
