@@ -154,6 +154,48 @@ def main() -> int:
     if not args.no_cpu and args.cpu_iters > 0:
         cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma)
 
+    if snnz:
+        roofline = {
+            "kernel": "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128]), per launch = "
+                      "one mode" if 64 < R <= 128 else
+                      "mttkrp3_seg_kernel (FP64 residual view), per launch = one mode",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "traffic_GBs": round(traffic_gbs, 1) if traffic_gbs else None,
+            "traffic_frac": round(traffic_gbs / HBM_PEAK_GBS, 4) if traffic_gbs else None,
+            "launch_ms": [round(x, 4) for x in launch_ms],
+            "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
+            "compulsory_bytes_per_launch": [int(b) for b in compulsory],
+            "note": "achieved = no-reuse gather model (every factor row read per nonzero) over "
+                    "the measured launch time; L2 and MALL serve most gathers, so it exceeds "
+                    "the HBM peak. traffic = rocprofv3 FETCH_SIZE*2.0 + WRITE_SIZE per launch "
+                    "(L2-miss bytes), traffic_GBs = traffic over the same launch time.",
+        }
+    else:
+        # no sparse residual (every nonzero in a dense tile): the MFMA tile
+        # kernel is the whole MTTKRP, 8192*R flops per tile per mode
+        ntiles = int(info.num_dense_tiles)
+        flops = 8192.0 * R * ntiles
+        tile_ms = [float(mt_ms[m]) / kit for m in range(3)]
+        tflops = flops * 3 / (sum(tile_ms) * 1e-3) / 1e12 if use_mfma and ntiles else 0.0
+        roofline = {
+            "kernel": "dense_tiles_kernel<mode,4,false,true> (16^3 tiles, FP32 MFMA, FP64 "
+                      "epilogue), per launch = one mode",
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "launch_ms": [round(x, 4) for x in tile_ms],
+            "flops_per_launch": flops,
+            "tile_bytes_per_launch": ntiles * 4096 * 4,
+        }
+
     line = {
         "metric": BASELINE_METRIC,
         "value": round(ms_per_step, 4),
@@ -179,24 +221,7 @@ def main() -> int:
         "mttkrp_gather_model_GBs": round(mtt_gbs, 1),
         "mttkrp_frac_of_hbm_peak": round(mtt_gbs / HBM_PEAK_GBS, 4),
         "fit_last": float(fits[-1]),
-        "roofline": {
-            "kernel": "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128]), per launch = one mode",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_GBs": round(traffic_gbs, 1) if traffic_gbs else None,
-            "traffic_frac": round(traffic_gbs / HBM_PEAK_GBS, 4) if traffic_gbs else None,
-            "launch_ms": [round(x, 4) for x in launch_ms],
-            "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
-            "compulsory_bytes_per_launch": [int(b) for b in compulsory],
-            "note": "achieved = no-reuse gather model (every factor row read per nonzero) over "
-                    "the measured launch time; L2 and MALL serve most gathers, so it exceeds "
-                    "the HBM peak. traffic = rocprofv3 FETCH_SIZE*2.0 + WRITE_SIZE per launch "
-                    "(L2-miss bytes), traffic_GBs = traffic over the same launch time.",
-        },
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     h.close()

@@ -29,6 +29,7 @@
 
 #include "cptc_hip.h"
 #include "hip_util.hpp"
+#include "host_util.hpp"
 #include "layout.hpp"
 
 namespace cptc {
@@ -222,7 +223,8 @@ int build_groups(Als3& h)
     for (int m = 0; m < 3; ++m)
     {
         size_t ng = 0;
-        CPTC_TRY(cptc_dense_groups(h.part.h_tiles4.data(), 4, nt, m, TILE_GROUP, order.data(),
+        const int cap = cptc::tile_group_cap(TILE_GROUP);
+        CPTC_TRY(cptc_dense_groups(h.part.h_tiles4.data(), 4, nt, m, cap, order.data(),
                                    goff.data(), &ng));
         CPTC_HIP(hipMalloc(&h.d_order[m], nt * sizeof(uint32_t)));
         CPTC_HIP(hipMalloc(&h.d_goff[m], (ng + 1) * sizeof(uint32_t)));

@@ -608,9 +608,10 @@ int build_unit_groups(const cptc::DevUnitsN& u, hipStream_t s, uint32_t* order[3
                             hipMemcpyDeviceToHost, s));
     CPTC_HIP(hipStreamSynchronize(s));
     std::vector<uint32_t> ord(nu), off(nu + 1);
+    const int cap = cptc::tile_group_cap(UNIT_GROUP);
     for (int q = 0; q < 3; ++q)
     {
-        CPTC_TRY(cptc_dense_groups(hdr.data(), 6, nu, q, UNIT_GROUP, ord.data(), off.data(), &ng[q]));
+        CPTC_TRY(cptc_dense_groups(hdr.data(), 6, nu, q, cap, ord.data(), off.data(), &ng[q]));
         CPTC_HIP(hipMalloc(&order[q], nu * sizeof(uint32_t)));
         CPTC_HIP(hipMalloc(&goff[q], (ng[q] + 1) * sizeof(uint32_t)));
         CPTC_HIP(hipMemcpyAsync(order[q], ord.data(), nu * sizeof(uint32_t), hipMemcpyHostToDevice, s));

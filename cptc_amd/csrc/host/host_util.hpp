@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -73,6 +74,20 @@ void radix_sort_pairs_u64(std::vector<uint64_t>& keys, std::vector<V>& vals, int
         keys.swap(k2);
         vals.swap(v2);
     }
+}
+
+// Group cap for the grouped MFMA tile / unit launches: a group of up to
+// `cap` tiles with one target row block is one wave, which sums the group in
+// LDS and issues one atomic per (row, rank) per group.  CPTC_TILE_GROUP=<n>
+// overrides the cap (tuning).
+inline int tile_group_cap(int cap)
+{
+    if (const char* e = std::getenv("CPTC_TILE_GROUP"))
+    {
+        const int g = std::atoi(e);
+        if (g >= 1) return g;
+    }
+    return cap;
 }
 
 }  // namespace cptc

@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <cstdlib>
 #include <vector>
 
 #include "../host/hip_util.hpp"
@@ -59,13 +60,19 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ goff, size_t ngroups,
     const double* __restrict__ A, const double* __restrict__ B, const double* __restrict__ C,
     const double* __restrict__ W, double* __restrict__ FtV, int R, int Rp, int dimI, int dimJ,
-    int dimK)
+    int dimK, int S)
 {
     extern __shared__ double gacc_lds[];
     // the wave index is uniform across the wave: say so, so that the tile
-    // loop, header loads and row pointers live in scalar registers
-    const size_t wid = size_t(blockIdx.x) * WAVES_PER_WG +
-                       size_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / WAVE)));
+    // loop, header loads and row pointers live in scalar registers.  S waves
+    // share one tile / group: wave slice s takes rank blocks s, s + S, ...
+    // (consecutive waves of a workgroup, so the tile cells they all read
+    // come from L1 / L2 after the first).
+    const size_t wall = size_t(blockIdx.x) * WAVES_PER_WG +
+                        size_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / WAVE)));
+    const size_t wid = wall / size_t(S);
+    const int rb0 = int(wall - wid * size_t(S)) * 16;
+    const int rstep = S * 16;
     size_t it0, it1;
     if constexpr (GROUPED)
     {
@@ -84,7 +91,7 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     const int hi = lane >> 4;
     double* gacc = gacc_lds + size_t(threadIdx.x / WAVE) * 16 * Rp;
     if constexpr (GROUPED)
-        for (int rb = 0; rb < R; rb += 16)
+        for (int rb = rb0; rb < R; rb += rstep)
 #pragma unroll
             for (int v = 0; v < 4; ++v) gacc[(4 * hi + v) * Rp + rb + lo] = 0.0;
 
@@ -169,10 +176,10 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     };
 
     size_t it = it0;
-    int rb = 0;
+    int rb = rb0;
     size_t t = tile_of(it);
     load_cells(t, cells);
-    load_factors(t, 0);
+    load_factors(t, rb0);
     int ob = 0;
     while (true)
     {
@@ -184,10 +191,10 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
         ob = hdr[HDR * t + MODE] * 16;
         const int r = rb + lo;
         size_t itn = it;
-        int rbn = rb + 16;
+        int rbn = rb + rstep;
         if (rbn >= R)
         {
-            rbn = 0;
+            rbn = rb0;
             ++itn;
         }
         const bool more = itn < it1;
@@ -196,7 +203,7 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
         // next tile's cells in registers (modes 0 / 1: mode 2's strided cell
         // loads leave no room for a second set)
         constexpr bool PF = GROUPED && MODE != 2;
-        const bool next_tile = PF && rb == 0 && it + 1 < it1;
+        const bool next_tile = PF && rb == rb0 && it + 1 < it1;
         if (next_tile) load_cells(tile_of(it + 1), ncells);
 
         floatx4 a0 = floatx4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
@@ -259,7 +266,7 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     }
     if constexpr (GROUPED)
     {
-        for (int rb2 = 0; rb2 < R; rb2 += 16)
+        for (int rb2 = rb0; rb2 < R; rb2 += rstep)
         {
             const int r = rb2 + lo;
             if (r >= R) continue;
@@ -321,6 +328,34 @@ namespace {
 
 constexpr int GROUP_LDS_MAX_R = 128;   // 4 waves x 16 rows x 128 ranks x 8 B = 64 KB
 
+// Rank-block split: S waves per tile / group (wave s takes the group's
+// 16-rank blocks s, s + S, ...; every (row, rank) is still summed by one
+// wave in the same order).  Used when the tiles or groups alone give fewer
+// waves than the chip has SIMDs; CPTC_TILE_SPLIT=<n> fixes it (tuning).
+int rank_split(size_t items, int R, hipStream_t s)
+{
+    const int nrb = (R + 15) / 16;
+    static const int fixed = [] {
+        const char* e = std::getenv("CPTC_TILE_SPLIT");
+        return e ? std::atoi(e) : 0;
+    }();
+    if (fixed > 0) return std::min(fixed, nrb);
+    static int simds[64] = {};
+    int dev = 0;
+    if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (simds[dev] == 0)
+    {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        simds[dev] = 4 * n;
+    }
+    const size_t want = size_t(simds[dev]);
+    if (items >= want) return 1;
+    return int(std::min<size_t>((want + items - 1) / items, size_t(nrb)));
+}
+
 template <int MODE, int HDR, bool HAS_W>
 int launch_tiles(const int32_t* hdr, const float* tiles, size_t ntiles, const uint32_t* order,
                  const uint32_t* goff, size_t ngroups, const double* A, const double* B,
@@ -329,23 +364,23 @@ int launch_tiles(const int32_t* hdr, const float* tiles, size_t ntiles, const ui
 {
     const dim3 block{WAVE * WAVES_PER_WG};
     const bool grouped = order && goff && ngroups > 0 && R <= GROUP_LDS_MAX_R;
+    const size_t items = grouped ? ngroups : ntiles;
+    const int S = rank_split(items, R, s);
+    const size_t wgs = (items * size_t(S) + WAVES_PER_WG - 1) / WAVES_PER_WG;
+    CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many tiles");
     if (grouped)
     {
         const int Rp = (R + 15) / 16 * 16;
-        const size_t wgs = (ngroups + WAVES_PER_WG - 1) / WAVES_PER_WG;
-        CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many groups");
         const size_t lds = size_t(WAVES_PER_WG) * 16 * Rp * sizeof(double);
         hipLaunchKernelGGL((dense_tiles_kernel<MODE, HDR, HAS_W, true>),
                            dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles, ntiles,
-                           order, goff, ngroups, A, B, C, W, FtV, R, Rp, dI, dJ, dK);
+                           order, goff, ngroups, A, B, C, W, FtV, R, Rp, dI, dJ, dK, S);
     }
     else
     {
-        const size_t wgs = (ntiles + WAVES_PER_WG - 1) / WAVES_PER_WG;
-        CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many tiles");
         hipLaunchKernelGGL((dense_tiles_kernel<MODE, HDR, HAS_W, false>),
                            dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ntiles,
-                           nullptr, nullptr, size_t(0), A, B, C, W, FtV, R, R, dI, dJ, dK);
+                           nullptr, nullptr, size_t(0), A, B, C, W, FtV, R, R, dI, dJ, dK, S);
     }
     CPTC_LAUNCHED();
     return CPTC_OK;

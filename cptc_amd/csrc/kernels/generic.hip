@@ -324,16 +324,18 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
 }
 
 // Ridge Cholesky + per-row substitution (generic.cu:746-819).  Every block
-// (one wave) factors FtF + eps I in registers: lane i holds row i, and step j
-// takes the pivot of lane j (readlane), scales column j and subtracts
-// L[i][j] L[k][j] from the trailing entries.  Each entry therefore receives
-// exactly the reference's sequence: (FtF + eps) minus the products for
-// k = 0, 1, ... in ascending order, then the division by the pivot.  L goes
-// to LDS; then each lane solves one row with its y / x vector in registers
-// (RT >= R, loops unrolled to RT with the ranks >= R switched off) while L is
-// read from LDS as a broadcast: the same k-ascending forward and backward
-// substitutions.  The grid covers the rows (every block factors FtF itself:
-// O(R^3 / 3) flops).
+// (one wave) factors FtF + eps I in registers: lane i holds row i.  Step j
+// broadcasts the pivot column through LDS, scales column j by the pivot's
+// square root and subtracts L[i][j] L[k][j] from the trailing entries.  Each
+// entry therefore receives exactly the reference's sequence: (FtF + eps)
+// minus the products for k = 0, 1, ... in ascending order, then the division
+// by the pivot.  Entries above the diagonal take the same updates without a
+// per-lane condition (they are never read), which keeps the unrolled code
+// at about one LDS read and one FMA per (j, k).  L goes to LDS; then each
+// lane solves one right-hand-side row with its y / x vector in LDS while L
+// is read as a broadcast: the same k-ascending forward and backward
+// substitutions.  The grid covers the rows (every block factors
+// FtF itself: O(R^3 / 3) flops).
 constexpr int CHOL_RM = 32;
 constexpr int CHOL_T = 64;
 
@@ -352,82 +354,66 @@ __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __rest
                                                             int R)
 {
     __shared__ double L[RT][RT + 1];
+    __shared__ double col[CHOL_T];
+    __shared__ double ys[RT][CHOL_T];
     const int tid = threadIdx.x;
-    const bool mine = tid < R;   // this lane holds row tid
+    const bool mine = tid < R;   // this lane holds row tid (rows >= R stay zero)
     double a[RT];
 #pragma unroll
     for (int k = 0; k < RT; ++k) a[k] = (mine && k < R) ? FtF[size_t(tid) * R + k] : 0.0;
-    // eps from the trace, summed in row order (the diagonal of row i is lane i's a[i])
+    // eps from the trace, summed in row order (the diagonal of row i is lane
+    // i's a[i]; rows >= R add exact zeros)
     double tr = 0.0;
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
-        if (i < R) tr += lane_double(a[i], i);
+    for (int i = 0; i < RT; ++i) tr += lane_double(a[i], i);
     const double eps = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
 #pragma unroll
     for (int i = 0; i < RT; ++i)
         if (tid == i) a[i] += eps;
+    // Padding rows R..RT-1 hold eps I: their steps give L[i][i] = sqrt(eps)
+    // and zeros elsewhere, and subtract exact zeros from the rows < R, so
+    // no loop below depends on R.
 #pragma unroll
     for (int j = 0; j < RT; ++j)
     {
-        if (j < R)
-        {
-            const double s = lane_double(a[j], j);
-            const double d = (s > 0.0) ? sqrt(s) : sqrt(eps);
-            if (tid == j) a[j] = d;
-            if (mine && tid > j) a[j] = a[j] / d;   // L[tid][j]
+        col[tid] = a[j];
+        __syncthreads();
+        const double s = col[j];
+        const double d = (s > 0.0) ? sqrt(s) : sqrt(eps);
+        a[j] = (tid == j) ? d : ((mine && tid > j) ? a[j] / d : a[j]);   // L[tid][j]
+        __syncthreads();
+        col[tid] = a[j];
+        __syncthreads();
+        // col[k] = L[k][j]
 #pragma unroll
-            for (int k = j + 1; k < RT; ++k)
-            {
-                if (k < R)
-                {
-                    const double lkj = lane_double(a[j], k);   // L[k][j]
-                    if (mine && tid >= k) a[k] -= a[j] * lkj;
-                }
-            }
-        }
+        for (int k = j + 1; k < RT; ++k) a[k] -= a[j] * col[k];
+        __syncthreads();
     }
-    if (mine)
+    // rows of L (entries above the diagonal are never read)
+    if (tid < RT)
 #pragma unroll
-        for (int k = 0; k < RT; ++k)
-            if (k <= tid) L[tid][k] = a[k];
-    __syncthreads();
-    // one row per lane (a row loop would let the compiler hoist all of L
-    // into registers)
+        for (int k = 0; k < RT; ++k) L[tid][k] = a[k];
+    // one right-hand-side row per lane, its y / x vector in LDS column tid
+    // (runtime loops over R keep this part of the code small): the
+    // reference's k-ascending forward and backward substitutions
     const size_t row = size_t(blockIdx.x) * CHOL_T + tid;
-    if (row < dim)
+    const bool live = row < dim;
+    for (int i = 0; i < R; ++i) ys[i][tid] = live ? FtV[row * R + i] : 0.0;
+    __syncthreads();
+    for (int i = 0; i < R; ++i)
     {
-        const double* b = FtV + row * R;
-        double y[RT];
-#pragma unroll
-        for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
-#pragma unroll
-        for (int i = 0; i < RT; ++i)
-        {
-            if (i < R)
-            {
-                double s = y[i];
-#pragma unroll
-                for (int k = 0; k < i; ++k) s -= L[i][k] * y[k];
-                y[i] = s / L[i][i];
-            }
-        }
-#pragma unroll
-        for (int i = RT - 1; i >= 0; --i)
-        {
-            if (i < R)
-            {
-                double s = y[i];
-#pragma unroll
-                for (int k = i + 1; k < RT; ++k)
-                    if (k < R) s -= L[k][i] * y[k];
-                y[i] = s / L[i][i];   // x[i]
-            }
-        }
-        double* out = F + row * R;
-#pragma unroll
-        for (int i = 0; i < RT; ++i)
-            if (i < R) out[i] = y[i];
+        double s = ys[i][tid];
+        for (int k = 0; k < i; ++k) s -= L[i][k] * ys[k][tid];
+        ys[i][tid] = s / L[i][i];
     }
+    for (int i = R - 1; i >= 0; --i)
+    {
+        double s = ys[i][tid];
+        for (int k = i + 1; k < R; ++k) s -= L[k][i] * ys[k][tid];
+        ys[i][tid] = s / L[i][i];   // x[i]
+    }
+    if (live)
+        for (int i = 0; i < R; ++i) F[row * R + i] = ys[i][tid];
 }
 
 // Column sums of squares: P partials of R each (deterministic).

@@ -267,6 +267,93 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
 }
 
 // ---------------------------------------------------------------------------
+// pinv, fast path for R <= 64: one wave, the matrix in registers.
+// Symmetric sweep (Beaton's SWEEP operator, i.e. Gauss-Jordan elimination
+// without pivoting in its symmetric form): sweeping pivot k maps
+//   a_kk -> -1 / a_kk,  a_ik -> a_ik / a_kk  (i != k),
+//   a_ij -> a_ij - a_ik a_kj / a_kk          (i, j != k),
+// and after every pivot the matrix holds -A^-1.  The matrix stays
+// symmetric, so pivot row k is column k.  The pivots are the LDL^T pivots
+// (the squared Cholesky diagonal), so the fast-path test is the Cholesky
+// one: a pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1 and
+// leaves Ainv to the Jacobi kernel.
+// Lane layout: RT >= R rows (16, 32 or 64), LPR = 64 / RT lanes per row,
+// each holding C = RT / LPR consecutive columns: lane = row + RT * part,
+// columns part * C .. part * C + C - 1.  Per pivot, the lanes owning column
+// k write it to LDS (one slot per row) and every lane reads its row's entry
+// and its C columns' entries back.
+// ---------------------------------------------------------------------------
+template <int RT>
+__global__ __launch_bounds__(WAVE) void sweep_inverse_kernel(const double* __restrict__ Ain, int R,
+                                                             double* __restrict__ Ainv,
+                                                             int* fallback)
+{
+    constexpr int LPR = WAVE / RT;
+    constexpr int C = RT / LPR;
+    __shared__ double col[RT];
+    const int lane = threadIdx.x;
+    const int row = lane % RT;
+    const int part = lane / RT;
+    const int c0 = part * C;
+    double a[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+        a[c] = (row < R && c0 + c < R) ? Ain[size_t(row) * R + c0 + c] : 0.0;
+    // largest diagonal entry: the lane holding (row, row) contributes it
+    double dg = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+        if (c0 + c == row) dg = a[c];
+    double md = dg;
+#pragma unroll
+    for (int o = WAVE / 2; o >= 1; o >>= 1) md = fmax(md, __shfl_xor(md, o));
+    const double tau = 1e-10 * md;
+    int ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
+    for (int k = 0; k < R && ok; ++k)
+    {
+        const int kp = k / C, kc = k - kp * C;
+        // column k (pre-sweep) through LDS: the owning lane of each row
+        double own = 0.0;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (c == kc) own = a[c];
+        if (part == kp) col[row] = own;
+        __syncthreads();
+        const double p = col[k];
+        if (!(p > tau) || !isfinite(p))
+        {
+            ok = 0;   // every lane read the same pivot: uniform exit
+            break;
+        }
+        const double ip = 1.0 / p;
+        const double f = col[row] * ip;        // a_ik / a_kk (1 on row k)
+        const bool prow = row == k;
+        const double g = prow ? 0.0 : f;
+        const double h = prow ? ip : 1.0;
+        double cj[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) cj[c] = col[c0 + c];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+        {
+            const double up = fma(-g, cj[c], a[c] * h);
+            a[c] = (part == kp && c == kc) ? (prow ? -ip : f) : up;
+        }
+        __syncthreads();
+    }
+    if (!ok)
+    {
+        if (lane == 0) *fallback = 1;
+        return;
+    }
+    if (lane == 0) *fallback = 0;
+    if (row < R)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (c0 + c < R) Ainv[size_t(row) * R + c0 + c] = -a[c];
+}
+
+// ---------------------------------------------------------------------------
 // pinv, exact path (runs only when *fallback != 0): parallel cyclic Jacobi
 // (round-robin pair ordering, Brent & Luk 1985) on A = V diag(l) V^T, then
 // Ainv = sum_{|l_i| > R ulp(max|l|)} v_i v_i^T / l_i — the truncated SVD
@@ -461,6 +548,32 @@ __global__ __launch_bounds__(256) void apply_kernel(const double* __restrict__ Y
             const double v = acc[p][q];
             F[i * R + c] = div ? v / div[c] : v;
         }
+    }
+}
+
+// F = FtV * Ainv for R <= 64: Ainv staged in LDS, one thread per output
+// entry (row x / R, column x % R); the R threads of a row read the same FtV
+// row.  Each entry is the same k-ascending FMA chain as apply_kernel's, so
+// the two give identical results.
+constexpr int APPLY_SMALL_R = 64;
+__global__ __launch_bounds__(256) void apply_small_kernel(const double* __restrict__ Y,
+                                                          const double* __restrict__ Ainv,
+                                                          double* __restrict__ F, size_t dim,
+                                                          int R, const double* __restrict__ div)
+{
+    __shared__ double sa[APPLY_SMALL_R * APPLY_SMALL_R];
+    for (int x = threadIdx.x; x < R * R; x += 256) sa[x] = Ainv[x];
+    __syncthreads();
+    const size_t n = dim * size_t(R);
+    for (size_t x = size_t(blockIdx.x) * 256 + threadIdx.x; x < n;
+         x += size_t(gridDim.x) * 256)
+    {
+        const size_t i = x / size_t(R);
+        const int c = int(x - i * size_t(R));
+        const double* __restrict__ y = Y + i * size_t(R);
+        double acc = 0.0;
+        for (int k = 0; k < R; ++k) acc = fma(y[k], sa[k * R + c], acc);
+        F[x] = div ? acc / div[c] : acc;
     }
 }
 
@@ -741,11 +854,41 @@ int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStre
                                      hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
         attr_set = true;
     }
-    hipLaunchKernelGGL(chol_inverse_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work,
-                       d_Ainv, flag, int(use_lds));
+    if (R <= 16)
+        hipLaunchKernelGGL(sweep_inverse_kernel<16>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+                           flag);
+    else if (R <= 32)
+        hipLaunchKernelGGL(sweep_inverse_kernel<32>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+                           flag);
+    else if (R <= 64)
+        hipLaunchKernelGGL(sweep_inverse_kernel<64>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+                           flag);
+    else
+        hipLaunchKernelGGL(chol_inverse_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R,
+                           work, d_Ainv, flag, int(use_lds));
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(jacobi_pinv_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work, V,
                        d_Ainv, flag, int(use_lds));
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+int apply_launch(const double* d_FtV, const double* d_Ainv, double* d_F, size_t dim, int R,
+                 const double* d_div, hipStream_t s)
+{
+    if (dim == 0) return CPTC_OK;
+    if (R <= APPLY_SMALL_R)
+    {
+        const unsigned grid = cptc::grid_for(dim * size_t(R), 256, 4096);
+        hipLaunchKernelGGL(apply_small_kernel, dim3(grid), dim3(256), 0, s, d_FtV, d_Ainv, d_F,
+                           dim, R, d_div);
+    }
+    else
+    {
+        dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
+        hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, s, d_FtV, d_Ainv, d_F, dim, R,
+                           d_div);
+    }
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
@@ -769,11 +912,7 @@ extern "C" int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double*
     CPTC_TRY(cptc::scratch_get(cptc::SCR_FLAGS, size_t(R) * R * sizeof(double) + 64, &buf));
     double* Ainv = static_cast<double*>(buf);
     CPTC_TRY(pinv_launch(d_FtF, Ainv, R, nullptr, s));
-    if (dim == 0) return CPTC_OK;
-    dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
-    hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, s, d_FtV, Ainv, d_F, dim, R, d_div);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    return apply_launch(d_FtV, Ainv, d_F, dim, R, d_div, s);
 }
 
 extern "C" int cptc_apply_pinv(const double* d_FtV, const double* d_Ainv, double* d_F,
@@ -781,12 +920,7 @@ extern "C" int cptc_apply_pinv(const double* d_FtV, const double* d_Ainv, double
 {
     CPTC_REQUIRE(R >= 1 && R <= 512 && d_FtV && d_Ainv && d_F, CPTC_ERR_ARG,
                  "cptc_apply_pinv: bad arguments (R %d, supported 1..512)", R);
-    if (dim == 0) return CPTC_OK;
-    dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
-    hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, cptc::as_stream(stream), d_FtV, d_Ainv,
-                       d_F, dim, R, d_div);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    return apply_launch(d_FtV, d_Ainv, d_F, dim, R, d_div, cptc::as_stream(stream));
 }
 
 namespace {

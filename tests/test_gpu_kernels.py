@@ -168,7 +168,7 @@ def test_gram(ca, dev, rows, R):
     assert rel_err(G.numpy(), F.T @ F) < 1e-13 if rows else np.all(G.numpy() == 0)
 
 
-@pytest.mark.parametrize("R", [1, 5, 16, 32, 128])
+@pytest.mark.parametrize("R", [1, 5, 16, 17, 32, 33, 63, 64, 65, 128])
 def test_solve_pinv_spd(ca, dev, R):
     rng = np.random.default_rng(R)
     Fa, Fb = rng.random((3 * R + 20, R)), rng.random((2 * R + 30, R))
@@ -191,12 +191,15 @@ def test_solve_pinv_spd(ca, dev, R):
     assert rel_err(out.numpy(), (Y @ inv) / lam) < 1e-9
 
 
-def test_pinv_singular_takes_jacobi_path(ca, orc, dev):
+@pytest.mark.parametrize("R", [24, 64, 100])
+def test_pinv_singular_takes_jacobi_path(ca, orc, dev, R):
+    """Rank-deficient FtF: the fast path (register sweep for R <= 64, blocked
+    Cholesky above) hands over to the Jacobi pseudoinverse."""
     rng = np.random.default_rng(3)
-    R = 24
-    F = rng.random((60, R))
+    F = rng.random((max(60, 2 * R), R))
     F[:, 7] = F[:, 3]
     F[:, 11] = 0.0
+    F[:, R - 1] = F[:, 0]
     A = F.T @ F
     dA = to_dev(ca, A)
     Ainv = zeros(ca, (R, R))
