@@ -176,6 +176,8 @@ SIGNATURES = {
                                   _I, _P]),
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
+    "cptc_chol_ridge_factor": (_I, [_P, _P, _I, _P]),
+    "cptc_chol_ridge_apply": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_gen_normalize": (_I, [_P, _Z, _I, _P, _P]),
     "cptc_residual_nd": (_I, [_I, _P, _P, _U64, _P, _P, _I, _P, _P]),
     "cptc_gen_default_opts": (None, [C.POINTER(GenOpts)]),

@@ -9,9 +9,9 @@
 //     pseudoinverse of FtF run on the side streams while the FP64 residual
 //     runs on the main one (both MTTKRP halves add into FtV atomically, the
 //     pseudoinverse only reads FtF), and the main stream joins them before
-//     the factor update.  No host synchronisation inside an iteration; the
-//     host waits once per iteration for the fit.  ALS_SERIAL=1 queues
-//     everything on the main stream;
+//     the factor update, when the work is large enough to pay for the
+//     cross-stream waits (choose_overlap).  No host synchronisation inside
+//     an iteration.  ALS_SERIAL=1 queues everything on the main stream;
 //   * Grams are cached per mode and refreshed right after that mode's update
 //     (the reference recomputes the same matrices from the same factors);
 //   * the solve is an on-device pseudoinverse (Cholesky inverse with an exact
@@ -147,6 +147,19 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
     if (h.overlap && dense) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
     return CPTC_OK;
+}
+
+// Side streams only pay when both sides of the fork run long: each fork /
+// join costs ~20 us of cross-queue waits here.  Measured on MI355X: config 1
+// (tiles only, R = 32) 0.31 ms per iteration overlapped vs 0.26 serial,
+// config 2 (3 M FP64 nonzeros, R = 32) equal, config 3 (37.8 M FP64
+// nonzeros + 82 k tiles, R = 128) 11.7 vs 15.5.  Overlap when the FP64
+// MTTKRP streams at least 2^28 nonzero-ranks or the pseudoinverse takes the
+// blocked Cholesky (R > 64, >= 0.1 ms); ALS_SERIAL=1 forces one stream.
+void choose_overlap(Als3& h)
+{
+    const double work = double(h.views.nnz + h.dviews.nnz) * double(h.R);
+    h.overlap = env_flag("ALS_SERIAL") == 0 && (h.R > 64 || work >= double(1u << 28));
 }
 
 // The main stream, the two side streams and the driver's events.
@@ -375,6 +388,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     }
 
     CPTC_TRY(build_groups(*h));
+    choose_overlap(*h);
     CPTC_TRY(alloc_buffers(*h));
     if (o.verbose)
         std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
@@ -585,6 +599,7 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
     };
     step(init_streams(*h));
     if (rc == CPTC_OK) step(build_groups(*h));
+    choose_overlap(*h);
     if (rc == CPTC_OK) step(alloc_buffers(*h));
     std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
     if (rc == CPTC_OK) step(run(*h, iters, fits.data(), nullptr, nullptr));

@@ -325,6 +325,7 @@ struct Gen
     double x2 = 0.0;
 
     hipStream_t s = nullptr;
+    double* d_L = nullptr;          // R x R Cholesky factor of FtF + eps I
     uint32_t* d_coords = nullptr;   // N x nnz (reordered)
     double* d_vals = nullptr;
     std::vector<double*> d_F;
@@ -389,6 +390,7 @@ struct Gen
             if (e) (void)hipEventDestroy(e);
         for (auto& e : ev_pool) (void)hipEventDestroy(e);
         dfree(d_fit_hist);
+        dfree(d_L);
         if (s) (void)hipStreamDestroy(s);
     }
 
@@ -475,10 +477,17 @@ struct Gen
             mark(mk++);
             CPTC_TRY(mttkrp(n));
             mark(mk++);
+            // One stream: factoring FtF on a second stream beside the MTTKRP
+            // measured slower (configs 4 and 5: 0.545 -> 0.60 and 1.54 ->
+            // 1.58 ms per iteration) because the cross-stream waits cost
+            // more than the factorization.
             if (opts.svd)
                 CPTC_TRY(cptc_solve_pinv(d_FtF, d_FtV, d_F[n], dims[n], R, nullptr, s));
             else
-                CPTC_TRY(cptc_chol_ridge_solve(d_FtF, d_FtV, d_F[n], dims[n], R, s));
+            {
+                CPTC_TRY(cptc_chol_ridge_factor(d_FtF, d_L, R, s));
+                CPTC_TRY(cptc_chol_ridge_apply(d_L, d_FtV, d_F[n], dims[n], R, s));
+            }
             mark(mk++);
             CPTC_TRY(cptc_gen_normalize(d_F[n], dims[n], R, d_lambda, s));
             CPTC_TRY(cptc_gram(d_F[n], dims[n], R, d_grams + size_t(n) * RR, s));
@@ -806,6 +815,7 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
     }
     GEN_TRY(dmalloc(&g->d_grams, RR * N));
     GEN_TRY(dmalloc(&g->d_FtF, RR));
+    GEN_TRY(dmalloc(&g->d_L, RR));
     GEN_TRY(dmalloc(&g->d_FtV, g->maxdim * R));
     GEN_TRY(dmalloc(&g->d_out2, size_t(2)));
 

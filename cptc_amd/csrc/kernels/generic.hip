@@ -323,19 +323,23 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
     }
 }
 
-// Ridge Cholesky + per-row substitution (generic.cu:746-819).  Every block
-// (one wave) factors FtF + eps I in registers: lane i holds row i.  Step j
-// broadcasts the pivot column through LDS, scales column j by the pivot's
-// square root and subtracts L[i][j] L[k][j] from the trailing entries.  Each
-// entry therefore receives exactly the reference's sequence: (FtF + eps)
-// minus the products for k = 0, 1, ... in ascending order, then the division
-// by the pivot.  Entries above the diagonal take the same updates without a
-// per-lane condition (they are never read), which keeps the unrolled code
-// at about one LDS read and one FMA per (j, k).  L goes to LDS; then each
-// lane solves one right-hand-side row with its y / x vector in LDS while L
-// is read as a broadcast: the same k-ascending forward and backward
-// substitutions.  The grid covers the rows (every block factors
-// FtF itself: O(R^3 / 3) flops).
+// Ridge Cholesky + per-row substitution (generic.cu:746-819), in two
+// kernels so that a driver can factor FtF while the MTTKRP that produces
+// FtV is still running.
+//
+// chol_factor_kernel (one wave) factors FtF + eps I in registers: lane i
+// holds row i.  Step j broadcasts the pivot column through LDS, scales
+// column j by the pivot's square root and subtracts L[i][j] L[k][j] from the
+// trailing entries.  Each entry therefore receives exactly the reference's
+// sequence: (FtF + eps) minus the products for k = 0, 1, ... in ascending
+// order, then the division by the pivot.  Entries above the diagonal take
+// the same updates without a per-lane condition (they are never read),
+// which keeps the unrolled code at about one LDS read and one FMA per
+// (j, k).  L (R x R row-major, zeros above the diagonal) goes to global.
+//
+// chol_apply_kernel stages L in LDS and solves one right-hand-side row per
+// lane, its y / x vector in LDS column `lane`: the reference's k-ascending
+// forward and backward substitutions.
 constexpr int CHOL_RM = 32;
 constexpr int CHOL_T = 64;
 
@@ -348,14 +352,10 @@ __device__ __forceinline__ double lane_double(double v, int l)
 }
 
 template <int RT>
-__global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __restrict__ FtF,
-                                                            const double* __restrict__ FtV,
-                                                            double* __restrict__ F, size_t dim,
-                                                            int R)
+__global__ __launch_bounds__(CHOL_T) void chol_factor_kernel(const double* __restrict__ FtF,
+                                                             int R, double* __restrict__ Lout)
 {
-    __shared__ double L[RT][RT + 1];
     __shared__ double col[CHOL_T];
-    __shared__ double ys[RT][CHOL_T];
     const int tid = threadIdx.x;
     const bool mine = tid < R;   // this lane holds row tid (rows >= R stay zero)
     double a[RT];
@@ -389,13 +389,21 @@ __global__ __launch_bounds__(CHOL_T) void chol_ridge_kernel(const double* __rest
         for (int k = j + 1; k < RT; ++k) a[k] -= a[j] * col[k];
         __syncthreads();
     }
-    // rows of L (entries above the diagonal are never read)
-    if (tid < RT)
+    if (mine)
 #pragma unroll
-        for (int k = 0; k < RT; ++k) L[tid][k] = a[k];
-    // one right-hand-side row per lane, its y / x vector in LDS column tid
-    // (runtime loops over R keep this part of the code small): the
-    // reference's k-ascending forward and backward substitutions
+        for (int k = 0; k < RT; ++k)
+            if (k < R) Lout[size_t(tid) * R + k] = (k <= tid) ? a[k] : 0.0;
+}
+
+__global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __restrict__ Lg,
+                                                            const double* __restrict__ FtV,
+                                                            double* __restrict__ F, size_t dim,
+                                                            int R)
+{
+    __shared__ double L[CHOL_RM][CHOL_RM + 1];
+    __shared__ double ys[CHOL_RM][CHOL_T];
+    const int tid = threadIdx.x;
+    for (int x = tid; x < R * R; x += CHOL_T) L[x / R][x % R] = Lg[x];
     const size_t row = size_t(blockIdx.x) * CHOL_T + tid;
     const bool live = row < dim;
     for (int i = 0; i < R; ++i) ys[i][tid] = live ? FtV[row * R + i] : 0.0;
@@ -637,27 +645,47 @@ extern "C" int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, in
     return CPTC_OK;
 }
 
+extern "C" int cptc_chol_ridge_factor(const double* d_FtF, double* d_L, int R, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= CHOL_RM, CPTC_ERR_ARG, "cptc_chol_ridge_factor: R %d (1..32)", R);
+    CPTC_REQUIRE(d_FtF && d_L, CPTC_ERR_ARG, "cptc_chol_ridge_factor: null pointer");
+    hipStream_t s = cptc::as_stream(stream);
+    if (R <= 8)
+        hipLaunchKernelGGL(chol_factor_kernel<8>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R, d_L);
+    else if (R <= 16)
+        hipLaunchKernelGGL(chol_factor_kernel<16>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R, d_L);
+    else
+        hipLaunchKernelGGL(chol_factor_kernel<CHOL_RM>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R,
+                           d_L);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_chol_ridge_apply(const double* d_L, const double* d_FtV, double* d_F,
+                                     size_t dim, int R, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= CHOL_RM, CPTC_ERR_ARG, "cptc_chol_ridge_apply: R %d (1..32)", R);
+    if (dim == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_L && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_apply: null pointer");
+    CPTC_REQUIRE(dim / CHOL_T < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_chol_ridge_apply: %zu rows", dim);
+    hipLaunchKernelGGL(chol_apply_kernel, dim3(unsigned((dim + CHOL_T - 1) / CHOL_T)),
+                       dim3(CHOL_T), 0, cptc::as_stream(stream), d_L, d_FtV, d_F, dim, R);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
 extern "C" int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, double* d_F,
                                      size_t dim, int R, void* stream)
 {
-    CPTC_REQUIRE(R >= 1 && R <= 32, CPTC_ERR_ARG, "cptc_chol_ridge_solve: R %d (1..32)", R);
+    CPTC_REQUIRE(R >= 1 && R <= CHOL_RM, CPTC_ERR_ARG, "cptc_chol_ridge_solve: R %d (1..32)", R);
     if (dim == 0) return CPTC_OK;
     CPTC_REQUIRE(d_FtF && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_solve: null pointer");
-    CPTC_REQUIRE(dim / CHOL_T < (size_t(1) << 31), CPTC_ERR_ARG,
-                 "cptc_chol_ridge_solve: %zu rows", dim);
-    const dim3 grid(unsigned((dim + CHOL_T - 1) / CHOL_T));
-    hipStream_t s = cptc::as_stream(stream);
-    if (R <= 8)
-        hipLaunchKernelGGL(chol_ridge_kernel<8>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F, dim,
-                           R);
-    else if (R <= 16)
-        hipLaunchKernelGGL(chol_ridge_kernel<16>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F,
-                           dim, R);
-    else
-        hipLaunchKernelGGL(chol_ridge_kernel<CHOL_RM>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F,
-                           dim, R);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, size_t(R) * R * sizeof(double), &buf));
+    double* L = static_cast<double*>(buf);
+    CPTC_TRY(cptc_chol_ridge_factor(d_FtF, L, R, stream));
+    return cptc_chol_ridge_apply(L, d_FtV, d_F, dim, R, stream);
 }
 
 extern "C" int cptc_gen_normalize(double* d_F, size_t rows, int R, double* d_lambda, void* stream)

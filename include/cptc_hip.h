@@ -423,9 +423,19 @@ int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double
 
 /* F = FtV (FtF + eps I)^-1 per row by Cholesky, eps = 1e-12 * tr(FtF) / R +
  * 1e-300 (tr <= 0: 1e-12 + 1e-300); a pivot s <= 0 becomes sqrt(eps).
- * g_chol_solve_kernel, generic.cu:746-819.  R <= 32. */
+ * g_chol_solve_kernel, generic.cu:746-819.  R <= 32.  Runs
+ * cptc_chol_ridge_factor into library scratch, then cptc_chol_ridge_apply. */
 int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
                           int R, void* stream);
+
+/* The two halves of cptc_chol_ridge_solve, so that the factorization can run
+ * while FtV is still being computed: d_L (R x R row-major, zeros above the
+ * diagonal) = the Cholesky factor of FtF + eps I (generic.cu:752-785), then
+ * F = FtV (L L^T)^-1 by the per-row forward and backward substitutions
+ * (generic.cu:788-818).  R <= 32. */
+int cptc_chol_ridge_factor(const double* d_FtF, double* d_L, int R, void* stream);
+int cptc_chol_ridge_apply(const double* d_L, const double* d_FtV, double* d_F, size_t dim, int R,
+                          void* stream);
 
 /* n_r = ||F[:, r]||_2 (non-finite or < 1e-14: 1); F[:, r] /= n_r;
  * lambda[r] = n_r.  g_col_norms2 + g_norms_finalize + g_normalize +

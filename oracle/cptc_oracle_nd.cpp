@@ -3,6 +3,7 @@
 #include "cptc_oracle_nd.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -287,8 +288,20 @@ void mttkrp_seg_nd(const CooN& t, const ViewN& v, int n, bool use_skip,
 {
     const int N = t.N;
     const size_t nnz = t.nnz();
+    // OpenMP over rows: a row's segments are consecutive and stay with one
+    // thread in view order, so every output entry sees the serial sequence
+    const size_t nseg = v.row[n].size();
+    std::vector<size_t> grp;
+    for (size_t s = 0; s < nseg; ++s)
+        if (s == 0 || v.row[n][s] != v.row[n][s - 1]) grp.push_back(s);
+    grp.push_back(nseg);
+    const size_t ngrp = grp.size() - 1;
+#pragma omp parallel
+    {
     std::vector<double> acc(static_cast<size_t>(R));
-    for (size_t s = 0; s < v.row[n].size(); ++s)
+#pragma omp for schedule(dynamic, 16)
+    for (size_t gi = 0; gi < ngrp; ++gi)
+    for (size_t s = grp[gi]; s < grp[gi + 1]; ++s)
     {
         std::fill(acc.begin(), acc.end(), 0.0);
         for (uint32_t e = v.start[n][s]; e < v.start[n][s] + v.cnt[n][s]; ++e)
@@ -316,6 +329,7 @@ void mttkrp_seg_nd(const CooN& t, const ViewN& v, int n, bool use_skip,
                 out[r] += acc[r];
         }
     }
+    }
 }
 
 // generic.cu:429-561, exact FP64
@@ -329,11 +343,25 @@ void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
     // slots: sl = target, p = contracted, q = sliced (generic.cu:500-540)
     const int p = (sl + 1) % 3, q = (sl + 2) % 3;
     const int mp = u.inner[p], mq = u.inner[q];
-    std::vector<double> T(4096), w(static_cast<size_t>(R)), acc(16 * static_cast<size_t>(R));
     const int N = t.N;
-    for (size_t k = 0; k < u.n_units(); ++k)
+    // OpenMP over units: each unit's 16 x R contribution is computed into its
+    // own buffer slot in parallel, then the slots are added to FtV in unit
+    // order, so every output entry sees the serial sequence.  Chunks of
+    // units bound the buffer.
+    constexpr size_t CHUNK = 4096;
+    const size_t RU = 16 * static_cast<size_t>(R);
+    std::vector<double> part(CHUNK * RU);
+    for (size_t c0 = 0; c0 < u.n_units(); c0 += CHUNK)
+    {
+    const size_t c1 = std::min(u.n_units(), c0 + CHUNK);
+#pragma omp parallel
+    {
+    std::vector<double> T(4096), w(static_cast<size_t>(R));
+#pragma omp for schedule(dynamic, 8)
+    for (size_t k = c0; k < c1; ++k)
     {
         const uint32_t* U = &u.unit6[6 * k];
+        double* acc = &part[(k - c0) * RU];
         std::fill(T.begin(), T.end(), 0.0);
         for (uint32_t e = 0; e < U[3]; ++e) T[u.lid[U[4] + e]] += u.val[U[4] + e];
         std::fill(w.begin(), w.end(), 1.0);
@@ -342,7 +370,7 @@ void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
             const uint32_t c = u.outer_coords[U[5] + oq];
             for (int r = 0; r < R; ++r) w[r] *= F[u.outer[oq]][size_t(c) * R + r];
         }
-        std::fill(acc.begin(), acc.end(), 0.0);
+        std::fill(acc, acc + RU, 0.0);
         const int base[3] = {int(U[0]) * 16, int(U[1]) * 16, int(U[2]) * 16};
         for (int lt = 0; lt < 16; ++lt)
             for (int lq = 0; lq < 16; ++lq)
@@ -364,12 +392,20 @@ void mttkrp_units_nd(const CooN& t, const UnitsN& u, int n,
                     acc[size_t(lt) * R + r] += g * F[mq][size_t(base[q] + lq) * R + r] * w[r];
                 }
             }
+    }
+    }
+    for (size_t k = c0; k < c1; ++k)
+    {
+        const uint32_t* U = &u.unit6[6 * k];
+        const double* acc = &part[(k - c0) * RU];
+        const int b0 = int(U[sl]) * 16;
         for (int lt = 0; lt < 16; ++lt)
         {
-            const int row = base[sl] + lt;
+            const int row = b0 + lt;
             if (row >= int(t.dims[n])) continue;
             for (int r = 0; r < R; ++r) FtV[size_t(row) * R + r] += acc[size_t(lt) * R + r];
         }
+    }
     }
 }
 
@@ -457,6 +493,7 @@ void als_nd(const CooN& t, const std::vector<std::vector<uint32_t>>& rank, const
     std::vector<double> FtF(RR), FtV(maxdim * R), Ainv(RR);
     for (int it = 0; it < iters; ++it)
     {
+        const auto t_it = std::chrono::steady_clock::now();
         for (int n = 0; n < N; ++n)
         {
             std::fill(FtF.begin(), FtF.end(), 1.0);
@@ -513,6 +550,9 @@ void als_nd(const CooN& t, const std::vector<std::vector<uint32_t>>& rank, const
         st.fits.push_back(Xn > 0.0 ? 1.0 - std::sqrt(res) / Xn : 0.0);
         st.iprod.push_back(iprod);
         st.model2.push_back(model2);
+        st.ms.push_back(
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_it)
+                .count());
     }
 }
 

@@ -100,6 +100,7 @@ struct AlsNState
     std::vector<std::vector<double>> F;
     std::vector<double> lambda;
     std::vector<double> fits, iprod, model2;
+    std::vector<double> ms;   // wall time of each iteration (CPU baseline)
 };
 
 // generic.cu:1639-2366 over a tensor that is already reordered; `rank` (old ->

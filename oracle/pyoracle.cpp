@@ -420,6 +420,24 @@ PYBIND11_MODULE(cptc_oracle, m)
     }, py::arg("coords"), py::arg("vals"), py::arg("dims"), py::arg("rank"), py::arg("R"),
        py::arg("seed"), py::arg("svd"), py::arg("dense"), py::arg("thr"), py::arg("iters"),
        py::arg("inner") = std::array<int, 3>{0, 1, 2});
+    // als_nd's fits and per-iteration wall times (ms): the generic CPU baseline
+    m.def("als_nd_timed", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims,
+                             py::list rank, int R, unsigned seed, double thr, int iters) {
+        CooN t = coon_from(coords, vals, dims);
+        std::vector<std::vector<uint32_t>> rk;
+        for (auto r : rank) rk.push_back(vec(r.cast<arr<uint32_t>>()));
+        AlsNOpts o;
+        o.R = R;
+        o.seed = seed;
+        o.dense = true;
+        o.threshold = thr;
+        AlsNState st;
+        {
+            py::gil_scoped_release rel;
+            als_nd(t, rk, o, iters, st);
+        }
+        return py::make_tuple(np(st.fits), np(st.ms));
+    });
     m.def("residual_nd", [](arr<uint32_t> coords, arr<double> vals, py::sequence dims, py::list F,
                             arr<double> lam, int R) {
         CooN t = coon_from(coords, vals, dims);

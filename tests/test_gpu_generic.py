@@ -367,6 +367,34 @@ def test_chol_ridge_solve(ca, orc, dev, R):
     assert rel_err(out.numpy(), ref) <= 1e-11
 
 
+@pytest.mark.parametrize("R", [1, 7, 16, 17, 32])
+def test_chol_ridge_factor_apply(ca, dev, R):
+    """The two halves of the ridge solve: L is the Cholesky factor of
+    FtF + eps I (eps = 1e-12 tr / R + 1e-300), and factor + apply gives the
+    same bits as cptc_chol_ridge_solve."""
+    rng = np.random.default_rng(100 + R)
+    A = rng.random((3 * R + 5, R))
+    FtF = A.T @ A
+    Y = rng.standard_normal((150, R))
+    dA, dY = dbuf(ca, FtF), dbuf(ca, Y)
+    L = ca.DevBuf.zeros((R, R))
+    out = ca.DevBuf.zeros((150, R))
+    ref = ca.DevBuf.zeros((150, R))
+    assert ca.lib.cptc_chol_ridge_factor(dA.data_ptr(), L.data_ptr(), R, None) == 0
+    assert ca.lib.cptc_chol_ridge_apply(L.data_ptr(), dY.data_ptr(), out.data_ptr(), 150, R,
+                                        None) == 0
+    assert ca.lib.cptc_chol_ridge_solve(dA.data_ptr(), dY.data_ptr(), ref.data_ptr(), 150, R,
+                                        None) == 0
+    ca.sync()
+    eps = 1e-12 * np.trace(FtF) / R + 1e-300
+    Lref = np.linalg.cholesky(FtF + eps * np.eye(R))
+    Lg = L.numpy()
+    assert np.all(np.triu(Lg, 1) == 0.0)
+    assert rel_err(Lg, Lref) <= 1e-12
+    assert np.array_equal(out.numpy(), ref.numpy())
+    assert rel_err(out.numpy(), np.linalg.solve(FtF + eps * np.eye(R), Y.T).T) <= 1e-10
+
+
 def test_chol_ridge_singular_pivot(ca, orc, dev):
     """A rank-deficient FtF hits the s <= 0 -> sqrt(eps) branch."""
     R = 6
@@ -516,9 +544,10 @@ def test_selftest(ca, dev):
     assert ca.gen_selftest(verbose=True) == 0
 
 
+@pytest.mark.timeout(300)
 def test_config4_full_size(ca, orc, dev):
-    """Config 4 (3.3 M elements, order 4, R = 16): layout bit-exact, MTTKRP of
-    every mode, three iterations' fit against the oracle."""
+    """Config 4 (3.3 M elements, order 4, R = 16): layout bit-exact, 20
+    iterations' fit against the oracle."""
     t = ca.synth_config(4)
     R = 16
     g = ca.Gen(t, R=R)
@@ -531,8 +560,32 @@ def test_config4_full_size(ca, orc, dev):
     got = g.units()
     assert np.array_equal(got["is_dense"], u["is_dense"])
     assert np.array_equal(got["lid"], u["lid"])
-    fit, _, _, _ = g.run(3)
-    rfit = orc.als_nd(ridx, t.val, t.dims, rrank, R, 42, False, True, 0.03, 3)[0]
+    fit, _, _, _ = g.run(20)
+    rfit = orc.als_nd(ridx, t.val, t.dims, rrank, R, 42, False, True, 0.03, 20)[0]
+    assert np.max(np.abs(fit - rfit)) <= 1e-4, (fit, rfit)
+
+
+@pytest.mark.timeout(600)
+def test_config5_full_size(ca, orc, dev):
+    """Config 5 (20 M elements, order 5, R = 32, 32 768 dense units): device
+    reorder and units bit-exact, 20 iterations' fit against the oracle."""
+    t = ca.synth_config(5)
+    R = 32
+    g = ca.Gen(t, R=R)
+    print(f"[cfg5] nnz {t.nnz} units {int(g.info.n_units)}", flush=True)
+    ridx, rrank = orc.reorder_nd(t.idx, t.val, t.dims, "hits", 3, 8000000)
+    assert np.array_equal(g.coords(), ridx)
+    for m in range(5):
+        assert np.array_equal(g.rank(m), rrank[m]), m
+    u = orc.dense_nd(ridx, t.val, t.dims, 0.03)
+    assert int(g.info.n_units) == len(u["unit6"])
+    got = g.units()
+    assert np.array_equal(got["unit6"].ravel(), np.asarray(u["unit6"]).ravel())
+    assert np.array_equal(got["is_dense"], u["is_dense"])
+    fit, _, _, _ = g.run(20)
+    g.close()
+    rfit = orc.als_nd(ridx, t.val, t.dims, rrank, R, 42, False, True, 0.03, 20)[0]
+    print(f"[cfg5] fit {fit[-1]:.10f} oracle {rfit[-1]:.10f}", flush=True)
     assert np.max(np.abs(fit - rfit)) <= 1e-4, (fit, rfit)
 
 
