@@ -267,9 +267,10 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
 }
 
 // ---------------------------------------------------------------------------
-// pinv, fast path for R <= 64: one wave, the matrix in registers.
-// Symmetric sweep (Beaton's SWEEP operator, i.e. Gauss-Jordan elimination
-// without pivoting in its symmetric form): sweeping pivot k maps
+// pinv, fast path for R <= 64: one workgroup of SWEEP_T threads, the matrix
+// in registers.  Symmetric sweep (Beaton's SWEEP operator, i.e.
+// Gauss-Jordan elimination without pivoting in its symmetric form):
+// sweeping pivot k maps
 //   a_kk -> -1 / a_kk,  a_ik -> a_ik / a_kk  (i != k),
 //   a_ij -> a_ij - a_ik a_kj / a_kk          (i, j != k),
 // and after every pivot the matrix holds -A^-1.  The matrix stays
@@ -277,76 +278,84 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
 // (the squared Cholesky diagonal), so the fast-path test is the Cholesky
 // one: a pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1 and
 // leaves Ainv to the Jacobi kernel.
-// Lane layout: RT >= R rows (16, 32 or 64), LPR = 64 / RT lanes per row,
-// each holding C = RT / LPR consecutive columns: lane = row + RT * part,
-// columns part * C .. part * C + C - 1.  Per pivot, the lanes owning column
-// k write it to LDS (one slot per row) and every lane reads its row's entry
-// and its C columns' entries back.
+// Thread layout: RT >= R rows (16, 32 or 64), LPR = SWEEP_T / RT threads
+// per row, each holding C = RT / LPR consecutive columns: thread = row + RT
+// * part, columns part * C .. part * C + C - 1 (C = 1, 4, 16).  Per pivot
+// the threads owning column k write it to LDS (one slot per row) and every
+// thread reads its row's entry and its C columns' entries back.
 // ---------------------------------------------------------------------------
+constexpr int SWEEP_T = 256;
+
 template <int RT>
-__global__ __launch_bounds__(WAVE) void sweep_inverse_kernel(const double* __restrict__ Ain, int R,
-                                                             double* __restrict__ Ainv,
-                                                             int* fallback)
+__global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __restrict__ Ain,
+                                                                int R,
+                                                                double* __restrict__ Ainv,
+                                                                int* fallback)
 {
-    constexpr int LPR = WAVE / RT;
+    constexpr int LPR = SWEEP_T / RT;
     constexpr int C = RT / LPR;
+    static_assert(C >= 1 && C <= 16, "sweep layout");
     __shared__ double col[RT];
-    const int lane = threadIdx.x;
-    const int row = lane % RT;
-    const int part = lane / RT;
+    __shared__ double wmax[SWEEP_T / WAVE];
+    const int tid = threadIdx.x;
+    const int row = tid % RT;
+    const int part = tid / RT;
     const int c0 = part * C;
     double a[C];
 #pragma unroll
     for (int c = 0; c < C; ++c)
         a[c] = (row < R && c0 + c < R) ? Ain[size_t(row) * R + c0 + c] : 0.0;
-    // largest diagonal entry: the lane holding (row, row) contributes it
-    double dg = 0.0;
+    // largest diagonal entry: the thread holding (row, row) contributes it
+    double md = 0.0;
 #pragma unroll
     for (int c = 0; c < C; ++c)
-        if (c0 + c == row) dg = a[c];
-    double md = dg;
+        if (c0 + c == row) md = a[c];
 #pragma unroll
     for (int o = WAVE / 2; o >= 1; o >>= 1) md = fmax(md, __shfl_xor(md, o));
+    if ((tid & (WAVE - 1)) == 0) wmax[tid / WAVE] = md;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < SWEEP_T / WAVE; ++w) md = fmax(md, wmax[w]);
     const double tau = 1e-10 * md;
     int ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
-    for (int k = 0; k < R && ok; ++k)
+    for (int kp = 0; kp < LPR && ok; ++kp)
     {
-        const int kp = k / C, kc = k - kp * C;
-        // column k (pre-sweep) through LDS: the owning lane of each row
-        double own = 0.0;
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-            if (c == kc) own = a[c];
-        if (part == kp) col[row] = own;
-        __syncthreads();
-        const double p = col[k];
-        if (!(p > tau) || !isfinite(p))
+        for (int kc = 0; kc < C; ++kc)
         {
-            ok = 0;   // every lane read the same pivot: uniform exit
-            break;
-        }
-        const double ip = 1.0 / p;
-        const double f = col[row] * ip;        // a_ik / a_kk (1 on row k)
-        const bool prow = row == k;
-        const double g = prow ? 0.0 : f;
-        const double h = prow ? ip : 1.0;
-        double cj[C];
+            const int k = kp * C + kc;
+            if (k >= R) break;
+            if (part == kp) col[row] = a[kc];
+            __syncthreads();
+            const double p = col[k];
+            if (!(p > tau) || !isfinite(p))
+            {
+                ok = 0;   // every thread read the same pivot: uniform exit
+                break;
+            }
+            const double ip = 1.0 / p;
+            const double f = col[row] * ip;    // a_ik / a_kk (1 on row k)
+            const bool prow = row == k;
+            const double g = prow ? 0.0 : f;
+            const double h = prow ? ip : 1.0;
+            double cj[C];
 #pragma unroll
-        for (int c = 0; c < C; ++c) cj[c] = col[c0 + c];
+            for (int c = 0; c < C; ++c) cj[c] = col[c0 + c];
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-        {
-            const double up = fma(-g, cj[c], a[c] * h);
-            a[c] = (part == kp && c == kc) ? (prow ? -ip : f) : up;
+            for (int c = 0; c < C; ++c)
+            {
+                const double up = fma(-g, cj[c], a[c] * h);
+                a[c] = (c == kc && part == kp) ? (prow ? -ip : f) : up;
+            }
+            __syncthreads();
         }
-        __syncthreads();
     }
     if (!ok)
     {
-        if (lane == 0) *fallback = 1;
+        if (tid == 0) *fallback = 1;
         return;
     }
-    if (lane == 0) *fallback = 0;
+    if (tid == 0) *fallback = 0;
     if (row < R)
 #pragma unroll
         for (int c = 0; c < C; ++c)
@@ -855,13 +864,13 @@ int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStre
         attr_set = true;
     }
     if (R <= 16)
-        hipLaunchKernelGGL(sweep_inverse_kernel<16>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+        hipLaunchKernelGGL(sweep_inverse_kernel<16>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
                            flag);
     else if (R <= 32)
-        hipLaunchKernelGGL(sweep_inverse_kernel<32>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+        hipLaunchKernelGGL(sweep_inverse_kernel<32>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
                            flag);
     else if (R <= 64)
-        hipLaunchKernelGGL(sweep_inverse_kernel<64>, dim3(1), dim3(WAVE), 0, s, d_FtF, R, d_Ainv,
+        hipLaunchKernelGGL(sweep_inverse_kernel<64>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
                            flag);
     else
         hipLaunchKernelGGL(chol_inverse_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R,
