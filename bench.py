@@ -81,9 +81,13 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="run only a streaming kernel of known size (PMC scaling)")
+    ap.add_argument("--ingest", action="store_true",
+                    help="time .tns load + device setup of the workload instead")
     args = ap.parse_args()
     if args.calib:
         return calib()
+    if args.ingest:
+        return ingest(args)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here "
@@ -299,6 +303,63 @@ def bench_generic(ca, args, spec, R) -> int:
     }
     g.close()
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def ingest(args) -> int:
+    """The ingest path (.tns text -> device layout): the workload is written
+    as a .tns file under $TMPDIR, then timed: the parallel loader
+    (load_tns_file / load_tns_generic) and the driver's setup (upload, CADR or
+    HITS reorder, partition or dense units, row-sorted views).  The
+    reference's published figure for this path: load + init 5.46 s of a
+    7.92 s run on NELL-2 (docs/rtx4090_comparison.md:17)."""
+    import shutil
+    import tempfile
+
+    import cptc_amd as ca
+
+    spec = CONFIG_SPEC[args.config]
+    R = args.R or spec["R"]
+    t = ca.synth_config(args.config, 42)
+    nnz = t.nnz
+    tmp = tempfile.mkdtemp(dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        path = os.path.join(tmp, f"cfg{args.config}.tns")
+        t0 = time.perf_counter()
+        ca.write_tns(path, t)
+        write_s = time.perf_counter() - t0
+        del t
+        size = os.path.getsize(path)
+        log(f"wrote {path}: {size / 1e9:.2f} GB in {write_s:.2f} s")
+        loads = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            t2 = ca.load_tns3(path) if args.config <= 3 else ca.load_tns_generic(path)
+            loads.append(time.perf_counter() - t0)
+            if len(loads) < 2:
+                del t2
+        log(f"load {[round(x, 3) for x in loads]} s")
+        t0 = time.perf_counter()
+        if args.config <= 3:
+            h = ca.Als3(t2, R=R, threshold=spec["thr"])
+        else:
+            h = ca.Gen(t2, R=R, reorder="hits", rounds=3, threshold=spec["thr"])
+        ca.sync()
+        setup_s = time.perf_counter() - t0
+        h.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    load_s = min(loads)
+    log(f"setup {setup_s:.3f} s")
+    print(json.dumps({
+        "metric": "ingest: .tns load + device setup (s)",
+        "value": round(load_s + setup_s, 3), "unit": "s", "higher_is_better": False,
+        "load_s": round(load_s, 3), "load_first_s": round(loads[0], 3),
+        "load_GBs": round(size / load_s / 1e9, 2), "file_bytes": size, "nnz": nnz,
+        "setup_s": round(setup_s, 3), "host_threads": os.cpu_count(),
+        "config": {"workload": spec["name"], "R": R},
+        "reference": "load + init 5.46 s, NELL-2 (76.9 M nnz), RTX 4090 host",
+    }), flush=True)
     return 0
 
 

@@ -115,18 +115,33 @@ class Tensor:
         return c, (idx, val)
 
 
+class _CooOwner:
+    """Owns a library-allocated COO; frees it (cptc_coo_free) when the last
+    numpy view of its arrays is gone."""
+
+    def __init__(self, c: Coo):
+        self.c = c
+
+    def __del__(self):
+        lib.cptc_coo_free(C.byref(self.c))
+
+
 def _take(c: Coo) -> Tensor:
-    try:
-        n, nm = int(c.nnz), int(c.nmodes)
-        if n:
-            idx = np.ctypeslib.as_array(c.idx, shape=(nm * n,)).reshape(nm, n).copy()
-            val = np.ctypeslib.as_array(c.val, shape=(n,)).copy()
-        else:
-            idx = np.zeros((nm, 0), np.uint32)
-            val = np.zeros(0, np.float64)
-        return Tensor(tuple(int(c.dims[m]) for m in range(nm)), idx, val)
-    finally:
+    """Tensor over the library's arrays without copying them (a 76.9 M-nonzero
+    tensor is 1.5 GB)."""
+    n, nm = int(c.nnz), int(c.nmodes)
+    dims = tuple(int(c.dims[m]) for m in range(nm))
+    if not n:
         lib.cptc_coo_free(C.byref(c))
+        return Tensor(dims, np.zeros((nm, 0), np.uint32), np.zeros(0, np.float64))
+    owner = _CooOwner(c)
+    bidx = (C.c_uint32 * (nm * n)).from_address(C.addressof(c.idx.contents))
+    bval = (C.c_double * n).from_address(C.addressof(c.val.contents))
+    bidx._owner = owner
+    bval._owner = owner
+    idx = np.frombuffer(bidx, dtype=np.uint32).reshape(nm, n)
+    val = np.frombuffer(bval, dtype=np.float64)
+    return Tensor(dims, idx, val)
 
 
 def synth_config(config: int, seed: int = 42) -> Tensor:

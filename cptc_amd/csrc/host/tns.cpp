@@ -5,36 +5,77 @@
 //     (m > 0 ? m - 1 : 0), dims = max(0-based) + 1;
 //   * N-order (generic.cu:971-1155): order from the first numeric line,
 //     dims = max(1-based) or 1, lines longer than 4 MiB rejected.
-// In both, strtod reads the value from the file buffer itself, so (as in the
-// reference) it skips '\r' / '\n' when a line ends right after its indices.
-// The file is read whole and parsed by OpenMP threads over newline-aligned
-// chunks; the chunk results are concatenated in file order.
+// In both, strtod reads the value from the file bytes themselves, so (as in
+// the reference) it skips '\r' / '\n' when a line ends right after its
+// indices.
+// The file is memory-mapped (read-only, with zero pages after its end, so
+// every scan and strtod stops at a NUL) and parsed in two OpenMP passes over
+// newline-aligned chunks: count the lines of each chunk, then parse each
+// chunk straight into the output arrays at its prefix offset (lines that do
+// not parse leave gaps, closed afterwards).  Output order = file order.
 #include <charconv>
 #include <cstdio>
+#include <system_error>
 #include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
 
+#include <fcntl.h>
 #include <omp.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include "cptc_hip.h"
 #include "hip_util.hpp"
 
 namespace {
 
-bool read_file(const char* path, std::vector<char>& buf)
+// Read-only mapping of a file followed by at least one zero page: bytes
+// [0, size) are the file, byte `size` and beyond (to the end of the span)
+// read as 0.
+struct Mapped
 {
-    FILE* f = std::fopen(path, "rb");
-    if (!f) return false;
-    std::fseek(f, 0, SEEK_END);
-    const long sz = std::ftell(f);
-    std::fseek(f, 0, SEEK_SET);
-    buf.resize(size_t(sz > 0 ? sz : 0) + 1);
-    const size_t got = sz > 0 ? std::fread(buf.data(), 1, size_t(sz), f) : 0;
-    std::fclose(f);
-    buf.resize(got + 1);
-    buf[got] = '\0';
+    const char* p = nullptr;
+    size_t size = 0;
+    size_t span = 0;
+    ~Mapped()
+    {
+        if (p) munmap(const_cast<char*>(p), span);
+    }
+};
+
+bool map_file(const char* path, Mapped& m)
+{
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return false;
+    struct stat st;
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode))
+    {
+        close(fd);
+        return false;
+    }
+    const size_t pg = size_t(sysconf(_SC_PAGESIZE));
+    const size_t sz = size_t(st.st_size);
+    const size_t span = (sz / pg + 2) * pg;
+    void* base = mmap(nullptr, span, PROT_READ, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+    if (base == MAP_FAILED)
+    {
+        close(fd);
+        return false;
+    }
+    if (sz > 0 &&
+        mmap(base, sz, PROT_READ, MAP_PRIVATE | MAP_FIXED, fd, 0) == MAP_FAILED)
+    {
+        munmap(base, span);
+        close(fd);
+        return false;
+    }
+    close(fd);
+    m.p = static_cast<const char*>(base);
+    m.size = sz;
+    m.span = span;
     return true;
 }
 
@@ -51,12 +92,35 @@ inline int digits(const char* s, const char** end)
     return v;
 }
 
-struct Chunk
+// The value field as strtod(p, &end) reads it (end = nullptr: no number).
+// Plain decimals starting at p ([-]digits or [-].digits, optional fraction
+// and exponent) go through std::from_chars, which rounds correctly like
+// strtod (the same double) at a quarter of the cost; such a number ends
+// before the line end `e`.  Anything else (a '+' sign, hex, inf / nan,
+// whitespace or a newline before the number, out-of-range results) takes
+// strtod itself.
+inline const char* parse_value(const char* p, const char* e, double* v)
 {
-    std::vector<uint32_t> idx[CPTC_MAX_MODES];
-    std::vector<double> val;
+    const char* q = (*p == '-') ? p + 1 : p;
+    if ((*q >= '0' && *q <= '9') || (*q == '.' && q[1] >= '0' && q[1] <= '9'))
+    {
+        const auto r = std::from_chars(p, e, *v);
+        if (r.ec == std::errc() && r.ptr < e + 1 && *r.ptr != 'x' && *r.ptr != 'X')
+            return r.ptr;
+    }
+    char* end = nullptr;
+    *v = std::strtod(p, &end);
+    return end == p ? nullptr : end;
+}
+
+// Where one chunk's parsed elements go: mode m's index of element e at
+// idx[m][e], the value at val[e]; n = elements written so far.
+struct Sink
+{
+    uint32_t* idx[CPTC_MAX_MODES] = {};
+    double* val = nullptr;
+    size_t n = 0;
     uint64_t mx[CPTC_MAX_MODES] = {};
-    bool too_long = false;
 };
 
 // Newline-aligned chunk boundaries over [0, n).
@@ -75,7 +139,7 @@ std::vector<size_t> chunk_bounds(const char* b, size_t n, int parts)
 }
 
 // tensor.cu:100-197
-void parse3_line(const char* s, size_t len, Chunk& c)
+void parse3_line(const char* s, size_t len, Sink& c)
 {
     if (len == 0 || s[0] == '#') return;
     const char* e = s + len;
@@ -91,20 +155,19 @@ void parse3_line(const char* s, size_t len, Chunk& c)
     }
     while (p < e && (*p == ' ' || *p == '\t')) ++p;
     if (p >= e) return;
-    char* endc = nullptr;
-    const double v = std::strtod(p, &endc);
-    if (endc == p) return;
+    double v = 0.0;
+    if (!parse_value(p, e, &v)) return;
     for (int f = 0; f < 3; ++f)
     {
         const uint32_t z = m[f] > 0 ? uint32_t(m[f] - 1) : 0u;
-        c.idx[f].push_back(z);
+        c.idx[f][c.n] = z;
         if (z > c.mx[f]) c.mx[f] = z;
     }
-    c.val.push_back(v);
+    c.val[c.n++] = v;
 }
 
 // generic.cu:1067-1096
-void parseN_line(const char* s, size_t len, int nmodes, Chunk& c)
+void parseN_line(const char* s, size_t len, int nmodes, Sink& c)
 {
     if (len == 0 || s[0] == '#') return;
     const char* p = s;
@@ -118,62 +181,100 @@ void parseN_line(const char* s, size_t len, int nmodes, Chunk& c)
         p = end;
     }
     while (*p == ' ' || *p == '\t') ++p;
-    char* endc = nullptr;
-    const double v = std::strtod(p, &endc);
-    if (endc == p) return;
+    double v = 0.0;
+    if (!parse_value(p, s + len, &v)) return;
     for (int f = 0; f < nmodes; ++f)
     {
-        c.idx[f].push_back(m[f] > 0 ? uint32_t(m[f] - 1) : 0u);
+        c.idx[f][c.n] = m[f] > 0 ? uint32_t(m[f] - 1) : 0u;
         if (uint64_t(m[f]) > c.mx[f]) c.mx[f] = uint64_t(m[f]);
     }
-    c.val.push_back(v);
+    c.val[c.n++] = v;
 }
 
+// Two passes over newline-aligned chunks of the mapping: line counts (and
+// the longest line) per chunk, then each chunk parses into `out` at the
+// prefix sum of the counts; gaps left by lines that did not parse are
+// closed in chunk order.  Fills out->nnz, idx, val and the per-mode maxima.
 template <class LineFn>
-void parse_chunks(const std::vector<char>& buf, std::vector<Chunk>& chunks, LineFn fn)
+int parse_file(const Mapped& f, int nmodes, size_t max_line, const char* path, cptc_coo* out,
+               uint64_t* mx, LineFn fn)
 {
-    const char* b = buf.data();
-    const size_t n = buf.size() - 1;
+    const char* b = f.p;
+    const size_t n = f.size;
     const int parts = std::max(1, std::min(omp_get_max_threads(), int(n / (1 << 20)) + 1));
-    chunks.assign(size_t(parts), Chunk{});
     const std::vector<size_t> cut = chunk_bounds(b, n, parts);
+    std::vector<size_t> lines(size_t(parts), 0), longest(size_t(parts), 0);
     #pragma omp parallel for schedule(static, 1) num_threads(parts)
     for (int t = 0; t < parts; ++t)
     {
-        size_t ls = cut[t];
-        for (size_t i = cut[t]; i < cut[t + 1]; ++i)
-            if (b[i] == '\n')
-            {
-                fn(b + ls, i - ls, chunks[t]);
-                ls = i + 1;
-            }
-        if (ls < cut[t + 1]) fn(b + ls, cut[t + 1] - ls, chunks[t]);
+        size_t cnt = 0, lmax = 0, ls = cut[t];
+        const char* q = b + cut[t];
+        const char* e = b + cut[t + 1];
+        while (q < e)
+        {
+            const char* nl = static_cast<const char*>(std::memchr(q, '\n', size_t(e - q)));
+            const char* le = nl ? nl : e;
+            lmax = std::max(lmax, size_t(le - (b + ls)));
+            ++cnt;
+            q = le + 1;
+            ls = size_t(q - b);
+        }
+        lines[t] = cnt;
+        longest[t] = lmax;
     }
-}
-
-int assemble(std::vector<Chunk>& chunks, int nmodes, cptc_coo* out)
-{
-    size_t nnz = 0;
-    for (auto& c : chunks) nnz += c.val.size();
+    size_t cap = 0, lmax = 0;
+    std::vector<size_t> base(size_t(parts) + 1, 0);
+    for (int t = 0; t < parts; ++t)
+    {
+        base[t + 1] = base[t] + lines[t];
+        lmax = std::max(lmax, longest[t]);
+    }
+    cap = base[parts];
+    CPTC_REQUIRE(lmax < max_line, CPTC_ERR_IO, "line longer than read buffer (%zu bytes) in %s",
+                 max_line, path);
     std::memset(out, 0, sizeof(*out));
     out->nmodes = nmodes;
-    out->nnz = nnz;
-    out->idx = static_cast<uint32_t*>(std::malloc(sizeof(uint32_t) * nmodes * (nnz ? nnz : 1)));
-    out->val = static_cast<double*>(std::malloc(sizeof(double) * (nnz ? nnz : 1)));
-    CPTC_REQUIRE(out->idx && out->val, CPTC_ERR_IO, "tns: out of host memory for %zu elements", nnz);
-    std::vector<size_t> base(chunks.size() + 1, 0);
-    for (size_t t = 0; t < chunks.size(); ++t) base[t + 1] = base[t] + chunks[t].val.size();
-    #pragma omp parallel for schedule(static, 1)
-    for (int64_t t = 0; t < int64_t(chunks.size()); ++t)
+    out->idx = static_cast<uint32_t*>(std::malloc(sizeof(uint32_t) * nmodes * (cap ? cap : 1)));
+    out->val = static_cast<double*>(std::malloc(sizeof(double) * (cap ? cap : 1)));
+    CPTC_REQUIRE(out->idx && out->val, CPTC_ERR_IO, "tns: out of host memory for %zu lines", cap);
+    std::vector<Sink> sinks(static_cast<size_t>(parts));
+    #pragma omp parallel for schedule(static, 1) num_threads(parts)
+    for (int t = 0; t < parts; ++t)
     {
-        Chunk& c = chunks[t];
-        for (int m = 0; m < nmodes; ++m)
-            if (!c.idx[m].empty())
-                std::memcpy(out->idx + size_t(m) * nnz + base[t], c.idx[m].data(),
-                            c.idx[m].size() * sizeof(uint32_t));
-        if (!c.val.empty())
-            std::memcpy(out->val + base[t], c.val.data(), c.val.size() * sizeof(double));
+        Sink& sk = sinks[t];
+        for (int m = 0; m < nmodes; ++m) sk.idx[m] = out->idx + size_t(m) * cap + base[t];
+        sk.val = out->val + base[t];
+        size_t ls = cut[t];
+        const char* q = b + cut[t];
+        const char* e = b + cut[t + 1];
+        while (q < e)
+        {
+            const char* nl = static_cast<const char*>(std::memchr(q, '\n', size_t(e - q)));
+            const char* le = nl ? nl : e;
+            fn(b + ls, size_t(le - (b + ls)), sk);
+            q = le + 1;
+            ls = size_t(q - b);
+        }
     }
+    // close the gaps (chunk order), then the mode stride becomes nnz
+    size_t nnz = 0;
+    for (int t = 0; t < parts; ++t)
+    {
+        const Sink& sk = sinks[t];
+        if (nnz != base[t] && sk.n)
+        {
+            for (int m = 0; m < nmodes; ++m)
+                std::memmove(out->idx + size_t(m) * cap + nnz, sk.idx[m], sk.n * sizeof(uint32_t));
+            std::memmove(out->val + nnz, sk.val, sk.n * sizeof(double));
+        }
+        nnz += sk.n;
+        for (int m = 0; m < nmodes; ++m) mx[m] = std::max(mx[m], sk.mx[m]);
+    }
+    if (nnz != cap)
+        for (int m = 1; m < nmodes; ++m)
+            std::memmove(out->idx + size_t(m) * nnz, out->idx + size_t(m) * cap,
+                         nnz * sizeof(uint32_t));
+    out->nnz = nnz;
     return CPTC_OK;
 }
 
@@ -182,17 +283,12 @@ int assemble(std::vector<Chunk>& chunks, int nmodes, cptc_coo* out)
 extern "C" int cptc_tns_load3(const char* path, cptc_coo* out)
 {
     CPTC_REQUIRE(path && out, CPTC_ERR_ARG, "cptc_tns_load3: null argument");
-    std::vector<char> buf;
-    CPTC_REQUIRE(read_file(path, buf), CPTC_ERR_IO, "cannot open file: %s", path);
-    std::vector<Chunk> chunks;
-    parse_chunks(buf, chunks, [](const char* s, size_t len, Chunk& c) { parse3_line(s, len, c); });
-    CPTC_TRY(assemble(chunks, 3, out));
-    for (int m = 0; m < 3; ++m)
-    {
-        uint64_t mx = 0;
-        for (auto& c : chunks) mx = std::max(mx, c.mx[m]);
-        out->dims[m] = mx + 1;
-    }
+    Mapped f;
+    CPTC_REQUIRE(map_file(path, f), CPTC_ERR_IO, "cannot open file: %s", path);
+    uint64_t mx[CPTC_MAX_MODES] = {};
+    CPTC_TRY(parse_file(f, 3, ~size_t(0), path, out, mx,
+                        [](const char* s, size_t len, Sink& c) { parse3_line(s, len, c); }));
+    for (int m = 0; m < 3; ++m) out->dims[m] = mx[m] + 1;
     return CPTC_OK;
 }
 
@@ -233,30 +329,14 @@ extern "C" int cptc_tns_load_generic(const char* path, cptc_coo* out)
     CPTC_REQUIRE(nmodes >= 2, CPTC_ERR_IO, "invalid tensor order %d in %s", nmodes, path);
     CPTC_REQUIRE(nmodes <= CPTC_MAX_MODES, CPTC_ERR_UNSUPPORTED, "tensor order %d > %d", nmodes,
                  CPTC_MAX_MODES);
-    std::vector<char> buf;
-    CPTC_REQUIRE(read_file(path, buf), CPTC_ERR_IO, "cannot open file: %s", path);
+    Mapped f;
+    CPTC_REQUIRE(map_file(path, f), CPTC_ERR_IO, "cannot open file: %s", path);
     // generic.cu:1132-1138: a line longer than the 4 MiB read buffer aborts
-    {
-        size_t ls = 0;
-        const size_t n = buf.size() - 1;
-        for (size_t i = 0; i <= n; ++i)
-            if (i == n || buf[i] == '\n')
-            {
-                CPTC_REQUIRE(i - ls < (size_t(1) << 22), CPTC_ERR_IO,
-                             "line longer than read buffer (4194304 bytes) in %s", path);
-                ls = i + 1;
-            }
-    }
-    std::vector<Chunk> chunks;
-    parse_chunks(buf, chunks,
-                 [nmodes](const char* s, size_t len, Chunk& c) { parseN_line(s, len, nmodes, c); });
-    CPTC_TRY(assemble(chunks, nmodes, out));
-    for (int m = 0; m < nmodes; ++m)
-    {
-        uint64_t mx = 0;
-        for (auto& c : chunks) mx = std::max(mx, c.mx[m]);
-        out->dims[m] = mx > 0 ? mx : 1;
-    }
+    uint64_t mx[CPTC_MAX_MODES] = {};
+    CPTC_TRY(parse_file(
+        f, nmodes, size_t(1) << 22, path, out, mx,
+        [nmodes](const char* s, size_t len, Sink& c) { parseN_line(s, len, nmodes, c); }));
+    for (int m = 0; m < nmodes; ++m) out->dims[m] = mx[m] > 0 ? mx[m] : 1;
     return CPTC_OK;
 }
 

@@ -100,3 +100,44 @@ def test_probe_nmodes_missing_and_order3(tmp_path, ca):
 def test_generic_rejects_order1(tmp_path, ca):
     with pytest.raises(ca.CptcError):
         ca.load_tns_generic(_write(tmp_path, "1 2.0\n2 3.0\n"))
+
+
+# Value spellings that strtod reads in its own ways; the loaders take plain
+# decimals through a faster correctly-rounded parser and must give strtod's
+# double for every one (Python's float() and the oracle's strtod agree on
+# the plain ones; the others are written out).
+VALUE_CASES = [
+    ("1.5", 1.5), ("-0", -0.0), ("-.25", -0.25), (".5", 0.5), ("1.", 1.0), ("007.5", 7.5),
+    ("1e5", 1e5), ("1E-5", 1e-5), ("2.5e+3", 2500.0), ("1.5e", 1.5), ("1e400", float("inf")),
+    ("-1e400", float("-inf")), ("1e-400", 0.0), ("4.9406564584124654e-324", 5e-324),
+    ("2.2250738585072011e-308", 2.2250738585072011e-308),
+    ("0.1000000000000000055511151231257827", 0.1), ("123456789012345678901234567890", 1.2345678901234568e29),
+    ("+3.5", 3.5), ("0x1p3", 8.0), ("0X10", 16.0), ("inf", float("inf")), ("-Infinity", float("-inf")),
+    ("1.7976931348623157e308", 1.7976931348623157e308), ("9007199254740993", 9007199254740992.0),
+]
+
+
+@pytest.mark.parametrize("load", ["load3", "generic"])
+def test_value_spellings_match_strtod(tmp_path, ca, orc, load):
+    text = "".join(f"{i + 1} 1 1 {s}\n" for i, (s, _) in enumerate(VALUE_CASES))
+    path = _write(tmp_path, text)
+    t = ca.load_tns3(path) if load == "load3" else ca.load_tns_generic(path)
+    _, _, _, ov, _ = orc.load_tns3(path)                 # the oracle: strtod itself
+    exp = np.array([v for _, v in VALUE_CASES])
+    assert np.array_equal(t.val, exp) and np.array_equal(np.signbit(t.val), np.signbit(exp))
+    assert np.array_equal(t.val.view(np.uint64), np.asarray(ov).view(np.uint64))
+
+
+def test_random_decimals_bit_exact(tmp_path, ca, orc):
+    """Shortest round-trip spellings of log-normal doubles, as the synthetic
+    generators write them, and truncated 6- to 20-digit spellings."""
+    rng = np.random.default_rng(7)
+    vals = np.concatenate([rng.lognormal(0.0, 3.0, 3000), -rng.lognormal(0.0, 30.0, 1000)])
+    strs = [repr(float(x)) for x in vals]
+    strs += [f"{x:.{d}g}" for x, d in zip(vals[:2000], rng.integers(6, 21, 2000))]
+    text = "".join(f"1 1 {i + 1} {s}\n" for i, s in enumerate(strs))
+    path = _write(tmp_path, text)
+    t = ca.load_tns3(path)
+    _, _, _, ov, _ = orc.load_tns3(path)
+    assert t.val.view(np.uint64).tolist() == np.asarray(ov).view(np.uint64).tolist()
+    assert t.val.tolist() == [float(s) for s in strs]
