@@ -327,101 +327,141 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
 // kernels so that a driver can factor FtF while the MTTKRP that produces
 // FtV is still running.
 //
-// chol_factor_kernel (one wave) factors FtF + eps I in registers: lane i
-// holds row i.  Step j broadcasts the pivot column through LDS, scales
-// column j by the pivot's square root and subtracts L[i][j] L[k][j] from the
-// trailing entries.  Each entry therefore receives exactly the reference's
-// sequence: (FtF + eps) minus the products for k = 0, 1, ... in ascending
-// order, then the division by the pivot.  Entries above the diagonal take
-// the same updates without a per-lane condition (they are never read),
-// which keeps the unrolled code at about one LDS read and one FMA per
-// (j, k).  L (R x R row-major, zeros above the diagonal) goes to global.
+// chol_factor_kernel (four waves) factors FtF + eps I in registers: row i
+// is split over 256 / RT threads, each holding RT^2 / 256 consecutive
+// columns.  Step j broadcasts the pivot column through LDS, scales column j
+// by the pivot's square root (the thread owning column j of each row) and
+// every thread subtracts L[i][j] L[k][j] from its entries k > j.  Each entry
+// therefore receives exactly the reference's sequence: (FtF + eps) minus
+// the products for k = 0, 1, ... in ascending order, then the division by
+// the pivot.  Entries above the diagonal take the same updates without a
+// per-thread condition (they are never read).  L (R x R row-major, zeros
+// above the diagonal) goes to global.
 //
 // chol_apply_kernel stages L in LDS and solves one right-hand-side row per
-// lane, its y / x vector in LDS column `lane`: the reference's k-ascending
-// forward and backward substitutions.
+// lane with its y / x vector in registers (loops unrolled to RT >= R): the
+// reference's k-ascending forward and backward substitutions.
 constexpr int CHOL_RM = 32;
-constexpr int CHOL_T = 64;
-
-__device__ __forceinline__ double lane_double(double v, int l)
-{
-    const uint64_t b = uint64_t(__double_as_longlong(v));
-    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l));
-    return __longlong_as_double((long long)((uint64_t(hi) << 32) | lo));
-}
+constexpr int CHOL_T = 64;     // chol_apply_kernel: one right-hand side per thread
+constexpr int CHOL_FT = 256;   // chol_factor_kernel
 
 template <int RT>
-__global__ __launch_bounds__(CHOL_T) void chol_factor_kernel(const double* __restrict__ FtF,
-                                                             int R, double* __restrict__ Lout)
+__global__ __launch_bounds__(CHOL_FT) void chol_factor_kernel(const double* __restrict__ FtF,
+                                                              int R, double* __restrict__ Lout)
 {
-    __shared__ double col[CHOL_T];
+    // thread = row + RT * part; the thread holds columns part*C .. part*C+C-1
+    constexpr int LPR = CHOL_FT / RT;
+    constexpr int C = RT / LPR;
+    static_assert(C >= 1 && C <= 16, "chol layout");
+    __shared__ double col[RT];    // column j before scaling (pivot on the diagonal)
+    __shared__ double lcol[RT];   // column j of L
+    __shared__ double trs;
     const int tid = threadIdx.x;
-    const bool mine = tid < R;   // this lane holds row tid (rows >= R stay zero)
-    double a[RT];
+    const int row = tid % RT;
+    const int part = tid / RT;
+    const int c0 = part * C;
+    const bool mine = row < R;    // rows >= R hold eps I (see below)
+    double a[C];
 #pragma unroll
-    for (int k = 0; k < RT; ++k) a[k] = (mine && k < R) ? FtF[size_t(tid) * R + k] : 0.0;
-    // eps from the trace, summed in row order (the diagonal of row i is lane
-    // i's a[i]; rows >= R add exact zeros)
-    double tr = 0.0;
+    for (int c = 0; c < C; ++c)
+        a[c] = (mine && c0 + c < R) ? FtF[size_t(row) * R + c0 + c] : 0.0;
+    // eps from the trace, summed in row order
 #pragma unroll
-    for (int i = 0; i < RT; ++i) tr += lane_double(a[i], i);
+    for (int c = 0; c < C; ++c)
+        if (c0 + c == row) col[row] = a[c];
+    __syncthreads();
+    if (tid == 0)
+    {
+        double tr = 0.0;
+        for (int i = 0; i < R; ++i) tr += col[i];
+        trs = tr;
+    }
+    __syncthreads();
+    const double tr = trs;
     const double eps = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
-        if (tid == i) a[i] += eps;
-    // Padding rows R..RT-1 hold eps I: their steps give L[i][i] = sqrt(eps)
-    // and zeros elsewhere, and subtract exact zeros from the rows < R, so
-    // no loop below depends on R.
-#pragma unroll
-    for (int j = 0; j < RT; ++j)
+    for (int c = 0; c < C; ++c)
+        if (c0 + c == row) a[c] += eps;
+    // Steps j < R only; rows >= R hold zeros off the diagonal, so they
+    // subtract exact zeros from the rows < R.
+    for (int jp = 0; jp * C < R; ++jp)
     {
-        col[tid] = a[j];
-        __syncthreads();
-        const double s = col[j];
-        const double d = (s > 0.0) ? sqrt(s) : sqrt(eps);
-        a[j] = (tid == j) ? d : ((mine && tid > j) ? a[j] / d : a[j]);   // L[tid][j]
-        __syncthreads();
-        col[tid] = a[j];
-        __syncthreads();
-        // col[k] = L[k][j]
 #pragma unroll
-        for (int k = j + 1; k < RT; ++k) a[k] -= a[j] * col[k];
-        __syncthreads();
+        for (int jc = 0; jc < C; ++jc)
+        {
+            const int j = jp * C + jc;
+            if (j >= R) break;
+            if (part == jp) col[row] = a[jc];
+            __syncthreads();
+            const double s = col[j];
+            const double d = (s > 0.0) ? sqrt(s) : sqrt(eps);
+            if (part == jp)
+            {
+                const double v = col[row];
+                lcol[row] = (row == j) ? d : ((mine && row > j) ? v / d : v);   // L[row][j]
+            }
+            __syncthreads();
+            const double lij = lcol[row];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+            {
+                if (part == jp && c == jc) a[c] = lij;
+                else if (c0 + c > j) a[c] -= lij * lcol[c0 + c];
+            }
+        }
     }
     if (mine)
 #pragma unroll
-        for (int k = 0; k < RT; ++k)
-            if (k < R) Lout[size_t(tid) * R + k] = (k <= tid) ? a[k] : 0.0;
+        for (int c = 0; c < C; ++c)
+            if (c0 + c < R) Lout[size_t(row) * R + c0 + c] = (c0 + c <= row) ? a[c] : 0.0;
 }
 
+template <int RT>
 __global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __restrict__ Lg,
                                                             const double* __restrict__ FtV,
                                                             double* __restrict__ F, size_t dim,
                                                             int R)
 {
-    __shared__ double L[CHOL_RM][CHOL_RM + 1];
-    __shared__ double ys[CHOL_RM][CHOL_T];
-    const int tid = threadIdx.x;
-    for (int x = tid; x < R * R; x += CHOL_T) L[x / R][x % R] = Lg[x];
-    const size_t row = size_t(blockIdx.x) * CHOL_T + tid;
-    const bool live = row < dim;
-    for (int i = 0; i < R; ++i) ys[i][tid] = live ? FtV[row * R + i] : 0.0;
+    // L padded to RT with the identity: padding entries of y stay 0 and
+    // only exact zeros are subtracted from the others, so the unrolled loops
+    // below need no condition on R
+    __shared__ double L[RT][RT + 1];
+    for (int x = threadIdx.x; x < RT * RT; x += CHOL_T)
+    {
+        const int i = x / RT, k = x % RT;
+        L[i][k] = (i < R && k < R) ? Lg[size_t(i) * R + k] : (i == k ? 1.0 : 0.0);
+    }
     __syncthreads();
-    for (int i = 0; i < R; ++i)
+    const size_t row = size_t(blockIdx.x) * CHOL_T + threadIdx.x;
+    if (row >= dim) return;
+    const double* b = FtV + row * R;
+    double y[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
+    // (the empty asm with a memory clobber keeps each step's LDS reads of L
+    // inside that step; hoisted, all of L would not fit the registers)
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
     {
-        double s = ys[i][tid];
-        for (int k = 0; k < i; ++k) s -= L[i][k] * ys[k][tid];
-        ys[i][tid] = s / L[i][i];
+        double s = y[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) s -= L[i][k] * y[k];
+        y[i] = s / L[i][i];
+        asm volatile("" ::: "memory");
     }
-    for (int i = R - 1; i >= 0; --i)
+#pragma unroll
+    for (int i = RT - 1; i >= 0; --i)
     {
-        double s = ys[i][tid];
-        for (int k = i + 1; k < R; ++k) s -= L[k][i] * ys[k][tid];
-        ys[i][tid] = s / L[i][i];   // x[i]
+        double s = y[i];
+#pragma unroll
+        for (int k = i + 1; k < RT; ++k) s -= L[k][i] * y[k];
+        y[i] = s / L[i][i];   // x[i]
+        asm volatile("" ::: "memory");
     }
-    if (live)
-        for (int i = 0; i < R; ++i) F[row * R + i] = ys[i][tid];
+    double* out = F + row * R;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+        if (i < R) out[i] = y[i];
 }
 
 // Column sums of squares: P partials of R each (deterministic).
@@ -650,12 +690,10 @@ extern "C" int cptc_chol_ridge_factor(const double* d_FtF, double* d_L, int R, v
     CPTC_REQUIRE(R >= 1 && R <= CHOL_RM, CPTC_ERR_ARG, "cptc_chol_ridge_factor: R %d (1..32)", R);
     CPTC_REQUIRE(d_FtF && d_L, CPTC_ERR_ARG, "cptc_chol_ridge_factor: null pointer");
     hipStream_t s = cptc::as_stream(stream);
-    if (R <= 8)
-        hipLaunchKernelGGL(chol_factor_kernel<8>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R, d_L);
-    else if (R <= 16)
-        hipLaunchKernelGGL(chol_factor_kernel<16>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R, d_L);
+    if (R <= 16)
+        hipLaunchKernelGGL(chol_factor_kernel<16>, dim3(1), dim3(CHOL_FT), 0, s, d_FtF, R, d_L);
     else
-        hipLaunchKernelGGL(chol_factor_kernel<CHOL_RM>, dim3(1), dim3(CHOL_T), 0, s, d_FtF, R,
+        hipLaunchKernelGGL(chol_factor_kernel<CHOL_RM>, dim3(1), dim3(CHOL_FT), 0, s, d_FtF, R,
                            d_L);
     CPTC_LAUNCHED();
     return CPTC_OK;
@@ -669,8 +707,16 @@ extern "C" int cptc_chol_ridge_apply(const double* d_L, const double* d_FtV, dou
     CPTC_REQUIRE(d_L && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_apply: null pointer");
     CPTC_REQUIRE(dim / CHOL_T < (size_t(1) << 31), CPTC_ERR_ARG,
                  "cptc_chol_ridge_apply: %zu rows", dim);
-    hipLaunchKernelGGL(chol_apply_kernel, dim3(unsigned((dim + CHOL_T - 1) / CHOL_T)),
-                       dim3(CHOL_T), 0, cptc::as_stream(stream), d_L, d_FtV, d_F, dim, R);
+    const dim3 grid(unsigned((dim + CHOL_T - 1) / CHOL_T));
+    hipStream_t s = cptc::as_stream(stream);
+    if (R <= 8)
+        hipLaunchKernelGGL(chol_apply_kernel<8>, grid, dim3(CHOL_T), 0, s, d_L, d_FtV, d_F, dim, R);
+    else if (R <= 16)
+        hipLaunchKernelGGL(chol_apply_kernel<16>, grid, dim3(CHOL_T), 0, s, d_L, d_FtV, d_F, dim,
+                           R);
+    else
+        hipLaunchKernelGGL(chol_apply_kernel<CHOL_RM>, grid, dim3(CHOL_T), 0, s, d_L, d_FtV, d_F,
+                           dim, R);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
