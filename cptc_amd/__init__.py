@@ -476,5 +476,7 @@ class Gen:
                                              "is_dense"))), "cptc_gen_units")
         return d
 
-    def dump(self, base: str) -> None:
-        check(lib.cptc_gen_dump(self._h, base.encode()), "cptc_gen_dump")
+    def dump(self, base: str, input_order: bool = False) -> None:
+        """GEN_DUMP to <base>.factors.txt (reordered rows, as the reference),
+        or with input_order=True in the input tensor's index order."""
+        check(lib.cptc_gen_dump_ex(self._h, base.encode(), int(input_order)), "cptc_gen_dump_ex")

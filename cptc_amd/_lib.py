@@ -196,6 +196,7 @@ SIGNATURES = {
     "cptc_gen_view": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P]),
     "cptc_gen_units": (_I, [_P, _P, _P, _P, _P, _P]),
     "cptc_gen_dump": (_I, [_P, C.c_char_p]),
+    "cptc_gen_dump_ex": (_I, [_P, C.c_char_p, _I]),
     "cptc_gen_destroy": (_I, [_P]),
     "cptc_gen_selftest": (_I, [_I, C.POINTER(_I)]),
 }

@@ -676,7 +676,9 @@ int run_generic_cp(GTensor& t, int max_iters, int R, unsigned int seed)
     if (rc == CPTC_OK)
         if (const char* base = std::getenv("GEN_DUMP"))
         {
-            if (cptc_gen_dump(h, base) == CPTC_OK)
+            const char* orig = std::getenv("GEN_DUMP_ORIGINAL");
+            const int input_order = (orig && std::atoi(orig) != 0) ? 1 : 0;
+            if (cptc_gen_dump_ex(h, base, input_order) == CPTC_OK)
                 std::cout << "[GEN] factors dumped to " << base << ".factors.txt" << std::endl;
             else
                 std::cerr << "[GEN] factor dump failed: " << cptc_last_error() << std::endl;

@@ -1139,6 +1139,11 @@ extern "C" int cptc_gen_units(void* handle, uint32_t* unit6, uint32_t* outer_coo
 
 extern "C" int cptc_gen_dump(void* handle, const char* base)
 {
+    return cptc_gen_dump_ex(handle, base, 0);
+}
+
+extern "C" int cptc_gen_dump_ex(void* handle, const char* base, int input_order)
+{
     CPTC_REQUIRE(handle && base, CPTC_ERR_ARG, "cptc_gen_dump: null argument");
     Gen* g = as_gen(handle);
     const std::string path = std::string(base) + ".factors.txt";
@@ -1146,6 +1151,7 @@ extern "C" int cptc_gen_dump(void* handle, const char* base)
     CPTC_REQUIRE(f, CPTC_ERR_IO, "cptc_gen_dump: cannot open %s", path.c_str());
     const int R = g->R;
     std::fprintf(f, "# cpTC factor dump (factors are column-normalised; lambda holds the norms)\n");
+    if (input_order) std::fprintf(f, "# rows in the input tensor's index order\n");
     std::fprintf(f, "order %d\nrank %d\ndims", g->N, R);
     for (int m = 0; m < g->N; ++m) std::fprintf(f, " %llu", (unsigned long long)g->dims[m]);
     std::fprintf(f, "\n");
@@ -1159,7 +1165,10 @@ extern "C" int cptc_gen_dump(void* handle, const char* base)
         std::fprintf(f, "mode %d %llu %d\n", m, (unsigned long long)g->dims[m], R);
         for (uint64_t i = 0; i < g->dims[m]; ++i)
         {
-            for (int r = 0; r < R; ++r) std::fprintf(f, r ? " %.17g" : "%.17g", buf[i * R + r]);
+            // row i of the input tensor is row rank[i] of the relabelled factor
+            const uint64_t src = (input_order && !g->rank.empty()) ? g->rank[m][i] : i;
+            for (int r = 0; r < R; ++r)
+                std::fprintf(f, r ? " %.17g" : "%.17g", buf[src * R + r]);
             std::fprintf(f, "\n");
         }
     }

@@ -318,20 +318,21 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
     for (int w = 0; w < SWEEP_T / WAVE; ++w) md = fmax(md, wmax[w]);
     const double tau = 1e-10 * md;
     int ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
-    for (int kp = 0; kp < LPR && ok; ++kp)
+#pragma unroll 1
+    for (int kp = 0; kp < LPR && kp * C < R && ok; ++kp)
     {
 #pragma unroll
         for (int kc = 0; kc < C; ++kc)
         {
             const int k = kp * C + kc;
-            if (k >= R) break;
+            if (k >= R || !ok) continue;   // uniform
             if (part == kp) col[row] = a[kc];
             __syncthreads();
             const double p = col[k];
             if (!(p > tau) || !isfinite(p))
             {
                 ok = 0;   // every thread read the same pivot: uniform exit
-                break;
+                continue;
             }
             const double ip = 1.0 / p;
             const double f = col[row] * ip;    // a_ik / a_kk (1 on row k)

@@ -537,6 +537,13 @@ int cptc_gen_units(void* handle, uint32_t* unit6, uint32_t* outer_coords, uint32
  * (generic.cu:2253-2287) to <base>.factors.txt. */
 int cptc_gen_dump(void* handle, const char* base);
 
+/* The same dump; input_order != 0 writes row i of each factor for index i of
+ * the input tensor (the reordered row rank[i]) and adds a comment line
+ * saying so.  No counterpart in the reference, whose dump stays in the
+ * reordered space (an external evaluator scoring it against the input file
+ * would pair the wrong rows); GEN_DUMP_ORIGINAL=1 selects it in the CLI. */
+int cptc_gen_dump_ex(void* handle, const char* base, int input_order);
+
 int cptc_gen_destroy(void* handle);
 
 /* The dense-unit known-answer test (run_dense_selftest,

@@ -589,6 +589,53 @@ def test_config5_full_size(ca, orc, dev):
     assert np.max(np.abs(fit - rfit)) <= 1e-4, (fit, rfit)
 
 
+def _parse_dump(path):
+    """GEN_DUMP text: order, rank, dims, N blocks of rows, lambda."""
+    lines = [ln for ln in open(path).read().split("\n") if ln and not ln.startswith("#")]
+    N = int(lines[0].split()[1])
+    R = int(lines[1].split()[1])
+    dims = [int(x) for x in lines[2].split()[1:]]
+    pos, F = 3, []
+    for m in range(N):
+        hdr = lines[pos].split()
+        assert hdr == ["mode", str(m), str(dims[m]), str(R)]
+        F.append(np.array([[float(x) for x in ln.split()] for ln in lines[pos + 1:pos + 1 + dims[m]]]))
+        pos += 1 + dims[m]
+    assert lines[pos].split() == ["lambda", str(R)]
+    lam = np.array([float(x) for x in lines[pos + 1].split()])
+    return F, lam
+
+
+def test_dump_input_order(ca, dev, tmp_path):
+    """GEN_DUMP in the input's index order (an opt-in fix: the reference's
+    dump is in the HITS-relabelled space): rows are the relabelled rows
+    permuted by the rank maps, and the model evaluated at the input tensor's
+    own coordinates gives the driver's exact residual."""
+    rng = np.random.default_rng(21)
+    dims = (60, 20, 90, 40)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.5, 4000), dims, rng)
+    g = ca.Gen(t, R=8, reorder="hits", rounds=3)
+    g.run(5)
+    res, x2 = g.residual()
+    g.dump(str(tmp_path / "a"))
+    g.dump(str(tmp_path / "b"), input_order=True)
+    ranks = [g.rank(m) for m in range(4)]
+    g.close()
+    Fa, la = _parse_dump(str(tmp_path / "a.factors.txt"))
+    Fb, lb = _parse_dump(str(tmp_path / "b.factors.txt"))
+    assert np.array_equal(la, lb)
+    assert any(not np.array_equal(r, np.arange(len(r))) for r in ranks)
+    for m in range(4):
+        assert np.array_equal(Fb[m], Fa[m][ranks[m].astype(np.int64)]), m
+    xhat = np.zeros(t.nnz)
+    for r in range(8):
+        p = np.full(t.nnz, lb[r])
+        for m in range(4):
+            p = p * Fb[m][t.idx[m].astype(np.int64), r]
+        xhat += p
+    assert abs(np.sum((t.val - xhat) ** 2) - res) <= 1e-9 * x2
+
+
 def test_cli_generic_and_selftest(ca, dev, tmp_path):
     rng = np.random.default_rng(8)
     dims = (40, 35, 48, 3)
