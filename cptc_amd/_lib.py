@@ -132,6 +132,7 @@ SIGNATURES = {
     "cptc_cadr3": (_I, [_P, _P, _P, _Z, _P, _P, _P, _P, _I]),
     "cptc_unpermute_factor": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_mttkrp_sparse3": (_I, [_I, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _P]),
+    "cptc_mttkrp_sparse3_range": (_I, [_I, _P, _P, _Z, _Z, _P, _P, _P, _I, _P]),
     "cptc_mttkrp_dense_tiles3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
                                       _I, _P]),
     "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),

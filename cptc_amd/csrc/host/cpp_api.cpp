@@ -377,16 +377,23 @@ void compute_sparse_mttkrp_async(const HybridCOOTensor& hybrid, int target_mode,
                                  double* d_FtV, double* d_FtF, int R, hipStream_t stream,
                                  size_t start_idx, size_t count)
 {
-    if (count == 0) return;
-    if (start_idx != 0 || count < hybrid.sparse_nnz)
+    // sparse.cu:877-955: clamp the range; the whole residual takes the
+    // row-sorted segment kernel, a strict sub-range the per-element one
+    if (!hybrid.mttkrp_ready || hybrid.sparse_nnz == 0 || count == 0 ||
+        start_idx >= hybrid.sparse_nnz)
+        return;
+    count = std::min(count, hybrid.sparse_nnz - start_idx);
+    if (start_idx == 0 && count == hybrid.sparse_nnz)
     {
-        std::cerr << "[cpTC] compute_sparse_mttkrp_async: the row-sorted views process the "
-                     "whole residual; sub-range ["
-                  << start_idx << ", " << start_idx + count << ") of " << hybrid.sparse_nnz
-                  << " is not supported" << std::endl;
-        std::exit(EXIT_FAILURE);
+        compute_sparse_mttkrp_async(hybrid, target_mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
+        return;
     }
-    compute_sparse_mttkrp_async(hybrid, target_mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
+    const int m = target_mode;
+    const double* F1 = m == 0 ? d_B : d_A;
+    const double* F2 = m == 2 ? d_B : d_C;
+    API_TRY("compute_sparse_mttkrp_async",
+            cptc_mttkrp_sparse3_range(m, hybrid.d_sp2_coords[m], hybrid.d_sp2_val[m], start_idx,
+                                      count, F1, F2, d_FtV, R, stream));
 }
 
 void compute_sparse_mttkrp(const HybridCOOTensor& hybrid, int target_mode, const double* d_A,

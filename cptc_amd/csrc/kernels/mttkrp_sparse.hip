@@ -427,7 +427,55 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
     return hipGetLastError();
 }
 
+// Elements [start, start + count) of one mode's row-sorted view, each
+// adding v * F1[o0, r] * F2[o1, r] (that product order) to FtV[target, r]
+// with one atomic per (element, rank), as mttkrp_range_generic_kernel
+// (sparse.cu:340-397).  One wave per element, lanes over ranks: the factor
+// rows are read and the atomics issued 64 ranks at a time, coalesced.
+__global__ __launch_bounds__(256) void mttkrp3_range_kernel(int mode,
+                                                            const uint64_t* __restrict__ coords,
+                                                            const double* __restrict__ vals,
+                                                            size_t start, size_t count,
+                                                            const double* __restrict__ F1,
+                                                            const double* __restrict__ F2,
+                                                            double* __restrict__ FtV, int R)
+{
+    const int lane = threadIdx.x & 63;
+    const size_t waves = size_t(gridDim.x) * (blockDim.x / 64);
+    for (size_t e = size_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64; e < count;
+         e += waves)
+    {
+        const uint64_t c = coords[start + e];
+        const double v = vals[start + e];
+        const uint32_t i = uint32_t(c >> 30), j = uint32_t(c >> 15) & 0x7FFFu,
+                       k = uint32_t(c) & 0x7FFFu;
+        const uint32_t t = mode == 0 ? i : (mode == 1 ? j : k);
+        const uint32_t o0 = mode == 0 ? j : i;
+        const uint32_t o1 = mode == 2 ? j : k;
+        const double* __restrict__ f1 = F1 + size_t(o0) * R;
+        const double* __restrict__ f2 = F2 + size_t(o1) * R;
+        double* __restrict__ out = FtV + size_t(t) * R;
+        for (int r = lane; r < R; r += 64) atomicAdd(out + r, v * f1[r] * f2[r]);
+    }
+}
+
 }  // namespace
+
+extern "C" int cptc_mttkrp_sparse3_range(int mode, const uint64_t* d_coords, const double* d_vals,
+                                         size_t start, size_t count, const double* d_F1,
+                                         const double* d_F2, double* d_FtV, int R, void* stream)
+{
+    CPTC_REQUIRE(mode >= 0 && mode < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_sparse3_range: mode %d R %d", mode, R);
+    if (count == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_coords && d_vals && d_F1 && d_F2 && d_FtV, CPTC_ERR_ARG,
+                 "cptc_mttkrp_sparse3_range: null pointer");
+    const unsigned grid = cptc::grid_for(count, 4, 1u << 16);
+    hipLaunchKernelGGL(mttkrp3_range_kernel, dim3(grid), dim3(256), 0, cptc::as_stream(stream),
+                       mode, d_coords, d_vals, start, count, d_F1, d_F2, d_FtV, R);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
 
 extern "C" int cptc_mttkrp_sparse3(int mode, const uint64_t* d_coords, const double* d_vals,
                                    const uint32_t* d_blk_row, const uint32_t* d_blk_start,

@@ -140,6 +140,15 @@ int cptc_mttkrp_sparse3(int mode, const uint64_t* d_coords, const double* d_vals
                         const uint32_t* d_blk_cnt, size_t nblocks, const double* d_F1,
                         const double* d_F2, double* d_FtV, int R, void* stream);
 
+/* The same sum over elements [start, start + count) of one mode's view only,
+ * one atomic per (element, rank) of v * F1[o0, r] * F2[o1, r]: the
+ * sub-range path of compute_sparse_mttkrp_async(..., start_idx, count)
+ * (mttkrp_range_generic_kernel, sparse.cu:340-397, 877-955).  The caller
+ * clamps the range to the view. */
+int cptc_mttkrp_sparse3_range(int mode, const uint64_t* d_coords, const double* d_vals,
+                              size_t start, size_t count, const double* d_F1, const double* d_F2,
+                              double* d_FtV, int R, void* stream);
+
 /* Dense 16^3 tiles of an order-3 tensor on FP32 MFMA with an FP64 epilogue.
  * d_tiles: ntiles x {bi, bj, bk, nnz} int32; d_tile_f32: ntiles x 4096 fp32
  * cell values (layout (li*16 + lj)*16 + lk), built by cptc_dense_tiles_pack3.

@@ -274,3 +274,44 @@ def test_gram_normalize_absorb_matches_steps(ca, dev, R):
     Fn = b_F.numpy()
     assert rel_err(G2.numpy(), Fn.T @ Fn) < 1e-13
     assert np.all(G2.numpy()[3] == 0.0) and np.all(G2.numpy()[:, 3] == 0.0)
+
+
+@pytest.mark.parametrize("R", [1, 7, 32, 100])
+def test_sparse_mttkrp_range(ca, orc, dev, R):
+    """compute_sparse_mttkrp_async's sub-range path (sparse.cu:877-955):
+    elements [start, start + count) of one mode's view, against a numpy sum
+    over the same elements (closed form on the packed coordinates); ranges
+    that partition the view add up to the whole-view segment kernel."""
+    dims = (500, 300, 900)
+    t, views = zipf_views(ca, orc, dims, 30000, 40 + R)
+    rng = np.random.default_rng(R)
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    for mode in range(3):
+        v = views[mode]
+        c = np.asarray(v["coords"], np.uint64)
+        i = (c >> np.uint64(30)).astype(np.int64)
+        j = ((c >> np.uint64(15)) & np.uint64(0x7FFF)).astype(np.int64)
+        k = (c & np.uint64(0x7FFF)).astype(np.int64)
+        tgt, o0, o1 = {0: (i, j, k), 1: (j, i, k), 2: (k, i, j)}[mode]
+        F1 = F[1] if mode == 0 else F[0]
+        F2 = F[1] if mode == 2 else F[2]
+        dF1 = dF[1] if mode == 0 else dF[0]
+        dF2 = dF[1] if mode == 2 else dF[2]
+        dc, dv = to_dev(ca, v["coords"]), to_dev(ca, v["vals"])
+        n = len(v["vals"])
+        cuts = [0, 1, 977, n // 2, n - 5, n]
+        total = zeros(ca, (dims[mode], R))
+        for a, b in zip(cuts[:-1], cuts[1:]):
+            out = zeros(ca, (dims[mode], R))
+            for o in (out, total):
+                assert ca.lib.cptc_mttkrp_sparse3_range(mode, dc.data_ptr(), dv.data_ptr(), a,
+                                                        b - a, dF1.data_ptr(), dF2.data_ptr(),
+                                                        o.data_ptr(), R, stream(ca)) == 0
+            ca.sync()
+            ref = np.zeros((dims[mode], R))
+            np.add.at(ref, tgt[a:b], (np.asarray(v["vals"])[a:b, None] * F1[o0[a:b]]) * F2[o1[a:b]])
+            assert rel_err(out.numpy(), ref) <= 1e-12, (mode, a, b)
+        full = orc.mttkrp3_view(views, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                                dims[mode]).reshape(dims[mode], R)
+        assert rel_err(total.numpy(), full) <= 1e-12, mode
