@@ -224,7 +224,8 @@ void destroy(Als3* h)
 int alloc_buffers(Als3& h);
 
 // Tiles of each mode grouped by target row block (at most TILE_GROUP per
-// wave); only for the MFMA path at R <= 128 (the grouped kernel's LDS limit).
+// wave, fewer when the tiles are few); only for the MFMA path at R <= 128
+// (the grouped kernel's LDS limit).
 constexpr int TILE_GROUP = 8;
 
 int build_groups(Als3& h)
@@ -236,7 +237,7 @@ int build_groups(Als3& h)
     for (int m = 0; m < 3; ++m)
     {
         size_t ng = 0;
-        const int cap = cptc::tile_group_cap(TILE_GROUP);
+        const int cap = cptc::tile_group_cap(nt, h.R, h.num_cus, TILE_GROUP);
         CPTC_TRY(cptc_dense_groups(h.part.h_tiles4.data(), 4, nt, m, cap, order.data(),
                                    goff.data(), &ng));
         CPTC_HIP(hipMalloc(&h.d_order[m], nt * sizeof(uint32_t)));

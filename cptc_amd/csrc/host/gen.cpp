@@ -598,11 +598,11 @@ struct Gen
 Gen* as_gen(void* h) { return static_cast<Gen*>(h); }
 
 // Units of each slot grouped by target row block for the grouped MFMA
-// launch (UNIT_GROUP units per wave at most).  Device arrays are allocated
-// here; the caller frees them.
+// launch (UNIT_GROUP units per wave at most, fewer when the units are few).
+// Device arrays are allocated here; the caller frees them.
 constexpr int UNIT_GROUP = 16;
 
-int build_unit_groups(const cptc::DevUnitsN& u, hipStream_t s, uint32_t* order[3],
+int build_unit_groups(const cptc::DevUnitsN& u, int R, hipStream_t s, uint32_t* order[3],
                       uint32_t* goff[3], size_t ng[3])
 {
     for (int q = 0; q < 3; ++q)
@@ -617,7 +617,10 @@ int build_unit_groups(const cptc::DevUnitsN& u, hipStream_t s, uint32_t* order[3
                             hipMemcpyDeviceToHost, s));
     CPTC_HIP(hipStreamSynchronize(s));
     std::vector<uint32_t> ord(nu), off(nu + 1);
-    const int cap = cptc::tile_group_cap(UNIT_GROUP);
+    int dev = 0, cus = 0;
+    CPTC_HIP(hipGetDevice(&dev));
+    CPTC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int cap = cptc::tile_group_cap(nu, R, cus, UNIT_GROUP);
     for (int q = 0; q < 3; ++q)
     {
         CPTC_TRY(cptc_dense_groups(hdr.data(), 6, nu, q, cap, ord.data(), off.data(), &ng[q]));
@@ -841,7 +844,7 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
             GEN_TRY(dmalloc(&g->d_W, g->units.nunits * R));
             GEN_TRY(cptc_units_pack_nd(g->units.d_unit6, g->units.nunits, g->units.d_lid,
                                        g->units.d_val, g->d_tiles, s));
-            GEN_TRY(build_unit_groups(g->units, s, g->d_uorder, g->d_ugoff, g->ungroups));
+            GEN_TRY(build_unit_groups(g->units, R, s, g->d_uorder, g->d_ugoff, g->ungroups));
         }
         g->prep_ms[1] = ms_since(t0);
         if (verbose)
@@ -1341,7 +1344,7 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_tiles), u.nunits * 4096 * sizeof(float)));
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_W), u.nunits * R * sizeof(double)));
                 CPTC_TRY(cptc_units_pack_nd(u.d_unit6, u.nunits, u.d_lid, u.d_val, d_tiles, s));
-                const int rcg = build_unit_groups(u, s, gorder, ggoff, gn);
+                const int rcg = build_unit_groups(u, R, s, gorder, ggoff, gn);
                 for (int q = 0; q < 3; ++q)
                 {
                     own.p.push_back(gorder[q]);
