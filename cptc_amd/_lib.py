@@ -171,6 +171,8 @@ SIGNATURES = {
     "cptc_pack_level_keys": (_I, [_I, _P, _U64, _P, _P, _I, _P]),
     "cptc_mttkrp_seg_nd_keys": (_I, [_I, _I, _P, _I, _P, _P, _P, _U64, _P, _P, _P, _P, _U64, _P,
                                      _P, _I, _P]),
+    "cptc_mttkrp_seg_nd_keys_dims": (_I, [_I, _I, _P, _I, _P, _P, _P, _U64, _P, _P, _P, _P,
+                                          _U64, _P, _P, _P, _I, _P]),
     "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,

@@ -435,10 +435,10 @@ struct Gen
         }
         const cptc::DevViewN& v = views[n];
         if (v.key_bytes > 0 && R % 2 == 0)
-            CPTC_TRY(cptc_mttkrp_seg_nd_keys(N, n, v.d_key, v.key_bytes, v.level_modes.data(),
-                                             v.level_bits.data(), v.d_vals, v.nnz, v.d_row,
-                                             v.d_start, v.d_cnt, v.d_single, v.nseg, F(), d_FtV,
-                                             R, s));
+            CPTC_TRY(cptc_mttkrp_seg_nd_keys_dims(
+                N, n, v.d_key, v.key_bytes, v.level_modes.data(), v.level_bits.data(), v.d_vals,
+                v.nnz, v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg, F(), dims.data(), d_FtV,
+                R, s));
         else
             CPTC_TRY(cptc_mttkrp_seg_nd(N, n, v.d_sc, v.level_modes.data(), v.d_vals, nullptr,
                                         v.nnz, v.d_row, v.d_start, v.d_cnt, v.d_single, v.nseg,

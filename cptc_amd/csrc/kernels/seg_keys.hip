@@ -66,12 +66,14 @@ __device__ __forceinline__ double2 row2(const double* __restrict__ base, uint32_
         return *reinterpret_cast<const double2*>(base + uint64_t(idx) * uint64_t(R) + r);
 }
 
-template <int NO, int RT, typename KEY, int U, bool OFF32>
-__global__ __launch_bounds__(256) void seg_keys_kernel(
-    KeyLevels lv, const KEY* __restrict__ keys, const double* __restrict__ vals,
+// One row segment (one workgroup).  LEAF_LDS: the last level's factor is
+// read from fleaf (LDS) instead of global memory.
+template <int NO, int RT, typename KEY, int U, bool OFF32, bool LEAF_LDS>
+__device__ __forceinline__ void seg_keys_segment(
+    const KeyLevels& lv, const KEY* __restrict__ keys, const double* __restrict__ vals,
     const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
     const uint32_t* __restrict__ seg_cnt, const uint8_t* __restrict__ single,
-    double* __restrict__ FtV, int R)
+    double* __restrict__ FtV, int R, uint32_t seg, const double* __restrict__ fleaf)
 {
     constexpr int VEC = 2;
     constexpr int LPE = RT / VEC;            // lanes per element
@@ -85,7 +87,6 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
     __shared__ double lval[WAVES][EPW][WIN];
     __shared__ double red[WAVES][RT];
 
-    const uint32_t seg = blockIdx.x;
     const uint32_t row = seg_row[seg];
     const uint32_t start = seg_start[seg];
     const uint32_t cnt = seg_cnt[seg];
@@ -190,7 +191,14 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
             {
                 gl[u] = make_double2(0.0, 0.0);
                 if (i0 + u < nvalid)
-                    gl[u] = row2<OFF32>(Fleaf, uint32_t((kk[u] >> sh_leaf) & mk_leaf), R, rr);
+                {
+                    const uint32_t li = uint32_t((kk[u] >> sh_leaf) & mk_leaf);
+                    if constexpr (LEAF_LDS)
+                        gl[u] = *reinterpret_cast<const double2*>(
+                            fleaf + (li * uint32_t(R) + uint32_t(rr)));
+                    else
+                        gl[u] = row2<OFF32>(Fleaf, li, R, rr);
+                }
             }
             if constexpr (NO > 1)
             {
@@ -269,12 +277,67 @@ __global__ __launch_bounds__(256) void seg_keys_kernel(
     }
 }
 
+// One workgroup per segment, leaf factor from global memory.
+template <int NO, int RT, typename KEY, int U, bool OFF32>
+__global__ __launch_bounds__(256) void seg_keys_kernel(
+    KeyLevels lv, const KEY* __restrict__ keys, const double* __restrict__ vals,
+    const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
+    const uint32_t* __restrict__ seg_cnt, const uint8_t* __restrict__ single,
+    double* __restrict__ FtV, int R)
+{
+    seg_keys_segment<NO, RT, KEY, U, OFF32, false>(lv, keys, vals, seg_row, seg_start, seg_cnt,
+                                                   single, FtV, R, blockIdx.x, nullptr);
+}
+
+// Persistent grid (workgroup b takes segments b, b + grid, ...): the last
+// level's factor (leaf_n doubles) is copied into LDS once per workgroup, so
+// the per-element row gathers read LDS instead of the L1 / texture path.
+template <int NO, int RT, typename KEY, int U>
+__global__ __launch_bounds__(256) void seg_keys_leaf_lds_kernel(
+    KeyLevels lv, const KEY* __restrict__ keys, const double* __restrict__ vals,
+    const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ seg_start,
+    const uint32_t* __restrict__ seg_cnt, const uint8_t* __restrict__ single,
+    double* __restrict__ FtV, int R, uint32_t nseg, uint32_t leaf_n)
+{
+    extern __shared__ double fleaf[];
+    const double* __restrict__ src = lv.F[NO - 1];
+    for (uint32_t x = threadIdx.x; x < leaf_n; x += blockDim.x) fleaf[x] = src[x];
+    __syncthreads();
+    for (uint32_t seg = blockIdx.x; seg < nseg; seg += gridDim.x)
+    {
+        seg_keys_segment<NO, RT, KEY, U, true, true>(lv, keys, vals, seg_row, seg_start, seg_cnt,
+                                                     single, FtV, R, seg, fleaf);
+        __syncthreads();   // lkey / lval / red are reused by the next segment
+    }
+}
+
+// Leaf-in-LDS plan: the leaf factor takes at most LEAF_LDS_MAX bytes, so
+// that five workgroups (the register-limited occupancy) still share a CU's
+// LDS; the grid is LEAF_LDS_WG_PER_CU workgroups per CU, used when there
+// are at least LEAF_LDS_MIN_SEGS segments per workgroup to amortise the copy.
+constexpr size_t LEAF_LDS_MAX = 24 * 1024;
+constexpr unsigned LEAF_LDS_WG_PER_CU = 5;
+constexpr uint64_t LEAF_LDS_MIN_SEGS = 4;
+
+struct LeafPlan
+{
+    unsigned grid = 0;      // 0: global-memory kernel
+    uint32_t n = 0;         // leaf factor size in doubles
+};
+
 template <int NO, int RT, typename KEY>
 void launch_rt(const KeyLevels& lv, const void* keys, const double* vals, const uint32_t* row,
                const uint32_t* st, const uint32_t* cn, const uint8_t* single, uint64_t nseg,
-               double* FtV, int R, hipStream_t s)
+               double* FtV, int R, const LeafPlan& lp, hipStream_t s)
 {
     constexpr int U = (NO <= 2) ? 8 : 4;
+    if (lp.grid > 0)
+    {
+        hipLaunchKernelGGL((seg_keys_leaf_lds_kernel<NO, RT, KEY, U>), dim3(lp.grid), dim3(256),
+                           size_t(lp.n) * sizeof(double), s, lv, static_cast<const KEY*>(keys),
+                           vals, row, st, cn, single, FtV, R, uint32_t(nseg), lp.n);
+        return;
+    }
     // 32-bit row offsets when every level's (field range x R) stays below 2^28
     bool off32 = true;
     for (int l = 0; l < NO; ++l)
@@ -292,30 +355,30 @@ void launch_rt(const KeyLevels& lv, const void* keys, const double* vals, const 
 template <int NO, typename KEY>
 void launch_r(const KeyLevels& lv, const void* keys, const double* vals, const uint32_t* row,
               const uint32_t* st, const uint32_t* cn, const uint8_t* single, uint64_t nseg,
-              double* FtV, int R, hipStream_t s)
+              double* FtV, int R, const LeafPlan& lp, hipStream_t s)
 {
     if (R <= 8)
-        launch_rt<NO, 8, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s);
+        launch_rt<NO, 8, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s);
     else if (R <= 16)
-        launch_rt<NO, 16, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s);
+        launch_rt<NO, 16, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s);
     else
-        launch_rt<NO, 32, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s);
+        launch_rt<NO, 32, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s);
 }
 
 template <typename KEY>
 void launch_n(int NO, const KeyLevels& lv, const void* keys, const double* vals,
               const uint32_t* row, const uint32_t* st, const uint32_t* cn, const uint8_t* single,
-              uint64_t nseg, double* FtV, int R, hipStream_t s)
+              uint64_t nseg, double* FtV, int R, const LeafPlan& lp, hipStream_t s)
 {
     switch (NO)
     {
-    case 1: launch_r<1, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    case 2: launch_r<2, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    case 3: launch_r<3, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    case 4: launch_r<4, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    case 5: launch_r<5, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    case 6: launch_r<6, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
-    default: launch_r<7, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, s); break;
+    case 1: launch_r<1, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    case 2: launch_r<2, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    case 3: launch_r<3, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    case 4: launch_r<4, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    case 5: launch_r<5, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    case 6: launch_r<6, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
+    default: launch_r<7, KEY>(lv, keys, vals, row, st, cn, single, nseg, FtV, R, lp, s); break;
     }
 }
 
@@ -398,6 +461,21 @@ extern "C" int cptc_mttkrp_seg_nd_keys(int nmodes, int mode, const void* d_keys,
                                        uint64_t nseg, const double* const* h_F, double* d_FtV,
                                        int R, void* stream)
 {
+    return cptc_mttkrp_seg_nd_keys_dims(nmodes, mode, d_keys, key_bytes, level_modes, level_bits,
+                                        d_vals, nnz, d_seg_row, d_seg_start, d_seg_cnt, d_single,
+                                        nseg, h_F, nullptr, d_FtV, R, stream);
+}
+
+extern "C" int cptc_mttkrp_seg_nd_keys_dims(int nmodes, int mode, const void* d_keys,
+                                            int key_bytes, const int* level_modes,
+                                            const int* level_bits, const double* d_vals,
+                                            uint64_t nnz, const uint32_t* d_seg_row,
+                                            const uint32_t* d_seg_start,
+                                            const uint32_t* d_seg_cnt, const uint8_t* d_single,
+                                            uint64_t nseg, const double* const* h_F,
+                                            const uint64_t* h_dims, double* d_FtV, int R,
+                                            void* stream)
+{
     CPTC_REQUIRE(nmodes >= 2 && nmodes <= MAXM && mode >= 0 && mode < nmodes, CPTC_ERR_ARG,
                  "cptc_mttkrp_seg_nd_keys: nmodes %d mode %d", nmodes, mode);
     CPTC_REQUIRE(R >= 2 && R <= 32 && R % 2 == 0, CPTC_ERR_ARG,
@@ -431,12 +509,40 @@ extern "C" int cptc_mttkrp_seg_nd_keys(int nmodes, int mode, const void* d_keys,
         lv.F[q] = h_F[m];
     }
     hipStream_t s = cptc::as_stream(stream);
+    // the last level's factor in LDS when its size is known and small
+    LeafPlan lp;
+    if (h_dims)
+    {
+        const uint64_t rows = h_dims[level_modes[nlev - 1]];
+        const uint64_t bytes = rows * uint64_t(R) * sizeof(double);
+        // the key field bounds every leaf coordinate by its width, the dims by rows
+        if (rows >= 1 && rows <= lv.mask[nlev - 1] + 1 && bytes <= LEAF_LDS_MAX)
+        {
+            // CU count per device, queried once (every caller stores the same value)
+            static int cu_count[64] = {};
+            int dev = 0;
+            CPTC_HIP(hipGetDevice(&dev));
+            int cus = (dev >= 0 && dev < 64) ? cu_count[dev] : 0;
+            if (cus <= 0)
+            {
+                CPTC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+                if (cus <= 0) cus = 256;
+                if (dev >= 0 && dev < 64) cu_count[dev] = cus;
+            }
+            const uint64_t grid = uint64_t(LEAF_LDS_WG_PER_CU) * uint64_t(cus);
+            if (nseg >= LEAF_LDS_MIN_SEGS * grid)
+            {
+                lp.grid = unsigned(grid);
+                lp.n = uint32_t(rows * uint64_t(R));
+            }
+        }
+    }
     if (key_bytes == 4)
         launch_n<uint32_t>(nlev, lv, d_keys, d_vals, d_seg_row, d_seg_start, d_seg_cnt, d_single,
-                           nseg, d_FtV, R, s);
+                           nseg, d_FtV, R, lp, s);
     else
         launch_n<uint64_t>(nlev, lv, d_keys, d_vals, d_seg_row, d_seg_start, d_seg_cnt, d_single,
-                           nseg, d_FtV, R, s);
+                           nseg, d_FtV, R, lp, s);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

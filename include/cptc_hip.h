@@ -400,6 +400,21 @@ int cptc_mttkrp_seg_nd_keys(int nmodes, int mode, const void* d_keys, int key_by
                             const uint32_t* d_seg_cnt, const uint8_t* d_single, uint64_t nseg,
                             const double* const* h_F, double* d_FtV, int R, void* stream);
 
+/* cptc_mttkrp_seg_nd_keys with the tensor's dims (host array, nmodes
+ * entries; NULL = unknown).  With the dims, when the last level's factor
+ * takes at most 24 KB (dim x R x 8 bytes) and there are at least 4 segments
+ * per workgroup of a persistent grid (5 per CU), that factor is staged in
+ * LDS once per workgroup and the per-element row gathers read LDS.  Same
+ * result as cptc_mttkrp_seg_nd_keys up to the order of the atomic adds
+ * (generic.cu:271-343 is the reference's segment kernel). */
+int cptc_mttkrp_seg_nd_keys_dims(int nmodes, int mode, const void* d_keys, int key_bytes,
+                                 const int* level_modes, const int* level_bits,
+                                 const double* d_vals, uint64_t nnz, const uint32_t* d_seg_row,
+                                 const uint32_t* d_seg_start, const uint32_t* d_seg_cnt,
+                                 const uint8_t* d_single, uint64_t nseg,
+                                 const double* const* h_F, const uint64_t* h_dims,
+                                 double* d_FtV, int R, void* stream);
+
 /* Dense units (GDUnit, generic.cu:422-427): d_unit6 = nunits x {bi, bj, bk,
  * nnz, start, outer_off}; pool lid = la * 256 + lb * 16 + lc (slot order).
  * Packs each unit's pool into a 16^3 FP32 tile (nunits x 4096 floats):

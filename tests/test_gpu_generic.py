@@ -289,6 +289,61 @@ def test_seg_keys_kernel_vs_closed_form(ca, dev, N, R, dims, order):
     assert kinds == {0, 1}, "both store and atomic rows exercised"
 
 
+@pytest.mark.parametrize("N,R,dims", [(2, 32, (9000, 90)), (3, 8, (20000, 100, 200)),
+                                      (4, 32, (8000, 40, 30, 20)), (5, 16, (8000, 64, 64, 32, 16)),
+                                      (2, 32, (9000, 250)), (4, 16, (3000, 24, 1140, 1717))])
+def test_seg_keys_leaf_lds(ca, dev, N, R, dims):
+    """The dims variant (last level's factor staged in LDS, persistent grid)
+    against the closed form and against the global-gather variant, on mode 0
+    with thousands of segments: the first four shapes' leaf factors fit 24 KB
+    (LDS path; the second has 4-byte keys), the last two do not."""
+    rng = np.random.default_rng(N * 31 + R)
+    nnz = 400000
+    idx = np.stack([np.minimum((rng.pareto(1.1, nnz) * d / 6).astype(np.int64), d - 1)
+                    for d in dims]).astype(np.uint32)
+    val = rng.standard_normal(nnz)
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [dbuf(ca, f) for f in F]
+    n = 0
+    lev = sorted(range(1, N), key=lambda m: dims[m])
+    bits = [max(1, int(dims[m] - 1).bit_length()) for m in lev]
+    lb = (C.c_int * len(lev))(*bits)
+    kb = ca.lib.cptc_level_key_bytes(len(lev), lb)
+    perm = np.lexsort(tuple(idx[m] for m in reversed(lev)) + (idx[n],))
+    sc = np.ascontiguousarray(np.stack([idx[m][perm] for m in lev]))
+    srow, sst, scnt, ssingle = seg_table(idx[n][perm])
+    assert len(srow) >= 2048 and set(ssingle.tolist()) == {0, 1}
+    b = {k: dbuf(ca, a) for k, a in (("sc", sc), ("val", val[perm]), ("row", srow),
+                                     ("st", sst), ("cnt", scnt), ("single", ssingle))}
+    keys = ca.DevBuf.zeros(nnz * kb // 8 + 1)
+    assert ca.lib.cptc_pack_level_keys(len(lev), b["sc"].data_ptr(), nnz, lb, keys.data_ptr(),
+                                       kb, None) == 0
+    init = rng.standard_normal((dims[n], R))
+    outs = []
+    for with_dims in (False, True):
+        out = dbuf(ca, init.copy())
+        args = [N, n, keys.data_ptr(), kb, (C.c_int * len(lev))(*lev), lb, b["val"].data_ptr(),
+                nnz, b["row"].data_ptr(), b["st"].data_ptr(), b["cnt"].data_ptr(),
+                b["single"].data_ptr(), len(srow), fptrs(dF)]
+        if with_dims:
+            rc = ca.lib.cptc_mttkrp_seg_nd_keys_dims(*args, (C.c_uint64 * N)(*dims),
+                                                     out.data_ptr(), R, None)
+        else:
+            rc = ca.lib.cptc_mttkrp_seg_nd_keys(*args, out.data_ptr(), R, None)
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        outs.append(out.numpy().reshape(dims[n], R))
+    contrib = val[:, None] * np.prod([F[m][idx[m]] for m in range(1, N)], axis=0)
+    M = np.zeros((dims[n], R))
+    np.add.at(M, idx[n], contrib)
+    exp = init.copy()
+    exp[srow[ssingle == 1]] = M[srow[ssingle == 1]]
+    multi = np.unique(srow[ssingle == 0])
+    exp[multi] += M[multi]
+    assert rel_err(outs[1], exp) <= 1e-10
+    assert rel_err(outs[1], outs[0]) <= 1e-13
+
+
 @pytest.mark.parametrize("N,R,inner,G", [(4, 8, (0, 1, 2), 0), (4, 16, (0, 1, 2), 4),
                                          (5, 32, (0, 1, 2), 16), (4, 20, (1, 2, 3), 0),
                                          (4, 8, (0, 2, 3), 2), (5, 16, (1, 3, 4), 16),
