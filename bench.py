@@ -257,8 +257,9 @@ def bench_generic(ca, args, spec, R) -> int:
     ca.sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
+    # kernel events on every 8th iteration and the last (the driver's sampling)
     seg_ms, unit_ms, kit = g.kernel_times(reset=True)
-    assert kit == args.steps
+    assert 1 <= kit <= args.steps
     dims = t.dims
     b_seg = [gather_bytes(knnz[m], dims[m], R, N) for m in range(N)]
     seg_launch = [float(seg_ms[m]) / kit for m in range(N)]

@@ -412,7 +412,9 @@ class Gen:
         return out, it.value
 
     def kernel_times(self, reset: bool = True):
-        """(segment-kernel ms per mode, unit-kernel ms per mode, iterations)."""
+        """(segment-kernel ms per mode, unit-kernel ms per mode, iterations
+        timed).  Queued runs time the kernels on every 8th iteration and on
+        the last one; verbose or profiled runs on every iteration."""
         out = np.zeros(16, np.float64)
         it = C.c_int()
         check(lib.cptc_gen_kernel_times(self._h, out.ctypes.data, C.byref(it), int(reset)),

@@ -533,7 +533,9 @@ int cptc_gen_profile(void* handle, double* out5, int* iters, int reset);
 /* Kernel times summed over cptc_gen_run iterations (hipEvents on the
  * driver's stream): out[m] = ms of mode m's segment MTTKRP kernel,
  * out[CPTC_MAX_MODES + m] = ms of its dense-unit kernel (0 when none);
- * *iters = iterations summed; reset != 0 zeroes the sums.  Measurement
+ * *iters = iterations summed; reset != 0 zeroes the sums.  A queued
+ * (quiet) run times every 8th iteration and its last one; a verbose or
+ * profiled run times every iteration.  Measurement
  * plumbing (GEN_PROFILE's phase events, generic.cu:2016-2240, are the
  * closest counterpart). */
 int cptc_gen_kernel_times(void* handle, double* out16, int* iters, int reset);
