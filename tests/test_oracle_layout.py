@@ -183,3 +183,79 @@ def test_views_reject_wide_dims(orc):
     with pytest.raises(RuntimeError):
         orc.views3(np.array([0], np.uint32), np.array([0], np.uint32), np.array([0], np.uint32),
                    np.array([1.0]), (40000, 2, 2))
+
+
+# -------------------------------------------------------------- dense views --
+
+def np_decode_pool(p):
+    """partition.cu:2335-2379: each tile's pool entries, in tile then pool order,
+    back to global coordinates (local id = (li*16 + lj)*16 + lk)."""
+    i, j, k, v = [], [], [], []
+    off = p["pool_off"]
+    for t, (b0, b1, b2, cnt) in enumerate(p["tiles"].tolist()):
+        lid = np.asarray(p["pool_lid"][off[t]:off[t] + cnt], np.int64)
+        assert len(lid) == cnt
+        i.append(b0 * 16 + (lid >> 8))
+        j.append(b1 * 16 + ((lid >> 4) & 15))
+        k.append(b2 * 16 + (lid & 15))
+        v.append(np.asarray(p["pool_val"][off[t]:off[t] + cnt]))
+    cat = (lambda xs, dt: np.concatenate(xs).astype(dt) if xs else np.zeros(0, dt))
+    return (cat(i, np.uint32), cat(j, np.uint32), cat(k, np.uint32), cat(v, np.float64))
+
+
+@pytest.mark.parametrize("dup", [False, True])
+def test_dense_views_match_numpy(orc, dup):
+    """dense_views3 (partition.cu:2387-2517) = the pool decoded in tile order, then
+    the same stable (target, o1, o0) sort and 1024-element segments as views3."""
+    rng = np.random.default_rng(21)
+    dims = (70, 45, 90)
+    idx, val = rand_coo(rng, dims, 6000, dup)
+    # clustered blocks (two full tiles' worth of candidates) so several tiles qualify
+    idx[:, :2500] = np.stack([rng.integers(0, 16, 2500), rng.integers(16, 32, 2500),
+                              rng.integers(32, 48, 2500)])
+    idx[:, 2500:4000] = np.stack([rng.integers(48, 64, 1500), rng.integers(0, 16, 1500),
+                                  rng.integers(64, 80, 1500)])
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    assert len(p["tiles"]) >= 2
+    got = orc.dense_views3(p, dims)
+    di, dj, dk, dv = np_decode_pool(p)
+    # multiset: the decoded pool is exactly the elements the partition put into tiles
+    sp = np.stack([p["sp_i"], p["sp_j"], p["sp_k"]]).astype(np.int64)
+    both = np.concatenate([np.stack([di, dj, dk]).astype(np.int64), sp], axis=1)
+    allv = np.concatenate([dv, p["sp_val"]])
+    o_in = np.lexsort((val, idx[2], idx[1], idx[0]))
+    o_out = np.lexsort((allv, both[2], both[1], both[0]))
+    assert np.array_equal(idx[:, o_in].astype(np.int64), both[:, o_out])
+    assert np.array_equal(val[o_in], allv[o_out])
+    ref = np_views(di, dj, dk, dv, dims)
+    for mode in range(3):
+        for key in ("coords", "vals", "blk_row", "blk_start", "blk_cnt"):
+            assert np.array_equal(np.asarray(got[mode][key]), np.asarray(ref[mode][key])), (mode, key)
+
+
+def test_dense_views_mttkrp_closed_form(orc):
+    """Residual view + dense view MTTKRP (the FP64 fallback path) equals the
+    closed form Y = X_(n) (KR of the other factors) over the whole tensor, with
+    duplicates summed (the FP64 kernels add every element)."""
+    rng = np.random.default_rng(22)
+    dims, R = (40, 37, 45), 5
+    cells = np.array(np.meshgrid(np.arange(32, 40), np.arange(16, 37), np.arange(0, 45),
+                                 indexing="ij")).reshape(3, -1)
+    dense_part = cells[:, rng.random(cells.shape[1]) < 0.6]
+    bg = np.stack([rng.integers(0, d, 900) for d in dims])
+    idx = np.concatenate([dense_part, bg, dense_part[:, :50]], axis=1).astype(np.int32)
+    val = rng.standard_normal(idx.shape[1])
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    assert len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
+    rv = orc.views3(p["sp_i"], p["sp_j"], p["sp_k"], p["sp_val"], dims)
+    dvw = orc.dense_views3(p, dims)
+    X = np.zeros(dims)
+    np.add.at(X, tuple(idx), val)
+    F = [rng.random((d, R)) for d in dims]
+    subs = ["ijk,jr,kr->ir", "ijk,ir,kr->jr", "ijk,ir,jr->kr"]
+    for mode in range(3):
+        got = sum(orc.mttkrp3_view(vw, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                                   dims[mode]).reshape(dims[mode], R) for vw in (rv, dvw))
+        others = [F[m] for m in range(3) if m != mode]
+        ref = np.einsum(subs[mode], X, *others)
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-13

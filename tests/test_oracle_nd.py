@@ -351,3 +351,57 @@ def test_selftest_tensor_shape(orc):
     assert 4000 < len(val) < 3 * 2 * 4096 + 3 * 8 * 8 * 4 + 4000
     assert all(len(F[m]) == dims[m] * 8 for m in range(4))
     assert np.all(idx.max(axis=1) < np.array(dims))
+
+
+def np_selftest_tensor():
+    """generic.cu:1389-1441 restated with numpy's MT19937 (legacy seeding =
+    std::mt19937(1234)) and libstdc++'s generate_canonical<double, 53> (two
+    32-bit draws per double). The residual scatter's push(...) arguments draw
+    right to left: that is g++'s order for this call (the reference's nvcc host
+    pass compiles it with g++), so the value is drawn first and i last."""
+    bg = np.random.MT19937()
+    bg._legacy_seeding(1234)
+    buf = []
+
+    def uv():
+        if not buf:
+            raw = bg.random_raw(2 * 4096).astype(np.float64)
+            buf.extend(((raw[0::2] + raw[1::2] * 2.0 ** 32) / 2.0 ** 64).tolist()[::-1])
+        return buf.pop()
+
+    dims = (40, 24, 36, 3)
+    co, vals = [[], [], [], []], []
+
+    def push(c, v):
+        for m in range(4):
+            co[m].append(c[m])
+        vals.append(v)
+
+    for l in range(dims[3]):
+        for t in ((0, 0, 0), (1, 0, 1)):
+            for a in range(16):
+                for b in range(16):
+                    for c in range(16):
+                        if uv() < 0.5:
+                            push((t[0] * 16 + a, t[1] * 16 + b, t[2] * 16 + c, l), 1.0 + uv())
+    for l in range(dims[3]):
+        for a in range(32, dims[0]):
+            for b in range(16, dims[1]):
+                for c in range(32, dims[2]):
+                    if uv() < 0.6:
+                        push((a, b, c, l), 1.0 + uv())
+    for _ in range(4000):
+        d = [uv() for _ in range(5)][::-1]        # right-to-left argument evaluation
+        push(tuple(int(d[m] * dims[m]) % dims[m] for m in range(4)), 1.0 + d[4])
+    F = [np.array([uv() for _ in range(dims[m] * 8)]) for m in range(4)]
+    return np.array(co, np.uint32), np.array(vals), dims, F
+
+
+def test_selftest_tensor_mt19937(orc):
+    idx, val, dims, F = orc.selftest_tensor()
+    ridx, rval, rdims, rF = np_selftest_tensor()
+    assert tuple(dims) == rdims
+    assert np.array_equal(idx, ridx)
+    assert np.array_equal(val, rval)
+    for m in range(4):
+        assert np.array_equal(np.asarray(F[m]), rF[m])
