@@ -116,8 +116,9 @@ __global__ void hadamard_kernel(const double* A, const double* B, double* C, siz
 //      split over the group and reduced with xor-shuffles), X^T stored in
 //      the free upper triangle;
 //   3. Ainv = X^T X.
-// Any pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1 and
-// leaves Ainv to the Jacobi kernel.
+// Any pivot <= 1e-10 * max diag (or non-finite), or a computed inverse
+// that fails fast_inverse_ok, sets *fallback = 1 and leaves Ainv to the
+// Jacobi kernel.
 // ---------------------------------------------------------------------------
 constexpr int PINV_THREADS = 1024;
 constexpr int CHOL_NB = 16;
@@ -127,6 +128,38 @@ __device__ inline void wave_sync_lds()
 {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
+}
+
+// Fast-path acceptance.  The reference keeps sigma_i > R ulp(sigma_max) and
+// drops the rest (solver.cu:957-966), so the truncated pseudoinverse equals
+// the inverse exactly when sigma_min > R ulp(sigma_max).  With
+// kappa_2 <= ||A||_F ||A^-1||_F and ulp(x) <= DBL_EPSILON x, the product
+// ||A||_F ||A^-1||_F < 1 / (64 R DBL_EPSILON) implies
+// sigma_min > 64 R ulp(sigma_max); the factor 64 covers the rounding of the
+// computed inverse.  Small pivots alone do not show this: A = L L^T with L
+// unit lower triangular and every sub-diagonal entry -1 has LDL^T pivots 1
+// and kappa ~ 4^R.
+__device__ inline bool fast_inverse_ok(double fro2_A, double fro2_inv, int R)
+{
+    const double lim = 1.0 / (64.0 * double(R) * DBL_EPSILON);
+    const double p = sqrt(fro2_A) * sqrt(fro2_inv);
+    return isfinite(p) && p < lim;
+}
+
+// Sum over a workgroup of NT threads (NT / 64 waves); every thread gets the
+// total.  red holds NT / 64 doubles; two barriers.
+template <int NT>
+__device__ inline double block_sum_all(double v, double* red)
+{
+#pragma unroll
+    for (int o = WAVE / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < NT / WAVE; ++w) t += red[w];
+    __syncthreads();
+    return t;
 }
 
 __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double* __restrict__ Ain,
@@ -143,9 +176,16 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
     const int lane = tid & (WAVE - 1);
     const int wave = tid / WAVE;
     const int n2 = R * R;
-    for (int x = tid; x < n2; x += PINV_THREADS) A[x] = Ain[x];
+    __shared__ double red[PINV_THREADS / WAVE];
+    double fa = 0.0;
+    for (int x = tid; x < n2; x += PINV_THREADS)
+    {
+        const double v = Ain[x];
+        A[x] = v;
+        fa += v * v;
+    }
     if (tid == 0) *fallback = 0;
-    __syncthreads();
+    const double fro2_A = block_sum_all<PINV_THREADS>(fa, red);
     if (tid == 0)
     {
         double md = 0.0;
@@ -235,6 +275,7 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
     // 4. Ainv = X^T X in 4 x 4 register blocks: Ainv[r][c] = sum_j X[j][r] X[j][c]
     //    (X[j][r] = 0 for j < r, so j starts at the block's smaller index)
     const int nb = (R + 3) / 4;
+    double fi = 0.0;
     for (int b = tid; b < nb * nb; b += PINV_THREADS)
     {
         const int r0 = 4 * (b / nb), c0 = 4 * (b % nb);
@@ -262,8 +303,16 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                if (r0 + i < R && c0 + k < R) Ainv[(r0 + i) * R + c0 + k] = acc[i][k];
+                if (r0 + i < R && c0 + k < R)
+                {
+                    Ainv[(r0 + i) * R + c0 + k] = acc[i][k];
+                    fi += acc[i][k] * acc[i][k];
+                }
     }
+    // 5. condition check (fast_inverse_ok); on failure the Jacobi kernel
+    //    overwrites Ainv with the truncated pseudoinverse
+    const double fro2_inv = block_sum_all<PINV_THREADS>(fi, red);
+    if (tid == 0 && !fast_inverse_ok(fro2_A, fro2_inv, R)) *fallback = 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -276,8 +325,9 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
 // and after every pivot the matrix holds -A^-1.  The matrix stays
 // symmetric, so pivot row k is column k.  The pivots are the LDL^T pivots
 // (the squared Cholesky diagonal), so the fast-path test is the Cholesky
-// one: a pivot <= 1e-10 * max diag (or non-finite) sets *fallback = 1 and
-// leaves Ainv to the Jacobi kernel.
+// one: a pivot <= 1e-10 * max diag (or non-finite), or an inverse that
+// fails fast_inverse_ok, sets *fallback = 1 and leaves Ainv to the Jacobi
+// kernel.
 // Thread layout: RT >= R rows (16, 32 or 64), LPR = SWEEP_T / RT threads
 // per row, each holding C = RT / LPR consecutive columns: thread = row + RT
 // * part, columns part * C .. part * C + C - 1 (C = 1, 4, 16).  Per pivot
@@ -297,6 +347,7 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
     static_assert(C >= 1 && C <= 16, "sweep layout");
     __shared__ double col[RT];
     __shared__ double wmax[SWEEP_T / WAVE];
+    __shared__ double wsum[SWEEP_T / WAVE];
     const int tid = threadIdx.x;
     const int row = tid % RT;
     const int part = tid / RT;
@@ -305,17 +356,34 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
 #pragma unroll
     for (int c = 0; c < C; ++c)
         a[c] = (row < R && c0 + c < R) ? Ain[size_t(row) * R + c0 + c] : 0.0;
-    // largest diagonal entry: the thread holding (row, row) contributes it
-    double md = 0.0;
+    // largest diagonal entry (the thread holding (row, row) contributes it)
+    // and ||A||_F^2
+    double md = 0.0, fa = 0.0;
 #pragma unroll
     for (int c = 0; c < C; ++c)
+    {
         if (c0 + c == row) md = a[c];
+        fa += a[c] * a[c];
+    }
 #pragma unroll
-    for (int o = WAVE / 2; o >= 1; o >>= 1) md = fmax(md, __shfl_xor(md, o));
-    if ((tid & (WAVE - 1)) == 0) wmax[tid / WAVE] = md;
+    for (int o = WAVE / 2; o >= 1; o >>= 1)
+    {
+        md = fmax(md, __shfl_xor(md, o));
+        fa += __shfl_xor(fa, o);
+    }
+    if ((tid & (WAVE - 1)) == 0)
+    {
+        wmax[tid / WAVE] = md;
+        wsum[tid / WAVE] = fa;
+    }
     __syncthreads();
+    double fro2_A = 0.0;
 #pragma unroll
-    for (int w = 0; w < SWEEP_T / WAVE; ++w) md = fmax(md, wmax[w]);
+    for (int w = 0; w < SWEEP_T / WAVE; ++w)
+    {
+        md = fmax(md, wmax[w]);
+        fro2_A += wsum[w];
+    }
     const double tau = 1e-10 * md;
     int ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
 #pragma unroll 1
@@ -352,6 +420,16 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
         }
     }
     if (!ok)
+    {
+        if (tid == 0) *fallback = 1;
+        return;
+    }
+    // condition check (fast_inverse_ok); padding entries are 0
+    double fi = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) fi += a[c] * a[c];
+    const double fro2_inv = block_sum_all<SWEEP_T>(fi, wsum);
+    if (!fast_inverse_ok(fro2_A, fro2_inv, R))
     {
         if (tid == 0) *fallback = 1;
         return;
@@ -844,16 +922,14 @@ extern "C" int cptc_hadamard(const double* d_A, const double* d_B, double* d_C, 
 }
 
 namespace {
-int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStream_t s)
+// The pinv kernels on caller-provided workspace: work (R x R, the matrix in
+// global memory; read only when R > 128), V (R x R Jacobi eigenvectors) and
+// flag (the path: 0 fast, 1 Jacobi).
+int pinv_launch_ws(const double* d_FtF, double* d_Ainv, int R, int* flag, double* work,
+                   double* V, hipStream_t s)
 {
     const size_t RR = size_t(R) * R;
     const bool use_lds = RR * sizeof(double) <= 128 * 1024;
-    // scratch: [work RR (global A when R > 128)] [V RR] [flag]
-    void* buf = nullptr;
-    CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, (2 * RR + 2) * sizeof(double), &buf));
-    double* work = static_cast<double*>(buf);
-    double* V = work + RR;
-    int* flag = d_path ? d_path : reinterpret_cast<int*>(V + RR);
     const size_t lds = use_lds ? RR * sizeof(double) : 0;
     static bool attr_set = false;
     if (!attr_set)
@@ -881,6 +957,18 @@ int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStre
                        d_Ainv, flag, int(use_lds));
     CPTC_LAUNCHED();
     return CPTC_OK;
+}
+
+int pinv_launch(const double* d_FtF, double* d_Ainv, int R, int* d_path, hipStream_t s)
+{
+    const size_t RR = size_t(R) * R;
+    // scratch: [work RR (global A when R > 128)] [V RR] [flag]
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, (2 * RR + 2) * sizeof(double), &buf));
+    double* work = static_cast<double*>(buf);
+    double* V = work + RR;
+    int* flag = d_path ? d_path : reinterpret_cast<int*>(V + RR);
+    return pinv_launch_ws(d_FtF, d_Ainv, R, flag, work, V, s);
 }
 
 int apply_launch(const double* d_FtV, const double* d_Ainv, double* d_F, size_t dim, int R,

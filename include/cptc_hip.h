@@ -205,8 +205,10 @@ int cptc_hadamard(const double* d_A, const double* d_B, double* d_C, size_t n, v
 
 /* F = FtV * pinv(FtF) (row-major dim x R), then F[:, r] /= div[r] when
  * d_div != NULL.  pinv by the truncated rule of the reference: singular
- * values <= R * ulp(sigma_max) are dropped.  SPD fast path (Cholesky
- * inverse) when every pivot exceeds 1e-9 * max diag; otherwise an on-device
+ * values <= R * ulp(sigma_max) are dropped.  SPD fast path (register sweep
+ * for R <= 64, blocked Cholesky inverse above) when every pivot exceeds
+ * 1e-10 * max diag and ||FtF||_F ||inverse||_F < 1 / (64 R DBL_EPSILON),
+ * which proves that no singular value is dropped; otherwise an on-device
  * cyclic Jacobi eigen-decomposition applies the truncation rule exactly.
  * Replaces solve_als_system_svd / _nosync + factor_divide_lambda_kernel
  * (solver.cu:900-1096; als.cu:345-360, 485-499). */

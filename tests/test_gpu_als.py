@@ -131,6 +131,32 @@ def test_als_fit_matches_oracle_20_iters(ca, orc, dev, kind, path, R):
             assert np.array_equal(h.factor(m, unpermuted=True), h.factor(m)[perms[m]])
 
 
+@pytest.mark.parametrize("kind,path,R", [("blocks", 1, 16), ("blocks", 2, 16), ("zipf", 2, 33)])
+def test_residual3_identical_factors(ca, orc, dev, kind, path, R):
+    """Exact residual (common.cu:251-650) on identical factors and lambda: the
+    device sum over the residual view, the FP64 dense view or the tile pools
+    equals the closed form sum_e (v_e - sum_r l_r a b c)^2 over the relabelled
+    COO (duplicates included, every element once) and the oracle's sum."""
+    t = make(ca, kind, 6)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+        h.run(2)                                    # lambda != 1 and factors of an ALS state
+        F = [h.factor(m) for m in range(3)]
+        lam = h.lam()
+        assert np.any(np.abs(lam - 1.0) > 1e-3)
+        res, x2 = h.residual()
+        mfma = int(h.info.use_mfma) == 1 and len(p["tiles"]) > 0
+    idx = [perms[m][t.idx[m]].astype(np.int64) for m in range(3)]
+    xhat = np.einsum("r,er,er,er->e", lam, F[0][idx[0]], F[1][idx[1]], F[2][idx[2]])
+    ref = float(np.sum((t.val - xhat) ** 2))
+    assert abs(x2 - float(np.sum(t.val ** 2))) <= 1e-13 * x2
+    assert abs(res - ref) <= 1e-12 * ref, (res, ref)
+    dv = orc.dense_views3(p, t.dims) if (not mfma and len(p["pool_val"])) else None
+    o = orc.Als3(v, dv, p if mfma else None, x2, t.dims, R, *(f.ravel() for f in F), lam)
+    ores, ox2 = o.residual(True)
+    assert abs(res - ores) <= 1e-12 * ores and abs(x2 - ox2) <= 1e-13 * ox2
+
+
 def test_cli_runs_and_exports(ca, dev, tmp_path):
     t = make(ca, "zipf", 5)
     path = str(tmp_path / "t.tns")

@@ -215,6 +215,63 @@ def test_pinv_singular_takes_jacobi_path(ca, orc, dev, R):
     assert rel_err(P @ A @ P, P) < 1e-8
 
 
+@pytest.mark.parametrize("R,c,scale", [(16, 3.0, 1.0), (32, 1.0, 1.0), (64, 1.0, 1e-3),
+                                         (128, 1.0, 1.0), (128, 1.0, 1e6)])
+def test_pinv_kahan_type_truncates(ca, orc, dev, R, c, scale):
+    """A = s L L^T, L unit lower triangular with every sub-diagonal entry -c:
+    every LDL^T pivot is s (no pivot test fires) but one eigenvalue lies far
+    below R ulp(sigma_max), so the reference's truncated pseudoinverse
+    (solver.cu:900-1002) drops it and the plain inverse (entries ~ (1+c)^(2R))
+    is wrong.  The fast path must hand over to the Jacobi pseudoinverse."""
+    L = np.eye(R) + np.tril(np.full((R, R), -c), -1)
+    A = scale * (L @ L.T)
+    w = np.linalg.eigvalsh(A)
+    tol = R * np.spacing(w.max())
+    assert np.sum(w <= tol) == 1 and np.sort(w)[1] > 1e6 * tol   # one dropped, clear gap
+    dA = to_dev(ca, A)
+    Ainv = zeros(ca, (R, R))
+    path = zeros(ca, (1,), np.int32)
+    assert ca.lib.cptc_pinv_sym(dA.data_ptr(), Ainv.data_ptr(), R, path.data_ptr(),
+                                stream(ca)) == 0
+    ca.sync()
+    assert int(path.numpy()[0]) == 1
+    P = Ainv.numpy()
+    ref, _ = orc.pinv_sym(A.ravel(), R)
+    ref = ref.reshape(R, R)
+    assert np.linalg.norm(P, 2) < 1.0 / tol                   # truncated, not the inverse
+    assert rel_err(P, ref) < 1e-8
+    assert rel_err(P @ A @ P, P) < 1e-8
+    # the solve entry point takes the same path
+    dim = 300
+    Y = np.random.default_rng(R).standard_normal((dim, R))
+    lam = np.ones(R)
+    dY, dl = to_dev(ca, Y), to_dev(ca, lam)
+    out = zeros(ca, (dim, R))
+    assert ca.lib.cptc_solve_pinv(dA.data_ptr(), dY.data_ptr(), out.data_ptr(), dim, R,
+                                  dl.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    assert rel_err(out.numpy(), Y @ ref) < 1e-8
+
+
+@pytest.mark.parametrize("R", [32, 128])
+def test_pinv_moderately_ill_conditioned_stays_fast(ca, dev, R):
+    """kappa ~ 1e8: far from truncation, so the fast path keeps the inverse."""
+    rng = np.random.default_rng(40 + R)
+    Q, _ = np.linalg.qr(rng.standard_normal((R, R)))
+    A = (Q * np.logspace(0, -8, R)) @ Q.T
+    A = 0.5 * (A + A.T)
+    dA = to_dev(ca, A)
+    Ainv = zeros(ca, (R, R))
+    path = zeros(ca, (1,), np.int32)
+    assert ca.lib.cptc_pinv_sym(dA.data_ptr(), Ainv.data_ptr(), R, path.data_ptr(),
+                                stream(ca)) == 0
+    ca.sync()
+    assert int(path.numpy()[0]) == 0
+    # a backward-stable inverse leaves ||P A - I|| ~ kappa * eps * R = 1e8 * 2.2e-16 * R
+    assert rel_err(Ainv.numpy() @ A, np.eye(R)) < 1e-4
+    assert rel_err(Ainv.numpy(), np.linalg.inv(A)) < 1e-4
+
+
 def test_norms_normalize_fit(ca, dev):
     rng = np.random.default_rng(8)
     rows, R = 3001, 32
