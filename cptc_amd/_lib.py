@@ -141,6 +141,7 @@ SIGNATURES = {
     "cptc_gram_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
+    "cptc_solve_pinv_noalloc": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),
     "cptc_apply_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_colnorms": (_I, [_P, _Z, _I, _P, _P]),

@@ -7,6 +7,7 @@
 
 #include <cfloat>
 #include <cmath>
+#include <mutex>
 
 #include "../host/hip_util.hpp"
 
@@ -1010,6 +1011,66 @@ extern "C" int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double*
     CPTC_TRY(cptc::scratch_get(cptc::SCR_FLAGS, size_t(R) * R * sizeof(double) + 64, &buf));
     double* Ainv = static_cast<double*>(buf);
     CPTC_TRY(pinv_launch(d_FtF, Ainv, R, nullptr, s));
+    return apply_launch(d_FtV, Ainv, d_F, dim, R, d_div, s);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free solve.  The solve's workspace lives in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the
+// process ends: [Ainv: NOALLOC_MAX_R^2 doubles] [V: NOALLOC_MAX_R^2 doubles]
+// [path flag].  Host code never passes `scratch` itself (in host code the
+// name is a host-side stand-in, not a device address): the first call on a
+// device takes the device address with hipGetSymbolAddress and keeps it per
+// device.  Nothing needs clearing between calls (the fast kernel writes the
+// flag before the Jacobi kernel reads it; Ainv and V are written before they
+// are read).  Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int NOALLOC_MAX_R = 128;
+constexpr size_t NOALLOC_RR = size_t(NOALLOC_MAX_R) * NOALLOC_MAX_R;
+constexpr int NOALLOC_MAX_DEV = 64;
+static_assert(NOALLOC_RR * sizeof(double) <= 128 * 1024, "R <= 128 keeps the matrix in LDS");
+
+static __device__ __align__(256) double scratch[2 * NOALLOC_RR + 32];
+
+std::mutex g_scratch_mu;
+double* g_scratch_ptr[NOALLOC_MAX_DEV] = {};
+
+int noalloc_scratch(double** out)
+{
+    int dev = 0;
+    CPTC_HIP(hipGetDevice(&dev));
+    CPTC_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEV, CPTC_ERR_ARG,
+                 "cptc_solve_pinv_noalloc: device %d beyond %d", dev, NOALLOC_MAX_DEV);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev])
+    {
+        void* p = nullptr;
+        CPTC_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        CPTC_REQUIRE(p != nullptr, CPTC_ERR_HIP, "cptc_solve_pinv_noalloc: no scratch address");
+        g_scratch_ptr[dev] = static_cast<double*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return CPTC_OK;
+}
+}  // namespace
+
+extern "C" int cptc_solve_pinv_noalloc(const double* d_FtF, const double* d_FtV, double* d_F,
+                                       size_t dim, int R, const double* d_div, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && d_FtF && d_FtV && d_F, CPTC_ERR_ARG,
+                 "cptc_solve_pinv_noalloc: bad arguments");
+    CPTC_REQUIRE(R <= NOALLOC_MAX_R, CPTC_ERR_ARG,
+                 "cptc_solve_pinv_noalloc: R = %d exceeds the allocation-free maximum %d "
+                 "(use cptc_solve_pinv)", R, NOALLOC_MAX_R);
+    hipStream_t s = cptc::as_stream(stream);
+    double* ws = nullptr;
+    CPTC_TRY(noalloc_scratch(&ws));
+    double* Ainv = ws;
+    double* V = ws + NOALLOC_RR;
+    int* flag = reinterpret_cast<int*>(ws + 2 * NOALLOC_RR);
+    // R <= 128: the kernels keep the matrix in LDS and never read `work`
+    CPTC_TRY(pinv_launch_ws(d_FtF, Ainv, R, flag, V, V, s));
     return apply_launch(d_FtV, Ainv, d_F, dim, R, d_div, s);
 }
 

@@ -215,6 +215,18 @@ int cptc_hadamard(const double* d_A, const double* d_B, double* d_C, size_t n, v
 int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim, int R,
                     const double* d_div, void* stream);
 
+/* cptc_solve_pinv without any device allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid hipMalloc).
+ * Same kernels and result as cptc_solve_pinv, for 1 <= R <= 128 (larger R
+ * returns CPTC_ERR_ARG).  The solve's workspace is a static device array
+ * of 2 * 128^2 doubles + 256 B (about 256 KB) that each GPU holds until the
+ * process ends; the first call on a device looks up its address.  Calls
+ * that overlap on one GPU (other streams or threads) share that array and
+ * race: serialise them. */
+int cptc_solve_pinv_noalloc(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
+                            int R, const double* d_div, void* stream);
+
 /* Writes pinv(FtF) (R x R) to d_Ainv with the same rule as cptc_solve_pinv;
  * *d_path (device int, may be NULL) receives 0 = Cholesky, 1 = Jacobi. */
 int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path, void* stream);

@@ -48,6 +48,8 @@ def test_version_and_no_device_here(ca):
     lambda l: l.cptc_gram(0, 10, 8, 0, None),
     lambda l: l.cptc_hadamard(0, 0, 0, 10, None),
     lambda l: l.cptc_solve_pinv(0, 0, 0, 10, 8, 0, None),
+    lambda l: l.cptc_solve_pinv_noalloc(0, 0, 0, 10, 8, 0, None),
+    lambda l: l.cptc_solve_pinv_noalloc(8, 8, 8, 10, 129, 0, None),
     lambda l: l.cptc_pinv_sym(0, 0, 1024, 0, None),
     lambda l: l.cptc_colnorms(0, 10, 8, 0, None),
     lambda l: l.cptc_normalize_absorb(0, 10, 8, 0, 0, None),
