@@ -221,12 +221,13 @@ class Als3:
 
     def __init__(self, t: Tensor, R: int = 32, threshold: float = 0.03, path: int = -1,
                  fill_min: float = -1.0, cadr: bool = True, seed: int = 42, verbose: bool = False,
-                 skip_dense: int = -1, skip_sparse: int = -1):
+                 skip_dense: int = -1, skip_sparse: int = -1, fused: int = -1):
         o = Als3Opts()
         lib.cptc_als3_default_opts(C.byref(o))
         o.R, o.threshold, o.path, o.fill_min = R, threshold, path, fill_min
         o.cadr, o.seed, o.verbose = int(cadr), seed, int(verbose)
         o.skip_dense, o.skip_sparse = skip_dense, skip_sparse
+        o.fused = fused
         c, keep = t.as_coo()
         h = C.c_void_p()
         check(lib.cptc_als3_create(C.byref(c), C.byref(o), C.byref(h)), "cptc_als3_create")
@@ -266,6 +267,12 @@ class Als3:
         check(lib.cptc_als3_kernel_times(self._h, out.ctypes.data, C.byref(it), int(reset)),
               "cptc_als3_kernel_times")
         return out[:3], out[3:], it.value
+
+    def tile_times(self) -> np.ndarray:
+        """MFMA tile-kernel ms per mode since the last kernel_times(reset=True)."""
+        out = np.zeros(3, np.float64)
+        check(lib.cptc_als3_tile_times(self._h, out.ctypes.data), "cptc_als3_tile_times")
+        return out
 
     def mttkrp(self, mode: int) -> np.ndarray:
         out = np.zeros((self.dims[mode], self.R), np.float64)

@@ -47,6 +47,7 @@ class Als3Opts(C.Structure):
         ("cadr", C.c_int),
         ("seed", C.c_uint64),
         ("verbose", C.c_int),
+        ("fused", C.c_int),
     ]
 
 
@@ -64,6 +65,7 @@ class Als3Info(C.Structure):
         ("segments", C.c_uint64 * 3),
         ("dense_view_segments", C.c_uint64 * 3),
         ("num_cus", C.c_int),
+        ("fused", C.c_int),
     ]
 
 
@@ -141,6 +143,8 @@ SIGNATURES = {
     "cptc_gram_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
+    "cptc_mttkrp_merged3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P, _P,
+                                 _P, _I, _I, _I, _I, _P]),
     "cptc_solve_pinv_noalloc": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),
     "cptc_apply_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
@@ -156,6 +160,7 @@ SIGNATURES = {
     "cptc_als3_run": (_I, [_P, _I, _P, _P, _P]),
     "cptc_als3_mttkrp": (_I, [_P, _I, _P]),
     "cptc_als3_kernel_times": (_I, [_P, _P, C.POINTER(_I), _I]),
+    "cptc_als3_tile_times": (_I, [_P, _P]),
     "cptc_als3_factor": (_I, [_P, _I, _I, _P]),
     "cptc_als3_set_factor": (_I, [_P, _I, _P]),
     "cptc_als3_lambda": (_I, [_P, _P]),

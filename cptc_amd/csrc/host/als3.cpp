@@ -68,6 +68,7 @@ struct Als3
     int64_t tiles_total = 0;
     uint64_t dense_nnz_total = 0;
     bool skip_dense = false, skip_sparse = false;
+    bool fused = false;   // merged single-grid MTTKRP (ALS_FUSED)
 
     double* d_F = nullptr;  // [A | B | C]
     double* F[3] = {nullptr, nullptr, nullptr};
@@ -82,7 +83,7 @@ struct Als3
     double x_sq = 0.0;
     hipEvent_t ev[8] = {};
     // around the FP64 residual-view kernel of each mode, accumulated
-    hipEvent_t kev[6] = {};
+    hipEvent_t kev[12] = {};   // [2m, 2m+1]: FP64 (or merged) kernel; [6+2m, 7+2m]: tiles
     // the event blocks of the iteration being queued (ev / kev, or a block of
     // the pool in a queued run), the pool and the per-iteration fit scalars
     hipEvent_t* ev_cur = ev;
@@ -90,11 +91,13 @@ struct Als3
     std::vector<hipEvent_t> ev_pool;
     double* d_fit_hist = nullptr;
     size_t fit_hist_cap = 0;
-    double k_sparse_ms[3] = {0, 0, 0}, k_mttkrp_ms[3] = {0, 0, 0};
+    double k_sparse_ms[3] = {0, 0, 0}, k_mttkrp_ms[3] = {0, 0, 0}, k_tile_ms[3] = {0, 0, 0};
+    bool tile_timed[3] = {false, false, false};
     int k_iters = 0;
     bool timing_kernels = false;
 
     double* G(int m) const { return d_G + size_t(m) * R * R; }
+    bool fused_active() const { return fused; }
 };
 
 // FtV = MTTKRP of `mode`; with_pinv also writes pinv(FtF) to d_Ainv (FtF
@@ -109,7 +112,9 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     const double* B = h.F[1];
     const double* C = h.F[2];
     const bool dense = h.use_mfma && !h.skip_dense && h.part.ntiles > 0;
-    const bool fork = h.overlap && (dense || with_pinv);
+    // ALS_FUSED: tiles and residual segments in one launch on the main stream
+    const bool merged = h.fused && dense && !h.skip_sparse && h.views.ready;
+    const bool fork = h.overlap && ((dense && !merged) || with_pinv);
     if (fork) CPTC_HIP(hipEventRecord(h.e_fork, h.s));
     if (with_pinv)
     {
@@ -118,17 +123,32 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
         CPTC_TRY(cptc_pinv_sym(h.d_FtF, h.d_Ainv, R, nullptr, ps));
         if (h.overlap) CPTC_HIP(hipEventRecord(h.e_pinv, ps));
     }
-    if (dense)
+    if (merged)
+    {
+        const DevViews3& v = h.views;
+        if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode], h.s));
+        CPTC_TRY(cptc_mttkrp_merged3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
+                                     h.d_order[mode], h.d_goff[mode], h.ngroups[mode],
+                                     v.d_coords[mode], v.d_vals[mode], v.d_blk_row[mode],
+                                     v.d_blk_start[mode], v.d_blk_cnt[mode], v.nseg[mode], A, B,
+                                     C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
+                                     int(h.dims[2]), h.s));
+        if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode + 1], h.s));
+    }
+    else if (dense)
     {
         hipStream_t ds = h.overlap ? h.s_dense : h.s;
         if (h.overlap) CPTC_HIP(hipStreamWaitEvent(ds, h.e_fork, 0));
+        if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[6 + 2 * mode], ds));
         CPTC_TRY(cptc_mttkrp_dense_tiles3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
                                           h.d_order[mode], h.d_goff[mode], h.ngroups[mode], A, B,
                                           C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
                                           int(h.dims[2]), ds));
+        if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[6 + 2 * mode + 1], ds));
+        h.tile_timed[mode] = h.timing_kernels;
         if (h.overlap) CPTC_HIP(hipEventRecord(h.e_dense, ds));
     }
-    if (!h.skip_sparse)
+    if (!h.skip_sparse && !merged)
     {
         const double* F1 = mode == 0 ? B : A;
         const double* F2 = mode == 2 ? B : C;
@@ -145,7 +165,7 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
         }
     }
     if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
-    if (h.overlap && dense) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
+    if (h.overlap && dense && !merged) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
     return CPTC_OK;
 }
 
@@ -156,6 +176,16 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
 // nonzeros + 82 k tiles, R = 128) 11.7 vs 15.5.  Overlap when the FP64
 // MTTKRP streams at least 2^28 nonzero-ranks or the pseudoinverse takes the
 // blocked Cholesky (R > 64, >= 0.1 ms); ALS_SERIAL=1 forces one stream.
+// ALS_FUSED (als.cu:28, 529-555): the merged single-grid launch when both
+// halves exist; the reference also requires R == 32, here any even R <= 128
+// (16-byte factor rows, the grouped tile role's LDS).
+void choose_fused(Als3& h, int opt)
+{
+    const bool want = opt < 0 ? env_flag("ALS_FUSED") != 0 : opt != 0;
+    h.fused = want && h.use_mfma && h.part.ntiles > 0 && h.views.ready && !h.dviews.ready &&
+              h.R <= 128 && h.R % 2 == 0;
+}
+
 void choose_overlap(Als3& h)
 {
     const double work = double(h.views.nnz + h.dviews.nnz) * double(h.R);
@@ -390,7 +420,11 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
 
     CPTC_TRY(build_groups(*h));
     choose_overlap(*h);
+    choose_fused(*h, o.fused);
     CPTC_TRY(alloc_buffers(*h));
+    if (o.verbose && h->fused)
+        std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
+                    "R=%d)\n", h->R);
     if (o.verbose)
         std::printf("[Main] dense_nnz=%llu sparse_nnz=%zu tiles=%lld avg_fill=%g (threshold %g) "
                     "-> %s\n",
@@ -490,6 +524,12 @@ int collect_iteration(Als3& h, int it, int iters, const double sc[2], double* fi
             float k = 0.0f;
             CPTC_HIP(hipEventElapsedTime(&k, h.kev_cur[2 * m], h.kev_cur[2 * m + 1]));
             h.k_sparse_ms[m] += k;
+            if (h.tile_timed[m])
+            {
+                float tk = 0.0f;
+                CPTC_HIP(hipEventElapsedTime(&tk, h.kev_cur[6 + 2 * m], h.kev_cur[7 + 2 * m]));
+                h.k_tile_ms[m] += tk;
+            }
         }
     }
     h.k_iters++;
@@ -499,6 +539,60 @@ int collect_iteration(Als3& h, int it, int iters, const double sc[2], double* fi
     if (h.o.verbose) std::printf("[ALS] iter %d/%d time=%g ms fit=%.10g\n", it + 1, iters, ms, fit);
     if (h.o.verbose && std::getenv("ALS_PROFILE"))
         std::printf("[ALS][profile] iter %d mttkrp=%g (iter=%g)\n", it + 1, mt, ms);
+    return CPTC_OK;
+}
+
+// ALS_DEBUG (als.cu:595-603, 731-746), verbose runs only: the mode-C
+// MTTKRP time of the iteration, then after its log line lambda[0..3],
+// A[0..3], the Gram-fit scalars X^2, iprod and model^2, the first four
+// per-rank terms lambda_r <C[:, r], M_C[:, r]> of iprod, FtV[0..3] (mode C's
+// MTTKRP) and the exact RMSE.  Values print with the reference's default
+// stream format (%g); with R < 4 only R values are printed.
+int debug_mode_c(Als3& h)
+{
+    float ms = 0.0f;
+    CPTC_HIP(hipEventElapsedTime(&ms, h.ev_cur[5], h.ev_cur[6]));
+    std::printf("[DBG] modeC mttkrp wall = %g ms %s\n", double(ms),
+                h.fused_active() ? "(fused)" : "(dual)");
+    return CPTC_OK;
+}
+
+int debug_state(Als3& h, const double sc[2])
+{
+    const int R = h.R;
+    const int n = R < 4 ? R : 4;
+    const size_t K = h.dims[2];
+    std::vector<double> lam(static_cast<size_t>(R)), a(static_cast<size_t>(n));
+    std::vector<double> c(K * static_cast<size_t>(R)), m(K * static_cast<size_t>(R));
+    CPTC_HIP(hipMemcpyAsync(lam.data(), h.d_lambda, lam.size() * sizeof(double),
+                            hipMemcpyDeviceToHost, h.s));
+    CPTC_HIP(hipMemcpyAsync(a.data(), h.F[0], a.size() * sizeof(double), hipMemcpyDeviceToHost,
+                            h.s));
+    CPTC_HIP(hipMemcpyAsync(c.data(), h.F[2], c.size() * sizeof(double), hipMemcpyDeviceToHost,
+                            h.s));
+    CPTC_HIP(hipMemcpyAsync(m.data(), h.d_FtV, m.size() * sizeof(double), hipMemcpyDeviceToHost,
+                            h.s));
+    CPTC_TRY(residual_launch(h, true));
+    double r2[2] = {0, 0};
+    CPTC_HIP(hipMemcpyAsync(r2, h.d_scal + 2, 2 * sizeof(double), hipMemcpyDeviceToHost, h.s));
+    CPTC_HIP(hipStreamSynchronize(h.s));
+    auto list = [&](const char* tag, auto get) {
+        std::printf(" %s[0..3]=", tag);
+        for (int r = 0; r < n; ++r) std::printf(r ? " %g" : "%g", get(r));
+    };
+    std::printf("[DBG]");
+    list("lambda", [&](int r) { return lam[size_t(r)]; });
+    list("A", [&](int r) { return a[size_t(r)]; });
+    std::printf(" X2=%g iprod=%g model2=%g", h.x_sq, sc[0], sc[1]);
+    list("work_r", [&](int r) {
+        double d = 0.0;
+        for (size_t k = 0; k < K; ++k) d += c[k * size_t(R) + size_t(r)] * m[k * size_t(R) + size_t(r)];
+        return lam[size_t(r)] * d;
+    });
+    list("FtV", [&](int r) { return m[size_t(r)]; });
+    std::printf("\n");
+    const double res = std::max(r2[0], 0.0);
+    std::printf("[DBG] exact RMSE=%g\n", h.nnz ? std::sqrt(res / double(h.nnz)) : 0.0);
     return CPTC_OK;
 }
 
@@ -526,11 +620,14 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
             CPTC_HIP(hipMemcpyAsync(sc, h.d_scal, 2 * sizeof(double), hipMemcpyDeviceToHost,
                                     h.s));
             CPTC_HIP(hipStreamSynchronize(h.s));
+            const bool dbg = std::getenv("ALS_DEBUG") != nullptr;
+            if (dbg) CPTC_TRY(debug_mode_c(h));
             CPTC_TRY(collect_iteration(h, it, iters, sc, fit_out, ms_out, mtt_out));
+            if (dbg) CPTC_TRY(debug_state(h, sc));
         }
         return CPTC_OK;
     }
-    constexpr size_t PER = 14;   // ev (8) + kev (6) per iteration
+    constexpr size_t PER = 20;   // ev (8) + kev (12) per iteration
     while (h.ev_pool.size() < PER * size_t(iters))
     {
         hipEvent_t e = nullptr;
@@ -601,6 +698,10 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
     step(init_streams(*h));
     if (rc == CPTC_OK) step(build_groups(*h));
     choose_overlap(*h);
+    choose_fused(*h, -1);
+    if (verbose && h->fused)
+        std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
+                    "R=%d)\n", R);
     if (rc == CPTC_OK) step(alloc_buffers(*h));
     std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
     if (rc == CPTC_OK) step(run(*h, iters, fits.data(), nullptr, nullptr));
@@ -637,6 +738,7 @@ extern "C" void cptc_als3_default_opts(cptc_als3_opts* o)
     o->cadr = 1;
     o->seed = 42;
     o->verbose = 0;
+    o->fused = -1;
 }
 
 extern "C" int cptc_als3_create(const cptc_coo* coo, const cptc_als3_opts* opts, void** handle)
@@ -680,6 +782,7 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->fill_min = h->fill_min;
     info->use_mfma = h->use_mfma ? 1 : 0;
     info->num_cus = h->num_cus;
+    info->fused = h->fused ? 1 : 0;
     return CPTC_OK;
 }
 
@@ -703,9 +806,17 @@ extern "C" int cptc_als3_kernel_times(void* handle, double* out6, int* iters, in
     *iters = h->k_iters;
     if (reset)
     {
-        for (int m = 0; m < 3; ++m) h->k_sparse_ms[m] = h->k_mttkrp_ms[m] = 0.0;
+        for (int m = 0; m < 3; ++m) h->k_sparse_ms[m] = h->k_mttkrp_ms[m] = h->k_tile_ms[m] = 0.0;
         h->k_iters = 0;
     }
+    return CPTC_OK;
+}
+
+extern "C" int cptc_als3_tile_times(void* handle, double* out3)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && out3, CPTC_ERR_ARG, "cptc_als3_tile_times: bad arguments");
+    for (int m = 0; m < 3; ++m) out3[m] = h->k_tile_ms[m];
     return CPTC_OK;
 }
 

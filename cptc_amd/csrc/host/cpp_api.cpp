@@ -429,6 +429,28 @@ void compute_mttkrp_merged_async(const HybridCOOTensor& hybrid, int mode, double
                                  double* d_B, double* d_C, double* d_FtV, double* d_FtF, int R,
                                  hipStream_t stream)
 {
+    // dense.cu:2258-2511: one grid for the tiles and the residual segments;
+    // shapes the merged kernel does not take (odd R, R > 128, unaligned
+    // factors) queue the two launches back to back instead
+    const bool aligned = ((reinterpret_cast<uintptr_t>(d_A) | reinterpret_cast<uintptr_t>(d_B) |
+                           reinterpret_cast<uintptr_t>(d_C)) & 15) == 0;
+    if (R % 2 == 0 && R <= 128 && aligned)
+    {
+        const int m = mode;
+        const bool views = hybrid.mttkrp_ready && hybrid.sparse_nnz > 0;
+        const float* t = hybrid.num_dense_tiles > 0 ? tiles_f32(hybrid, stream) : nullptr;
+        API_TRY("compute_mttkrp_merged_async",
+                cptc_mttkrp_merged3(m, hybrid.d_tiles4, t, size_t(std::max<int64_t>(0, hybrid.num_dense_tiles)),
+                                    nullptr, nullptr, 0, views ? hybrid.d_sp2_coords[m] : nullptr,
+                                    views ? hybrid.d_sp2_val[m] : nullptr,
+                                    views ? hybrid.d_blk_row[m] : nullptr,
+                                    views ? hybrid.d_blk_start[m] : nullptr,
+                                    views ? hybrid.d_blk_cnt[m] : nullptr,
+                                    views ? size_t(hybrid.mttkrp_blocks[m]) : 0, d_A, d_B, d_C,
+                                    d_FtV, R, int(hybrid.dims[0]), int(hybrid.dims[1]),
+                                    int(hybrid.dims[2]), stream));
+        return;
+    }
     compute_dense_mttkrp_async(hybrid, mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
     compute_sparse_mttkrp_async(hybrid, mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
 }

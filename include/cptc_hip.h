@@ -227,6 +227,21 @@ int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_
 int cptc_solve_pinv_noalloc(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
                             int R, const double* d_div, void* stream);
 
+/* One launch for both halves of an order-3 mode's MTTKRP: the MFMA dense
+ * tiles (as cptc_mttkrp_dense_tiles3; grouped when d_order / d_group_off are
+ * given) and the FP64 residual segments (as cptc_mttkrp_sparse3) in one grid
+ * whose workgroups interleave the two kinds of work.  Replaces
+ * compute_mttkrp_merged_async / mttkrp_merged_kernel (dense.cu:1914-2058,
+ * 2258-2511), the reference's ALS_FUSED path (als.cu:28, 529-555; R == 32
+ * there).  Even R <= 128 and 16-byte aligned factors, else
+ * CPTC_ERR_UNSUPPORTED.  d_FtV is accumulated into (the caller zeroes it). */
+int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float* d_tile_f32, size_t ntiles,
+                        const uint32_t* d_order, const uint32_t* d_group_off, size_t ngroups,
+                        const uint64_t* d_coords, const double* d_vals, const uint32_t* d_blk_row,
+                        const uint32_t* d_blk_start, const uint32_t* d_blk_cnt, size_t nblocks,
+                        const double* d_A, const double* d_B, const double* d_C, double* d_FtV,
+                        int R, int dimI, int dimJ, int dimK, void* stream);
+
 /* Writes pinv(FtF) (R x R) to d_Ainv with the same rule as cptc_solve_pinv;
  * *d_path (device int, may be NULL) receives 0 = Cholesky, 1 = Jacobi. */
 int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path, void* stream);
@@ -288,6 +303,9 @@ typedef struct cptc_als3_opts {
     int cadr;            /* 1 = CADR relabel (the reference always does) */
     uint64_t seed;       /* factor-init seed (common.cu:83: 42) */
     int verbose;         /* 1 = reference-style stdout lines */
+    int fused;           /* -1 env ALS_FUSED, 0/1: one merged launch per mode
+                            (cptc_mttkrp_merged3) when MFMA tiles and the
+                            residual view are both present, R even and <= 128 */
 } cptc_als3_opts;
 
 void cptc_als3_default_opts(cptc_als3_opts* o);
@@ -310,6 +328,7 @@ typedef struct cptc_als3_info {
     uint64_t segments[3];     /* residual view segments per mode */
     uint64_t dense_view_segments[3];
     int num_cus;
+    int fused;                /* 1 = the merged single-grid MTTKRP is in use */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
@@ -323,11 +342,17 @@ int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter, float* m
 
 /* Kernel times accumulated over cptc_als3_run iterations (hipEvents on the
  * driver's stream): out6[m] = ms of the FP64 residual-view sparse MTTKRP
- * kernel of mode m, out6[3 + m] = ms of all MTTKRP launches of mode m;
+ * kernel of mode m (of the merged tiles + residual kernel when the fused
+ * path is active), out6[3 + m] = ms of all MTTKRP launches of mode m;
  * *iters = iterations accumulated.  reset != 0 zeroes the sums after reading.
  * No reference counterpart (measurement plumbing; ALS_PROFILE's
  * per-phase events, als.cu:642-651, are the closest). */
 int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset);
+/* ms of the MFMA tile kernel per mode (hipEvents on the tile stream),
+ * accumulated over the same iterations as cptc_als3_kernel_times and reset
+ * with it; 0 for modes whose tiles ran in the merged grid or not at all.
+ * Measurement helper, no reference counterpart. */
+int cptc_als3_tile_times(void* handle, double* out3);
 
 /* One mode's MTTKRP with the current factors into a host buffer (dim x R),
  * through the same launches as the ALS loop.  For parity tests. */

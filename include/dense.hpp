@@ -16,9 +16,10 @@ void compute_dense_mttkrp_async(const HybridCOOTensor& hybrid, int mode, double*
 void compute_dense_mttkrp(const HybridCOOTensor& hybrid, int mode, double* d_A, double* d_B,
                           double* d_C, double* d_FtV, double* d_FtF, int R);
 
-// dense.cu:1569-1621 (the reference's single-grid R == 32 kernel): here the
-// dense tiles and the sparse views are queued back to back on `stream`,
-// any R.
+// dense.cu:1914-2058, 2258-2511 (the reference's single-grid R == 32
+// kernel): one launch of cptc_mttkrp_merged3 over the dense tiles and the
+// residual segments for even R <= 128 with 16-byte aligned factors; other
+// shapes queue the two launches back to back on `stream`.
 void compute_mttkrp_merged_async(const HybridCOOTensor& hybrid, int mode, double* d_A,
                                  double* d_B, double* d_C, double* d_FtV, double* d_FtF, int R,
                                  hipStream_t stream);

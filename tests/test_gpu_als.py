@@ -157,6 +157,38 @@ def test_residual3_identical_factors(ca, orc, dev, kind, path, R):
     assert abs(res - ores) <= 1e-12 * ores and abs(x2 - ox2) <= 1e-13 * ox2
 
 
+@pytest.mark.parametrize("R", [16, 32, 128])
+def test_fused_path_matches_oracle(ca, orc, dev, R):
+    """ALS_FUSED (als.cu:28, 529-555): one merged launch per mode.  MTTKRP of
+    every mode within the MFMA bound of the oracle, 20 iterations within 1e-4
+    of the oracle's fits and within 1e-6 of the two-stream driver's."""
+    t = clustered(ca, 9)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    assert len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
+    with ca.Als3(t, R=R, threshold=0.03, path=1, fused=1) as h:
+        assert int(h.info.fused) == 1
+        F = [h.factor(m).ravel() for m in range(3)]
+        for mode in range(3):
+            ref = orc.mttkrp3_view(v, mode, *F, R, t.dims[mode])
+            ref = ref + orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+            assert rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R)) <= 1e-5, mode
+        fit, ms, mt = h.run(20)
+        sp, _, kit = h.kernel_times()
+        assert kit == 20 and np.all(sp > 0)
+    o = orc.Als3(v, None, p, float(np.sum(t.val ** 2)), t.dims, R, *F, None)
+    ofit, _, _ = o.iterate(20)
+    assert np.max(np.abs(fit - ofit)) <= 1e-4, (fit[-3:], ofit[-3:])
+    with ca.Als3(t, R=R, threshold=0.03, path=1, fused=0) as h2:
+        assert int(h2.info.fused) == 0
+        fit2, _, _ = h2.run(20)
+    assert np.max(np.abs(fit - fit2)) <= 1e-6
+    # the FP64 path and odd R never take the merged grid
+    with ca.Als3(t, R=R, threshold=0.03, path=2, fused=1) as h3:
+        assert int(h3.info.fused) == 0
+    with ca.Als3(t, R=R + 1, threshold=0.03, path=1, fused=1) as h4:
+        assert int(h4.info.fused) == 0
+
+
 def test_cli_runs_and_exports(ca, dev, tmp_path):
     t = make(ca, "zipf", 5)
     path = str(tmp_path / "t.tns")
@@ -174,8 +206,57 @@ def test_cli_runs_and_exports(ca, dev, tmp_path):
     assert lam[:3] == ["vector", "1", "8"]
 
 
+def test_cli_export_bytes_and_debug(ca, dev, tmp_path):
+    """ALS_EXPORT_FACTORS (main.cu:595-621): 'matrix\\n2\\n<dim> <R>' then one
+    '%.20lf' line per entry, rows in the input's index order, row-major
+    (j * R + i); '<p>.lambda.out' = 'vector\\n1\\n<R>' then '%.20lf' lines.
+    The files are byte-for-byte the rendering of their own values, and the
+    values are the C-ABI driver's unpermuted factors and lambda after the same
+    iteration.  ALS_DEBUG (als.cu:595-603, 731-746) adds its lines."""
+    t = make(ca, "zipf", 7)
+    fpath = str(tmp_path / "t.tns")
+    ca.write_tns(fpath, t)
+    R = 8
+    env = dict(os.environ, ALS_EXPORT_FACTORS=str(tmp_path / "f"), ALS_DEBUG="1")
+    for k in ("ALS_FORCE_CUDA", "ALS_FORCE_WMMA", "ALS_SERIAL"):
+        env.pop(k, None)
+    out = subprocess.run([ca.CLI_PATH, fpath, "1", str(R)], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.splitlines()
+    it = [i for i, l in enumerate(lines) if l.startswith("[ALS] iter 1/1")]
+    assert len(it) == 1
+    assert lines[it[0] - 1].startswith("[DBG] modeC mttkrp wall = ")
+    assert lines[it[0] - 1].endswith(" ms (dual)")
+    dbg = lines[it[0] + 1]
+    for key in ("[DBG] lambda[0..3]=", " A[0..3]=", " X2=", " iprod=", " model2=",
+                " work_r[0..3]=", " FtV[0..3]="):
+        assert key in dbg, key
+    assert lines[it[0] + 2].startswith("[DBG] exact RMSE=")
+    t2 = ca.load_tns3(fpath)
+    with ca.Als3(t2, R=R) as h:
+        h.run(1)
+        F = [h.factor(m, unpermuted=True) for m in range(3)]
+        lam = h.lam()
+    for m in range(3):
+        raw = open(str(tmp_path / f"f.{m}.out"), "rb").read()
+        head = f"matrix\n2\n{t.dims[m]} {R}\n".encode()
+        assert raw.startswith(head)
+        vals = [float(x) for x in raw[len(head):].decode().split("\n") if x]
+        assert len(vals) == t.dims[m] * R
+        assert raw == head + "".join("%.20lf\n" % x for x in vals).encode()
+        got = np.array(vals).reshape(t.dims[m], R)
+        assert rel_err(got, F[m]) <= 1e-12, m
+    raw = open(str(tmp_path / "f.lambda.out"), "rb").read()
+    head = f"vector\n1\n{R}\n".encode()
+    vals = [float(x) for x in raw[len(head):].decode().split("\n") if x]
+    assert raw == head + "".join("%.20lf\n" % x for x in vals).encode()
+    assert rel_err(vals, lam) <= 1e-12
+
+
 @pytest.mark.parametrize("env_path,path", [({}, -1), ({"ALS_FORCE_CUDA": "1"}, 2),
-                                           ({"ALS_FORCE_WMMA": "1"}, 1)])
+                                           ({"ALS_FORCE_WMMA": "1"}, 1),
+                                           ({"ALS_FORCE_WMMA": "1", "ALS_FUSED": "1"}, 1)])
 def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
     """The CLI runs main.cu's flow on the C++ interface (load_tns_file,
     compute/apply_cadr_reordering, init_factors_random, create_hybrid_format,
@@ -186,7 +267,7 @@ def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
     fpath = str(tmp_path / "t.tns")
     ca.write_tns(fpath, t)
     env = dict(os.environ, **env_path)
-    for k in ("ALS_FORCE_CUDA", "ALS_FORCE_WMMA"):
+    for k in ("ALS_FORCE_CUDA", "ALS_FORCE_WMMA", "ALS_FUSED"):
         if k not in env_path:
             env.pop(k, None)
     out = subprocess.run([ca.CLI_PATH, fpath, "6", "16"], env=env, capture_output=True,
@@ -198,6 +279,8 @@ def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
     for s in ("[CADR] Total reordering time", "[Main] density check:", "[Fit Report] final R=16",
               "[ALS] Final RMSE=", "[Main] Final CP weights:", "Unpermutation!"):
         assert any(s in l for l in lines), s
+    fused_line = any(l.startswith("[ALS] FUSED path active") for l in lines)
+    assert fused_line == ("ALS_FUSED" in env_path)
     t2 = ca.load_tns3(fpath)
     with ca.Als3(t2, R=16, path=path) as h:
         ref, _, _ = h.run(6)

@@ -587,6 +587,32 @@ def test_profile_and_dump(ca, dev, tmp_path):
     assert np.allclose([float(x) for x in lines[-1].split()], g.lam(), rtol=1e-15)
 
 
+def test_dump_bytes(ca, dev, tmp_path):
+    """GEN_DUMP (generic.cu:2253-2287) byte for byte: the comment line, 'order',
+    'rank', 'dims', per mode 'mode m dim R' and one line per row, values
+    space-separated as an ostream at precision 17 writes them (= '%.17g'),
+    then 'lambda R' and the lambda line."""
+    rng = np.random.default_rng(9)
+    dims = (40, 35, 48, 3)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.5, 4000), dims, rng)
+    R = 5
+    g = ca.Gen(t, R=R)
+    g.run(2)
+    F = [g.factor(m) for m in range(4)]
+    lam = g.lam()
+    base = str(tmp_path / "d")
+    g.dump(base)
+    g.close()
+    fmt = lambda row: " ".join("%.17g" % x for x in row)
+    exp = ["# cpTC factor dump (factors are column-normalised; lambda holds the norms)",
+           "order 4", f"rank {R}", "dims " + " ".join(str(d) for d in dims)]
+    for m in range(4):
+        exp.append(f"mode {m} {dims[m]} {R}")
+        exp.extend(fmt(F[m].reshape(dims[m], R)[i]) for i in range(dims[m]))
+    exp += [f"lambda {R}", fmt(lam)]
+    assert open(base + ".factors.txt", "rb").read() == ("\n".join(exp) + "\n").encode()
+
+
 def test_rejects_unsupported(ca, dev):
     t = ca.Tensor((4, 4, 4, 4), np.zeros((4, 3), np.uint32), np.ones(3))
     with pytest.raises(ca.CptcError):

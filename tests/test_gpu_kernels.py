@@ -107,6 +107,64 @@ def tile_groups(ca, hdr, words, slot, G):
     return to_dev(ca, order), to_dev(ca, off[:ng.value + 1].copy()), ng.value
 
 
+@pytest.mark.parametrize("R,G", [(8, 0), (32, 0), (32, 8), (64, 4), (100, 8), (128, 0), (128, 8)])
+def test_merged_mttkrp_vs_oracle(ca, orc, dev, R, G):
+    """cptc_mttkrp_merged3 (dense.cu:1914-2058, 2258-2511): tiles and residual
+    segments of a mode in one grid = the oracle's tiles + view MTTKRP
+    (<= 1e-5, the MFMA bound), grouped (G tiles per wave) and per tile."""
+    rng = np.random.default_rng(70 + R + G)
+    dims = (40, 45, 37)
+    idx, val = block_tensor(rng, dims)
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    nt = len(p["tiles"])
+    assert nt >= 4 and len(p["sp_val"]) > 500
+    v = orc.views3(p["sp_i"], p["sp_j"], p["sp_k"], p["sp_val"], dims)
+    F = [rng.random((d, R)) - 0.3 for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    tiles = to_dev(ca, p["tiles"].astype(np.int32))
+    off, lid, pv = to_dev(ca, p["pool_off"]), to_dev(ca, p["pool_lid"]), to_dev(ca, p["pool_val"])
+    tf = zeros(ca, (nt * 4096,), np.float32)
+    assert ca.lib.cptc_dense_tiles_pack3(lid.data_ptr(), pv.data_ptr(), off.data_ptr(), nt,
+                                         tf.data_ptr(), stream(ca)) == 0
+    for mode in range(3):
+        ref = orc.mttkrp3_tiles(p, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R, dims)
+        ref = (ref + orc.mttkrp3_view(v, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                                      dims[mode])).reshape(dims[mode], R)
+        vm = v[mode]
+        dc, dv = to_dev(ca, vm["coords"]), to_dev(ca, vm["vals"])
+        br, bs, bc = (to_dev(ca, vm[k]) for k in ("blk_row", "blk_start", "blk_cnt"))
+        grp = (None, None, 0)
+        if G:
+            go, gf, ng = tile_groups(ca, p["tiles"], 4, mode, G)
+            grp = (go.data_ptr(), gf.data_ptr(), ng)
+        out = zeros(ca, (dims[mode], R))
+        rc = ca.lib.cptc_mttkrp_merged3(mode, tiles.data_ptr(), tf.data_ptr(), nt, *grp,
+                                        dc.data_ptr(), dv.data_ptr(), br.data_ptr(),
+                                        bs.data_ptr(), bc.data_ptr(), len(vm["blk_row"]),
+                                        dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
+                                        out.data_ptr(), R, *dims, stream(ca))
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        assert rel_err(out.numpy(), ref) <= 1e-5, (mode, R, G)
+    # only one side present: the grid degenerates to that side
+    out = zeros(ca, (dims[0], R))
+    assert ca.lib.cptc_mttkrp_merged3(0, tiles.data_ptr(), tf.data_ptr(), nt, None, None, 0, None,
+                                      None, None, None, None, 0, dF[0].data_ptr(),
+                                      dF[1].data_ptr(), dF[2].data_ptr(), out.data_ptr(), R,
+                                      *dims, stream(ca)) == 0
+    ca.sync()
+    ref = orc.mttkrp3_tiles(p, 0, F[0].ravel(), F[1].ravel(), F[2].ravel(), R, dims)
+    assert rel_err(out.numpy(), ref.reshape(dims[0], R)) <= 1e-5
+
+
+def test_merged_rejects_odd_rank(ca, dev):
+    d = zeros(ca, (16,))
+    rc = ca.lib.cptc_mttkrp_merged3(0, None, None, 0, None, None, 0, None, None, None, None, None,
+                                    0, d.data_ptr(), d.data_ptr(), d.data_ptr(), d.data_ptr(), 33,
+                                    4, 4, 4, stream(ca))
+    assert rc != 0 and b"even R" in ca.lib.cptc_last_error()
+
+
 @pytest.mark.parametrize("R,G", [(8, 0), (16, 0), (20, 0), (32, 0), (128, 0), (8, 3), (32, 8),
                                  (128, 8), (200, 8)])
 def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G):
