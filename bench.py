@@ -6,11 +6,19 @@ Zipf(1.1), log-normal values, R = 128, dense threshold 0.03) with every input
 resident in HBM.  Prints ONE JSON line on stdout; progress goes to stderr.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--R 128]
-                  [--cpu-iters 1] [--no-cpu]
+                  [--cpu-iters 4] [--no-cpu] [--fused]
 
 The CPU baseline runs the CPU oracle's OpenMP ALS (the reference's semantics)
-on the same row-sorted views, copied from the device, for --cpu-iters
-iterations on the full tensor.
+on the same row-sorted views, copied from the device, from the same initial
+factors, for --cpu-iters iterations on the full tensor; the first iteration
+is dropped and the median and mean of the rest are reported.
+
+roofline (the FP64 sparse kernel, per launch): achieved = HBM bytes per
+launch measured by rocprofv3 --pmc (profiles/mttkrp_sparse3_<workload>_pmc.json,
+valid only while the kernel's sources hash to the value recorded there) over
+the launch time measured here with hipEvents; the no-reuse gather model and
+the compulsory bytes over the same time are reported beside it.
+--fused runs the merged single-grid MTTKRP (ALS_FUSED).
 
 --config 4 / 5 run the generic N-order path on BASELINE configs 4 and 5
 instead (secondary measurements; same JSON shape, the segment MTTKRP as the
@@ -56,18 +64,51 @@ def gather_bytes(nnz: int, dim_n: int, R: int, N: int = 3) -> float:
     return nnz * (4 * N + 8) + nnz * (N - 1) * R * 8 + dim_n * R * 8
 
 
+SPARSE3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_sparse.hip", "cptc_amd/csrc/kernels/seg3_body.hpp")
+
+
+def sources_sha(paths) -> str:
+    """sha256 (first 16 hex digits) of the kernel's source files, in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def load_traffic(workload: str):
-    """HBM bytes per sparse-kernel launch from the committed rocprofv3 --pmc summary."""
-    path = os.path.join(ROOT, "profiles", "mttkrp_sparse3_cfg3_pmc.json")
+    """Measured HBM traffic of one sparse-kernel launch (rocprofv3 --pmc summary
+    under profiles/), or None when there is none for this workload or the
+    kernel's sources changed since it was measured."""
+    path = os.path.join(ROOT, "profiles", f"mttkrp_sparse3_{workload}_pmc.json")
     if not os.path.exists(path):
         return None
     try:
         d = json.load(open(path))
-        if d.get("workload") != workload:
-            return None
-        return d.get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
+    if d.get("workload") != workload or d.get("kernel_src_sha") != sources_sha(SPARSE3_SOURCES):
+        return None
+    return d
+
+
+SEG_ND_SOURCES = ("cptc_amd/csrc/kernels/seg_keys.hip",)
+
+
+def load_traffic_seg(workload: str):
+    """Measured HBM traffic of one generic segment-kernel launch, as load_traffic."""
+    path = os.path.join(ROOT, "profiles", f"mttkrp_seg_nd_{workload}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != workload or d.get("kernel_src_sha") != sources_sha(SEG_ND_SOURCES):
+        return None
+    return d
 
 
 def main() -> int:
@@ -77,7 +118,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIG_SPEC))
     ap.add_argument("--R", type=int, default=0)
-    ap.add_argument("--cpu-iters", type=int, default=1)
+    ap.add_argument("--cpu-iters", type=int, default=4)
+    ap.add_argument("--fused", action="store_true",
+                    help="merged single-grid MTTKRP (ALS_FUSED) on the order-3 path")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="run only a streaming kernel of known size (PMC scaling)")
@@ -111,7 +154,7 @@ def main() -> int:
         f"{time.perf_counter() - t0:.1f} s")
 
     t0 = time.perf_counter()
-    h = ca.Als3(t, R=R, threshold=thr)
+    h = ca.Als3(t, R=R, threshold=thr, fused=1 if args.fused else 0)
     info = h.info
     setup_s = time.perf_counter() - t0
     use_mfma = bool(info.use_mfma) and int(info.num_dense_tiles) > 0
@@ -120,6 +163,8 @@ def main() -> int:
         f"fill_min {info.fill_min:.4f} -> {'MFMA+FP64' if use_mfma else 'FP64'}; "
         f"segments {list(info.segments)} CUs {info.num_cus}")
 
+    # the CPU baseline starts from the same initial factors (lambda = 1)
+    F_init = [h.factor(m).ravel().copy() for m in range(3)] if not args.no_cpu else None
     if args.warmup:
         h.run(args.warmup)
         log(f"warmup {args.warmup} iterations done")
@@ -133,6 +178,7 @@ def main() -> int:
     ca.sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
+    tile_ms_acc = h.tile_times()
     sp_ms, mt_ms, kit = h.kernel_times(reset=True)
     assert kit == args.steps
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter (host wall), event median "
@@ -141,7 +187,7 @@ def main() -> int:
 
     dims = t.dims
     nnz = t.nnz
-    # headline: all MTTKRP launches of an iteration vs the gather model over all nnz
+    # all MTTKRP launches of an iteration vs the gather model over all nnz
     b_iter = sum(gather_bytes(nnz, dims[m], R) for m in range(3))
     mtt_ms_iter = float(np.sum(mt_ms)) / kit
     mtt_gbs = b_iter / (mtt_ms_iter * 1e-3) / 1e9
@@ -149,45 +195,62 @@ def main() -> int:
     snnz = int(info.sparse_nnz)
     b_launch = [gather_bytes(snnz, dims[m], R) for m in range(3)]
     launch_ms = [float(sp_ms[m]) / kit for m in range(3)]
-    achieved = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
-    workload = f"cfg{args.config}-R{R}"
-    traffic = load_traffic(workload)
-    traffic_gbs = (traffic / (sum(launch_ms) / 3 * 1e-3) / 1e9) if (traffic and snnz) else None
+    mean_ms = sum(launch_ms) / 3
+    gather_gbs = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
+    workload = f"cfg{args.config}-R{R}" + ("-fused" if args.fused else "")
     # compulsory traffic per launch: the view stream + every factor row once + output rows
     compulsory = [snnz * 20 + sum(dims) * R * 8 + dims[m] * R * 8 for m in range(3)]
+    comp_gbs = sum(compulsory) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
+    prof = load_traffic(workload)
+    # tiles: 8192 R flops per tile per mode (16^3 x R multiply-adds)
+    ntiles = int(info.num_dense_tiles)
+    tile_flops = 8192.0 * R * ntiles
+    tile_ms = [float(x) / kit for x in tile_ms_acc]
+    tiles_timed = use_mfma and ntiles and all(x > 0 for x in tile_ms)
 
     cpu = None
     if not args.no_cpu and args.cpu_iters > 0:
-        cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma)
+        cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma, F_init)
 
     if snnz:
+        traffic = dram = None
+        if prof:
+            traffic = prof["hbm_bytes_per_launch"]
+            dram = traffic / (mean_ms * 1e-3) / 1e9
         roofline = {
-            "kernel": "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128]), per launch = "
-                      "one mode" if 64 < R <= 128 else
-                      "mttkrp3_seg_kernel (FP64 residual view), per launch = one mode",
+            "kernel": ("mttkrp3_merged_kernel (MFMA tiles + FP64 residual in one grid)"
+                       if args.fused else
+                       "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128])"
+                       if 64 < R <= 128 else
+                       "mttkrp3_seg_kernel (FP64 residual view)") + ", per launch = one mode",
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": round(dram, 1) if dram else None,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_GBs": round(traffic_gbs, 1) if traffic_gbs else None,
-            "traffic_frac": round(traffic_gbs / HBM_PEAK_GBS, 4) if traffic_gbs else None,
+            "frac": round(dram / HBM_PEAK_GBS, 4) if dram else None,
+            "traffic": int(traffic) if traffic else None,
             "launch_ms": [round(x, 4) for x in launch_ms],
+            "gather_model_GBs": round(gather_gbs, 1),
+            "gather_model_frac": round(gather_gbs / HBM_PEAK_GBS, 4),
+            "compulsory_GBs": round(comp_gbs, 1),
+            "compulsory_frac": round(comp_gbs / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
             "compulsory_bytes_per_launch": [int(b) for b in compulsory],
-            "note": "achieved = no-reuse gather model (every factor row read per nonzero) over "
-                    "the measured launch time; L2 and MALL serve most gathers, so it exceeds "
-                    "the HBM peak. traffic = rocprofv3 FETCH_SIZE*2.0 + WRITE_SIZE per launch "
-                    "(L2-miss bytes), traffic_GBs = traffic over the same launch time.",
+            "traffic_source": (f"profiles/mttkrp_sparse3_{workload}_pmc.json "
+                               f"(kernel sources sha {prof['kernel_src_sha']})") if prof else
+                              "none for these kernel sources: achieved/frac null",
+            "note": "achieved = HBM bytes per launch measured by rocprofv3 --pmc (L2-to-fabric "
+                    "read + write bytes, calibrated on a copy kernel; MALL hits count as "
+                    "fabric traffic, so this bounds the DRAM bytes from above) over the launch "
+                    "time measured here; gather_model = the no-reuse gather model (every "
+                    "factor row read per nonzero, L1/L2/MALL hits included, so it exceeds the "
+                    "HBM peak); compulsory = view stream + every factor row once + output.",
         }
     else:
         # no sparse residual (every nonzero in a dense tile): the MFMA tile
-        # kernel is the whole MTTKRP, 8192*R flops per tile per mode
-        ntiles = int(info.num_dense_tiles)
-        flops = 8192.0 * R * ntiles
-        tile_ms = [float(mt_ms[m]) / kit for m in range(3)]
-        tflops = flops * 3 / (sum(tile_ms) * 1e-3) / 1e12 if use_mfma and ntiles else 0.0
+        # kernel is the whole MTTKRP
+        mt_launch = [float(mt_ms[m]) / kit for m in range(3)]
+        tflops = tile_flops * 3 / (sum(mt_launch) * 1e-3) / 1e12 if use_mfma and ntiles else 0.0
         roofline = {
             "kernel": "dense_tiles_kernel<mode,4,false,true> (16^3 tiles, FP32 MFMA, FP64 "
                       "epilogue), per launch = one mode",
@@ -197,9 +260,19 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
             "traffic": None,
-            "launch_ms": [round(x, 4) for x in tile_ms],
-            "flops_per_launch": flops,
+            "launch_ms": [round(x, 4) for x in mt_launch],
+            "flops_per_launch": tile_flops,
             "tile_bytes_per_launch": ntiles * 4096 * 4,
+        }
+    roofline_tiles = None
+    if tiles_timed and snnz:
+        ttf = tile_flops * 3 / (sum(tile_ms) * 1e-3) / 1e12
+        roofline_tiles = {
+            "kernel": "dense_tiles_kernel<mode,4,false,true> (16^3 tiles, FP32 MFMA), per mode, "
+                      "beside the FP64 kernel on a second stream",
+            "bound": "mfma", "achieved": round(ttf, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(ttf / FP32_MFMA_PEAK_TFLOPS, 4),
+            "flops_per_launch": tile_flops, "launch_ms": [round(x, 4) for x in tile_ms],
         }
 
     line = {
@@ -220,14 +293,16 @@ def main() -> int:
             "R": R, "nnz": nnz, "dims": list(dims), "dense_threshold": thr,
             "dense_tiles": int(info.num_dense_tiles), "dense_nnz": int(info.dense_nnz),
             "sparse_nnz": snnz, "path": "mfma+fp64" if use_mfma else "fp64",
+            "fused": bool(info.fused),
             "parallelism": "single GPU",
         },
         "ms_per_iter_event_median": round(float(np.median(ms_iter)), 4),
         "mttkrp_ms_per_iter": round(mtt_ms_iter, 4),
         "mttkrp_gather_model_GBs": round(mtt_gbs, 1),
-        "mttkrp_frac_of_hbm_peak": round(mtt_gbs / HBM_PEAK_GBS, 4),
+        "mttkrp_gather_model_frac": round(mtt_gbs / HBM_PEAK_GBS, 4),
         "fit_last": float(fits[-1]),
         "roofline": roofline,
+        "roofline_tiles": roofline_tiles,
         "cpu_baseline": cpu,
     }
     h.close()
@@ -264,6 +339,9 @@ def bench_generic(ca, args, spec, R) -> int:
     b_seg = [gather_bytes(knnz[m], dims[m], R, N) for m in range(N)]
     seg_launch = [float(seg_ms[m]) / kit for m in range(N)]
     achieved = sum(b_seg) / (sum(seg_launch) * 1e-3) / 1e9
+    workload = f"cfg{args.config}-R{R}"
+    prof = load_traffic_seg(workload)
+    hbm = (prof["hbm_bytes_per_launch"] / (sum(seg_launch) / N * 1e-3) / 1e9) if prof else None
     inner = [m for m in range(N) if info.dense_enabled and m in tuple(info.inner)]
     unit_launch = [float(unit_ms[m]) / kit for m in inner]
     flops = 8192.0 * R * int(info.n_units)
@@ -288,11 +366,18 @@ def bench_generic(ca, args, spec, R) -> int:
                    "path": "generic N-order", "parallelism": "single GPU"},
         "fit_last": float(fits[-1]),
         "roofline": {
-            "kernel": "seg_nd_kernel (FP64 segment MTTKRP), per launch = one mode",
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
+                      "packed level keys), per launch = one mode",
+            "bound": "hbm", "achieved": round(hbm, 1) if hbm else None, "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4) if hbm else None,
+            "traffic": int(prof["hbm_bytes_per_launch"]) if prof else None,
             "launch_ms": [round(x, 4) for x in seg_launch],
+            "gather_model_GBs": round(achieved, 1),
+            "gather_model_frac": round(achieved / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_launch": [int(b) for b in b_seg],
+            "traffic_source": (f"profiles/mttkrp_seg_nd_{workload}_pmc.json (kernel sources "
+                               f"sha {prof['kernel_src_sha']})") if prof else
+                              "none for these kernel sources: achieved/frac null",
         },
         "roofline_units": {
             "kernel": "dense_tiles_kernel<slot,6,true> (dense units, FP32 MFMA), per inner mode",
@@ -380,6 +465,36 @@ def calib() -> int:
     return 0
 
 
+def host_info() -> dict:
+    """nproc, the OpenMP thread count and the CPU model of this host."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
+            "cpu_model": model}
+
+
+def summarize_cpu(ms, extra: dict) -> dict:
+    """BASELINE.md's plan: drop iteration 1, median and mean of the rest."""
+    kept = ms[1:] if len(ms) > 1 else ms
+    out = {
+        "value": round(float(np.median(kept)), 1),
+        "unit": "ms/iteration",
+        "median_ms": round(float(np.median(kept)), 1),
+        "mean_ms": round(float(np.mean(kept)), 1),
+        "iterations_ms": [round(float(x), 1) for x in ms],
+        "dropped_first": len(ms) > 1,
+    }
+    out.update(extra)
+    return out
+
+
 def cpu_baseline_generic(g, t, R, thr, iters):
     """The oracle's N-order ALS (C++ with OpenMP MTTKRPs, the reference's
     semantics) on the device-reordered tensor, timed per iteration on this
@@ -395,20 +510,20 @@ def cpu_baseline_generic(g, t, R, thr, iters):
     _, ms = orc.als_nd_timed(coords, t.val, t.dims, ranks, R, 42, thr, iters)
     ms = [float(x) for x in ms]
     log(f"CPU baseline: {[round(x, 3) for x in ms]} ms/iter")
-    return {
-        "value": round(float(np.mean(ms)), 1),
-        "unit": "ms/iteration",
+    return summarize_cpu(ms, {
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{iters} full ALS iteration(s) of the same workload (all {t.nnz} nnz, R={R}, "
-                  f"HITS-reordered on the GPU, dense units and views built by the oracle), "
-                  f"from the reference's initial factors",
-    }
+        "sample": f"{iters} full ALS iterations of the same workload (all {t.nnz} nnz, R={R}, "
+                  f"HITS-reordered on the GPU, dense units and views built by the oracle), from "
+                  f"the reference's initial factors; first iteration dropped",
+        "host": host_info(),
+    })
 
 
-def cpu_baseline(ca, h, t, R, iters, use_mfma):
+def cpu_baseline(ca, h, t, R, iters, use_mfma, F_init):
     """The oracle's OpenMP ALS over the device-built views (test infrastructure
-    used as the CPU baseline only), timed on this host."""
+    used as the CPU baseline only), timed on this host from the same initial
+    factors as the GPU run (lambda = 1)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle", "_build"))
     import cptc_oracle as orc
 
@@ -423,26 +538,26 @@ def cpu_baseline(ca, h, t, R, iters, use_mfma):
             tiles = tl
         else:
             dv = [h.view(1, m) for m in range(3)]
-    F = [h.factor(m).ravel() for m in range(3)]
-    lam = h.lam()
     x_sq = float(np.sum(t.val * t.val))
-    o = orc.Als3(views, dv, tiles, x_sq, t.dims, R, F[0], F[1], F[2], lam)
+    o = orc.Als3(views, dv, tiles, x_sq, t.dims, R, F_init[0], F_init[1], F_init[2], None)
     del views, dv, tiles
     threads = orc.max_threads()
     log(f"CPU baseline: data staged in {time.perf_counter() - t0:.1f} s; running {iters} "
         f"ALS iteration(s) with {threads} OpenMP threads")
     _, ms, mm = o.iterate(iters)
     ms = [float(x) for x in ms]
-    log(f"CPU baseline: {ms} ms/iter (MTTKRP {[round(float(x), 1) for x in mm]} ms)")
-    return {
-        "value": round(float(np.mean(ms)), 1),
-        "unit": "ms/iteration",
+    mm = [float(x) for x in mm]
+    log(f"CPU baseline: {[round(x, 1) for x in ms]} ms/iter (MTTKRP {[round(x, 1) for x in mm]} ms)")
+    kept = mm[1:] if len(mm) > 1 else mm
+    return summarize_cpu(ms, {
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{iters} full ALS iteration(s) of the same workload (all {t.nnz} nnz, R={R}), "
-                  f"starting from the GPU run's factors; views built on the GPU and copied to host",
-        "mttkrp_ms": round(float(np.mean(mm)), 1),
-    }
+        "sample": f"{iters} full ALS iterations of the same workload (all {t.nnz} nnz, R={R}) "
+                  f"from the GPU run's initial factors, views built on the GPU and copied to "
+                  f"host; first iteration dropped",
+        "mttkrp_ms_median": round(float(np.median(kept)), 1),
+        "host": host_info(),
+    })
 
 
 if __name__ == "__main__":
