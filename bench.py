@@ -121,6 +121,9 @@ def main() -> int:
     ap.add_argument("--cpu-iters", type=int, default=4)
     ap.add_argument("--fused", action="store_true",
                     help="merged single-grid MTTKRP (ALS_FUSED) on the order-3 path")
+    ap.add_argument("--sgd", action="store_true",
+                    help="CP-SGD (ALS_SGD) on the order-3 residual instead of ALS; default "
+                         "R = 32 (the reference's SGD rank), batch 2^20, gamma 1e-9")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib", action="store_true",
                     help="run only a streaming kernel of known size (PMC scaling)")
@@ -147,6 +150,8 @@ def main() -> int:
     thr = spec["thr"]
     if args.config in (4, 5):
         return bench_generic(ca, args, spec, R)
+    if args.sgd:
+        return bench_sgd(ca, args, spec, args.R or 32)
 
     t0 = time.perf_counter()
     t = ca.synth_config(args.config, 42)
@@ -307,6 +312,41 @@ def main() -> int:
     }
     h.close()
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_sgd(ca, args, spec, R) -> int:
+    """CP-SGD (sgd.cu:302-467): one step = one SGD iteration (sample 2^20
+    residual elements, one asynchronous gradient step each; every fifth
+    iteration the column normalisation, every tenth the batch loss)."""
+    batch, gamma = 1 << 20, 1e-9
+    t = ca.synth_config(args.config, 42)
+    h = ca.Als3(t, R=R, threshold=spec["thr"])
+    snnz = int(h.info.sparse_nnz)
+    if args.warmup:
+        h.sgd(args.warmup, gamma, batch, 7)
+    ca.sync()
+    t0 = time.perf_counter()
+    rm = h.sgd(args.steps, gamma, batch, 42)
+    ca.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    h.close()
+    # per element: index + packed coordinate + value, three factor rows read
+    # and three rows of atomic steps (read-modify-write counted once each)
+    b_elem = 4 + 16 + 6 * R * 8
+    log(f"CP-SGD {args.steps} iterations: {ms:.3f} ms/iter, batch rmse {rm[rm > 0].tolist()}")
+    print(json.dumps({
+        "metric": "ms per CP-SGD iteration (order-3 residual, batch 2^20)",
+        "value": round(ms, 4), "unit": "ms/iteration", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic (deterministic generator, seed 42)",
+        "config": {"workload": spec["name"], "R": R, "batch": batch, "gamma": gamma,
+                   "sparse_nnz": snnz, "parallelism": "single GPU"},
+        "element_steps_per_s": round(batch / (ms * 1e-3), 1),
+        "gather_model_GBs": round(batch * b_elem / (ms * 1e-3) / 1e9, 1),
+        "batch_rmse": [float(x) for x in rm if x > 0],
+    }), flush=True)
     return 0
 
 

@@ -274,6 +274,15 @@ class Als3:
         check(lib.cptc_als3_tile_times(self._h, out.ctypes.data), "cptc_als3_tile_times")
         return out
 
+    def sgd(self, iters: int, gamma: float = 1e-9, batch: int = 1 << 20,
+            seed: int = 42) -> np.ndarray:
+        """CP-SGD on the residual (ALS_SGD); batch RMSE per iteration (-1 where
+        the loop does not evaluate it)."""
+        out = np.zeros(max(iters, 1), np.float64)
+        check(lib.cptc_als3_sgd(self._h, iters, gamma, batch, seed, out.ctypes.data),
+              "cptc_als3_sgd")
+        return out[:iters]
+
     def mttkrp(self, mode: int) -> np.ndarray:
         out = np.zeros((self.dims[mode], self.R), np.float64)
         check(lib.cptc_als3_mttkrp(self._h, mode, out.ctypes.data), "cptc_als3_mttkrp")

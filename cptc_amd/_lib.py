@@ -161,6 +161,13 @@ SIGNATURES = {
     "cptc_als3_mttkrp": (_I, [_P, _I, _P]),
     "cptc_als3_kernel_times": (_I, [_P, _P, C.POINTER(_I), _I]),
     "cptc_als3_tile_times": (_I, [_P, _P]),
+    "cptc_als3_sgd": (_I, [_P, _I, _D, C.c_uint32, C.c_uint64, _P]),
+    "cptc_sgd3_sample": (_I, [_P, C.c_uint32, C.c_uint64, C.c_uint64, _P]),
+    "cptc_sgd3_update": (_I, [_P, _P, _P, C.c_uint32, _P, _P, _P, _P, _I, _D, _P]),
+    "cptc_sgd3_loss": (_I, [_P, _P, _P, C.c_uint32, _P, _P, _P, _P, _I, _P, _P]),
+    "cptc_sgd3_normalize": (_I, [_P, _Z, _I, _P, _P]),
+    "cptc_sgd3_run": (_I, [_P, _P, C.c_uint64, _P, _P, _P, _P, _P, _I, _I, _D, C.c_uint32,
+                           C.c_uint64, _I, _P, _P]),
     "cptc_als3_factor": (_I, [_P, _I, _I, _P]),
     "cptc_als3_set_factor": (_I, [_P, _I, _P]),
     "cptc_als3_lambda": (_I, [_P, _P]),

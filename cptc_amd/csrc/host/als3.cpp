@@ -812,6 +812,21 @@ extern "C" int cptc_als3_kernel_times(void* handle, double* out6, int* iters, in
     return CPTC_OK;
 }
 
+extern "C" int cptc_als3_sgd(void* handle, int iters, double gamma, uint32_t batch,
+                             uint64_t seed, double* batch_rmse)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && iters >= 0 && batch >= 1, CPTC_ERR_ARG, "cptc_als3_sgd: bad arguments");
+    CPTC_REQUIRE(h->views.ready && h->views.nnz > 0, CPTC_ERR_STATE,
+                 "[SGD] sparse views not ready.");
+    const cptc::DevViews3& v = h->views;
+    const int rc = cptc_sgd3_run(v.d_coords[0], v.d_vals[0], v.nnz, h->F[0], h->F[1], h->F[2],
+                                 h->dims, h->d_lambda, h->R, iters, gamma, batch, seed,
+                                 h->o.verbose, batch_rmse, h->s);
+    for (bool& g : h->gram_ok) g = false;   // the factors changed
+    return rc;
+}
+
 extern "C" int cptc_als3_tile_times(void* handle, double* out3)
 {
     Als3* h = cptc::as_h(handle);

@@ -25,6 +25,7 @@
 #include "generic.hpp"
 #include "layout.hpp"
 #include "partition.hpp"
+#include "sgd.hpp"
 #include "solver.hpp"
 #include "sparse.hpp"
 
@@ -453,6 +454,25 @@ void compute_mttkrp_merged_async(const HybridCOOTensor& hybrid, int mode, double
     }
     compute_dense_mttkrp_async(hybrid, mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
     compute_sparse_mttkrp_async(hybrid, mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);
+}
+
+// ------------------------------------------------------------------ sgd --
+
+void execute_sgd_decomposition(const HybridCOOTensor& hybrid, double* d_A, double* d_B,
+                               double* d_C, double* d_lambda_out, int R, int max_iters,
+                               double gamma, int batch_size, unsigned long long seed)
+{
+    // sgd.cu:315-319
+    if (hybrid.sparse_nnz == 0 || !hybrid.mttkrp_ready)
+    {
+        std::cerr << "[SGD] sparse views not ready." << std::endl;
+        return;
+    }
+    const uint64_t dims[3] = {hybrid.dims[0], hybrid.dims[1], hybrid.dims[2]};
+    API_TRY("execute_sgd_decomposition",
+            cptc_sgd3_run(hybrid.d_sp2_coords[0], hybrid.d_sp2_val[0], hybrid.sparse_nnz, d_A,
+                          d_B, d_C, dims, d_lambda_out, R, max_iters, gamma,
+                          uint32_t(batch_size > 0 ? batch_size : 1), seed, 1, nullptr, nullptr));
 }
 
 // --------------------------------------------------------------- solver --

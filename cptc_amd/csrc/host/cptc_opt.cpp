@@ -23,6 +23,7 @@
 #include "cptc_hip.h"
 #include "generic.hpp"
 #include "partition.hpp"
+#include "sgd.hpp"
 #include "tensor.hpp"
 
 namespace {
@@ -126,11 +127,21 @@ int run_order3(const std::string& filename, int max_iters, int R, double thresho
     CHECK_HIP(hipMemset(d_lambda, 0, size_t(R) * sizeof(double)));
     if (std::getenv("ALS_SGD"))
     {
-        std::fprintf(stderr, "[Main] ALS_SGD: the CP-SGD driver is not part of this build\n");
-        return 1;
+        // main.cu:466-501: lambda starts at 1; learning rate ALS_SGD_GAMMA
+        // (1e-9), batch ALS_SGD_BATCH (2^20), seed 42
+        const std::vector<double> ones(static_cast<size_t>(R), 1.0);
+        CHECK_HIP(hipMemcpy(d_lambda, ones.data(), ones.size() * sizeof(double),
+                            hipMemcpyHostToDevice));
+        const char* g = std::getenv("ALS_SGD_GAMMA");
+        const char* b = std::getenv("ALS_SGD_BATCH");
+        execute_sgd_decomposition(hybrid, d_factors_perm[0], d_factors_perm[1],
+                                  d_factors_perm[2], d_lambda, R, max_iters,
+                                  g ? std::atof(g) : 1e-9, b ? std::atoi(b) : (1 << 20), 42);
     }
-    execute_als_decomposition(tensor, hybrid, hybrid_dense, d_factors_perm[0], d_factors_perm[1],
-                              d_factors_perm[2], d_lambda, R, max_iters, 1e-4);
+    else
+        execute_als_decomposition(tensor, hybrid, hybrid_dense, d_factors_perm[0],
+                                  d_factors_perm[1], d_factors_perm[2], d_lambda, R, max_iters,
+                                  1e-4);
 
     // back to the input's index order (main.cu:525-545)
     double* d_factors_orig[3] = {nullptr, nullptr, nullptr};

@@ -55,7 +55,8 @@ __device__ __forceinline__ void wave_sync()
 }
 
 // The two ranks r, r + 1 of row idx.  OFF32: the element offset idx R + r
-// fits 28 bits for every level (checked at launch), so it is formed in 32-bit
+// fits 28 bits for every level (launch_rt checks it before choosing either
+// OFF32 kernel, the leaf-in-LDS one included), so it is formed in 32-bit
 // arithmetic from the wave-uniform factor base.
 template <bool OFF32>
 __device__ __forceinline__ double2 row2(const double* __restrict__ base, uint32_t idx, int R, int r)
@@ -314,8 +315,11 @@ __global__ __launch_bounds__(256) void seg_keys_leaf_lds_kernel(
 // Leaf-in-LDS plan: the leaf factor takes at most LEAF_LDS_MAX bytes, so
 // that five workgroups (the register-limited occupancy) still share a CU's
 // LDS; the grid is LEAF_LDS_WG_PER_CU workgroups per CU, used when there
-// are at least LEAF_LDS_MIN_SEGS segments per workgroup to amortise the copy.
+// are at least LEAF_LDS_MIN_SEGS segments per workgroup to amortise the copy,
+// every level's row offsets fit 32 bits, and five workgroups' leaf plus
+// static LDS fit a CU (launch_rt checks the last two).
 constexpr size_t LEAF_LDS_MAX = 24 * 1024;
+constexpr size_t CU_LDS_BYTES = 160 * 1024;   // LDS per CU on gfx950
 constexpr unsigned LEAF_LDS_WG_PER_CU = 5;
 constexpr uint64_t LEAF_LDS_MIN_SEGS = 4;
 
@@ -331,17 +335,29 @@ void launch_rt(const KeyLevels& lv, const void* keys, const double* vals, const 
                double* FtV, int R, const LeafPlan& lp, hipStream_t s)
 {
     constexpr int U = (NO <= 2) ? 8 : 4;
-    if (lp.grid > 0)
-    {
-        hipLaunchKernelGGL((seg_keys_leaf_lds_kernel<NO, RT, KEY, U>), dim3(lp.grid), dim3(256),
-                           size_t(lp.n) * sizeof(double), s, lv, static_cast<const KEY*>(keys),
-                           vals, row, st, cn, single, FtV, R, uint32_t(nseg), lp.n);
-        return;
-    }
     // 32-bit row offsets when every level's (field range x R) stays below 2^28
     bool off32 = true;
     for (int l = 0; l < NO; ++l)
         if ((lv.mask[l] + 1) * uint64_t(R) >= (uint64_t(1) << 28)) off32 = false;
+    // the leaf-in-LDS kernel reads its non-leaf rows with 32-bit offsets, and
+    // LEAF_LDS_WG_PER_CU of its workgroups (leaf + static LDS) must share a CU
+    if (lp.grid > 0 && off32)
+    {
+        static const size_t static_lds = [] {
+            hipFuncAttributes a{};
+            const void* k = reinterpret_cast<const void*>(seg_keys_leaf_lds_kernel<NO, RT, KEY, U>);
+            return hipFuncGetAttributes(&a, k) == hipSuccess ? size_t(a.sharedSizeBytes)
+                                                              : CU_LDS_BYTES;
+        }();
+        if (LEAF_LDS_WG_PER_CU * (static_lds + size_t(lp.n) * sizeof(double)) <= CU_LDS_BYTES)
+        {
+            hipLaunchKernelGGL((seg_keys_leaf_lds_kernel<NO, RT, KEY, U>), dim3(lp.grid),
+                               dim3(256), size_t(lp.n) * sizeof(double), s, lv,
+                               static_cast<const KEY*>(keys), vals, row, st, cn, single, FtV, R,
+                               uint32_t(nseg), lp.n);
+            return;
+        }
+    }
     if (off32)
         hipLaunchKernelGGL((seg_keys_kernel<NO, RT, KEY, U, true>), dim3(unsigned(nseg)),
                            dim3(256), 0, s, lv, static_cast<const KEY*>(keys), vals, row, st, cn,

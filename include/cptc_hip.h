@@ -242,6 +242,39 @@ int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float* d_tile_f3
                         const double* d_A, const double* d_B, const double* d_C, double* d_FtV,
                         int R, int dimI, int dimJ, int dimK, void* stream);
 
+/* CP-SGD on the order-3 sparse residual (sgd.cu:51-467; ALS_SGD,
+ * main.cu:467-501).  cptc_sgd3_sample: d_idx[b] = SplitMix64-finalised
+ * (seed + b * 0x9E3779B97F4A7C15) mod nnz (cpsgd_sample_kernel).
+ * cptc_sgd3_update: every sampled element of the packed (i<<30|j<<15|k) view
+ * takes one asynchronous step A[i] += g e (B[j] o C[k]), B[j] += g e (A[i] o
+ * C[k]), C[k] += g e (A[i] o B[j]), e = v - sum_r lambda_r A B C
+ * (cpsgd_update_kernel; atomics, so concurrent steps on a shared row land in
+ * hardware order).  cptc_sgd3_loss: *d_loss = sum_b e_b^2 over the sample
+ * (cpsgd_loss_kernel; deterministic reduction).  cptc_sgd3_normalize:
+ * F[:, r] /= n_r and lambda_r = n_r, both 0 when n_r < 1e-14
+ * (sgd_column_norms_kernel + sgd_normalize_absorb_kernel).  1 <= R <= 128;
+ * the reference runs R == 32 only. */
+int cptc_sgd3_sample(uint32_t* d_idx, uint32_t batch, uint64_t nnz, uint64_t seed, void* stream);
+int cptc_sgd3_update(const uint64_t* d_coords, const double* d_vals, const uint32_t* d_idx,
+                     uint32_t batch, double* d_A, double* d_B, double* d_C,
+                     const double* d_lambda, int R, double gamma, void* stream);
+int cptc_sgd3_loss(const uint64_t* d_coords, const double* d_vals, const uint32_t* d_idx,
+                   uint32_t batch, const double* d_A, const double* d_B, const double* d_C,
+                   const double* d_lambda, int R, double* d_loss, void* stream);
+int cptc_sgd3_normalize(double* d_F, size_t rows, int R, double* d_lambda, void* stream);
+
+/* The reference's SGD loop (execute_sgd_decomposition, sgd.cu:302-467):
+ * for it in [0, iters): sample with seed + it, update, normalise A, B, C
+ * when it % 5 == 0, and when it % 10 == 0 or it is the last the batch RMSE
+ * sqrt(loss / batch) goes to batch_rmse[it] (-1 for the other iterations;
+ * batch_rmse may be NULL).  verbose prints the reference's "[SGD]" lines.
+ * dims[3] are the factor row counts; the elements are the first nnz of the
+ * mode-0 residual view.  Waits for the stream before returning. */
+int cptc_sgd3_run(const uint64_t* d_coords, const double* d_vals, uint64_t nnz, double* d_A,
+                  double* d_B, double* d_C, const uint64_t* dims, double* d_lambda, int R,
+                  int iters, double gamma, uint32_t batch, uint64_t seed, int verbose,
+                  double* batch_rmse, void* stream);
+
 /* Writes pinv(FtF) (R x R) to d_Ainv with the same rule as cptc_solve_pinv;
  * *d_path (device int, may be NULL) receives 0 = Cholesky, 1 = Jacobi. */
 int cptc_pinv_sym(const double* d_FtF, double* d_Ainv, int R, int* d_path, void* stream);
@@ -353,6 +386,14 @@ int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset);
  * with it; 0 for modes whose tiles ran in the merged grid or not at all.
  * Measurement helper, no reference counterpart. */
 int cptc_als3_tile_times(void* handle, double* out3);
+
+/* CP-SGD (cptc_sgd3_run) on the handle's mode-0 residual view, factors and
+ * lambda (main.cu:467-501 starts it with lambda = 1, which a fresh handle
+ * has); the cached Grams are refreshed afterwards.  The handle's verbose
+ * flag selects the reference's "[SGD]" lines.  CPTC_ERR_STATE when the
+ * residual is empty (the reference: "[SGD] sparse views not ready."). */
+int cptc_als3_sgd(void* handle, int iters, double gamma, uint32_t batch, uint64_t seed,
+                  double* batch_rmse);
 
 /* One mode's MTTKRP with the current factors into a host buffer (dim x R),
  * through the same launches as the ALS loop.  For parity tests. */

@@ -20,9 +20,11 @@
 
 struct HybridCOOTensor;
 
-// Range form (sparse.cu:856-900).  With views built the whole residual is
-// processed when [start_idx, start_idx + count) covers it; a strict
-// sub-range is not supported by the row-sorted layout and exits.
+// Range form (sparse.cu:856-965).  With views built, a range covering the
+// whole residual runs the row-sorted segment kernel; a strict sub-range runs
+// cptc_mttkrp_sparse3_range over those elements of the target mode's view
+// (one atomic per element and rank, as mttkrp_range_generic_kernel).  The
+// range is clamped to the residual; nothing runs before build_mttkrp_views.
 void compute_sparse_mttkrp_async(const HybridCOOTensor& hybrid, int target_mode,
                                  const double* d_A, const double* d_B, const double* d_C,
                                  double* d_FtV, double* d_FtF, int R, hipStream_t stream,

@@ -667,4 +667,90 @@ void residual3(const Als3Input& in, const Als3State& st, bool with_lambda, doubl
 
 void set_num_cus(int n) { g_num_cus = n > 0 ? n : 256; }
 
+// ---------------------------------------------------------------------------
+// sgd.cu:51-288 (CP-SGD kernels), sequential restatement
+// ---------------------------------------------------------------------------
+std::vector<uint32_t> sgd3_sample(uint64_t seed, uint32_t batch, uint64_t nnz)
+{
+    // sgd.cu:195-215
+    std::vector<uint32_t> idx(batch);
+    for (uint32_t b = 0; b < batch; ++b)
+    {
+        uint64_t x = seed + uint64_t(b) * 0x9E3779B97F4A7C15ull;
+        x ^= x >> 30;
+        x *= 0xBF58476D1CE4E5B9ull;
+        x ^= x >> 27;
+        x *= 0x94D049BB133111EBull;
+        x ^= x >> 31;
+        idx[b] = uint32_t(x % nnz);
+    }
+    return idx;
+}
+
+namespace {
+double sgd3_xhat(const double* a, const double* b, const double* c, const double* lambda, int R)
+{
+    double x = 0.0;
+    for (int r = 0; r < R; ++r) x += lambda[r] * a[r] * b[r] * c[r];
+    return x;
+}
+}  // namespace
+
+void sgd3_step(const std::vector<uint64_t>& coords, const std::vector<double>& vals,
+               const std::vector<uint32_t>& idx, double* A, double* B, double* C,
+               const double* lambda, int R, double gamma)
+{
+    // sgd.cu:51-130: read the three rows, xhat, e, then the three steps from
+    // the values read
+    const size_t nr = static_cast<size_t>(R);
+    std::vector<double> a(nr), b(nr), c(nr);
+    for (uint32_t e : idx)
+    {
+        const uint64_t pc = coords[e];
+        double* pa = A + size_t((pc >> 30) & 0x7FFF) * R;
+        double* pb = B + size_t((pc >> 15) & 0x7FFF) * R;
+        double* pcc = C + size_t(pc & 0x7FFF) * R;
+        std::copy(pa, pa + R, a.begin());
+        std::copy(pb, pb + R, b.begin());
+        std::copy(pcc, pcc + R, c.begin());
+        const double err = vals[e] - sgd3_xhat(a.data(), b.data(), c.data(), lambda, R);
+        for (int r = 0; r < R; ++r)
+        {
+            pa[r] += gamma * err * b[r] * c[r];
+            pb[r] += gamma * err * a[r] * c[r];
+            pcc[r] += gamma * err * a[r] * b[r];
+        }
+    }
+}
+
+void sgd3_normalize(double* F, size_t rows, int R, double* lambda)
+{
+    // sgd.cu:219-288
+    for (int r = 0; r < R; ++r)
+    {
+        double acc = 0.0;
+        for (size_t i = 0; i < rows; ++i) acc += F[i * R + r] * F[i * R + r];
+        const double n = std::sqrt(acc);
+        for (size_t i = 0; i < rows; ++i) F[i * R + r] = n < 1e-14 ? 0.0 : F[i * R + r] / n;
+        lambda[r] = n < 1e-14 ? 0.0 : n;
+    }
+}
+
+double sgd3_loss(const std::vector<uint64_t>& coords, const std::vector<double>& vals,
+                 const std::vector<uint32_t>& idx, const double* A, const double* B,
+                 const double* C, const double* lambda, int R)
+{
+    // sgd.cu:133-192
+    double s = 0.0;
+    for (uint32_t e : idx)
+    {
+        const uint64_t pc = coords[e];
+        const double x = sgd3_xhat(A + size_t((pc >> 30) & 0x7FFF) * R,
+                                   B + size_t((pc >> 15) & 0x7FFF) * R,
+                                   C + size_t(pc & 0x7FFF) * R, lambda, R);
+        s += (vals[e] - x) * (vals[e] - x);
+    }
+    return s;
+}
+
 }  // namespace oracle

@@ -136,4 +136,18 @@ void als3_iterate(const Als3Input& in, Als3State& st, int iters, double* fits, d
 void residual3(const Als3Input& in, const Als3State& st, bool with_lambda, double* res_sq,
                double* x_sq);
 
+// CP-SGD (sgd.cu:51-467).  sgd3_sample: cpsgd_sample_kernel's hash.
+// sgd3_step: the batch's elements applied one after another in batch order
+// (the reference runs them concurrently with atomics; both agree when no two
+// elements of the batch share a factor row).  sgd3_normalize: F[:, r] /= n_r,
+// lambda_r = n_r (both 0 below 1e-14).  sgd3_loss: sum of (v - xhat)^2.
+std::vector<uint32_t> sgd3_sample(uint64_t seed, uint32_t batch, uint64_t nnz);
+void sgd3_step(const std::vector<uint64_t>& coords, const std::vector<double>& vals,
+               const std::vector<uint32_t>& idx, double* A, double* B, double* C,
+               const double* lambda, int R, double gamma);
+void sgd3_normalize(double* F, size_t rows, int R, double* lambda);
+double sgd3_loss(const std::vector<uint64_t>& coords, const std::vector<double>& vals,
+                 const std::vector<uint32_t>& idx, const double* A, const double* B,
+                 const double* C, const double* lambda, int R);
+
 }  // namespace oracle

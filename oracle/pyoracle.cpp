@@ -452,6 +452,29 @@ PYBIND11_MODULE(cptc_oracle, m)
                               flist_np(F));
     });
 
+    m.def("sgd3_sample", [](uint64_t seed, uint32_t batch, uint64_t nnz) {
+        return np(sgd3_sample(seed, batch, nnz));
+    });
+    // one SGD step over `idx` on copies of the factors; returns (A, B, C)
+    m.def("sgd3_step", [](arr<uint64_t> coords, arr<double> vals, arr<uint32_t> idx,
+                          arr<double> A, arr<double> B, arr<double> C, arr<double> lam, int R,
+                          double gamma) {
+        std::vector<double> a = vec(A), b = vec(B), c = vec(C);
+        sgd3_step(vec(coords), vec(vals), vec(idx), a.data(), b.data(), c.data(), lam.data(), R,
+                  gamma);
+        return py::make_tuple(np(a), np(b), np(c));
+    });
+    m.def("sgd3_normalize", [](arr<double> F, size_t rows, int R) {
+        std::vector<double> f = vec(F), lam(static_cast<size_t>(R));
+        sgd3_normalize(f.data(), rows, R, lam.data());
+        return py::make_tuple(np(f), np(lam));
+    });
+    m.def("sgd3_loss", [](arr<uint64_t> coords, arr<double> vals, arr<uint32_t> idx,
+                          arr<double> A, arr<double> B, arr<double> C, arr<double> lam, int R) {
+        return sgd3_loss(vec(coords), vec(vals), vec(idx), A.data(), B.data(), C.data(),
+                         lam.data(), R);
+    });
+
     py::class_<PyAls3>(m, "Als3")
         .def(py::init([](py::list residual, py::object dense_view, py::object tiles, double x_sq,
                          py::sequence dims, int R, arr<double> A, arr<double> B, arr<double> C,

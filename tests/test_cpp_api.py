@@ -11,6 +11,7 @@ import cptc_amd as ca
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = ["tensor.hpp", "cadr.hpp", "partition.hpp", "sparse.hpp", "dense.hpp", "solver.hpp",
+           "sgd.hpp",
            "als.hpp", "common.hpp", "compute_fit.hpp", "generic.hpp"]
 
 # every non-inline function the headers declare (reference names)
@@ -20,6 +21,7 @@ FUNCTIONS = [
     "partition_tensor_hybrid_gpu", "free_hybrid_tensor", "build_mttkrp_views",
     "build_dense_mttkrp_views", "compute_sparse_mttkrp_async", "compute_sparse_mttkrp",
     "compute_dense_mttkrp_async", "compute_dense_mttkrp", "compute_mttkrp_merged_async",
+    "execute_sgd_decomposition",
     "init_svd_workspace", "free_svd_workspace", "solve_als_system_svd",
     "solve_als_system_svd_nosync", "execute_als_decomposition", "debug_device_state",
     "init_factors_random", "clamp_factor_thrust", "calculate_rmse",

@@ -289,14 +289,21 @@ def test_seg_keys_kernel_vs_closed_form(ca, dev, N, R, dims, order):
     assert kinds == {0, 1}, "both store and atomic rows exercised"
 
 
-@pytest.mark.parametrize("N,R,dims", [(2, 32, (9000, 90)), (3, 8, (20000, 100, 200)),
-                                      (4, 32, (8000, 40, 30, 20)), (5, 16, (8000, 64, 64, 32, 16)),
-                                      (2, 32, (9000, 250)), (4, 16, (3000, 24, 1140, 1717))])
-def test_seg_keys_leaf_lds(ca, dev, N, R, dims):
+@pytest.mark.parametrize("N,R,dims,rev", [(2, 32, (9000, 90), False),
+                                          (3, 8, (20000, 100, 200), False),
+                                          (4, 32, (8000, 40, 30, 20), False),
+                                          (4, 32, (8000, 40, 30, 20), True),
+                                          (5, 16, (8000, 64, 64, 32, 16), False),
+                                          (5, 16, (8000, 64, 64, 32, 16), True),
+                                          (2, 32, (9000, 250), False),
+                                          (4, 16, (3000, 24, 1140, 1717), False)])
+def test_seg_keys_leaf_lds(ca, dev, N, R, dims, rev):
     """The dims variant (last level's factor staged in LDS, persistent grid)
     against the closed form and against the global-gather variant, on mode 0
     with thousands of segments: the first four shapes' leaf factors fit 24 KB
-    (LDS path; the second has 4-byte keys), the last two do not."""
+    (LDS path; the second has 4-byte keys), the last two do not.  rev: levels
+    in descending dimension order, so the leaf is the smallest factor and
+    the non-leaf levels are larger than it."""
     rng = np.random.default_rng(N * 31 + R)
     nnz = 400000
     idx = np.stack([np.minimum((rng.pareto(1.1, nnz) * d / 6).astype(np.int64), d - 1)
@@ -305,7 +312,7 @@ def test_seg_keys_leaf_lds(ca, dev, N, R, dims):
     F = [rng.standard_normal((d, R)) for d in dims]
     dF = [dbuf(ca, f) for f in F]
     n = 0
-    lev = sorted(range(1, N), key=lambda m: dims[m])
+    lev = sorted(range(1, N), key=lambda m: dims[m], reverse=rev)
     bits = [max(1, int(dims[m] - 1).bit_length()) for m in lev]
     lb = (C.c_int * len(lev))(*bits)
     kb = ca.lib.cptc_level_key_bytes(len(lev), lb)
