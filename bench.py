@@ -65,6 +65,7 @@ def gather_bytes(nnz: int, dim_n: int, R: int, N: int = 3) -> float:
 
 
 SPARSE3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_sparse.hip", "cptc_amd/csrc/kernels/seg3_body.hpp")
+BLK3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_blk.hip",)
 
 
 def sources_sha(paths) -> str:
@@ -78,7 +79,7 @@ def sources_sha(paths) -> str:
     return h.hexdigest()[:16]
 
 
-def load_traffic(workload: str):
+def load_traffic(workload: str, sources=SPARSE3_SOURCES):
     """Measured HBM traffic of one sparse-kernel launch (rocprofv3 --pmc summary
     under profiles/), or None when there is none for this workload or the
     kernel's sources changed since it was measured."""
@@ -89,7 +90,7 @@ def load_traffic(workload: str):
         d = json.load(open(path))
     except (OSError, ValueError):
         return None
-    if d.get("workload") != workload or d.get("kernel_src_sha") != sources_sha(SPARSE3_SOURCES):
+    if d.get("workload") != workload or d.get("kernel_src_sha") != sources_sha(sources):
         return None
     return d
 
@@ -202,11 +203,12 @@ def main() -> int:
     launch_ms = [float(sp_ms[m]) / kit for m in range(3)]
     mean_ms = sum(launch_ms) / 3
     gather_gbs = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
-    workload = f"cfg{args.config}-R{R}" + ("-fused" if args.fused else "")
+    blocked = bool(info.sparse_blocked) and not args.fused
+    workload = f"cfg{args.config}-R{R}" + ("-fused" if args.fused else "-blocked" if blocked else "")
     # compulsory traffic per launch: the view stream + every factor row once + output rows
     compulsory = [snnz * 20 + sum(dims) * R * 8 + dims[m] * R * 8 for m in range(3)]
     comp_gbs = sum(compulsory) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
-    prof = load_traffic(workload)
+    prof = load_traffic(workload, BLK3_SOURCES if blocked else SPARSE3_SOURCES)
     # tiles: 8192 R flops per tile per mode (16^3 x R multiply-adds)
     ntiles = int(info.num_dense_tiles)
     tile_flops = 8192.0 * R * ntiles
@@ -225,6 +227,8 @@ def main() -> int:
         roofline = {
             "kernel": ("mttkrp3_merged_kernel (MFMA tiles + FP64 residual in one grid)"
                        if args.fused else
+                       "mttkrp3_blk_kernel (FP64 residual, blocked layout, R in (64,128])"
+                       if blocked else
                        "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128])"
                        if 64 < R <= 128 else
                        "mttkrp3_seg_kernel (FP64 residual view)") + ", per launch = one mode",
@@ -298,7 +302,7 @@ def main() -> int:
             "R": R, "nnz": nnz, "dims": list(dims), "dense_threshold": thr,
             "dense_tiles": int(info.num_dense_tiles), "dense_nnz": int(info.dense_nnz),
             "sparse_nnz": snnz, "path": "mfma+fp64" if use_mfma else "fp64",
-            "fused": bool(info.fused),
+            "fused": bool(info.fused), "sparse_blocked": bool(info.sparse_blocked),
             "parallelism": "single GPU",
         },
         "ms_per_iter_event_median": round(float(np.median(ms_iter)), 4),

@@ -66,6 +66,7 @@ class Als3Info(C.Structure):
         ("dense_view_segments", C.c_uint64 * 3),
         ("num_cus", C.c_int),
         ("fused", C.c_int),
+        ("sparse_blocked", C.c_int),
     ]
 
 
@@ -143,6 +144,8 @@ SIGNATURES = {
     "cptc_gram_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
+    "cptc_mttkrp_sparse3_blk": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I,
+                                     C.c_uint64, C.c_uint64, _P]),
     "cptc_mttkrp_merged3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P, _P,
                                  _P, _I, _I, _I, _I, _P]),
     "cptc_solve_pinv_noalloc": (_I, [_P, _P, _P, _Z, _I, _P, _P]),

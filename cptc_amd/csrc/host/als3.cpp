@@ -58,6 +58,7 @@ struct Als3
     int32_t* d_perm[3] = {nullptr, nullptr, nullptr};
     DevPartition3 part;
     DevViews3 views, dviews;
+    DevBlk3 blk;   // blocked residual views (R in (64, 128]), for the FP64 kernel
     float* d_tile_f32 = nullptr;
     // per-mode tile groups (one target row block each) for the grouped MFMA launch
     uint32_t* d_order[3] = {nullptr, nullptr, nullptr};
@@ -157,10 +158,20 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
             if (!v->ready) continue;
             const bool timed = h.timing_kernels && v == &h.views;
             if (timed) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode], h.s));
-            CPTC_TRY(cptc_mttkrp_sparse3(mode, v->d_coords[mode], v->d_vals[mode],
-                                         v->d_blk_row[mode], v->d_blk_start[mode],
-                                         v->d_blk_cnt[mode], v->nseg[mode], F1, F2, h.d_FtV, R,
-                                         h.s));
+            if (v == &h.views && h.blk.ready)
+            {
+                const DevBlk3& b = h.blk;
+                CPTC_TRY(cptc_mttkrp_sparse3_blk(
+                    mode, b.d_coords[mode], b.d_vals[mode], b.d_span_start[mode],
+                    b.d_span_cnt[mode], b.d_span_kb[mode], b.d_chunk_span0[mode],
+                    b.d_chunk_nspan[mode], b.d_chunk_tb[mode], b.nchunk[mode], F1, F2, h.d_FtV, R,
+                    h.dims[mode], h.dims[mode == 2 ? 1 : 2], h.s));
+            }
+            else
+                CPTC_TRY(cptc_mttkrp_sparse3(mode, v->d_coords[mode], v->d_vals[mode],
+                                             v->d_blk_row[mode], v->d_blk_start[mode],
+                                             v->d_blk_cnt[mode], v->nseg[mode], F1, F2, h.d_FtV,
+                                             R, h.s));
             if (timed) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode + 1], h.s));
         }
     }
@@ -184,6 +195,26 @@ void choose_fused(Als3& h, int opt)
     const bool want = opt < 0 ? env_flag("ALS_FUSED") != 0 : opt != 0;
     h.fused = want && h.use_mfma && h.part.ntiles > 0 && h.views.ready && !h.dviews.ready &&
               h.R <= 128 && h.R % 2 == 0;
+}
+
+// Blocked residual views for R in (64, 128] (the one-element-per-wave
+// kernels): 16 target rows x 8 run-level rows per block pair (the kernel's
+// CPTC_BLK3_LG_TB / CPTC_BLK3_LG_KB), 4096 elements per workgroup, run-level
+// rows staged from 64 elements of a block pair on.  Used when the FP64
+// residual kernel runs without the MFMA tile kernel beside it: alone it is
+// faster than the row-segment kernel (config 3: 3.0 against 3.1-3.4 ms per
+// launch), beside the tiles it is not (its LDS keeps tile workgroups off the
+// CUs: 11.9-13.0 against 11.7 ms per iteration).  ALS_SPARSE_BLOCKED=1 / 0
+// forces it on / off.
+int build_blk(Als3& h)
+{
+    if (!h.views.ready || h.views.nnz == 0 || h.R <= 64 || h.R > 128 || h.R % 2 != 0)
+        return CPTC_OK;
+    const char* e = std::getenv("ALS_SPARSE_BLOCKED");
+    const bool beside_tiles = h.use_mfma && h.part.ntiles > 0 && h.overlap && !h.skip_dense;
+    const bool want = e ? std::strcmp(e, "0") != 0 : !beside_tiles;
+    if (!want) return CPTC_OK;
+    return blk_views3_device(h.views, h.dims, 4, 3, 4096, 64, h.blk, h.s);
 }
 
 void choose_overlap(Als3& h)
@@ -230,6 +261,7 @@ void destroy(Als3* h)
     free_partition(h->part);
     free_views(h->views);
     free_views(h->dviews);
+    free_blk(h->blk);
     for (auto& p : h->d_perm)
         if (p) (void)hipFree(p);
     for (int m = 0; m < 3; ++m)
@@ -421,6 +453,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     CPTC_TRY(build_groups(*h));
     choose_overlap(*h);
     choose_fused(*h, o.fused);
+    CPTC_TRY(build_blk(*h));
     CPTC_TRY(alloc_buffers(*h));
     if (o.verbose && h->fused)
         std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
@@ -699,6 +732,7 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
     if (rc == CPTC_OK) step(build_groups(*h));
     choose_overlap(*h);
     choose_fused(*h, -1);
+    if (rc == CPTC_OK) step(build_blk(*h));
     if (verbose && h->fused)
         std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
                     "R=%d)\n", R);
@@ -783,6 +817,7 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->use_mfma = h->use_mfma ? 1 : 0;
     info->num_cus = h->num_cus;
     info->fused = h->fused ? 1 : 0;
+    info->sparse_blocked = h->blk.ready ? 1 : 0;
     return CPTC_OK;
 }
 

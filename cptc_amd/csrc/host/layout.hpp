@@ -51,9 +51,31 @@ struct DevViews3
     uint32_t* d_blk_cnt[3] = {nullptr, nullptr, nullptr};
 };
 
+// Blocked residual views for mttkrp3_blk_kernel (R in (64, 128]): per mode
+// the reference view re-sorted by (target >> lg_tb, o1 >> lg_kb), stable, so
+// each block pair keeps (target, o1, o0) order; spans = one staged block pair
+// or consecutive unstaged ones (span_kb = o1 block | 1 << 31 when staged);
+// chunks = consecutive spans of one target row block (one workgroup each).
+struct DevBlk3
+{
+    bool ready = false;
+    size_t nnz = 0;
+    int lg_tb = 5, lg_kb = 4;
+    uint64_t* d_coords[3] = {nullptr, nullptr, nullptr};
+    double* d_vals[3] = {nullptr, nullptr, nullptr};
+    size_t nspan[3] = {0, 0, 0}, nchunk[3] = {0, 0, 0};
+    uint32_t* d_span_start[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_span_cnt[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_span_kb[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_chunk_span0[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_chunk_nspan[3] = {nullptr, nullptr, nullptr};
+    uint32_t* d_chunk_tb[3] = {nullptr, nullptr, nullptr};
+};
+
 void free_coo(DevCoo3& c);
 void free_partition(DevPartition3& p);
 void free_views(DevViews3& v);
+void free_blk(DevBlk3& b);
 
 // COO host arrays (uint32 mode-major, as cptc_coo) -> device int32 + values.
 int upload_coo3(const uint32_t* idx, const double* val, size_t nnz, const uint64_t dims[3],
@@ -73,6 +95,12 @@ int partition3_device(const DevCoo3& c, double threshold, int num_cus, DevPartit
 int views3_device(const uint32_t* d_i, const uint32_t* d_j, const uint32_t* d_k,
                   const double* d_val, size_t nnz, const uint64_t dims[3], DevViews3& out,
                   hipStream_t s);
+
+// Blocked views of the residual views v (see DevBlk3); chunk = elements per
+// workgroup, stage_min = elements of a block pair from which its run-level
+// rows are staged in LDS.
+int blk_views3_device(const DevViews3& v, const uint64_t dims[3], int lg_tb, int lg_kb,
+                      uint32_t chunk, uint32_t stage_min, DevBlk3& out, hipStream_t s);
 
 // Dense-pool decode + views (partition.cu:2335-2517).
 int dense_views3_device(const DevPartition3& p, const uint64_t dims[3], DevViews3& out,

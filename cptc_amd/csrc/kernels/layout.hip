@@ -246,6 +246,39 @@ int degrees(const int32_t* d_m, size_t nnz, uint64_t dim, unsigned* d_deg, hipSt
     return CPTC_OK;
 }
 
+// Blocked-view sort key: (target >> lg_tb, o1 >> lg_kb) of the packed
+// (i<<30 | j<<15 | k) coordinate, target / o1 by mode as the views.
+__global__ void blk_keys_kernel(const uint64_t* __restrict__ coords, size_t n, int mode,
+                                int lg_tb, int lg_kb, uint32_t* __restrict__ key,
+                                uint32_t* __restrict__ idx)
+{
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    const int kbits = 15 - lg_kb;
+    for (size_t e = size_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride)
+    {
+        const uint64_t pc = coords[e];
+        const uint32_t i = uint32_t(pc >> 30) & 0x7FFFu, j = uint32_t(pc >> 15) & 0x7FFFu,
+                       k = uint32_t(pc) & 0x7FFFu;
+        const uint32_t t = mode == 0 ? i : (mode == 1 ? j : k);
+        const uint32_t o1 = mode == 2 ? j : k;
+        key[e] = ((t >> lg_tb) << kbits) | (o1 >> lg_kb);
+        idx[e] = uint32_t(e);
+    }
+}
+
+__global__ void blk_gather_kernel(const uint32_t* __restrict__ idx,
+                                  const uint64_t* __restrict__ cin, const double* __restrict__ vin,
+                                  size_t n, uint64_t* __restrict__ cout, double* __restrict__ vout)
+{
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t e = size_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n; e += stride)
+    {
+        const uint32_t s = idx[e];
+        cout[e] = cin[s];
+        vout[e] = vin[s];
+    }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------- lifecycle --
@@ -269,6 +302,21 @@ void free_partition(DevPartition3& p)
     p.dense_nnz = p.sparse_nnz = 0;
     p.h_tiles4.clear();
     p.h_pool_off.clear();
+}
+
+void free_blk(DevBlk3& b)
+{
+    for (int m = 0; m < 3; ++m)
+    {
+        dfree(b.d_coords[m]);
+        dfree(b.d_vals[m]);
+        for (uint32_t** p : {&b.d_span_start[m], &b.d_span_cnt[m], &b.d_span_kb[m],
+                             &b.d_chunk_span0[m], &b.d_chunk_nspan[m], &b.d_chunk_tb[m]})
+            dfree(*p);
+        b.nspan[m] = b.nchunk[m] = 0;
+    }
+    b.nnz = 0;
+    b.ready = false;
 }
 
 void free_views(DevViews3& v)
@@ -552,6 +600,118 @@ int views3_device(const uint32_t* d_i, const uint32_t* d_j, const uint32_t* d_k,
                                 hipMemcpyHostToDevice, s));
         CPTC_HIP(hipStreamSynchronize(s));
     }
+    out.ready = true;
+    return CPTC_OK;
+}
+
+int blk_views3_device(const DevViews3& v, const uint64_t dims[3], int lg_tb, int lg_kb,
+                      uint32_t chunk, uint32_t stage_min, DevBlk3& out, hipStream_t s)
+{
+    free_blk(out);
+    CPTC_REQUIRE(v.ready && lg_tb >= 0 && lg_tb <= 15 && lg_kb >= 0 && lg_kb <= 15 && chunk >= 1,
+                 CPTC_ERR_ARG, "blocked views: bad arguments");
+    out.lg_tb = lg_tb;
+    out.lg_kb = lg_kb;
+    out.nnz = v.nnz;
+    const size_t n = v.nnz;
+    if (n == 0)
+    {
+        out.ready = true;
+        return CPTC_OK;
+    }
+    const int kbits = 15 - lg_kb;
+    const int end_bit = (15 - lg_tb) + kbits;
+    const unsigned g = grid_for(n, 256, 8192);
+    Tmp<uint32_t> kin, kout, iin, iout, ukeys, counts, nruns;
+    CPTC_TRY(kin.alloc(n));
+    CPTC_TRY(kout.alloc(n));
+    CPTC_TRY(iin.alloc(n));
+    CPTC_TRY(iout.alloc(n));
+    CPTC_TRY(ukeys.alloc(n));
+    CPTC_TRY(counts.alloc(n));
+    CPTC_TRY(nruns.alloc(1));
+    for (int mode = 0; mode < 3; ++mode)
+    {
+        hipLaunchKernelGGL(blk_keys_kernel, dim3(g), dim3(256), 0, s, v.d_coords[mode], n, mode,
+                           lg_tb, lg_kb, kin.p, iin.p);
+        CPTC_LAUNCHED();
+        CPTC_TRY(sort_pairs(kin.p, kout.p, iin.p, iout.p, n, end_bit, s));
+        CPTC_TRY(dalloc(&out.d_coords[mode], n));
+        CPTC_TRY(dalloc(&out.d_vals[mode], n));
+        hipLaunchKernelGGL(blk_gather_kernel, dim3(g), dim3(256), 0, s, iout.p,
+                           v.d_coords[mode], v.d_vals[mode], n, out.d_coords[mode],
+                           out.d_vals[mode]);
+        CPTC_LAUNCHED();
+        CPTC_TRY(dev::run_length(kout.p, n, ukeys.p, counts.p, nruns.p, s));
+        uint32_t nr = 0;
+        CPTC_TRY(d2h_one(&nr, nruns.p, s));
+        std::vector<uint32_t> hk(nr), hc(nr);
+        CPTC_HIP(hipMemcpyAsync(hk.data(), ukeys.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        CPTC_HIP(hipMemcpyAsync(hc.data(), counts.p, nr * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+        CPTC_HIP(hipStreamSynchronize(s));
+        // spans: a staged block pair (split into pieces of <= chunk elements),
+        // or consecutive unstaged block pairs of one row block (<= chunk)
+        std::vector<uint32_t> ss, sc, sk, stb;
+        uint64_t start = 0;
+        for (uint32_t r = 0; r < nr; ++r)
+        {
+            const uint32_t tb = hk[r] >> kbits, kb = hk[r] & ((1u << kbits) - 1);
+            const uint32_t cnt = hc[r];
+            if (cnt >= stage_min)
+            {
+                for (uint32_t c0 = 0; c0 < cnt; c0 += chunk)
+                {
+                    ss.push_back(uint32_t(start + c0));
+                    sc.push_back(std::min(chunk, cnt - c0));
+                    sk.push_back(kb | 0x80000000u);
+                    stb.push_back(tb);
+                }
+            }
+            else if (!ss.empty() && stb.back() == tb && (sk.back() >> 31) == 0 &&
+                     uint64_t(sc.back()) + cnt <= chunk)
+                sc.back() += cnt;
+            else
+            {
+                ss.push_back(uint32_t(start));
+                sc.push_back(cnt);
+                sk.push_back(kb);
+                stb.push_back(tb);
+            }
+            start += cnt;
+        }
+        // chunks: consecutive spans of one row block, <= chunk elements (or one span)
+        std::vector<uint32_t> c0v, cnv, ctv;
+        uint64_t tot = 0;
+        for (uint32_t x = 0; x < uint32_t(ss.size()); ++x)
+        {
+            if (!c0v.empty() && ctv.back() == stb[x] && tot + sc[x] <= chunk)
+            {
+                cnv.back()++;
+                tot += sc[x];
+                continue;
+            }
+            c0v.push_back(x);
+            cnv.push_back(1);
+            ctv.push_back(stb[x]);
+            tot = sc[x];
+        }
+        out.nspan[mode] = ss.size();
+        out.nchunk[mode] = c0v.size();
+        auto up = [&](uint32_t** dst, const std::vector<uint32_t>& src) -> int {
+            CPTC_TRY(dalloc(dst, src.size()));
+            CPTC_HIP(hipMemcpyAsync(*dst, src.data(), src.size() * sizeof(uint32_t),
+                                    hipMemcpyHostToDevice, s));
+            return CPTC_OK;
+        };
+        CPTC_TRY(up(&out.d_span_start[mode], ss));
+        CPTC_TRY(up(&out.d_span_cnt[mode], sc));
+        CPTC_TRY(up(&out.d_span_kb[mode], sk));
+        CPTC_TRY(up(&out.d_chunk_span0[mode], c0v));
+        CPTC_TRY(up(&out.d_chunk_nspan[mode], cnv));
+        CPTC_TRY(up(&out.d_chunk_tb[mode], ctv));
+        CPTC_HIP(hipStreamSynchronize(s));
+    }
+    (void)dims;
     out.ready = true;
     return CPTC_OK;
 }

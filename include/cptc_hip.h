@@ -227,6 +227,19 @@ int cptc_solve_pinv(const double* d_FtF, const double* d_FtV, double* d_F, size_
 int cptc_solve_pinv_noalloc(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
                             int R, const double* d_div, void* stream);
 
+/* The FP64 residual MTTKRP of cptc_mttkrp_sparse3 over the blocked layout the
+ * order-3 driver builds for R in (64, 128] (even R): the mode's view re-sorted
+ * by (target row block, run-level row block) with span and chunk tables
+ * (span_kb = run-level block | 1 << 31 when that block's rows are staged in
+ * LDS; one workgroup per chunk of one target row block).  Same sum as
+ * sparse.cu:614-711 reassociated; no reference counterpart for the layout. */
+int cptc_mttkrp_sparse3_blk(int mode, const uint64_t* d_coords, const double* d_vals,
+                            const uint32_t* d_span_start, const uint32_t* d_span_cnt,
+                            const uint32_t* d_span_kb, const uint32_t* d_chunk_span0,
+                            const uint32_t* d_chunk_nspan, const uint32_t* d_chunk_tb,
+                            size_t nchunk, const double* d_F1, const double* d_F2, double* d_FtV,
+                            int R, uint64_t dim_target, uint64_t dim_f2, void* stream);
+
 /* One launch for both halves of an order-3 mode's MTTKRP: the MFMA dense
  * tiles (as cptc_mttkrp_dense_tiles3; grouped when d_order / d_group_off are
  * given) and the FP64 residual segments (as cptc_mttkrp_sparse3) in one grid
@@ -362,6 +375,7 @@ typedef struct cptc_als3_info {
     uint64_t dense_view_segments[3];
     int num_cus;
     int fused;                /* 1 = the merged single-grid MTTKRP is in use */
+    int sparse_blocked;       /* 1 = the residual runs over the blocked layout */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 

@@ -189,6 +189,42 @@ def test_fused_path_matches_oracle(ca, orc, dev, R):
         assert int(h4.info.fused) == 0
 
 
+@pytest.mark.parametrize("R,path", [(128, 2), (100, 2), (66, 2), (128, 1)])
+def test_blocked_sparse_view_matches_oracle(ca, orc, dev, R, path, monkeypatch):
+    """R in (64, 128]: the FP64 residual MTTKRP over the blocked layout
+    (target-row x run-level blocks, staged run-level rows in LDS,
+    ALS_SPARSE_BLOCKED=1); every mode within 1e-10 of the oracle on the
+    reference view (FP64 path) and of the row-segment kernel
+    (ALS_SPARSE_BLOCKED=0), hot Zipf rows (staged block pairs) and cold ones
+    (unstaged spans) alike.  Unforced, the driver picks the blocked layout only
+    when no MFMA tile kernel runs beside the residual one."""
+    t = ca.synth_zipf((3000, 2000, 5000), (1.1, 1.1, 1.1), 400000, 0, 17)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    outs = []
+    for blocked in ("1", "0"):
+        monkeypatch.setenv("ALS_SPARSE_BLOCKED", blocked)
+        with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+            assert int(h.info.sparse_blocked) == int(blocked)
+            F = [h.factor(m).ravel() for m in range(3)]
+            outs.append([h.mttkrp(m) for m in range(3)])
+            mfma = int(h.info.use_mfma) == 1 and len(p["tiles"]) > 0
+            dv = orc.dense_views3(p, t.dims) if (not mfma and len(p["pool_val"])) else None
+    for mode in range(3):
+        ref = orc.mttkrp3_view(v, mode, *F, R, t.dims[mode])
+        if mfma:
+            ref = ref + orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+        elif dv is not None:
+            ref = ref + orc.mttkrp3_view(dv, mode, *F, R, t.dims[mode])
+        ref = ref.reshape(t.dims[mode], R)
+        tol = 1e-5 if mfma else 1e-10
+        assert rel_err(outs[0][mode], ref) <= tol, mode
+        assert rel_err(outs[0][mode], outs[1][mode]) <= (1e-5 if mfma else 1e-12), mode
+    monkeypatch.delenv("ALS_SPARSE_BLOCKED")
+    with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+        tiles_beside = int(h.info.use_mfma) == 1 and int(h.info.num_dense_tiles) > 0
+        assert int(h.info.sparse_blocked) == int(not tiles_beside)
+
+
 def test_cli_runs_and_exports(ca, dev, tmp_path):
     t = make(ca, "zipf", 5)
     path = str(tmp_path / "t.tns")
