@@ -42,6 +42,33 @@ sys.path.insert(0, ROOT)
 BASELINE_METRIC = "ms per ALS iteration + sparse MTTKRP HBM GB/s (% of peak), order-3 R=128"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor figure
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, vendor figure
+
+
+def tile_roof(info, R, ntiles, launch_ms, where):
+    """MFMA roofline of the dense-tile kernel over its mean launch time: the
+    split-bf16 kernel (three bf16 products per term, 32-rank blocks) against
+    the bf16 matrix peak, the FP32 kernel against the FP32 matrix peak; the
+    useful flops (8192 R per tile) and the tile image's bytes beside them."""
+    b3 = bool(info.tile_bf16x3)
+    rq = (R + 31) // 32 * 32
+    useful = 8192.0 * R * ntiles
+    executed = 3 * 8192.0 * rq * ntiles if b3 else 8192.0 * ((R + 15) // 16 * 16) * ntiles
+    peak = BF16_MFMA_PEAK_TFLOPS if b3 else FP32_MFMA_PEAK_TFLOPS
+    mean_s = sum(launch_ms) / len(launch_ms) * 1e-3
+    ach = executed / mean_s / 1e12
+    return {
+        "kernel": ("dense_tiles_b3_kernel (16^3 tiles, split-bf16 v_mfma_f32_32x32x16_bf16, "
+                   "FP32 weights, FP64 output)" if b3 else
+                   "dense_tiles_kernel (16^3 tiles, FP32 MFMA, FP64 output)") + ", " + where,
+        "bound": "mfma", "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+        "frac": round(ach / peak, 4),
+        "flops_per_launch": executed, "useful_flops_per_launch": useful,
+        "useful_TFLOPs": round(useful / mean_s / 1e12, 2),
+        "tile_image_bytes_per_launch": ntiles * 4096 * 4,
+        "tile_image_GBs": round(ntiles * 4096 * 4 / mean_s / 1e9, 1),
+        "launch_ms": [round(x, 4) for x in launch_ms],
+    }
 
 CONFIG_SPEC = {
     1: dict(R=32, thr=0.03, name="cfg1: order-3 256^3 CP-rank-8 + noise, p=0.9 (~15.1M nnz)"),
@@ -211,7 +238,6 @@ def main() -> int:
     prof = load_traffic(workload, BLK3_SOURCES if blocked else SPARSE3_SOURCES)
     # tiles: 8192 R flops per tile per mode (16^3 x R multiply-adds)
     ntiles = int(info.num_dense_tiles)
-    tile_flops = 8192.0 * R * ntiles
     tile_ms = [float(x) / kit for x in tile_ms_acc]
     tiles_timed = use_mfma and ntiles and all(x > 0 for x in tile_ms)
 
@@ -259,30 +285,18 @@ def main() -> int:
         # no sparse residual (every nonzero in a dense tile): the MFMA tile
         # kernel is the whole MTTKRP
         mt_launch = [float(mt_ms[m]) / kit for m in range(3)]
-        tflops = tile_flops * 3 / (sum(mt_launch) * 1e-3) / 1e12 if use_mfma and ntiles else 0.0
-        roofline = {
-            "kernel": "dense_tiles_kernel<mode,4,false,true> (16^3 tiles, FP32 MFMA, FP64 "
-                      "epilogue), per launch = one mode",
-            "bound": "mfma",
-            "achieved": round(tflops, 2),
-            "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
-            "launch_ms": [round(x, 4) for x in mt_launch],
-            "flops_per_launch": tile_flops,
-            "tile_bytes_per_launch": ntiles * 4096 * 4,
-        }
+        if use_mfma and ntiles:
+            roofline = tile_roof(info, R, ntiles, mt_launch, "the whole MTTKRP (no residual)")
+        else:
+            roofline = {"kernel": "FP64 dense-view MTTKRP", "bound": "hbm", "achieved": None,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+                        "launch_ms": [round(x, 4) for x in mt_launch]}
+        roofline["traffic"] = None
     roofline_tiles = None
     if tiles_timed and snnz:
-        ttf = tile_flops * 3 / (sum(tile_ms) * 1e-3) / 1e12
-        roofline_tiles = {
-            "kernel": "dense_tiles_kernel<mode,4,false,true> (16^3 tiles, FP32 MFMA), per mode, "
-                      "beside the FP64 kernel on a second stream",
-            "bound": "mfma", "achieved": round(ttf, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(ttf / FP32_MFMA_PEAK_TFLOPS, 4),
-            "flops_per_launch": tile_flops, "launch_ms": [round(x, 4) for x in tile_ms],
-        }
+        where = ("beside the FP64 kernel on a second stream" if info.tiles_beside else
+                 "on the main stream before the FP64 kernel")
+        roofline_tiles = tile_roof(info, R, ntiles, tile_ms, where)
 
     line = {
         "metric": BASELINE_METRIC,
@@ -295,7 +309,9 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64" if not use_mfma else "f64 (dense tiles: fp32 MFMA, f64 epilogue)",
+        "dtype": "f64" if not use_mfma else (
+            "f64 (dense tiles: split-bf16 MFMA, fp32 weights, f64 output)" if info.tile_bf16x3
+            else "f64 (dense tiles: fp32 MFMA, f64 output)"),
         "data": "synthetic (deterministic generator, seed 42)",
         "config": {
             "workload": spec["name"] if R == spec["R"] else f"{spec['name']} (R={R})",
@@ -303,6 +319,8 @@ def main() -> int:
             "dense_tiles": int(info.num_dense_tiles), "dense_nnz": int(info.dense_nnz),
             "sparse_nnz": snnz, "path": "mfma+fp64" if use_mfma else "fp64",
             "fused": bool(info.fused), "sparse_blocked": bool(info.sparse_blocked),
+            "tile_kernel": "bf16x3" if info.tile_bf16x3 else "fp32",
+            "tiles_beside": bool(info.tiles_beside),
             "parallelism": "single GPU",
         },
         "ms_per_iter_event_median": round(float(np.median(ms_iter)), 4),
@@ -388,8 +406,7 @@ def bench_generic(ca, args, spec, R) -> int:
     hbm = (prof["hbm_bytes_per_launch"] / (sum(seg_launch) / N * 1e-3) / 1e9) if prof else None
     inner = [m for m in range(N) if info.dense_enabled and m in tuple(info.inner)]
     unit_launch = [float(unit_ms[m]) / kit for m in inner]
-    flops = 8192.0 * R * int(info.n_units)
-    tflops = (flops * len(inner) / (sum(unit_launch) * 1e-3) / 1e12) if unit_launch else 0.0
+
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter; seg launch ms "
         f"{[round(x, 4) for x in seg_launch]}; unit launch ms {[round(x, 4) for x in unit_launch]}")
     cpu = None
@@ -402,12 +419,14 @@ def bench_generic(ca, args, spec, R) -> int:
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f64 (dense units: fp32 MFMA, f64 epilogue)",
+        "dtype": ("f64 (dense units: split-bf16 MFMA, fp32 weights, f64 output)"
+                  if info.tile_bf16x3 else "f64 (dense units: fp32 MFMA, f64 output)"),
         "data": "synthetic (deterministic generator, seed 42)",
         "config": {"workload": spec["name"] if R == spec["R"] else f"{spec['name']} (R={R})",
                    "R": R, "nnz": t.nnz, "dims": list(dims), "dense_units": int(info.n_units),
                    "dense_nnz": int(info.dense_nnz), "kernel_view_nnz": knnz,
-                   "path": "generic N-order", "parallelism": "single GPU"},
+                   "path": "generic N-order", "parallelism": "single GPU",
+                   "tile_kernel": "bf16x3" if info.tile_bf16x3 else "fp32"},
         "fit_last": float(fits[-1]),
         "roofline": {
             "kernel": "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
@@ -423,12 +442,9 @@ def bench_generic(ca, args, spec, R) -> int:
                                f"sha {prof['kernel_src_sha']})") if prof else
                               "none for these kernel sources: achieved/frac null",
         },
-        "roofline_units": {
-            "kernel": "dense_tiles_kernel<slot,6,true> (dense units, FP32 MFMA), per inner mode",
-            "bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "flops_per_launch": flops, "launch_ms": [round(x, 4) for x in unit_launch],
-        },
+        "roofline_units": (tile_roof(info, R, int(info.n_units), unit_launch,
+                                     "dense units with FP64 outer weights, per inner mode")
+                           if unit_launch else None),
         "cpu_baseline": cpu,
     }
     g.close()

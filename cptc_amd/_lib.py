@@ -67,6 +67,8 @@ class Als3Info(C.Structure):
         ("num_cus", C.c_int),
         ("fused", C.c_int),
         ("sparse_blocked", C.c_int),
+        ("tile_bf16x3", C.c_int),
+        ("tiles_beside", C.c_int),
     ]
 
 
@@ -102,6 +104,7 @@ class GenInfo(C.Structure):
         ("nseg", C.c_uint64 * CPTC_MAX_MODES),
         ("prep_ms", C.c_double * 3),
         ("kernel_nnz", C.c_uint64 * CPTC_MAX_MODES),
+        ("tile_bf16x3", C.c_int),
     ]
 
 
@@ -138,6 +141,9 @@ SIGNATURES = {
     "cptc_mttkrp_sparse3_range": (_I, [_I, _P, _P, _Z, _Z, _P, _P, _P, _I, _P]),
     "cptc_mttkrp_dense_tiles3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
                                       _I, _P]),
+    "cptc_tile_operands_bytes": (_Z, [C.c_uint64, _I]),
+    "cptc_mttkrp_dense_tiles3_ws": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
+                                         _I, _P, _Z, _P]),
     "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),
     "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
     "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),
@@ -193,6 +199,8 @@ SIGNATURES = {
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,
                                   _I, _P]),
+    "cptc_mttkrp_units_nd_ws": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I,
+                                     _P, _I, _P, _Z, _P]),
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_chol_ridge_factor": (_I, [_P, _P, _I, _P]),

@@ -60,6 +60,11 @@ struct Als3
     DevViews3 views, dviews;
     DevBlk3 blk;   // blocked residual views (R in (64, 128]), for the FP64 kernel
     float* d_tile_f32 = nullptr;
+    // split-bf16 tile kernel (choose_tiles) and its per-launch operand images
+    bool tile_b3 = false;
+    bool dense_beside = false;   // tile kernel on the side stream, beside the FP64 kernel
+    void* d_tile_ws = nullptr;
+    size_t tile_ws_bytes = 0;
     // per-mode tile groups (one target row block each) for the grouped MFMA launch
     uint32_t* d_order[3] = {nullptr, nullptr, nullptr};
     uint32_t* d_goff[3] = {nullptr, nullptr, nullptr};
@@ -115,7 +120,8 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     const bool dense = h.use_mfma && !h.skip_dense && h.part.ntiles > 0;
     // ALS_FUSED: tiles and residual segments in one launch on the main stream
     const bool merged = h.fused && dense && !h.skip_sparse && h.views.ready;
-    const bool fork = h.overlap && ((dense && !merged) || with_pinv);
+    const bool dense_side = h.overlap && h.dense_beside && dense && !merged;
+    const bool fork = dense_side || (h.overlap && with_pinv);
     if (fork) CPTC_HIP(hipEventRecord(h.e_fork, h.s));
     if (with_pinv)
     {
@@ -138,16 +144,22 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     }
     else if (dense)
     {
-        hipStream_t ds = h.overlap ? h.s_dense : h.s;
-        if (h.overlap) CPTC_HIP(hipStreamWaitEvent(ds, h.e_fork, 0));
+        hipStream_t ds = dense_side ? h.s_dense : h.s;
+        if (dense_side) CPTC_HIP(hipStreamWaitEvent(ds, h.e_fork, 0));
         if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[6 + 2 * mode], ds));
-        CPTC_TRY(cptc_mttkrp_dense_tiles3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
-                                          h.d_order[mode], h.d_goff[mode], h.ngroups[mode], A, B,
-                                          C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
-                                          int(h.dims[2]), ds));
+        if (h.tile_b3)
+            CPTC_TRY(cptc_mttkrp_dense_tiles3_ws(
+                mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles), h.d_order[mode],
+                h.d_goff[mode], h.ngroups[mode], A, B, C, h.d_FtV, R, int(h.dims[0]),
+                int(h.dims[1]), int(h.dims[2]), h.d_tile_ws, h.tile_ws_bytes, ds));
+        else
+            CPTC_TRY(cptc_mttkrp_dense_tiles3(
+                mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles), h.d_order[mode],
+                h.d_goff[mode], h.ngroups[mode], A, B, C, h.d_FtV, R, int(h.dims[0]),
+                int(h.dims[1]), int(h.dims[2]), ds));
         if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[6 + 2 * mode + 1], ds));
         h.tile_timed[mode] = h.timing_kernels;
-        if (h.overlap) CPTC_HIP(hipEventRecord(h.e_dense, ds));
+        if (dense_side) CPTC_HIP(hipEventRecord(h.e_dense, ds));
     }
     if (!h.skip_sparse && !merged)
     {
@@ -176,7 +188,7 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
         }
     }
     if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
-    if (h.overlap && dense && !merged) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
+    if (dense_side) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
     return CPTC_OK;
 }
 
@@ -197,24 +209,48 @@ void choose_fused(Als3& h, int opt)
               h.R <= 128 && h.R % 2 == 0;
 }
 
+// Dense tile kernel: the split-bf16 one unless R <= 16 (half of its 32-rank
+// block would idle; the FP32 kernel's 16-rank blocks measured faster there),
+// fewer than TILE_B3_MIN_ITEMS tile x 32-rank-block items (its operand-image
+// launch then costs more than it saves: config 1, 4096 tiles at R = 32,
+// 0.248 against 0.236 ms per iteration) or the merged grid (which keeps the
+// FP32 tile body) is in use; ALS_TILE_KERNEL=fp32 / bf16x3 forces it.  Where it runs: beside
+// the FP64 residual kernel on the side stream for the FP32 kernel (config
+// 3: 1.1 ms alone, the two sharing the GPU take 3.8 ms per mode against
+// 4.1 back to back), on the main stream before it for the split-bf16 kernel
+// (0.45 ms alone; beside the FP64 kernel both slow down: 3.7 ms per mode
+// against 3.45 back to back).  ALS_TILES_BESIDE=1 / 0 forces the choice.
+void choose_tiles(Als3& h)
+{
+    const size_t nt = size_t(std::max<int64_t>(h.part.ntiles, 0));
+    const int sw = cptc::tile_kernel_switch("ALS_TILE_KERNEL");
+    h.tile_b3 = h.use_mfma && nt > 0 && !h.fused && (sw < 0 ? cptc::tile_b3_auto(nt, h.R) : sw == 1);
+    const char* e = std::getenv("ALS_TILES_BESIDE");
+    const bool beside = e ? std::strcmp(e, "0") != 0 : !h.tile_b3;
+    h.dense_beside = h.overlap && beside;
+}
+
 // Blocked residual views for R in (64, 128] (the one-element-per-wave
-// kernels): 16 target rows x 8 run-level rows per block pair (the kernel's
-// CPTC_BLK3_LG_TB / CPTC_BLK3_LG_KB), 4096 elements per workgroup, run-level
-// rows staged from 64 elements of a block pair on.  Used when the FP64
+// kernels): 32 target rows x 16 run-level rows per block pair (the kernel's
+// CPTC_BLK3_LG_TB / CPTC_BLK3_LG_KB), 2048 elements per workgroup, run-level
+// rows staged from 64 elements of a block pair on (config 3, per launch:
+// 16 x 8 blocks 2.45-2.71, 32 x 8 2.46-2.52, 32 x 32 2.93-3.00; chunks of
+// 8192 / 4096 / 1024 elements 2.48-2.69 / 2.46-2.55 / 2.43-2.52; staging
+// from 32 / 128 elements 2.54-2.58 / 2.43-2.54 ms).  Used when the FP64
 // residual kernel runs without the MFMA tile kernel beside it: alone it is
-// faster than the row-segment kernel (config 3: 3.0 against 3.1-3.4 ms per
-// launch), beside the tiles it is not (its LDS keeps tile workgroups off the
-// CUs: 11.9-13.0 against 11.7 ms per iteration).  ALS_SPARSE_BLOCKED=1 / 0
-// forces it on / off.
+// faster than the row-segment kernel (config 3: 2.45 against 3.1-3.4 ms per
+// launch), beside the FP32 tile kernel it is not (its LDS keeps tile
+// workgroups off the CUs: 11.9-13.0 against 11.7 ms per iteration).
+// ALS_SPARSE_BLOCKED=1 / 0 forces it on / off.
 int build_blk(Als3& h)
 {
     if (!h.views.ready || h.views.nnz == 0 || h.R <= 64 || h.R > 128 || h.R % 2 != 0)
         return CPTC_OK;
     const char* e = std::getenv("ALS_SPARSE_BLOCKED");
-    const bool beside_tiles = h.use_mfma && h.part.ntiles > 0 && h.overlap && !h.skip_dense;
+    const bool beside_tiles = h.use_mfma && h.part.ntiles > 0 && h.dense_beside && !h.skip_dense;
     const bool want = e ? std::strcmp(e, "0") != 0 : !beside_tiles;
     if (!want) return CPTC_OK;
-    return blk_views3_device(h.views, h.dims, 4, 3, 4096, 64, h.blk, h.s);
+    return blk_views3_device(h.views, h.dims, 5, 4, 2048, 64, h.blk, h.s);
 }
 
 void choose_overlap(Als3& h)
@@ -267,7 +303,7 @@ void destroy(Als3* h)
     for (int m = 0; m < 3; ++m)
         for (void* p : {(void*)h->d_order[m], (void*)h->d_goff[m]})
             if (p) (void)hipFree(p);
-    for (void* p : {(void*)h->d_tile_f32, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
+    for (void* p : {(void*)h->d_tile_f32, (void*)h->d_tile_ws, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
                     (void*)h->d_FtF, (void*)h->d_Ainv, (void*)h->d_FtV, (void*)h->d_norms,
                     (void*)h->d_scal, (void*)h->d_fit_hist})
         if (p) (void)hipFree(p);
@@ -299,7 +335,7 @@ int build_groups(Als3& h)
     for (int m = 0; m < 3; ++m)
     {
         size_t ng = 0;
-        const int cap = cptc::tile_group_cap(nt, h.R, h.num_cus, TILE_GROUP);
+        const int cap = cptc::tile_group_cap(nt, h.R, h.num_cus, TILE_GROUP, h.tile_b3 ? 32 : 16);
         CPTC_TRY(cptc_dense_groups(h.part.h_tiles4.data(), 4, nt, m, cap, order.data(),
                                    goff.data(), &ng));
         CPTC_HIP(hipMalloc(&h.d_order[m], nt * sizeof(uint32_t)));
@@ -450,9 +486,10 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
         }
     }
 
-    CPTC_TRY(build_groups(*h));
     choose_overlap(*h);
     choose_fused(*h, o.fused);
+    choose_tiles(*h);
+    CPTC_TRY(build_groups(*h));
     CPTC_TRY(build_blk(*h));
     CPTC_TRY(alloc_buffers(*h));
     if (o.verbose && h->fused)
@@ -474,6 +511,11 @@ int alloc_buffers(Als3& hr)
     const int R = h->R;
     const size_t RR = size_t(R) * R;
     const uint64_t maxdim = std::max({h->dims[0], h->dims[1], h->dims[2]});
+    if (h->tile_b3)
+    {
+        h->tile_ws_bytes = cptc_tile_operands_bytes(maxdim, R);
+        CPTC_HIP(hipMalloc(&h->d_tile_ws, h->tile_ws_bytes));
+    }
     CPTC_HIP(hipMalloc(&h->d_lambda, size_t(R) * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_G, 3 * RR * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_FtF, RR * sizeof(double)));
@@ -729,9 +771,10 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
         if (rc == CPTC_OK) rc = r;
     };
     step(init_streams(*h));
-    if (rc == CPTC_OK) step(build_groups(*h));
     choose_overlap(*h);
     choose_fused(*h, -1);
+    choose_tiles(*h);
+    if (rc == CPTC_OK) step(build_groups(*h));
     if (rc == CPTC_OK) step(build_blk(*h));
     if (verbose && h->fused)
         std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
@@ -818,6 +861,8 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->num_cus = h->num_cus;
     info->fused = h->fused ? 1 : 0;
     info->sparse_blocked = h->blk.ready ? 1 : 0;
+    info->tile_bf16x3 = h->tile_b3 ? 1 : 0;
+    info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }
 

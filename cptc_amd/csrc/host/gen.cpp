@@ -340,6 +340,10 @@ struct Gen
     cptc::DevUnitsN units;
     float* d_tiles = nullptr;
     double* d_W = nullptr;
+    // split-bf16 unit kernel (GEN_TILE_KERNEL / the automatic rule)
+    bool tile_b3 = false;
+    void* d_tile_ws = nullptr;
+    size_t tile_ws_bytes = 0;
     // per-slot unit groups (one target row block each) for the grouped MFMA launch
     uint32_t* d_uorder[3] = {nullptr, nullptr, nullptr};
     uint32_t* d_ugoff[3] = {nullptr, nullptr, nullptr};
@@ -377,6 +381,7 @@ struct Gen
         dfree(d_FtV);
         dfree(d_out2);
         dfree(d_tiles);
+        dfree(d_tile_ws);
         dfree(d_W);
         for (int q = 0; q < 3; ++q)
         {
@@ -422,11 +427,17 @@ struct Gen
             }
             const int* in3 = units.inner;
             const int sl = slot_of(n);
-            CPTC_TRY(cptc_mttkrp_units_nd(sl, units.d_unit6, units.nunits, d_tiles, d_W,
-                                          d_uorder[sl], d_ugoff[sl], ungroups[sl],
-                                          d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
-                                          int(dims[in3[0]]), int(dims[in3[1]]),
-                                          int(dims[in3[2]]), d_FtV, R, s));
+            if (tile_b3)
+                CPTC_TRY(cptc_mttkrp_units_nd_ws(
+                    sl, units.d_unit6, units.nunits, d_tiles, d_W, d_uorder[sl], d_ugoff[sl],
+                    ungroups[sl], d_F[in3[0]], d_F[in3[1]], d_F[in3[2]], int(dims[in3[0]]),
+                    int(dims[in3[1]]), int(dims[in3[2]]), d_FtV, R, d_tile_ws, tile_ws_bytes, s));
+            else
+                CPTC_TRY(cptc_mttkrp_units_nd(sl, units.d_unit6, units.nunits, d_tiles, d_W,
+                                              d_uorder[sl], d_ugoff[sl], ungroups[sl],
+                                              d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
+                                              int(dims[in3[0]]), int(dims[in3[1]]),
+                                              int(dims[in3[2]]), d_FtV, R, s));
         }
         if (timing)
         {
@@ -616,7 +627,7 @@ Gen* as_gen(void* h) { return static_cast<Gen*>(h); }
 constexpr int UNIT_GROUP = 16;
 
 int build_unit_groups(const cptc::DevUnitsN& u, int R, hipStream_t s, uint32_t* order[3],
-                      uint32_t* goff[3], size_t ng[3])
+                      uint32_t* goff[3], size_t ng[3], int rank_block)
 {
     for (int q = 0; q < 3; ++q)
     {
@@ -633,7 +644,7 @@ int build_unit_groups(const cptc::DevUnitsN& u, int R, hipStream_t s, uint32_t* 
     int dev = 0, cus = 0;
     CPTC_HIP(hipGetDevice(&dev));
     CPTC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    const int cap = cptc::tile_group_cap(nu, R, cus, UNIT_GROUP);
+    const int cap = cptc::tile_group_cap(nu, R, cus, UNIT_GROUP, rank_block);
     for (int q = 0; q < 3; ++q)
     {
         CPTC_TRY(cptc_dense_groups(hdr.data(), 6, nu, q, cap, ord.data(), off.data(), &ng[q]));
@@ -857,7 +868,18 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
             GEN_TRY(dmalloc(&g->d_W, g->units.nunits * R));
             GEN_TRY(cptc_units_pack_nd(g->units.d_unit6, g->units.nunits, g->units.d_lid,
                                        g->units.d_val, g->d_tiles, s));
-            GEN_TRY(build_unit_groups(g->units, R, s, g->d_uorder, g->d_ugoff, g->ungroups));
+            // split-bf16 units for R > 16 and enough units (the order-3
+            // driver's rule); GEN_TILE_KERNEL=fp32 / bf16x3 forces the choice
+            const int sw = cptc::tile_kernel_switch("GEN_TILE_KERNEL");
+            g->tile_b3 = sw < 0 ? cptc::tile_b3_auto(g->units.nunits, R) : sw == 1;
+            GEN_TRY(build_unit_groups(g->units, R, s, g->d_uorder, g->d_ugoff, g->ungroups,
+                                      g->tile_b3 ? 32 : 16));
+            if (g->tile_b3)
+            {
+                const uint64_t md = std::max({g->dims[in[0]], g->dims[in[1]], g->dims[in[2]]});
+                g->tile_ws_bytes = cptc_tile_operands_bytes(md, R);
+                GEN_HIP(hipMalloc(&g->d_tile_ws, g->tile_ws_bytes));
+            }
         }
         g->prep_ms[1] = ms_since(t0);
         if (verbose)
@@ -933,6 +955,7 @@ extern "C" int cptc_gen_info_get(void* handle, cptc_gen_info* info)
     info->n_units = g->units.nunits;
     info->dense_nnz = g->units.dense_nnz;
     for (int m = 0; m < g->N; ++m) info->kernel_nnz[m] = g->views[m].nnz;
+    info->tile_bf16x3 = (g->dense && g->tile_b3) ? 1 : 0;
     for (int q = 0; q < 3; ++q) info->prep_ms[q] = g->prep_ms[q];
     return CPTC_OK;
 }
@@ -1349,15 +1372,25 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
                             100.0 * double(u.dense_nnz) / double(nnz));
             float* d_tiles = nullptr;
             double* d_W = nullptr;
+            void* d_ws = nullptr;   // split-bf16 operand images (the driver's kernel)
+            size_t ws_bytes = 0;
+            const int tsw = cptc::tile_kernel_switch("GEN_TILE_KERNEL");
+            const bool b3 = tsw < 0 ? cptc::tile_b3_auto(u.nunits, R) : tsw == 1;
             uint32_t* gorder[3] = {nullptr, nullptr, nullptr};
             uint32_t* ggoff[3] = {nullptr, nullptr, nullptr};
             size_t gn[3] = {0, 0, 0};
             if (u.nunits)
             {
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_tiles), u.nunits * 4096 * sizeof(float)));
+                if (b3)
+                {
+                    ws_bytes = cptc_tile_operands_bytes(
+                        uint64_t(std::max({T.dims[inner[0]], T.dims[inner[1]], T.dims[inner[2]]})), R);
+                    CPTC_TRY(dal(&d_ws, ws_bytes));
+                }
                 CPTC_TRY(dal(reinterpret_cast<void**>(&d_W), u.nunits * R * sizeof(double)));
                 CPTC_TRY(cptc_units_pack_nd(u.d_unit6, u.nunits, u.d_lid, u.d_val, d_tiles, s));
-                const int rcg = build_unit_groups(u, R, s, gorder, ggoff, gn);
+                const int rcg = build_unit_groups(u, R, s, gorder, ggoff, gn, b3 ? 32 : 16);
                 for (int q = 0; q < 3; ++q)
                 {
                     own.p.push_back(gorder[q]);
@@ -1372,7 +1405,14 @@ extern "C" int cptc_gen_selftest(int verbose, int* failures)
             {
                 const int n = inner[ii];
                 CPTC_HIP(hipMemsetAsync(d_FtV, 0, size_t(maxd) * R * sizeof(double), s));
-                if (u.nunits)
+                if (u.nunits && b3)
+                    CPTC_TRY(cptc_mttkrp_units_nd_ws(ii, u.d_unit6, u.nunits, d_tiles, d_W,
+                                                     gorder[ii], ggoff[ii], gn[ii],
+                                                     dF[inner[0]], dF[inner[1]], dF[inner[2]],
+                                                     T.dims[inner[0]], T.dims[inner[1]],
+                                                     T.dims[inner[2]], d_FtV, R, d_ws, ws_bytes,
+                                                     s));
+                else if (u.nunits)
                     CPTC_TRY(cptc_mttkrp_units_nd(ii, u.d_unit6, u.nunits, d_tiles, d_W,
                                                   gorder[ii], ggoff[ii], gn[ii],
                                                   dF[inner[0]], dF[inner[1]], dF[inner[2]],

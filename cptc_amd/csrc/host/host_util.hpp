@@ -80,11 +80,35 @@ void radix_sort_pairs_u64(std::vector<uint64_t>& keys, std::vector<V>& vals, int
 // `cap` tiles with one target row block is one wave, which sums the group in
 // LDS and issues one atomic per (row, rank) per group.  Large groups save
 // atomics; enough groups keep the SIMDs busy: the cap is the number of
-// tile x rank-block items per SIMD, clamped to [1, cap].  Measured: config
+// tile x rank-block items per SIMD (16-rank blocks for the FP32 kernel,
+// 32-rank blocks for the split-bf16 one), clamped to [1, cap].  Measured: config
 // 4 (3847 units, R = 16) 0.518 -> 0.406 ms per iteration at 4 instead of 16;
 // config 5 (32768 units) slows at anything below 16 (atomic contention on
 // 64-row targets).  CPTC_TILE_GROUP=<n> fixes it (tuning).
-inline int tile_group_cap(size_t ntiles, int R, int num_cus, int cap)
+// Smallest tile (unit) x 32-rank-block count for which the drivers take the
+// split-bf16 tile kernel (config 5's 32 768 units at R = 32 gain, config 1's
+// 4096 tiles at R = 32 lose to its extra operand-image launch).
+constexpr size_t TILE_B3_MIN_ITEMS = 16384;
+
+// Tile kernel choice from a switch (ALS_TILE_KERNEL / GEN_TILE_KERNEL):
+// "fp32" -> 0, "bf16x3" -> 1, unset or anything else -> -1 (automatic).
+inline int tile_kernel_switch(const char* name)
+{
+    const char* e = std::getenv(name);
+    if (!e) return -1;
+    if (std::strcmp(e, "fp32") == 0) return 0;
+    if (std::strcmp(e, "bf16x3") == 0) return 1;
+    return -1;
+}
+
+// The automatic choice: the split-bf16 kernel for R > 16 and at least
+// TILE_B3_MIN_ITEMS tile x 32-rank-block items.
+inline bool tile_b3_auto(size_t ntiles, int R)
+{
+    return R > 16 && ntiles * size_t((R + 31) / 32) >= TILE_B3_MIN_ITEMS;
+}
+
+inline int tile_group_cap(size_t ntiles, int R, int num_cus, int cap, int rank_block = 16)
 {
     if (const char* e = std::getenv("CPTC_TILE_GROUP"))
     {
@@ -92,7 +116,7 @@ inline int tile_group_cap(size_t ntiles, int R, int num_cus, int cap)
         if (g >= 1) return g;
     }
     const size_t simds = size_t(num_cus > 0 ? num_cus : 256) * 4;
-    const size_t items = ntiles * size_t((R + 15) / 16);
+    const size_t items = ntiles * size_t((R + rank_block - 1) / rank_block);
     const size_t g = (items + simds - 1) / simds;
     return int(std::max<size_t>(1, std::min<size_t>(g, size_t(cap))));
 }

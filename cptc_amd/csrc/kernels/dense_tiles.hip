@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "../host/hip_util.hpp"
+#include "tiles_b3_body.hpp"
 #include "tiles_body.hpp"
 
 namespace {
@@ -49,6 +50,70 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
     cptc_k::dense_tiles_body<MODE, HDR, HAS_W, GROUPED>(blockIdx.x, gacc_lds, hdr, tile_f32,
                                                         ntiles, order, goff, ngroups, A, B, C, W,
                                                         FtV, R, Rp, dimI, dimJ, dimK, S);
+}
+
+// Split-bf16 variant (cptc_k::dense_tiles_b3_body in tiles_b3_body.hpp).
+template <int MODE, int HDR, bool HAS_W, bool GROUPED>
+__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_b3_kernel(
+    const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32, size_t ntiles,
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ goff, size_t ngroups,
+    const cptc_k::u32x4* __restrict__ fs_hi, const cptc_k::u32x4* __restrict__ fs_lo,
+    const float4* __restrict__ fw, const double* __restrict__ W, double* __restrict__ FtV, int R,
+    int Rq, int odim, int S)
+{
+    extern __shared__ double gacc_lds[];
+    cptc_k::dense_tiles_b3_body<MODE, HDR, HAS_W, GROUPED>(blockIdx.x, gacc_lds, hdr, tile_f32,
+                                                           ntiles, order, goff, ngroups, fs_hi,
+                                                           fs_lo, fw, W, FtV, R, Rq, odim, S);
+}
+
+// Operand images of the split-bf16 kernel for one target slot: the
+// contracted factor Fc split into bf16 hi / lo, 8 rows of one rank per 16
+// bytes ([row / 8][Rq]), and the weight factor in FP32, 16 rows of one rank
+// per 64 bytes ([row / 16][Rq]); rows past the factor and ranks >= R are 0.
+__global__ __launch_bounds__(256) void tile_operands_kernel(
+    const double* __restrict__ Fc, int cdim, const double* __restrict__ Fw, int wdim, int R,
+    int Rq, size_t nc, size_t nw, cptc_k::u32x4* __restrict__ fs_hi,
+    cptc_k::u32x4* __restrict__ fs_lo, float4* __restrict__ fw)
+{
+    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (idx < nc)
+    {
+        const int b = int(idx / size_t(Rq)), r = int(idx % size_t(Rq));
+        float x[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+        {
+            const int row = 8 * b + q;
+            x[q] = (row < cdim && r < R) ? float(Fc[size_t(row) * R + r]) : 0.0f;
+        }
+        cptc_k::u32x4 hv, lv;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+        {
+            uint32_t hh, ll;
+            cptc_k::split_bf16x2(x[2 * s], x[2 * s + 1], hh, ll);
+            hv[s] = hh;
+            lv[s] = ll;
+        }
+        fs_hi[idx] = hv;
+        fs_lo[idx] = lv;
+    }
+    else if (idx < nc + nw)
+    {
+        const size_t k = idx - nc;
+        const int b = int(k / size_t(Rq)), r = int(k % size_t(Rq));
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+        {
+            const int row = 16 * b + u;
+            x[u] = (row < wdim && r < R) ? float(Fw[size_t(row) * R + r]) : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            fw[k * 4 + s] = make_float4(x[4 * s], x[4 * s + 1], x[4 * s + 2], x[4 * s + 3]);
+    }
 }
 
 // Tile materialisation: cell value of the last pool entry per lid (pool
@@ -156,6 +221,76 @@ int launch_tiles(const int32_t* hdr, const float* tiles, size_t ntiles, const ui
     return CPTC_OK;
 }
 
+// Workspace of the split-bf16 kernel: operand images for contracted and
+// weight factors of up to `maxdim` rows.
+size_t b3_bytes(uint64_t maxdim, int R)
+{
+    const size_t Rq = size_t(R + 31) / 32 * 32;
+    const size_t d16 = size_t((maxdim + 15) / 16) * 16;
+    return Rq * d16 * 4 /* hi + lo bf16 */ + Rq * d16 * 4 /* FP32 */ + 256;
+}
+
+template <int MODE, int HDR, bool HAS_W>
+int launch_tiles_b3(const int32_t* hdr, const float* tiles, size_t ntiles, const uint32_t* order,
+                    const uint32_t* goff, size_t ngroups, const double* Fc, int cdim,
+                    const double* Fw, int wdim, const double* W, double* FtV, int R, int odim,
+                    void* ws, size_t ws_bytes, hipStream_t s)
+{
+    const int Rq = (R + 31) / 32 * 32;
+    const size_t nc = size_t((cdim + 15) / 16) * 2 * size_t(Rq);   // 8-row blocks x Rq
+    const size_t nw = size_t((wdim + 15) / 16) * size_t(Rq);        // 16-row blocks x Rq
+    const size_t need = nc * 32 + nw * 64;
+    CPTC_REQUIRE(ws && ws_bytes >= need && (reinterpret_cast<uintptr_t>(ws) & 255) == 0,
+                 CPTC_ERR_ARG, "dense tiles (bf16 split): workspace %zu bytes, need %zu (256-aligned)",
+                 ws_bytes, need);
+    auto* fs_hi = static_cast<cptc_k::u32x4*>(ws);
+    auto* fs_lo = fs_hi + nc;
+    auto* fw = reinterpret_cast<float4*>(fs_lo + nc);
+    const size_t nthreads = nc + nw;
+    hipLaunchKernelGGL(tile_operands_kernel, dim3(unsigned((nthreads + 255) / 256)), dim3(256), 0,
+                       s, Fc, cdim, Fw, wdim, R, Rq, nc, nw, fs_hi, fs_lo, fw);
+    CPTC_LAUNCHED();
+    const dim3 block{WAVE * WAVES_PER_WG};
+    const bool grouped = order && goff && ngroups > 0 && Rq <= GROUP_LDS_MAX_R;
+    const size_t items = grouped ? ngroups : ntiles;
+    const int S = rank_split(items, Rq / 2, s);   // 32-rank blocks
+    const size_t wgs = (items * size_t(S) + WAVES_PER_WG - 1) / WAVES_PER_WG;
+    CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many tiles");
+    if (grouped)
+    {
+        const size_t lds = size_t(WAVES_PER_WG) * 16 * Rq * sizeof(double);   // <= 64 KB
+        hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, true>),
+                           dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles, ntiles,
+                           order, goff, ngroups, fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
+    }
+    else
+    {
+        hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, false>),
+                           dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ntiles,
+                           nullptr, nullptr, size_t(0), fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
+    }
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+// slot 0: contract slot 1, weight slot 2; slot 1: contract 0, weight 2;
+// slot 2: contract 0, weight 1
+template <int HDR, bool HAS_W>
+int launch_slot_b3(int slot, const int32_t* hdr, const float* tiles, size_t ntiles,
+                   const uint32_t* order, const uint32_t* goff, size_t ngroups, const double* F0,
+                   const double* F1, const double* F2, const double* W, double* FtV, int R,
+                   int d0, int d1, int d2, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    if (slot == 0)
+        return launch_tiles_b3<0, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F1, d1, F2,
+                                              d2, W, FtV, R, d0, ws, ws_bytes, s);
+    if (slot == 1)
+        return launch_tiles_b3<1, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F0, d0, F2,
+                                              d2, W, FtV, R, d1, ws, ws_bytes, s);
+    return launch_tiles_b3<2, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F0, d0, F1, d1,
+                                          W, FtV, R, d2, ws, ws_bytes, s);
+}
+
 template <int HDR, bool HAS_W>
 int launch_slot(int slot, const int32_t* hdr, const float* tiles, size_t ntiles,
                 const uint32_t* order, const uint32_t* goff, size_t ngroups, const double* A,
@@ -189,6 +324,48 @@ extern "C" int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const 
     return launch_slot<4, false>(mode, d_tiles, d_tile_f32, ntiles, d_order, d_group_off, ngroups,
                                  d_A, d_B, d_C, nullptr, d_FtV, R, dimI, dimJ, dimK,
                                  cptc::as_stream(stream));
+}
+
+extern "C" size_t cptc_tile_operands_bytes(uint64_t max_dim, int R)
+{
+    return R >= 1 ? b3_bytes(max_dim, R) : 0;
+}
+
+extern "C" int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles,
+                                           const float* d_tile_f32, size_t ntiles,
+                                           const uint32_t* d_order, const uint32_t* d_group_off,
+                                           size_t ngroups, const double* d_A, const double* d_B,
+                                           const double* d_C, double* d_FtV, int R, int dimI,
+                                           int dimJ, int dimK, void* d_ws, size_t ws_bytes,
+                                           void* stream)
+{
+    CPTC_REQUIRE(mode >= 0 && mode < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_dense_tiles3_ws: mode %d R %d", mode, R);
+    if (ntiles == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_tiles && d_tile_f32 && d_A && d_B && d_C && d_FtV, CPTC_ERR_ARG,
+                 "cptc_mttkrp_dense_tiles3_ws: null pointer");
+    return launch_slot_b3<4, false>(mode, d_tiles, d_tile_f32, ntiles, d_order, d_group_off,
+                                    ngroups, d_A, d_B, d_C, nullptr, d_FtV, R, dimI, dimJ, dimK,
+                                    d_ws, ws_bytes, cptc::as_stream(stream));
+}
+
+extern "C" int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                                       const float* d_tiles, const double* d_W,
+                                       const uint32_t* d_order, const uint32_t* d_group_off,
+                                       size_t ngroups, const double* d_F0, const double* d_F1,
+                                       const double* d_F2, int dim0, int dim1, int dim2,
+                                       double* d_FtV, int R, void* d_ws, size_t ws_bytes,
+                                       void* stream)
+{
+    CPTC_REQUIRE(slot >= 0 && slot < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd_ws: slot %d R %d", slot, R);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_tiles && d_W && d_F0 && d_F1 && d_F2 && d_FtV, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd_ws: null pointer");
+    return launch_slot_b3<6, true>(slot, reinterpret_cast<const int32_t*>(d_unit6), d_tiles,
+                                   size_t(nunits), d_order, d_group_off, ngroups, d_F0, d_F1, d_F2,
+                                   d_W, d_FtV, R, dim0, dim1, dim2, d_ws, ws_bytes,
+                                   cptc::as_stream(stream));
 }
 
 extern "C" int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,

@@ -10,18 +10,22 @@
 
 // Target rows per block and run-level rows per staged block, as log2.
 #ifndef CPTC_BLK3_LG_TB
-#define CPTC_BLK3_LG_TB 4
+#define CPTC_BLK3_LG_TB 5
 #endif
 #ifndef CPTC_BLK3_LG_KB
-#define CPTC_BLK3_LG_KB 3
+#define CPTC_BLK3_LG_KB 4
 #endif
 #ifndef CPTC_BLK3_UNROLL
-#define CPTC_BLK3_UNROLL 8   // gathers in flight per wave
+#define CPTC_BLK3_UNROLL 4   // gathers in flight per wave
 #endif
 
 namespace {
 
 constexpr int WAVE = 64;
+// 8 waves per workgroup, 6 resident per SIMD (<= 80 VGPRs; 3 workgroups'
+// 52 KB of LDS per CU): config 3 measured 2.45-2.48 ms per launch against
+// 3.0 with 4 waves, 3 per SIMD and 8 gathers in flight per wave.
+constexpr int BLK_WAVES = 8;
 
 // Blocked residual view, R in (64, 128] (one element per wave, as the
 // wave-uniform kernel).  The view of a mode is re-sorted by (target row
@@ -37,7 +41,7 @@ constexpr int WAVE = 64;
 // global atomic per (row, rank) per chunk.  Same sum as mttkrp3_seg_kernel,
 // reassociated: sum over runs of F2[o1] * sum over the run of v F1[o0].
 template <int MODE, int LG_TB, int LG_KB, int WAVES, int UNROLL>
-__global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 3))) void mttkrp3_blk_kernel(
+__global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 6))) void mttkrp3_blk_kernel(
     const uint64_t* __restrict__ coords, const double* __restrict__ vals,
     const uint32_t* __restrict__ span_start, const uint32_t* __restrict__ span_cnt,
     const uint32_t* __restrict__ span_kb, const uint32_t* __restrict__ chunk_span0,
@@ -238,9 +242,9 @@ hipError_t launch_blk(const uint64_t* coords, const double* vals, const uint32_t
                       const double* F2, double* FtV, int R, uint32_t dimT, uint32_t dimF2,
                       hipStream_t s)
 {
-    hipLaunchKernelGGL((mttkrp3_blk_kernel<MODE, CPTC_BLK3_LG_TB, CPTC_BLK3_LG_KB, 4,
+    hipLaunchKernelGGL((mttkrp3_blk_kernel<MODE, CPTC_BLK3_LG_TB, CPTC_BLK3_LG_KB, BLK_WAVES,
                                            CPTC_BLK3_UNROLL>),
-                       dim3(unsigned(nchunk)), dim3(WAVE * 4), 0, s, coords, vals, ss, sc, sk, c0,
+                       dim3(unsigned(nchunk)), dim3(WAVE * BLK_WAVES), 0, s, coords, vals, ss, sc, sk, c0,
                        cn, ct, F1, F2, FtV, R, dimT, dimF2);
     return hipGetLastError();
 }

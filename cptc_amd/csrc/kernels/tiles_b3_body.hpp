@@ -1,0 +1,317 @@
+// Dense 16^3 tile / unit MTTKRP on the bf16 matrix cores with a three-term
+// split (gfx950 v_mfma_f32_32x32x16_bf16), the fast counterpart of
+// dense_tiles_body (tiles_body.hpp): same sum, same grouping, same FP64
+// output accumulation.
+//
+// Contraction.  For target slot t, contracted slot c and weight slot w
+// (mode 0: t = i, c = j, w = k; mode 1: t = j, c = i, w = k; mode 2:
+// t = k, c = i, w = j):
+//   M[a, w, r] = sum_c T[a, c, w] * Fc[c, r]          (bf16 matrix cores)
+//   out[a, r]  = sum_w M[a, w, r] * Fw[w, r]           (FP32 VALU)
+// One 32 x 32 x 16 product per (w pair, 32-rank block): its 32 rows are
+// (w half, a) = (m / 16, m % 16) and its K dimension the tile's 16
+// contracted rows, so one instruction contracts two w slices (w = p and
+// w = 8 + p for instruction p = 0..7) and the lane multiplies each of its 16
+// results by its own rank's Fw value.
+//
+// Split.  x = hi + lo with hi = bf16(x) and lo = bf16(x - hi) (both round
+// to nearest even), so |x - hi - lo| <= 2^-18 |x|; the product
+// x * y ~ hi_x hi_y + hi_x lo_y + lo_x hi_y (the lo_x lo_y term, <= 2^-18 |xy|,
+// is dropped), accumulated in FP32, smallest terms first.  The relative error
+// per product is a few 2^-18 at most (~1e-5 worst case, ~1e-6 typical), below
+// the reference's TF32 (2^-11) inputs.
+//
+// Operands.  The tile cells come from the FP32 tile image (hi taken from the
+// value clamped to the bf16 range, so it never overflows) and are split once
+// per tile; the contracted factor arrives pre-split and the weight factor in
+// FP32 (cptc_tile_operands), in the lanes' order:
+//   fs_hi / fs_lo [c / 8][Rq] = 8 bf16 (rows 8 (c / 8) .. + 7 of one rank)
+//   fw [w / 16][Rq] = 16 floats (rows 16 (w / 16) .. + 15 of one rank)
+// Rq = R rounded up to 32, rows padded to 16 with zeros.
+//
+// Lane layout of v_mfma_f32_32x32x16_bf16 (checked on gfx950):
+//   A[m][k]: lane = m + 32 * (k / 8), element k % 8;
+//   B[k][n]: lane = n + 32 * (k / 8), element k % 8;
+//   D[m][n]: lane = n + 32 * ((m / 4) % 2), element 4 * (m / 8) + m % 4.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cptc_k {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float BF16_MAX = 3.38953139e38f;   // (2 - 2^-7) * 2^127
+
+// hi / lo bf16 pair of two values, packed as (first, second) in one dword
+// each.  hi is taken from c0 / c1 (the values, or the values clamped to the
+// bf16 range), lo from the values minus hi.
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo,
+                                             float c0, float c1)
+{
+    const __bf16 h0 = static_cast<__bf16>(c0), h1 = static_cast<__bf16>(c1);
+    const uint32_t b0 = __builtin_bit_cast(uint16_t, h0), b1 = __builtin_bit_cast(uint16_t, h1);
+    const float f0 = __builtin_bit_cast(float, b0 << 16), f1 = __builtin_bit_cast(float, b1 << 16);
+    const __bf16 l0 = static_cast<__bf16>(x0 - f0), l1 = static_cast<__bf16>(x1 - f1);
+    hi = b0 | (b1 << 16);
+    lo = uint32_t(__builtin_bit_cast(uint16_t, l0)) | (uint32_t(__builtin_bit_cast(uint16_t, l1)) << 16);
+}
+
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, uint32_t& lo)
+{
+    split_bf16x2(x0, x1, hi, lo, x0, x1);
+}
+
+// MODE = target slot; HDR = int32 words per tile header (block indices of
+// slots 0, 1, 2 first); HAS_W: FP64 outer weights W[t, r] scale the tile's
+// contribution (generic N-order units); GROUPED: a wave sums a group of
+// tiles with one target block (order[goff[g] .. goff[g + 1]]) in its own LDS
+// block (16 x Rq doubles, each lane owns its entries) and flushes one atomic
+// per (row, rank) per group.  S waves share one tile / group, wave s taking
+// the 32-rank blocks s, s + S, ...
+template <int MODE, int HDR, bool HAS_W, bool GROUPED>
+__device__ __forceinline__ void dense_tiles_b3_body(
+    size_t wg, double* gacc_lds, const int32_t* __restrict__ hdr,
+    const float* __restrict__ tile_f32, size_t ntiles, const uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ goff, size_t ngroups, const u32x4* __restrict__ fs_hi,
+    const u32x4* __restrict__ fs_lo, const float4* __restrict__ fw,
+    const double* __restrict__ W, double* __restrict__ FtV, int R, int Rq, int odim, int S)
+{
+    constexpr int WAVES = 4;
+    constexpr int CS = (MODE == 0) ? 1 : 0;   // contracted slot
+    constexpr int WS = (MODE == 2) ? 1 : 2;   // weight slot
+    const size_t wall = wg * WAVES + size_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / 64)));
+    const size_t wid = wall / size_t(S);
+    const int rb0 = int(wall - wid * size_t(S)) * 32;
+    const int rstep = S * 32;
+    size_t it0, it1;
+    if constexpr (GROUPED)
+    {
+        if (wid >= ngroups) return;
+        it0 = goff[wid];
+        it1 = goff[wid + 1];
+    }
+    else
+    {
+        if (wid >= ntiles) return;
+        it0 = wid;
+        it1 = wid + 1;
+    }
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 31;   // rank within the block; B column, D column
+    const int h = lane >> 5;   // K group (A, B); row quad parity (D)
+    const int m = lane & 31;   // A row: (w half, target row)
+    const int ww = m >> 4, am = m & 15;
+    double* gacc = gacc_lds + size_t(threadIdx.x / 64) * 16 * Rq;
+    // the lane's 8 D rows: target row a(o) = 8 (o / 4) + 4 h + o % 4, o = 0..7
+    auto arow = [&](int o) { return 8 * (o >> 2) + 4 * h + (o & 3); };
+    if constexpr (GROUPED)
+        for (int rb = rb0; rb < Rq; rb += rstep)
+#pragma unroll
+            for (int o = 0; o < 8; ++o) gacc[arow(o) * Rq + rb + n] = 0.0;
+
+    auto tile_of = [&](size_t it) -> size_t { return GROUPED ? size_t(order[it]) : it; };
+
+    // the lane's 64 cells: cells[q][p] = T at (target am, contracted 8 h + q,
+    // weight 8 ww + p)
+    float cells[8][8];
+    auto load_cells = [&](size_t t) {
+        const float* __restrict__ T = tile_f32 + t * 4096;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+        {
+            const int c = 8 * h + q;
+            if constexpr (MODE == 0 || MODE == 1)
+            {
+                // (i, j, k) = (am, c, w) or (c, am, w): the 8 w values are contiguous
+                const int base = (MODE == 0) ? (am * 16 + c) * 16 : (c * 16 + am) * 16;
+                const float4* pp = reinterpret_cast<const float4*>(T + base + 8 * ww);
+                const float4 v0 = pp[0], v1 = pp[1];
+                cells[q][0] = v0.x;
+                cells[q][1] = v0.y;
+                cells[q][2] = v0.z;
+                cells[q][3] = v0.w;
+                cells[q][4] = v1.x;
+                cells[q][5] = v1.y;
+                cells[q][6] = v1.z;
+                cells[q][7] = v1.w;
+            }
+            else
+            {
+                // (i, j, k) = (c, w, am)
+#pragma unroll
+                for (int p = 0; p < 8; ++p) cells[q][p] = T[(c * 16 + 8 * ww + p) * 16 + am];
+            }
+        }
+    };
+    bf16x8 ahi[8], alo[8];
+    auto split_cells = [&]() {
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+        {
+            u32x4 hv, lv;
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+            {
+                // FP32 values beyond the bf16 range (the image clamps to
+                // +-FLT_MAX) keep hi finite: hi = the range limit, lo = rest
+                const float x0 = cells[2 * s][p], x1 = cells[2 * s + 1][p];
+                uint32_t hh, ll;
+                split_bf16x2(x0, x1, hh, ll, __builtin_amdgcn_fmed3f(x0, -BF16_MAX, BF16_MAX),
+                             __builtin_amdgcn_fmed3f(x1, -BF16_MAX, BF16_MAX));
+                hv[s] = hh;
+                lv[s] = ll;
+            }
+            ahi[p] = __builtin_bit_cast(bf16x8, hv);
+            alo[p] = __builtin_bit_cast(bf16x8, lv);
+        }
+    };
+
+    u32x4 bh, bl;
+    float4 cw4[4];
+    auto load_ops = [&](size_t t, int rb) {
+        const int cb = hdr[HDR * t + CS];   // contracted block (16 rows)
+        const int wb = hdr[HDR * t + WS];   // weight block
+        const size_t bi = (size_t(2 * cb + h) * size_t(Rq)) + size_t(rb + n);
+        bh = fs_hi[bi];
+        bl = fs_lo[bi];
+        const float4* pw = fw + (size_t(wb) * size_t(Rq) + size_t(rb + n)) * 4;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) cw4[s] = pw[s];
+    };
+
+    size_t it = it0;
+    int rb = rb0;
+    size_t t = tile_of(it);
+    load_cells(t);
+    split_cells();
+    load_ops(t, rb);
+    int ob = 0;
+    while (true)
+    {
+        float cw[16];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+        {
+            cw[4 * s + 0] = cw4[s].x;
+            cw[4 * s + 1] = cw4[s].y;
+            cw[4 * s + 2] = cw4[s].z;
+            cw[4 * s + 3] = cw4[s].w;
+        }
+        ob = hdr[HDR * t + MODE] * 16;
+        const int r = rb + n;
+        size_t itn = it;
+        int rbn = rb + rstep;
+        if (rbn >= Rq)
+        {
+            rbn = rb0;
+            ++itn;
+        }
+        const bool more = itn < it1;
+        const size_t tn = more ? tile_of(itn) : t;
+        // modes 0 / 1: the next tile's cells load while this rank block
+        // computes (the raw cell registers are free once the current tile is
+        // split; mode 2's 64 scalar loads leave no room for that)
+        const bool next_tile = more && itn != it;
+        if (MODE != 2 && next_tile) load_cells(tn);
+
+        // Software pipeline over the four w pairs: the products of pair
+        // pp + 1 are issued before the FMAs of pair pp consume theirs, so
+        // the matrix cores and the VALU overlap within the wave, and at most
+        // 4 accumulators (64 registers) are live, not 8.
+        float out[8];
+#pragma unroll
+        for (int o = 0; o < 8; ++o) out[o] = 0.0f;
+        auto products = [&](int p, floatx16& a0, floatx16& a1) {
+            const bf16x8 bhi = __builtin_bit_cast(bf16x8, bh), blo = __builtin_bit_cast(bf16x8, bl);
+            const floatx16 z = {};
+            a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[p], bhi, z, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(alo[p + 1], bhi, z, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[p], blo, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[p + 1], blo, a1, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[p], bhi, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ahi[p + 1], bhi, a1, 0, 0, 0);
+        };
+        auto weigh = [&](int p, const floatx16& a0, const floatx16& a1) {
+#pragma unroll
+            for (int o = 0; o < 8; ++o)
+            {
+                // element o: w = p (first w half); element 8 + o: w = 8 + p
+                out[o] = __builtin_fmaf(a0[o], cw[p], out[o]);
+                out[o] = __builtin_fmaf(a0[o + 8], cw[8 + p], out[o]);
+                out[o] = __builtin_fmaf(a1[o], cw[p + 1], out[o]);
+                out[o] = __builtin_fmaf(a1[o + 8], cw[9 + p], out[o]);
+            }
+        };
+        // ordering fence (no instructions): the FMAs issued so far complete
+        // their `out` values here, and the products after it read a B
+        // operand "redefined" here, so neither moves across
+        auto fence = [&]() {
+#pragma unroll
+            for (int o = 0; o < 8; ++o) asm volatile("" : "+v"(out[o]));
+            asm volatile("" : "+v"(bh), "+v"(bl));
+        };
+        floatx16 x0, x1, y0, y1;
+        products(0, x0, x1);
+        products(2, y0, y1);
+        weigh(0, x0, x1);
+        fence();
+        products(4, x0, x1);
+        weigh(2, y0, y1);
+        fence();
+        products(6, y0, y1);
+        weigh(4, x0, x1);
+        fence();
+        weigh(6, y0, y1);
+        if (more) load_ops(tn, rbn);
+        // unconditional epilogue (ranks >= R hold zeros and are not flushed),
+        // so the FMAs above are not sunk into a branch
+        double wr = 1.0;
+        if constexpr (HAS_W) wr = (r < R) ? W[t * size_t(R) + r] : 0.0;
+#pragma unroll
+        for (int o = 0; o < 8; ++o)
+        {
+            double tot = double(out[o]);
+            if constexpr (HAS_W) tot *= wr;
+            if constexpr (GROUPED)
+            {
+                gacc[arow(o) * Rq + r] += tot;
+            }
+            else
+            {
+                const int row = ob + arow(o);
+                if (r < R && row < odim && tot != 0.0) atomicAdd(FtV + size_t(row) * R + r, tot);
+            }
+        }
+        if (!more) break;
+        if (next_tile)
+        {
+            if (MODE == 2) load_cells(tn);
+            split_cells();
+        }
+        it = itn;
+        rb = rbn;
+        t = tn;
+    }
+    if constexpr (GROUPED)
+    {
+        for (int rb2 = rb0; rb2 < Rq; rb2 += rstep)
+        {
+            const int r = rb2 + n;
+            if (r >= R) continue;
+#pragma unroll
+            for (int o = 0; o < 8; ++o)
+            {
+                const int row = ob + arow(o);
+                const double x = gacc[arow(o) * Rq + r];
+                if (row < odim && x != 0.0) atomicAdd(FtV + size_t(row) * R + r, x);
+            }
+        }
+    }
+}
+
+}  // namespace cptc_k

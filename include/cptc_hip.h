@@ -160,6 +160,26 @@ int cptc_mttkrp_dense_tiles3(int mode, const int32_t* d_tiles, const float* d_ti
                              const double* d_C, double* d_FtV, int R, int dimI, int dimJ,
                              int dimK, void* stream);
 
+/* The same sum on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16) with a
+ * three-term split: every tile cell and contracted-factor value x is
+ * hi + lo (bf16, round to nearest even), x*y ~ hi*hi + hi*lo + lo*hi in
+ * FP32, the third factor applied in FP32 on the vector ALUs, the output in
+ * FP64 as above.  Relative error per product a few 2^-18 (inputs finer than
+ * the reference's TF32, coarser than FP32).  d_ws: device workspace of
+ * ws_bytes >= cptc_tile_operands_bytes(max(dimI, dimJ, dimK), R), 256-byte
+ * aligned, rewritten by every call (the split operand images): calls that
+ * share one workspace must be ordered.  Same tile, group and output
+ * conventions as cptc_mttkrp_dense_tiles3, which it replaces in the drivers
+ * for R > 16 and enough tiles (ALS_TILE_KERNEL=fp32 / bf16x3 forces the
+ * choice). */
+size_t cptc_tile_operands_bytes(uint64_t max_dim, int R);
+int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles, const float* d_tile_f32,
+                                size_t ntiles, const uint32_t* d_order,
+                                const uint32_t* d_group_off, size_t ngroups, const double* d_A,
+                                const double* d_B, const double* d_C, double* d_FtV, int R,
+                                int dimI, int dimJ, int dimK, void* d_ws, size_t ws_bytes,
+                                void* stream);
+
 /* Tile groups for the grouped MFMA launches (no reference counterpart; the
  * reference issues one atomic per (row, rank, tile)).  hdr: ntiles x
  * hdr_words int32 on the host ({bi, bj, bk, ...}: 4 words for order-3 tiles,
@@ -233,6 +253,13 @@ int cptc_solve_pinv_noalloc(const double* d_FtF, const double* d_FtV, double* d_
  * (span_kb = run-level block | 1 << 31 when that block's rows are staged in
  * LDS; one workgroup per chunk of one target row block).  Same sum as
  * sparse.cu:614-711 reassociated; no reference counterpart for the layout. */
+/* The order-3 residual MTTKRP of cptc_mttkrp_sparse3 (sparse.cu:614-711)
+ * over a blocked copy of one mode's view, even R in (64, 128], 16-byte
+ * aligned factors, dims below 2^15: elements re-sorted by (target-row block
+ * of 32, run-level block of 16) with the (target, o1, o0) order kept inside
+ * a block pair; spans (block pairs, staged when span_kb's top bit is set) and
+ * chunks (spans of one target-row block, one workgroup each) as built by the
+ * driver's layout step.  Same sum up to the order of FP64 additions. */
 int cptc_mttkrp_sparse3_blk(int mode, const uint64_t* d_coords, const double* d_vals,
                             const uint32_t* d_span_start, const uint32_t* d_span_cnt,
                             const uint32_t* d_span_kb, const uint32_t* d_chunk_span0,
@@ -376,6 +403,8 @@ typedef struct cptc_als3_info {
     int num_cus;
     int fused;                /* 1 = the merged single-grid MTTKRP is in use */
     int sparse_blocked;       /* 1 = the residual runs over the blocked layout */
+    int tile_bf16x3;          /* 1 = dense tiles on the split-bf16 kernel, 0 = FP32 MFMA */
+    int tiles_beside;         /* 1 = tile kernel on a side stream beside the FP64 kernel */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
@@ -534,6 +563,15 @@ int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
                          const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
                          double* d_FtV, int R, void* stream);
 
+/* The same on the split-bf16 kernel of cptc_mttkrp_dense_tiles3_ws (same
+ * workspace rule, max_dim = max(dim0, dim1, dim2)); the generic driver's
+ * choice under the same rule (GEN_TILE_KERNEL=fp32 / bf16x3 forces it). */
+int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                            const float* d_tiles, const double* d_W, const uint32_t* d_order,
+                            const uint32_t* d_group_off, size_t ngroups, const double* d_F0,
+                            const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
+                            double* d_FtV, int R, void* d_ws, size_t ws_bytes, void* stream);
+
 /* out = prod_{g != skip} G_g over `ngram` consecutive R x R Grams (all ones
  * when none remain): g_fill_kernel + g_mul_kernel, generic.cu:2044-2052. */
 int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double* d_out,
@@ -601,6 +639,7 @@ typedef struct cptc_gen_info {
     double prep_ms[3];       /* reorder, dense units, views */
     uint64_t kernel_nnz[CPTC_MAX_MODES];   /* elements of the MTTKRP kernel's view per mode
                                               (the inner modes' dense elements dropped) */
+    int tile_bf16x3;         /* 1 = dense units on the split-bf16 kernel, 0 = FP32 MFMA */
 } cptc_gen_info;
 
 /* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)

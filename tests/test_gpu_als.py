@@ -105,14 +105,23 @@ def test_mttkrp_every_mode(ca, orc, dev, kind, path, R):
             assert rel_err(got, ref.reshape(t.dims[mode], R)) <= tol, mode
 
 
-@pytest.mark.parametrize("kind,path,R", [("zipf", 2, 16), ("blocks", 1, 16), ("blocks", 2, 16),
-                                         ("zipf", 0, 64)])
-def test_als_fit_matches_oracle_20_iters(ca, orc, dev, kind, path, R):
+@pytest.mark.parametrize("kind,path,R,tk", [("zipf", 2, 16, None), ("blocks", 1, 16, None),
+                                            ("blocks", 2, 16, None), ("zipf", 0, 64, None),
+                                            ("blocks", 1, 32, "bf16x3"),
+                                            ("blocks", 1, 48, "bf16x3")])
+def test_als_fit_matches_oracle_20_iters(ca, orc, dev, kind, path, R, tk, monkeypatch):
+    """20 iterations within 1e-4 of the oracle's fits (the FP64 oracle runs
+    the same tile sums exactly); tk forces the tile kernel
+    (ALS_TILE_KERNEL)."""
+    if tk:
+        monkeypatch.setenv("ALS_TILE_KERNEL", tk)
     t = make(ca, kind, 4)
     perms, p, v = oracle_layout(orc, t, 0.03)
     with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
         F = [h.factor(m).ravel() for m in range(3)]
         mfma = int(h.info.use_mfma) == 1 and len(p["tiles"]) > 0
+        if tk:
+            assert mfma and int(h.info.tile_bf16x3) == int(tk == "bf16x3")
         tiles = p if mfma else None
         dv = orc.dense_views3(p, t.dims) if (not mfma and len(p["pool_val"])) else None
         o = orc.Als3(v, dv, tiles, float(np.sum(t.val ** 2)), t.dims, R, *F, None)
@@ -158,15 +167,16 @@ def test_residual3_identical_factors(ca, orc, dev, kind, path, R):
 
 
 @pytest.mark.parametrize("R", [16, 32, 128])
-def test_fused_path_matches_oracle(ca, orc, dev, R):
+def test_fused_path_matches_oracle(ca, orc, dev, R, monkeypatch):
     """ALS_FUSED (als.cu:28, 529-555): one merged launch per mode.  MTTKRP of
     every mode within the MFMA bound of the oracle, 20 iterations within 1e-4
-    of the oracle's fits and within 1e-6 of the two-stream driver's."""
+    of the oracle's fits and within 1e-6 of the two-stream driver's with the
+    same (FP32) tile arithmetic (ALS_TILE_KERNEL=fp32)."""
     t = clustered(ca, 9)
     perms, p, v = oracle_layout(orc, t, 0.03)
     assert len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
     with ca.Als3(t, R=R, threshold=0.03, path=1, fused=1) as h:
-        assert int(h.info.fused) == 1
+        assert int(h.info.fused) == 1 and int(h.info.tile_bf16x3) == 0
         F = [h.factor(m).ravel() for m in range(3)]
         for mode in range(3):
             ref = orc.mttkrp3_view(v, mode, *F, R, t.dims[mode])
@@ -178,9 +188,11 @@ def test_fused_path_matches_oracle(ca, orc, dev, R):
     o = orc.Als3(v, None, p, float(np.sum(t.val ** 2)), t.dims, R, *F, None)
     ofit, _, _ = o.iterate(20)
     assert np.max(np.abs(fit - ofit)) <= 1e-4, (fit[-3:], ofit[-3:])
+    monkeypatch.setenv("ALS_TILE_KERNEL", "fp32")
     with ca.Als3(t, R=R, threshold=0.03, path=1, fused=0) as h2:
-        assert int(h2.info.fused) == 0
+        assert int(h2.info.fused) == 0 and int(h2.info.tile_bf16x3) == 0
         fit2, _, _ = h2.run(20)
+    monkeypatch.delenv("ALS_TILE_KERNEL")
     assert np.max(np.abs(fit - fit2)) <= 1e-6
     # the FP64 path and odd R never take the merged grid
     with ca.Als3(t, R=R, threshold=0.03, path=2, fused=1) as h3:
@@ -197,7 +209,8 @@ def test_blocked_sparse_view_matches_oracle(ca, orc, dev, R, path, monkeypatch):
     reference view (FP64 path) and of the row-segment kernel
     (ALS_SPARSE_BLOCKED=0), hot Zipf rows (staged block pairs) and cold ones
     (unstaged spans) alike.  Unforced, the driver picks the blocked layout only
-    when no MFMA tile kernel runs beside the residual one."""
+    when no MFMA tile kernel runs beside the residual one (the FP32 tile
+    kernel runs beside it; the split-bf16 one before it)."""
     t = ca.synth_zipf((3000, 2000, 5000), (1.1, 1.1, 1.1), 400000, 0, 17)
     perms, p, v = oracle_layout(orc, t, 0.03)
     outs = []
@@ -220,9 +233,21 @@ def test_blocked_sparse_view_matches_oracle(ca, orc, dev, R, path, monkeypatch):
         assert rel_err(outs[0][mode], ref) <= tol, mode
         assert rel_err(outs[0][mode], outs[1][mode]) <= (1e-5 if mfma else 1e-12), mode
     monkeypatch.delenv("ALS_SPARSE_BLOCKED")
-    with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
-        tiles_beside = int(h.info.use_mfma) == 1 and int(h.info.num_dense_tiles) > 0
-        assert int(h.info.sparse_blocked) == int(not tiles_beside)
+    for kern in ("fp32", "bf16x3"):
+        monkeypatch.setenv("ALS_TILE_KERNEL", kern)
+        with ca.Als3(t, R=R, threshold=0.03, path=path) as h:
+            mf = int(h.info.use_mfma) == 1 and int(h.info.num_dense_tiles) > 0
+            assert int(h.info.tile_bf16x3) == int(mf and kern == "bf16x3")
+            assert int(h.info.tiles_beside) == int(mf and kern == "fp32")
+            assert int(h.info.sparse_blocked) == int(not h.info.tiles_beside)
+            if mf and kern == "bf16x3":
+                # the driver's MTTKRP with the split-bf16 tiles, against the oracle
+                F = [h.factor(m).ravel() for m in range(3)]
+                for mode in range(3):
+                    ref = orc.mttkrp3_view(v, mode, *F, R, t.dims[mode])
+                    ref = ref + orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+                    assert rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R)) <= 1e-5, mode
+    monkeypatch.delenv("ALS_TILE_KERNEL")
 
 
 def test_cli_runs_and_exports(ca, dev, tmp_path):
@@ -318,7 +343,7 @@ def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
     fused_line = any(l.startswith("[ALS] FUSED path active") for l in lines)
     assert fused_line == ("ALS_FUSED" in env_path)
     t2 = ca.load_tns3(fpath)
-    with ca.Als3(t2, R=16, path=path) as h:
+    with ca.Als3(t2, R=16, path=path, fused=1 if "ALS_FUSED" in env_path else 0) as h:
         ref, _, _ = h.run(6)
         lam = h.lam()
     # Same layout, factors and kernels; the FP64 atomic adds of the MTTKRP

@@ -351,11 +351,12 @@ def test_seg_keys_leaf_lds(ca, dev, N, R, dims, rev):
     assert rel_err(outs[1], outs[0]) <= 1e-13
 
 
+@pytest.mark.parametrize("kern", ["fp32", "bf16x3"])
 @pytest.mark.parametrize("N,R,inner,G", [(4, 8, (0, 1, 2), 0), (4, 16, (0, 1, 2), 4),
                                          (5, 32, (0, 1, 2), 16), (4, 20, (1, 2, 3), 0),
                                          (4, 8, (0, 2, 3), 2), (5, 16, (1, 3, 4), 16),
                                          (4, 3, (0, 1, 3), 0)])
-def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G):
+def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G, kern):
     rng = np.random.default_rng(N * 7 + R)
     dims = (40, 30, 36, 33, 34)[:N]
     idx = clustered(rng, dims, inner, 0.5, 3000)
@@ -402,12 +403,15 @@ def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G):
                                             off.ctypes.data, C.byref(ng)) == 0
             gbufs = (dbuf(ca, order), dbuf(ca, off[:ng.value + 1].copy()))
             grp = (gbufs[0].data_ptr(), gbufs[1].data_ptr(), ng.value)
-        rc = ca.lib.cptc_mttkrp_units_nd(slot, d6.data_ptr(), nu, tiles.data_ptr(), W.data_ptr(),
-                                         *grp,
-                                         dF[inner[0]].data_ptr(), dF[inner[1]].data_ptr(),
-                                         dF[inner[2]].data_ptr(), dims[inner[0]],
-                                         dims[inner[1]], dims[inner[2]], out.data_ptr(), R,
-                                         None)
+        args = [slot, d6.data_ptr(), nu, tiles.data_ptr(), W.data_ptr(), *grp,
+                dF[inner[0]].data_ptr(), dF[inner[1]].data_ptr(), dF[inner[2]].data_ptr(),
+                dims[inner[0]], dims[inner[1]], dims[inner[2]], out.data_ptr(), R]
+        if kern == "fp32":
+            rc = ca.lib.cptc_mttkrp_units_nd(*args, None)
+        else:
+            nb = ca.lib.cptc_tile_operands_bytes(max(dims[m] for m in inner), R)
+            ws = ca.DevBuf.zeros((nb,), np.uint8)
+            rc = ca.lib.cptc_mttkrp_units_nd_ws(*args, ws.data_ptr(), nb, None)
         assert rc == 0, ca.lib.cptc_last_error()
         ca.sync()
         ref = orc.mttkrp_units_nd(idx, val, dims, u, n, [f.ravel() for f in F], R)
@@ -502,9 +506,10 @@ def test_normalize_hadamard_residual(ca, orc, dev):
     Fs = [rng.random((d, R)) for d in dims]
     lamv = rng.random(R)
     o2 = ca.DevBuf.zeros(2)
-    assert ca.lib.cptc_residual_nd(4, dbuf(ca, idx).data_ptr(), dbuf(ca, val).data_ptr(), nnz,
-                                   fptrs([dbuf(ca, f) for f in Fs]), dbuf(ca, lamv).data_ptr(), R,
-                                   o2.data_ptr(), None) == 0
+    bufs = [dbuf(ca, idx), dbuf(ca, val), dbuf(ca, lamv)]   # alive until the kernel is done
+    dFs = [dbuf(ca, f) for f in Fs]
+    assert ca.lib.cptc_residual_nd(4, bufs[0].data_ptr(), bufs[1].data_ptr(), nnz, fptrs(dFs),
+                                   bufs[2].data_ptr(), R, o2.data_ptr(), None) == 0
     ca.sync()
     ref = orc.residual_nd(idx, val, dims, [f.ravel() for f in Fs], lamv, R)
     assert abs(o2.numpy()[0] - ref) <= 1e-10 * ref

@@ -165,9 +165,13 @@ def test_merged_rejects_odd_rank(ca, dev):
     assert rc != 0 and b"even R" in ca.lib.cptc_last_error()
 
 
+@pytest.mark.parametrize("kern", ["fp32", "bf16x3"])
 @pytest.mark.parametrize("R,G", [(8, 0), (16, 0), (20, 0), (32, 0), (128, 0), (8, 3), (32, 8),
-                                 (128, 8), (200, 8)])
-def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G):
+                                 (128, 8), (200, 8), (64, 2), (100, 8)])
+def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G, kern):
+    """FP32 MFMA kernel (cptc_mttkrp_dense_tiles3) and split-bf16 kernel
+    (cptc_mttkrp_dense_tiles3_ws) against the FP64 oracle of the tile sum,
+    <= 1e-5 relative, boundary tiles in every mode, grouped and per tile."""
     rng = np.random.default_rng(50 + R)
     dims = (40, 45, 37)               # boundary tiles in every mode
     idx, val = block_tensor(rng, dims)
@@ -191,12 +195,63 @@ def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G):
         if G:
             go, gf, ng = tile_groups(ca, p["tiles"], 4, mode, G)
             grp = (go.data_ptr(), gf.data_ptr(), ng)
-        rc = ca.lib.cptc_mttkrp_dense_tiles3(mode, tiles.data_ptr(), tf.data_ptr(), nt, *grp,
-                                             dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
-                                             out.data_ptr(), R, *dims, stream(ca))
+        if kern == "fp32":
+            rc = ca.lib.cptc_mttkrp_dense_tiles3(mode, tiles.data_ptr(), tf.data_ptr(), nt, *grp,
+                                                 dF[0].data_ptr(), dF[1].data_ptr(),
+                                                 dF[2].data_ptr(), out.data_ptr(), R, *dims,
+                                                 stream(ca))
+        else:
+            nb = ca.lib.cptc_tile_operands_bytes(max(dims), R)
+            ws = zeros(ca, (nb,), np.uint8)
+            rc = ca.lib.cptc_mttkrp_dense_tiles3_ws(mode, tiles.data_ptr(), tf.data_ptr(), nt,
+                                                    *grp, dF[0].data_ptr(), dF[1].data_ptr(),
+                                                    dF[2].data_ptr(), out.data_ptr(), R, *dims,
+                                                    ws.data_ptr(), nb, stream(ca))
         assert rc == 0, ca.lib.cptc_last_error()
         ca.sync()
         assert rel_err(out.numpy(), ref) <= 1e-5, (mode, R)
+
+
+def test_dense_tiles_bf16x3_split_error(ca, orc, dev):
+    """The split-bf16 kernel's error is that of ~16-bit inputs (each operand
+    kept to ~2^-17 by its two bf16 terms): inside the 1e-5 bar with
+    zero-mean factors, whose sums cancel (measured 4.4-4.6e-6 here), and
+    far below plain bf16 (2^-9 per operand); a dropped split term (hi*lo or
+    lo*hi) would leave ~1e-3.  A workspace that is too small is an error,
+    not a fault."""
+    rng = np.random.default_rng(77)
+    dims = (48, 40, 44)
+    idx, val = block_tensor(rng, dims)
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    nt = len(p["tiles"])
+    R = 64
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    tiles = to_dev(ca, p["tiles"].astype(np.int32))
+    tf = zeros(ca, (nt * 4096,), np.float32)
+    pools = [to_dev(ca, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]   # kept alive
+    assert ca.lib.cptc_dense_tiles_pack3(*(b.data_ptr() for b in pools), nt, tf.data_ptr(),
+                                         stream(ca)) == 0
+    nb = ca.lib.cptc_tile_operands_bytes(max(dims), R)
+    ws = zeros(ca, (nb,), np.uint8)
+    errs = []
+    for mode in range(3):
+        ref = orc.mttkrp3_tiles(p, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                                dims).reshape(dims[mode], R)
+        out = zeros(ca, (dims[mode], R))
+        assert ca.lib.cptc_mttkrp_dense_tiles3_ws(mode, tiles.data_ptr(), tf.data_ptr(), nt, None,
+                                                  None, 0, dF[0].data_ptr(), dF[1].data_ptr(),
+                                                  dF[2].data_ptr(), out.data_ptr(), R, *dims,
+                                                  ws.data_ptr(), nb, stream(ca)) == 0
+        ca.sync()
+        errs.append(rel_err(out.numpy(), ref))
+    assert max(errs) <= 1e-5, errs
+    out = zeros(ca, (dims[0], R))
+    rc = ca.lib.cptc_mttkrp_dense_tiles3_ws(0, tiles.data_ptr(), tf.data_ptr(), nt, None, None, 0,
+                                            dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
+                                            out.data_ptr(), R, *dims, ws.data_ptr(), nb // 4,
+                                            stream(ca))
+    assert rc != 0 and b"workspace" in ca.lib.cptc_last_error()
 
 
 def test_dense_tile_pack_last_write_wins(ca, orc, dev):
