@@ -69,6 +69,7 @@ class Als3Info(C.Structure):
         ("sparse_blocked", C.c_int),
         ("tile_bf16x3", C.c_int),
         ("tiles_beside", C.c_int),
+        ("tile_compact", C.c_int),
     ]
 
 
@@ -144,6 +145,10 @@ SIGNATURES = {
     "cptc_tile_operands_bytes": (_Z, [C.c_uint64, _I]),
     "cptc_mttkrp_dense_tiles3_ws": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
                                          _I, _P, _Z, _P]),
+    "cptc_dense_tiles_compact3_mask": (_I, [_P, _Z, _P, _P, C.POINTER(C.c_uint64), _P]),
+    "cptc_dense_tiles_compact3_fill": (_I, [_P, _Z, _P, _P, _P, _P]),
+    "cptc_mttkrp_dense_tiles3_cws": (_I, [_I, _P, _P, _P, _P, C.c_uint64, _Z, _P, _P, _Z, _P, _P,
+                                          _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),
     "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
     "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),

@@ -52,19 +52,71 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
                                                         FtV, R, Rp, dimI, dimJ, dimK, S);
 }
 
-// Split-bf16 variant (cptc_k::dense_tiles_b3_body in tiles_b3_body.hpp).
-template <int MODE, int HDR, bool HAS_W, bool GROUPED>
+// Split-bf16 variant (cptc_k::dense_tiles_b3_body in tiles_b3_body.hpp);
+// COMPACT reads the compacted tile image (cmask / csegoff / cseg).
+template <int MODE, int HDR, bool HAS_W, bool GROUPED, bool COMPACT>
 __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_b3_kernel(
-    const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32, size_t ntiles,
-    const uint32_t* __restrict__ order, const uint32_t* __restrict__ goff, size_t ngroups,
-    const cptc_k::u32x4* __restrict__ fs_hi, const cptc_k::u32x4* __restrict__ fs_lo,
-    const float4* __restrict__ fw, const double* __restrict__ W, double* __restrict__ FtV, int R,
-    int Rq, int odim, int S)
+    const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32,
+    const uint32_t* __restrict__ cmask, const uint32_t* __restrict__ csegoff,
+    const float4* __restrict__ cseg, size_t ntiles, const uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ goff, size_t ngroups, const cptc_k::u32x4* __restrict__ fs_hi,
+    const cptc_k::u32x4* __restrict__ fs_lo, const float4* __restrict__ fw,
+    const double* __restrict__ W, double* __restrict__ FtV, int R, int Rq, int odim, int S)
 {
     extern __shared__ double gacc_lds[];
-    cptc_k::dense_tiles_b3_body<MODE, HDR, HAS_W, GROUPED>(blockIdx.x, gacc_lds, hdr, tile_f32,
-                                                           ntiles, order, goff, ngroups, fs_hi,
-                                                           fs_lo, fw, W, FtV, R, Rq, odim, S);
+    cptc_k::dense_tiles_b3_body<MODE, HDR, HAS_W, GROUPED, COMPACT>(
+        blockIdx.x, gacc_lds, hdr, tile_f32, cmask, csegoff, cseg, ntiles, order, goff, ngroups,
+        fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
+}
+
+// Compacted tile image, pass 1: per tile the occupancy bits of its 1024
+// 16-byte segments (any nonzero bit in the segment's 4 cells) and the
+// running counts before each 32-bit mask word; counts[t] = occupied segments.
+__global__ __launch_bounds__(256) void compact_tiles_mask_kernel(const float* __restrict__ tiles,
+                                                                 uint32_t* __restrict__ cmask,
+                                                                 uint32_t* __restrict__ counts)
+{
+    __shared__ uint32_t wmask[32];
+    const size_t t = blockIdx.x;
+    if (threadIdx.x < 32) wmask[threadIdx.x] = 0u;
+    __syncthreads();
+    const uint4* __restrict__ src = reinterpret_cast<const uint4*>(tiles + t * 4096);
+    for (int sg = threadIdx.x; sg < 1024; sg += 256)
+    {
+        const uint4 v = src[sg];
+        if ((v.x | v.y | v.z | v.w) != 0u) atomicOr(&wmask[sg >> 5], 1u << (sg & 31));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        uint32_t run = 0;
+        for (int w = 0; w < 32; ++w)
+        {
+            cmask[t * 64 + w] = wmask[w];
+            cmask[t * 64 + 32 + w] = run;
+            run += uint32_t(__builtin_popcount(wmask[w]));
+        }
+        counts[t] = run;
+    }
+}
+
+// Pass 2: the occupied segments of tile t, in segment order, at segoff[t].
+__global__ __launch_bounds__(256) void compact_tiles_fill_kernel(const float* __restrict__ tiles,
+                                                                 const uint32_t* __restrict__ cmask,
+                                                                 const uint32_t* __restrict__ segoff,
+                                                                 float4* __restrict__ cseg)
+{
+    const size_t t = blockIdx.x;
+    const float4* __restrict__ src = reinterpret_cast<const float4*>(tiles + t * 4096);
+    const uint32_t* __restrict__ mp = cmask + t * 64;
+    for (int sg = threadIdx.x; sg < 1024; sg += 256)
+    {
+        const int w = sg >> 5, b = sg & 31;
+        const uint32_t m = mp[w];
+        if ((m >> b) & 1u)
+            cseg[size_t(segoff[t]) + mp[32 + w] + uint32_t(__builtin_popcount(m & ((1u << b) - 1u)))] =
+                src[sg];
+    }
 }
 
 // Operand images of the split-bf16 kernel for one target slot: the
@@ -230,12 +282,21 @@ size_t b3_bytes(uint64_t maxdim, int R)
     return Rq * d16 * 4 /* hi + lo bf16 */ + Rq * d16 * 4 /* FP32 */ + 256;
 }
 
-template <int MODE, int HDR, bool HAS_W>
-int launch_tiles_b3(const int32_t* hdr, const float* tiles, size_t ntiles, const uint32_t* order,
-                    const uint32_t* goff, size_t ngroups, const double* Fc, int cdim,
-                    const double* Fw, int wdim, const double* W, double* FtV, int R, int odim,
-                    void* ws, size_t ws_bytes, hipStream_t s)
+// compacted tile image (all null: the dense tile_f32 image)
+struct CompactImg
 {
+    const uint32_t* mask = nullptr;
+    const uint32_t* segoff = nullptr;
+    const float4* seg = nullptr;
+};
+
+template <int MODE, int HDR, bool HAS_W>
+int launch_tiles_b3(const int32_t* hdr, const float* tiles, CompactImg ci, size_t ntiles,
+                    const uint32_t* order, const uint32_t* goff, size_t ngroups, const double* Fc,
+                    int cdim, const double* Fw, int wdim, const double* W, double* FtV, int R,
+                    int odim, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    const bool compact = ci.mask != nullptr;
     const int Rq = (R + 31) / 32 * 32;
     const size_t nc = size_t((cdim + 15) / 16) * 2 * size_t(Rq);   // 8-row blocks x Rq
     const size_t nw = size_t((wdim + 15) / 16) * size_t(Rq);        // 16-row blocks x Rq
@@ -259,15 +320,29 @@ int launch_tiles_b3(const int32_t* hdr, const float* tiles, size_t ntiles, const
     if (grouped)
     {
         const size_t lds = size_t(WAVES_PER_WG) * 16 * Rq * sizeof(double);   // <= 64 KB
-        hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, true>),
-                           dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles, ntiles,
-                           order, goff, ngroups, fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
+        if (compact)
+            hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, true, true>),
+                               dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles,
+                               ci.mask, ci.segoff, ci.seg, ntiles, order, goff, ngroups, fs_hi,
+                               fs_lo, fw, W, FtV, R, Rq, odim, S);
+        else
+            hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, true, false>),
+                               dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles,
+                               ci.mask, ci.segoff, ci.seg, ntiles, order, goff, ngroups, fs_hi,
+                               fs_lo, fw, W, FtV, R, Rq, odim, S);
     }
     else
     {
-        hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, false>),
-                           dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ntiles,
-                           nullptr, nullptr, size_t(0), fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
+        if (compact)
+            hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, false, true>),
+                               dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ci.mask,
+                               ci.segoff, ci.seg, ntiles, nullptr, nullptr, size_t(0), fs_hi,
+                               fs_lo, fw, W, FtV, R, Rq, odim, S);
+        else
+            hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, false, false>),
+                               dim3(static_cast<unsigned>(wgs)), block, 0, s, hdr, tiles, ci.mask,
+                               ci.segoff, ci.seg, ntiles, nullptr, nullptr, size_t(0), fs_hi,
+                               fs_lo, fw, W, FtV, R, Rq, odim, S);
     }
     CPTC_LAUNCHED();
     return CPTC_OK;
@@ -276,19 +351,19 @@ int launch_tiles_b3(const int32_t* hdr, const float* tiles, size_t ntiles, const
 // slot 0: contract slot 1, weight slot 2; slot 1: contract 0, weight 2;
 // slot 2: contract 0, weight 1
 template <int HDR, bool HAS_W>
-int launch_slot_b3(int slot, const int32_t* hdr, const float* tiles, size_t ntiles,
+int launch_slot_b3(int slot, const int32_t* hdr, const float* tiles, CompactImg ci, size_t ntiles,
                    const uint32_t* order, const uint32_t* goff, size_t ngroups, const double* F0,
                    const double* F1, const double* F2, const double* W, double* FtV, int R,
                    int d0, int d1, int d2, void* ws, size_t ws_bytes, hipStream_t s)
 {
     if (slot == 0)
-        return launch_tiles_b3<0, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F1, d1, F2,
-                                              d2, W, FtV, R, d0, ws, ws_bytes, s);
+        return launch_tiles_b3<0, HDR, HAS_W>(hdr, tiles, ci, ntiles, order, goff, ngroups, F1, d1,
+                                              F2, d2, W, FtV, R, d0, ws, ws_bytes, s);
     if (slot == 1)
-        return launch_tiles_b3<1, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F0, d0, F2,
-                                              d2, W, FtV, R, d1, ws, ws_bytes, s);
-    return launch_tiles_b3<2, HDR, HAS_W>(hdr, tiles, ntiles, order, goff, ngroups, F0, d0, F1, d1,
-                                          W, FtV, R, d2, ws, ws_bytes, s);
+        return launch_tiles_b3<1, HDR, HAS_W>(hdr, tiles, ci, ntiles, order, goff, ngroups, F0, d0,
+                                              F2, d2, W, FtV, R, d1, ws, ws_bytes, s);
+    return launch_tiles_b3<2, HDR, HAS_W>(hdr, tiles, ci, ntiles, order, goff, ngroups, F0, d0, F1,
+                                          d1, W, FtV, R, d2, ws, ws_bytes, s);
 }
 
 template <int HDR, bool HAS_W>
@@ -344,7 +419,93 @@ extern "C" int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles,
     if (ntiles == 0) return CPTC_OK;
     CPTC_REQUIRE(d_tiles && d_tile_f32 && d_A && d_B && d_C && d_FtV, CPTC_ERR_ARG,
                  "cptc_mttkrp_dense_tiles3_ws: null pointer");
-    return launch_slot_b3<4, false>(mode, d_tiles, d_tile_f32, ntiles, d_order, d_group_off,
+    return launch_slot_b3<4, false>(mode, d_tiles, d_tile_f32, CompactImg{}, ntiles, d_order,
+                                    d_group_off, ngroups, d_A, d_B, d_C, nullptr, d_FtV, R, dimI,
+                                    dimJ, dimK, d_ws, ws_bytes, cptc::as_stream(stream));
+}
+
+extern "C" int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles,
+                                              uint32_t* d_cmask, uint32_t* d_segoff,
+                                              uint64_t* total_segments, void* stream)
+{
+    CPTC_REQUIRE(total_segments, CPTC_ERR_ARG, "cptc_dense_tiles_compact3_mask: null total");
+    *total_segments = 0;
+    if (ntiles == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_tile_f32 && d_cmask && d_segoff && ntiles < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_dense_tiles_compact3_mask: bad arguments");
+    hipStream_t s = cptc::as_stream(stream);
+    uint32_t* counts = nullptr;
+    CPTC_HIP(hipMallocAsync(reinterpret_cast<void**>(&counts), ntiles * sizeof(uint32_t), s));
+    hipLaunchKernelGGL(compact_tiles_mask_kernel, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                       d_tile_f32, d_cmask, counts);
+    hipError_t le = hipGetLastError();
+    std::vector<uint32_t> h(ntiles);
+    hipError_t ce = hipMemcpyAsync(h.data(), counts, ntiles * sizeof(uint32_t),
+                                   hipMemcpyDeviceToHost, s);
+    hipError_t se = hipStreamSynchronize(s);
+    (void)hipFreeAsync(counts, s);
+    CPTC_REQUIRE(le == hipSuccess && ce == hipSuccess && se == hipSuccess, CPTC_ERR_HIP,
+                 "cptc_dense_tiles_compact3_mask: %s",
+                 hipGetErrorString(le != hipSuccess ? le : ce != hipSuccess ? ce : se));
+    std::vector<uint32_t> off(ntiles + 1);
+    uint64_t run = 0;
+    for (size_t t = 0; t < ntiles; ++t)
+    {
+        off[t] = uint32_t(run);
+        run += h[t];
+    }
+    CPTC_REQUIRE(run < (uint64_t(1) << 32), CPTC_ERR_UNSUPPORTED,
+                 "cptc_dense_tiles_compact3_mask: %llu segments exceed 32-bit offsets",
+                 (unsigned long long)run);
+    off[ntiles] = uint32_t(run);
+    CPTC_HIP(hipMemcpyAsync(d_segoff, off.data(), off.size() * sizeof(uint32_t),
+                            hipMemcpyHostToDevice, s));
+    CPTC_HIP(hipStreamSynchronize(s));
+    *total_segments = run;
+    return CPTC_OK;
+}
+
+extern "C" int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles,
+                                              const uint32_t* d_cmask, const uint32_t* d_segoff,
+                                              float* d_seg, void* stream)
+{
+    if (ntiles == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_tile_f32 && d_cmask && d_segoff && d_seg && ntiles < (size_t(1) << 31),
+                 CPTC_ERR_ARG, "cptc_dense_tiles_compact3_fill: bad arguments");
+    CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_seg) & 15) == 0, CPTC_ERR_ARG,
+                 "cptc_dense_tiles_compact3_fill: segments must be 16-byte aligned");
+    hipLaunchKernelGGL(compact_tiles_fill_kernel, dim3(unsigned(ntiles)), dim3(256), 0,
+                       cptc::as_stream(stream), d_tile_f32, d_cmask, d_segoff,
+                       reinterpret_cast<float4*>(d_seg));
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles,
+                                            const uint32_t* d_cmask, const uint32_t* d_segoff,
+                                            const float* d_seg, uint64_t nseg, size_t ntiles,
+                                            const uint32_t* d_order, const uint32_t* d_group_off,
+                                            size_t ngroups, const double* d_A, const double* d_B,
+                                            const double* d_C, double* d_FtV, int R, int dimI,
+                                            int dimJ, int dimK, void* d_ws, size_t ws_bytes,
+                                            void* stream)
+{
+    CPTC_REQUIRE(mode >= 0 && mode < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_dense_tiles3_cws: mode %d R %d", mode, R);
+    if (ntiles == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_tiles && d_cmask && d_segoff && d_seg && d_A && d_B && d_C && d_FtV,
+                 CPTC_ERR_ARG, "cptc_mttkrp_dense_tiles3_cws: null pointer");
+    CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_seg) & 15) == 0, CPTC_ERR_ARG,
+                 "cptc_mttkrp_dense_tiles3_cws: segments must be 16-byte aligned");
+    // the kernel's 32-bit buffer offsets (an unoccupied segment reads at 2^32 - 16)
+    CPTC_REQUIRE(nseg * 16u < 0xFFFFFFF0ull, CPTC_ERR_UNSUPPORTED,
+                 "cptc_mttkrp_dense_tiles3_cws: %llu segments exceed 32-bit byte offsets",
+                 (unsigned long long)nseg);
+    CompactImg ci;
+    ci.mask = d_cmask;
+    ci.segoff = d_segoff;
+    ci.seg = reinterpret_cast<const float4*>(d_seg);
+    return launch_slot_b3<4, false>(mode, d_tiles, nullptr, ci, ntiles, d_order, d_group_off,
                                     ngroups, d_A, d_B, d_C, nullptr, d_FtV, R, dimI, dimJ, dimK,
                                     d_ws, ws_bytes, cptc::as_stream(stream));
 }
@@ -363,9 +524,9 @@ extern "C" int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64
     CPTC_REQUIRE(d_unit6 && d_tiles && d_W && d_F0 && d_F1 && d_F2 && d_FtV, CPTC_ERR_ARG,
                  "cptc_mttkrp_units_nd_ws: null pointer");
     return launch_slot_b3<6, true>(slot, reinterpret_cast<const int32_t*>(d_unit6), d_tiles,
-                                   size_t(nunits), d_order, d_group_off, ngroups, d_F0, d_F1, d_F2,
-                                   d_W, d_FtV, R, dim0, dim1, dim2, d_ws, ws_bytes,
-                                   cptc::as_stream(stream));
+                                   CompactImg{}, size_t(nunits), d_order, d_group_off, ngroups,
+                                   d_F0, d_F1, d_F2, d_W, d_FtV, R, dim0, dim1, dim2, d_ws,
+                                   ws_bytes, cptc::as_stream(stream));
 }
 
 extern "C" int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,

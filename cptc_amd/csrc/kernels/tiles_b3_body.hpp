@@ -73,10 +73,18 @@ __device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, u
 // block (16 x Rq doubles, each lane owns its entries) and flushes one atomic
 // per (row, rank) per group.  S waves share one tile / group, wave s taking
 // the 32-rank blocks s, s + S, ...
-template <int MODE, int HDR, bool HAS_W, bool GROUPED>
+//
+// COMPACT: the tile cells come from the compacted image instead of tile_f32:
+// cmask[64 t .. 64 t + 31] = occupancy bits of the tile's 1024 16-byte
+// segments (4 consecutive cells along the image's fastest axis; bit s % 32
+// of word s / 32), cmask[64 t + 32 + w] = set bits in words 0 .. w - 1, and
+// the occupied segments in order at cseg[csegoff[t] ..].
+template <int MODE, int HDR, bool HAS_W, bool GROUPED, bool COMPACT = false>
 __device__ __forceinline__ void dense_tiles_b3_body(
     size_t wg, double* gacc_lds, const int32_t* __restrict__ hdr,
-    const float* __restrict__ tile_f32, size_t ntiles, const uint32_t* __restrict__ order,
+    const float* __restrict__ tile_f32, const uint32_t* __restrict__ cmask,
+    const uint32_t* __restrict__ csegoff, const float4* __restrict__ cseg,
+    size_t ntiles, const uint32_t* __restrict__ order,
     const uint32_t* __restrict__ goff, size_t ngroups, const u32x4* __restrict__ fs_hi,
     const u32x4* __restrict__ fs_lo, const float4* __restrict__ fw,
     const double* __restrict__ W, double* __restrict__ FtV, int R, int Rq, int odim, int S)
@@ -119,7 +127,78 @@ __device__ __forceinline__ void dense_tiles_b3_body(
     // the lane's 64 cells: cells[q][p] = T at (target am, contracted 8 h + q,
     // weight 8 ww + p)
     float cells[8][8];
+    // compacted image: buffer loads over the segments (byte offsets below
+    // 2^32, checked by the launcher); an unoccupied segment's load takes an
+    // offset past the buffer's end, which reads zeros
+    const __amdgpu_buffer_rsrc_t rseg = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float4*>(cseg), short(0), int(0xFFFFFFF0u), 0x00020000);
+    constexpr uint32_t OOB = 0xFFFFFFF0u;
+    // the header of the tile whose cells load next: lane x holds word x of
+    // its 64 (occupancy words 0..31, running counts 32..63), loaded with one
+    // coalesced 256-byte load a tile ahead; the lanes fetch the words they
+    // need from it by lane shuffles
+    uint32_t hdr_w = 0, hdr_so = 0;
+    auto load_hdr = [&](size_t tt) {
+        if constexpr (COMPACT)
+        {
+            hdr_w = cmask[tt * 64 + size_t(lane)];
+            hdr_so = csegoff[tt];
+        }
+    };
+    // byte offset of segment sgi of the header's tile (OOB when unoccupied)
+    auto seg_off = [&](int sgi) -> uint32_t {
+        const int w = sgi >> 5, b = sgi & 31;
+        const uint32_t m = uint32_t(__shfl(int(hdr_w), w));
+        const uint32_t pre = uint32_t(__shfl(int(hdr_w), 32 + w));
+        const uint32_t idx = hdr_so + pre + uint32_t(__builtin_popcount(m & ((1u << b) - 1u)));
+        return ((m >> b) & 1u) ? idx * 16u : OOB;
+    };
     auto load_cells = [&](size_t t) {
+        if constexpr (COMPACT)
+        {
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+            {
+                const int c = 8 * h + q;
+                if constexpr (MODE == 0 || MODE == 1)
+                {
+                    const int base = (MODE == 0) ? (am * 16 + c) * 16 : (c * 16 + am) * 16;
+                    const int s0 = (base + 8 * ww) >> 2;
+                    // (the load's vector indexed directly: a __builtin_bit_cast of it
+                    // to another 4 x 32-bit vector type compiled to a one-dword load)
+                    const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rseg, seg_off(s0), 0, 0);
+                    const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rseg, seg_off(s0 + 1), 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        cells[q][e] = __builtin_bit_cast(float, uint32_t(v0[e]));
+                        cells[q][4 + e] = __builtin_bit_cast(float, uint32_t(v1[e]));
+                    }
+                }
+                else
+                {
+                    // the 8 cells (c, 8 ww + p, am) lie in segments
+                    // (c 16 + 8 ww + p) 4 + am / 4 of one mask word (2 c + ww),
+                    // bits 4 p + am / 4
+                    const int w = 2 * c + ww;
+                    const uint32_t m = uint32_t(__shfl(int(hdr_w), w));
+                    const uint32_t base = (hdr_so + uint32_t(__shfl(int(hdr_w), 32 + w))) * 16u +
+                                          uint32_t(am & 3) * 4u;
+#pragma unroll
+                    for (int p = 0; p < 8; ++p)
+                    {
+                        const int b = 4 * p + (am >> 2);
+                        const uint32_t off =
+                            ((m >> b) & 1u)
+                                ? base + uint32_t(__builtin_popcount(m & ((1u << b) - 1u))) * 16u
+                                : OOB;
+                        cells[q][p] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rseg, off, 0, 0));
+                    }
+                }
+            }
+            return;
+        }
         const float* __restrict__ T = tile_f32 + t * 4096;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -187,8 +266,10 @@ __device__ __forceinline__ void dense_tiles_b3_body(
     size_t it = it0;
     int rb = rb0;
     size_t t = tile_of(it);
+    load_hdr(t);
     load_cells(t);
     split_cells();
+    if (it + 1 < it1) load_hdr(tile_of(it + 1));
     load_ops(t, rb);
     int ob = 0;
     while (true)
@@ -213,11 +294,13 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         }
         const bool more = itn < it1;
         const size_t tn = more ? tile_of(itn) : t;
-        // modes 0 / 1: the next tile's cells load while this rank block
-        // computes (the raw cell registers are free once the current tile is
-        // split; mode 2's 64 scalar loads leave no room for that)
+        // modes 0 / 1 of the dense image: the next tile's cells load while
+        // this rank block computes (the raw cell registers are free once the
+        // current tile is split; mode 2's 64 scalar loads leave no room for
+        // that, and the compacted image prefetches the tile header instead)
         const bool next_tile = more && itn != it;
-        if (MODE != 2 && next_tile) load_cells(tn);
+        constexpr bool PF_CELLS = MODE != 2 && !COMPACT;
+        if (PF_CELLS && next_tile) load_cells(tn);
 
         // Software pipeline over the four w pairs: the products of pair
         // pp + 1 are issued before the FMAs of pair pp consume theirs, so
@@ -290,8 +373,9 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         if (!more) break;
         if (next_tile)
         {
-            if (MODE == 2) load_cells(tn);
+            if (!PF_CELLS) load_cells(tn);
             split_cells();
+            if (itn + 1 < it1) load_hdr(tile_of(itn + 1));
         }
         it = itn;
         rb = rbn;

@@ -180,6 +180,29 @@ int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles, const float* d
                                 int dimI, int dimJ, int dimK, void* d_ws, size_t ws_bytes,
                                 void* stream);
 
+/* Compacted tile image for the split-bf16 kernel: the 1024 16-byte segments
+ * of every tile (4 consecutive cells along the image's last axis) with at
+ * least one nonzero bit, in order, plus per tile 32 occupancy words and 32
+ * running counts.  _mask: d_cmask (ntiles x 64 uint32) and d_segoff
+ * (ntiles + 1 uint32: first segment of each tile, then the total), the total
+ * in *total_segments (host; synchronises the stream).  _fill: the segments
+ * into d_seg (total x 16 bytes, 16-byte aligned).  No reference counterpart
+ * (the reference builds dense tiles per call, dense.cu:150-190). */
+int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles, uint32_t* d_cmask,
+                                   uint32_t* d_segoff, uint64_t* total_segments, void* stream);
+int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles, const uint32_t* d_cmask,
+                                   const uint32_t* d_segoff, float* d_seg, void* stream);
+
+/* cptc_mttkrp_dense_tiles3_ws over the compacted image (nseg segments,
+ * nseg * 16 below 2^32 - 16); the same FP64 contributions per tile. */
+int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles, const uint32_t* d_cmask,
+                                 const uint32_t* d_segoff, const float* d_seg, uint64_t nseg,
+                                 size_t ntiles, const uint32_t* d_order,
+                                 const uint32_t* d_group_off, size_t ngroups, const double* d_A,
+                                 const double* d_B, const double* d_C, double* d_FtV, int R,
+                                 int dimI, int dimJ, int dimK, void* d_ws, size_t ws_bytes,
+                                 void* stream);
+
 /* Tile groups for the grouped MFMA launches (no reference counterpart; the
  * reference issues one atomic per (row, rank, tile)).  hdr: ntiles x
  * hdr_words int32 on the host ({bi, bj, bk, ...}: 4 words for order-3 tiles,
@@ -405,6 +428,7 @@ typedef struct cptc_als3_info {
     int sparse_blocked;       /* 1 = the residual runs over the blocked layout */
     int tile_bf16x3;          /* 1 = dense tiles on the split-bf16 kernel, 0 = FP32 MFMA */
     int tiles_beside;         /* 1 = tile kernel on a side stream beside the FP64 kernel */
+    int tile_compact;         /* 1 = the split-bf16 kernel reads the compacted tile image */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 

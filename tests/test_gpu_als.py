@@ -241,6 +241,7 @@ def test_blocked_sparse_view_matches_oracle(ca, orc, dev, R, path, monkeypatch):
             assert int(h.info.tiles_beside) == int(mf and kern == "fp32")
             assert int(h.info.sparse_blocked) == int(not h.info.tiles_beside)
             if mf and kern == "bf16x3":
+                assert int(h.info.tile_compact) == 1
                 # the driver's MTTKRP with the split-bf16 tiles, against the oracle
                 F = [h.factor(m).ravel() for m in range(3)]
                 for mode in range(3):

@@ -5,6 +5,8 @@ Bars: sparse FP64 MTTKRP <= 1e-10 relative; dense-tile FP32-MFMA MTTKRP
 <= 1e-5 relative to FP64; Gram / pinv / norms / fit FP64 to ~1e-12 (1e-9 for
 the inverse of conditioned systems).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -212,6 +214,79 @@ def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G, kern):
         assert rel_err(out.numpy(), ref) <= 1e-5, (mode, R)
 
 
+@pytest.mark.parametrize("R,G", [(32, 0), (128, 8), (100, 3), (200, 0)])
+def test_dense_tiles_compact_image(ca, orc, dev, R, G):
+    """The compacted tile image (cptc_dense_tiles_compact3_mask / _fill):
+    occupancy words, running counts, segment offsets and packed segments equal
+    a numpy construction from the dense image; the split-bf16 kernel over it
+    (cptc_mttkrp_dense_tiles3_cws) gives the dense-image kernel's results up
+    to the order of the FP64 atomic adds, every mode, grouped and per tile."""
+    rng = np.random.default_rng(90 + R)
+    dims = (40, 45, 37)
+    idx, val = block_tensor(rng, dims, fill=0.15)
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    nt = len(p["tiles"])
+    assert nt >= 4
+    F = [rng.random((d, R)) - 0.3 for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    tiles = to_dev(ca, p["tiles"].astype(np.int32))
+    tf = zeros(ca, (nt * 4096,), np.float32)
+    pools = [to_dev(ca, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]
+    assert ca.lib.cptc_dense_tiles_pack3(*(b.data_ptr() for b in pools), nt, tf.data_ptr(),
+                                         stream(ca)) == 0
+    cm = zeros(ca, (nt * 64,), np.uint32)
+    so = zeros(ca, (nt + 1,), np.uint32)
+    tot = C.c_uint64()
+    assert ca.lib.cptc_dense_tiles_compact3_mask(tf.data_ptr(), nt, cm.data_ptr(), so.data_ptr(),
+                                                 C.byref(tot), stream(ca)) == 0
+    nseg = tot.value
+    seg = zeros(ca, (max(nseg, 1) * 4,), np.float32)
+    assert ca.lib.cptc_dense_tiles_compact3_fill(tf.data_ptr(), nt, cm.data_ptr(), so.data_ptr(),
+                                                 seg.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    img = tf.numpy().reshape(nt, 1024, 4)
+    occ = img.view(np.uint32).any(axis=2)                     # (nt, 1024)
+    bits = occ.reshape(nt, 32, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)
+    words = bits.sum(axis=2).astype(np.uint32)
+    run = np.concatenate([np.zeros((nt, 1), np.uint32),
+                          np.cumsum(occ.reshape(nt, 32, 32).sum(axis=2), axis=1)[:, :-1]],
+                         axis=1).astype(np.uint32)
+    got_m = cm.numpy().reshape(nt, 64)
+    assert np.array_equal(got_m[:, :32], words) and np.array_equal(got_m[:, 32:], run)
+    cnt = occ.sum(axis=1)
+    assert nseg == int(cnt.sum()) and 0 < nseg < nt * 1024
+    assert np.array_equal(so.numpy(), np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32))
+    assert np.array_equal(seg.numpy()[:nseg * 4].reshape(nseg, 4), img[occ])
+    nb = ca.lib.cptc_tile_operands_bytes(max(dims), R)
+    ws = zeros(ca, (nb,), np.uint8)
+    for mode in range(3):
+        grp = (None, None, 0)
+        if G:
+            go, gf, ng = tile_groups(ca, p["tiles"], 4, mode, G)
+            grp = (go.data_ptr(), gf.data_ptr(), ng)
+        outs = []
+        for compact in (False, True):
+            out = zeros(ca, (dims[mode], R))
+            if compact:
+                rc = ca.lib.cptc_mttkrp_dense_tiles3_cws(
+                    mode, tiles.data_ptr(), cm.data_ptr(), so.data_ptr(), seg.data_ptr(), nseg,
+                    nt, *grp, dF[0].data_ptr(), dF[1].data_ptr(), dF[2].data_ptr(),
+                    out.data_ptr(), R, *dims, ws.data_ptr(), nb, stream(ca))
+            else:
+                rc = ca.lib.cptc_mttkrp_dense_tiles3_ws(
+                    mode, tiles.data_ptr(), tf.data_ptr(), nt, *grp, dF[0].data_ptr(),
+                    dF[1].data_ptr(), dF[2].data_ptr(), out.data_ptr(), R, *dims, ws.data_ptr(),
+                    nb, stream(ca))
+            assert rc == 0, ca.lib.cptc_last_error()
+            ca.sync()
+            outs.append(out.numpy())
+        ref = orc.mttkrp3_tiles(p, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                                dims).reshape(dims[mode], R)
+        assert rel_err(outs[1], ref) <= 1e-5, (mode, R)
+        # the same FP64 contributions; only the order of the atomic adds differs
+        assert rel_err(outs[1], outs[0]) <= 1e-14, (mode, R)
+
+
 def test_dense_tiles_bf16x3_split_error(ca, orc, dev):
     """The split-bf16 kernel's error is that of ~16-bit inputs (each operand
     kept to ~2^-17 by its two bf16 terms): inside the 1e-5 bar with
@@ -281,7 +356,7 @@ def test_gram(ca, dev, rows, R):
     assert rel_err(G.numpy(), F.T @ F) < 1e-13 if rows else np.all(G.numpy() == 0)
 
 
-@pytest.mark.parametrize("R", [1, 5, 16, 17, 32, 33, 63, 64, 65, 128])
+@pytest.mark.parametrize("R", [1, 5, 16, 17, 32, 33, 63, 64, 65, 100, 128, 129, 200])
 def test_solve_pinv_spd(ca, dev, R):
     rng = np.random.default_rng(R)
     Fa, Fb = rng.random((3 * R + 20, R)), rng.random((2 * R + 30, R))
