@@ -529,6 +529,35 @@ extern "C" int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64
                                    ws_bytes, cptc::as_stream(stream));
 }
 
+extern "C" int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                                        const uint32_t* d_cmask, const uint32_t* d_segoff,
+                                        const float* d_seg, uint64_t nseg, const double* d_W,
+                                        const uint32_t* d_order, const uint32_t* d_group_off,
+                                        size_t ngroups, const double* d_F0, const double* d_F1,
+                                        const double* d_F2, int dim0, int dim1, int dim2,
+                                        double* d_FtV, int R, void* d_ws, size_t ws_bytes,
+                                        void* stream)
+{
+    CPTC_REQUIRE(slot >= 0 && slot < 3 && R >= 1, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd_cws: slot %d R %d", slot, R);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_cmask && d_segoff && d_seg && d_W && d_F0 && d_F1 && d_F2 && d_FtV,
+                 CPTC_ERR_ARG, "cptc_mttkrp_units_nd_cws: null pointer");
+    CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_seg) & 15) == 0, CPTC_ERR_ARG,
+                 "cptc_mttkrp_units_nd_cws: segments must be 16-byte aligned");
+    CPTC_REQUIRE(nseg * 16u < 0xFFFFFFF0ull, CPTC_ERR_UNSUPPORTED,
+                 "cptc_mttkrp_units_nd_cws: %llu segments exceed 32-bit byte offsets",
+                 (unsigned long long)nseg);
+    CompactImg ci;
+    ci.mask = d_cmask;
+    ci.segoff = d_segoff;
+    ci.seg = reinterpret_cast<const float4*>(d_seg);
+    return launch_slot_b3<6, true>(slot, reinterpret_cast<const int32_t*>(d_unit6), nullptr, ci,
+                                   size_t(nunits), d_order, d_group_off, ngroups, d_F0, d_F1, d_F2,
+                                   d_W, d_FtV, R, dim0, dim1, dim2, d_ws, ws_bytes,
+                                   cptc::as_stream(stream));
+}
+
 extern "C" int cptc_mttkrp_units_nd(int slot, const uint32_t* d_unit6, uint64_t nunits,
                                     const float* d_tiles, const double* d_W,
                                     const uint32_t* d_order, const uint32_t* d_group_off,

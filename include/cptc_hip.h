@@ -596,6 +596,15 @@ int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64_t nunits,
                             const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
                             double* d_FtV, int R, void* d_ws, size_t ws_bytes, void* stream);
 
+/* cptc_mttkrp_units_nd_ws over the units' compacted image
+ * (cptc_dense_tiles_compact3_mask / _fill over the unit tiles). */
+int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint64_t nunits,
+                             const uint32_t* d_cmask, const uint32_t* d_segoff, const float* d_seg,
+                             uint64_t nseg, const double* d_W, const uint32_t* d_order,
+                             const uint32_t* d_group_off, size_t ngroups, const double* d_F0,
+                             const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
+                             double* d_FtV, int R, void* d_ws, size_t ws_bytes, void* stream);
+
 /* out = prod_{g != skip} G_g over `ngram` consecutive R x R Grams (all ones
  * when none remain): g_fill_kernel + g_mul_kernel, generic.cu:2044-2052. */
 int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double* d_out,

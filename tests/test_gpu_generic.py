@@ -351,7 +351,7 @@ def test_seg_keys_leaf_lds(ca, dev, N, R, dims, rev):
     assert rel_err(outs[1], outs[0]) <= 1e-13
 
 
-@pytest.mark.parametrize("kern", ["fp32", "bf16x3"])
+@pytest.mark.parametrize("kern", ["fp32", "bf16x3", "bf16x3c"])
 @pytest.mark.parametrize("N,R,inner,G", [(4, 8, (0, 1, 2), 0), (4, 16, (0, 1, 2), 4),
                                          (5, 32, (0, 1, 2), 16), (4, 20, (1, 2, 3), 0),
                                          (4, 8, (0, 2, 3), 2), (5, 16, (1, 3, 4), 16),
@@ -411,7 +411,25 @@ def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G, kern):
         else:
             nb = ca.lib.cptc_tile_operands_bytes(max(dims[m] for m in inner), R)
             ws = ca.DevBuf.zeros((nb,), np.uint8)
-            rc = ca.lib.cptc_mttkrp_units_nd_ws(*args, ws.data_ptr(), nb, None)
+            if kern == "bf16x3":
+                rc = ca.lib.cptc_mttkrp_units_nd_ws(*args, ws.data_ptr(), nb, None)
+            else:
+                # the compacted unit image (the order-3 tiles' format)
+                cm = ca.DevBuf.zeros((nu * 64,), np.uint32)
+                so = ca.DevBuf.zeros((nu + 1,), np.uint32)
+                tot = C.c_uint64()
+                assert ca.lib.cptc_dense_tiles_compact3_mask(tiles.data_ptr(), nu, cm.data_ptr(),
+                                                             so.data_ptr(), C.byref(tot),
+                                                             None) == 0
+                sg = ca.DevBuf.zeros((max(tot.value, 1) * 4,), np.float32)
+                assert ca.lib.cptc_dense_tiles_compact3_fill(tiles.data_ptr(), nu, cm.data_ptr(),
+                                                             so.data_ptr(), sg.data_ptr(),
+                                                             None) == 0
+                rc = ca.lib.cptc_mttkrp_units_nd_cws(
+                    slot, d6.data_ptr(), nu, cm.data_ptr(), so.data_ptr(), sg.data_ptr(),
+                    tot.value, W.data_ptr(), *grp, dF[inner[0]].data_ptr(),
+                    dF[inner[1]].data_ptr(), dF[inner[2]].data_ptr(), dims[inner[0]],
+                    dims[inner[1]], dims[inner[2]], out.data_ptr(), R, ws.data_ptr(), nb, None)
         assert rc == 0, ca.lib.cptc_last_error()
         ca.sync()
         ref = orc.mttkrp_units_nd(idx, val, dims, u, n, [f.ravel() for f in F], R)
