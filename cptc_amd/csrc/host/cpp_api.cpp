@@ -23,6 +23,7 @@
 #include "cptc_hip.h"
 #include "dense.hpp"
 #include "generic.hpp"
+#include "host_util.hpp"
 #include "layout.hpp"
 #include "partition.hpp"
 #include "sgd.hpp"
@@ -320,6 +321,9 @@ void free_hybrid_tensor(HybridCOOTensor& hybrid)
     dfree(hybrid.d_tiles4);
     dfree(hybrid.d_pool_off);
     dfree(hybrid.d_tile_f32);
+    dfree(hybrid.d_tile_cmask);
+    dfree(hybrid.d_tile_segoff);
+    dfree(hybrid.d_tile_cseg);
     hybrid = HybridCOOTensor{};
 }
 
@@ -412,6 +416,39 @@ void compute_dense_mttkrp_async(const HybridCOOTensor& hybrid, int mode, double*
     (void)d_FtF;
     if (hybrid.num_dense_tiles <= 0) return;
     const float* t = tiles_f32(hybrid, stream);
+    const size_t nt = size_t(hybrid.num_dense_tiles);
+    const int sw = cptc::tile_kernel_switch("ALS_TILE_KERNEL");
+    if (sw < 0 ? cptc::tile_b3_auto(nt, R) : sw == 1)
+    {
+        // the split-bf16 kernel over the compacted image (built once per
+        // tensor); its operand workspace is per call and stream-ordered, so
+        // calls on different streams do not share it
+        if (!hybrid.d_tile_cseg)
+        {
+            hybrid.d_tile_cmask = dalloc<uint32_t>(nt * 64);
+            hybrid.d_tile_segoff = dalloc<uint32_t>(nt + 1);
+            API_TRY("dense tile compaction",
+                    cptc_dense_tiles_compact3_mask(t, nt, hybrid.d_tile_cmask,
+                                                   hybrid.d_tile_segoff, &hybrid.tile_nseg,
+                                                   stream));
+            hybrid.d_tile_cseg = dalloc<float>(std::max<uint64_t>(hybrid.tile_nseg, 1) * 4);
+            API_TRY("dense tile compaction",
+                    cptc_dense_tiles_compact3_fill(t, nt, hybrid.d_tile_cmask,
+                                                   hybrid.d_tile_segoff, hybrid.d_tile_cseg,
+                                                   stream));
+        }
+        const uint64_t md = uint64_t(std::max({hybrid.dims[0], hybrid.dims[1], hybrid.dims[2]}));
+        const size_t wsb = cptc_tile_operands_bytes(md, R);
+        void* ws = nullptr;
+        CHECK_HIP(hipMallocAsync(&ws, wsb, stream));
+        const int rc = cptc_mttkrp_dense_tiles3_cws(
+            mode, hybrid.d_tiles4, hybrid.d_tile_cmask, hybrid.d_tile_segoff, hybrid.d_tile_cseg,
+            hybrid.tile_nseg, nt, nullptr, nullptr, 0, d_A, d_B, d_C, d_FtV, R,
+            int(hybrid.dims[0]), int(hybrid.dims[1]), int(hybrid.dims[2]), ws, wsb, stream);
+        CHECK_HIP(hipFreeAsync(ws, stream));
+        API_TRY("compute_dense_mttkrp_async", rc);
+        return;
+    }
     API_TRY("compute_dense_mttkrp_async",
             cptc_mttkrp_dense_tiles3(mode, hybrid.d_tiles4, t, size_t(hybrid.num_dense_tiles),
                                      nullptr, nullptr, 0, d_A,

@@ -8,7 +8,9 @@
 #include "tensor.hpp"
 
 // dense.cu:2072-2246: every dense tile of `hybrid` for `mode` on `stream`.
-// The FP32 tile images are built from the pools on first use.
+// The FP32 tile images (and, for the split-bf16 kernel the drivers' rule
+// picks — R > 16 and enough tiles, ALS_TILE_KERNEL to force — the compacted
+// image) are built from the pools on first use.
 void compute_dense_mttkrp_async(const HybridCOOTensor& hybrid, int mode, double* d_A,
                                 double* d_B, double* d_C, double* d_FtV, double* d_FtF, int R,
                                 hipStream_t stream);
