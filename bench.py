@@ -213,7 +213,8 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     tile_ms_acc = h.tile_times()
     sp_ms, mt_ms, kit = h.kernel_times(reset=True)
-    assert kit == args.steps
+    # a queued run records kernel events on every 8th iteration and its last
+    assert kit == sum(1 for it in range(args.steps) if it % 8 == 0 or it == args.steps - 1)
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter (host wall), event median "
         f"{float(np.median(ms_iter)):.3f} ms, MTTKRP median {float(np.median(ms_mtt)):.3f} ms, "
         f"fit {fits[-1]:.6f}")

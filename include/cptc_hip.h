@@ -445,6 +445,8 @@ int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter, float* m
  * kernel of mode m (of the merged tiles + residual kernel when the fused
  * path is active), out6[3 + m] = ms of all MTTKRP launches of mode m;
  * *iters = iterations accumulated.  reset != 0 zeroes the sums after reading.
+ * A queued (quiet) run times every 8th iteration and its last one; a verbose
+ * run times every iteration.
  * No reference counterpart (measurement plumbing; ALS_PROFILE's
  * per-phase events, als.cu:642-651, are the closest). */
 int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset);

@@ -184,7 +184,7 @@ def test_fused_path_matches_oracle(ca, orc, dev, R, monkeypatch):
             assert rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R)) <= 1e-5, mode
         fit, ms, mt = h.run(20)
         sp, _, kit = h.kernel_times()
-        assert kit == 20 and np.all(sp > 0)
+        assert kit == 4 and np.all(sp > 0)   # a queued run times iterations 0, 8, 16 and 19
     o = orc.Als3(v, None, p, float(np.sum(t.val ** 2)), t.dims, R, *F, None)
     ofit, _, _ = o.iterate(20)
     assert np.max(np.abs(fit - ofit)) <= 1e-4, (fit[-3:], ofit[-3:])
