@@ -145,8 +145,8 @@ SIGNATURES = {
     "cptc_tile_operands_bytes": (_Z, [C.c_uint64, _I]),
     "cptc_mttkrp_dense_tiles3_ws": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _I, _I, _I,
                                          _I, _P, _Z, _P]),
-    "cptc_dense_tiles_compact3_mask": (_I, [_P, _Z, _P, _P, C.POINTER(C.c_uint64), _P]),
-    "cptc_dense_tiles_compact3_fill": (_I, [_P, _Z, _P, _P, _P, _P]),
+    "cptc_dense_tiles_compact3_mask": (_I, [_P, _Z, _I, _P, _P, C.POINTER(C.c_uint64), _P]),
+    "cptc_dense_tiles_compact3_fill": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
     "cptc_mttkrp_dense_tiles3_cws": (_I, [_I, _P, _P, _P, _P, C.c_uint64, _Z, _P, _P, _Z, _P, _P,
                                           _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "cptc_dense_groups": (_I, [_P, _I, _Z, _I, _I, _P, _P, C.POINTER(_Z)]),

@@ -31,6 +31,7 @@
 #include "hip_util.hpp"
 #include "host_util.hpp"
 #include "layout.hpp"
+#include "split_img.hpp"
 
 namespace cptc {
 
@@ -66,10 +67,7 @@ struct Als3
     void* d_tile_ws = nullptr;
     size_t tile_ws_bytes = 0;
     // compacted tile image of the split-bf16 kernel (ALS_TILE_COMPACT=0: dense)
-    uint32_t* d_cmask = nullptr;
-    uint32_t* d_segoff = nullptr;
-    float* d_cseg = nullptr;
-    uint64_t nseg = 0;
+    SplitImg timg[3];   // compacted split tile image per target mode
     // per-mode tile groups (one target row block each) for the grouped MFMA launch
     uint32_t* d_order[3] = {nullptr, nullptr, nullptr};
     uint32_t* d_goff[3] = {nullptr, nullptr, nullptr};
@@ -153,9 +151,10 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
         hipStream_t ds = dense_side ? h.s_dense : h.s;
         if (dense_side) CPTC_HIP(hipStreamWaitEvent(ds, h.e_fork, 0));
         if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[6 + 2 * mode], ds));
-        if (h.tile_b3 && h.d_cseg)
+        if (h.tile_b3 && h.timg[mode].ready())
             CPTC_TRY(cptc_mttkrp_dense_tiles3_cws(
-                mode, h.part.d_tiles4, h.d_cmask, h.d_segoff, h.d_cseg, h.nseg,
+                mode, h.part.d_tiles4, h.timg[mode].cmask, h.timg[mode].segoff,
+                h.timg[mode].seg, h.timg[mode].nseg,
                 size_t(h.part.ntiles), h.d_order[mode], h.d_goff[mode], h.ngroups[mode], A, B, C,
                 h.d_FtV, R, int(h.dims[0]), int(h.dims[1]), int(h.dims[2]), h.d_tile_ws,
                 h.tile_ws_bytes, ds));
@@ -315,8 +314,7 @@ void destroy(Als3* h)
     for (int m = 0; m < 3; ++m)
         for (void* p : {(void*)h->d_order[m], (void*)h->d_goff[m]})
             if (p) (void)hipFree(p);
-    for (void* p : {(void*)h->d_cmask, (void*)h->d_segoff, (void*)h->d_cseg})
-        if (p) (void)hipFree(p);
+    for (SplitImg& g : h->timg) free_split_img(g);
     for (void* p : {(void*)h->d_tile_f32, (void*)h->d_tile_ws, (void*)h->d_F, (void*)h->d_lambda, (void*)h->d_G,
                     (void*)h->d_FtF, (void*)h->d_Ainv, (void*)h->d_FtV, (void*)h->d_norms,
                     (void*)h->d_scal, (void*)h->d_fit_hist})
@@ -529,23 +527,13 @@ int alloc_buffers(Als3& hr)
     {
         h->tile_ws_bytes = cptc_tile_operands_bytes(maxdim, R);
         CPTC_HIP(hipMalloc(&h->d_tile_ws, h->tile_ws_bytes));
-        // compacted image: the dense image's 16-byte segments with a nonzero
-        // bit (config 3: 39 % of them), read instead of the dense image
+        // compacted split images, one per target mode: the kernel's A operand
+        // halves of every 8-cell segment with a nonzero bit, read instead of
+        // splitting the dense image on every launch
         const char* e = std::getenv("ALS_TILE_COMPACT");
         if (!(e && std::strcmp(e, "0") == 0) && h->d_tile_f32)
-        {
-            const size_t nt = size_t(h->part.ntiles);
-            CPTC_HIP(hipMalloc(&h->d_cmask, nt * 64 * sizeof(uint32_t)));
-            CPTC_HIP(hipMalloc(&h->d_segoff, (nt + 1) * sizeof(uint32_t)));
-            CPTC_TRY(cptc_dense_tiles_compact3_mask(h->d_tile_f32, nt, h->d_cmask, h->d_segoff,
-                                                    &h->nseg, h->s));
-            if (h->nseg * 16u < 0xFFFFFFF0ull)
-            {
-                CPTC_HIP(hipMalloc(&h->d_cseg, std::max<uint64_t>(h->nseg, 1) * 16));
-                CPTC_TRY(cptc_dense_tiles_compact3_fill(h->d_tile_f32, nt, h->d_cmask,
-                                                        h->d_segoff, h->d_cseg, h->s));
-            }
-        }
+            for (int m = 0; m < 3; ++m)
+                CPTC_TRY(build_split_img(h->d_tile_f32, size_t(h->part.ntiles), m, h->timg[m], h->s));
     }
     CPTC_HIP(hipMalloc(&h->d_lambda, size_t(R) * sizeof(double)));
     CPTC_HIP(hipMalloc(&h->d_G, 3 * RR * sizeof(double)));
@@ -905,7 +893,8 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->fused = h->fused ? 1 : 0;
     info->sparse_blocked = h->blk.ready ? 1 : 0;
     info->tile_bf16x3 = h->tile_b3 ? 1 : 0;
-    info->tile_compact = (h->tile_b3 && h->d_cseg) ? 1 : 0;
+    info->tile_compact =
+        (h->tile_b3 && h->timg[0].ready() && h->timg[1].ready() && h->timg[2].ready()) ? 1 : 0;
     info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }

@@ -321,9 +321,13 @@ void free_hybrid_tensor(HybridCOOTensor& hybrid)
     dfree(hybrid.d_tiles4);
     dfree(hybrid.d_pool_off);
     dfree(hybrid.d_tile_f32);
-    dfree(hybrid.d_tile_cmask);
-    dfree(hybrid.d_tile_segoff);
-    dfree(hybrid.d_tile_cseg);
+    for (int m = 0; m < 3; ++m)
+    {
+        dfree(hybrid.d_tile_cmask[m]);
+        dfree(hybrid.d_tile_segoff[m]);
+        dfree(hybrid.d_tile_cseg[m]);
+        hybrid.tile_nseg[m] = 0;
+    }
     hybrid = HybridCOOTensor{};
 }
 
@@ -420,31 +424,43 @@ void compute_dense_mttkrp_async(const HybridCOOTensor& hybrid, int mode, double*
     const int sw = cptc::tile_kernel_switch("ALS_TILE_KERNEL");
     if (sw < 0 ? cptc::tile_b3_auto(nt, R) : sw == 1)
     {
-        // the split-bf16 kernel over the compacted image (built once per
-        // tensor); its operand workspace is per call and stream-ordered, so
-        // calls on different streams do not share it
-        if (!hybrid.d_tile_cseg)
+        // the split-bf16 kernel over the mode's compacted split image (built
+        // once per tensor and mode; the dense image when the compacted one
+        // exceeds the kernel's 32-bit offsets); its operand workspace is per
+        // call and stream-ordered, so calls on different streams do not share it
+        if (!hybrid.d_tile_cmask[mode])
         {
-            hybrid.d_tile_cmask = dalloc<uint32_t>(nt * 64);
-            hybrid.d_tile_segoff = dalloc<uint32_t>(nt + 1);
+            hybrid.d_tile_cmask[mode] = dalloc<uint32_t>(nt * 64);
+            hybrid.d_tile_segoff[mode] = dalloc<uint32_t>(nt + 1);
             API_TRY("dense tile compaction",
-                    cptc_dense_tiles_compact3_mask(t, nt, hybrid.d_tile_cmask,
-                                                   hybrid.d_tile_segoff, &hybrid.tile_nseg,
-                                                   stream));
-            hybrid.d_tile_cseg = dalloc<float>(std::max<uint64_t>(hybrid.tile_nseg, 1) * 4);
-            API_TRY("dense tile compaction",
-                    cptc_dense_tiles_compact3_fill(t, nt, hybrid.d_tile_cmask,
-                                                   hybrid.d_tile_segoff, hybrid.d_tile_cseg,
-                                                   stream));
+                    cptc_dense_tiles_compact3_mask(t, nt, mode, hybrid.d_tile_cmask[mode],
+                                                   hybrid.d_tile_segoff[mode],
+                                                   &hybrid.tile_nseg[mode], stream));
+            if (hybrid.tile_nseg[mode] * 16u < 0xFFFFFFF0ull)
+            {
+                hybrid.d_tile_cseg[mode] =
+                    dalloc<uint32_t>(std::max<uint64_t>(hybrid.tile_nseg[mode], 1) * 4);
+                API_TRY("dense tile compaction",
+                        cptc_dense_tiles_compact3_fill(t, nt, mode, hybrid.d_tile_cmask[mode],
+                                                       hybrid.d_tile_segoff[mode],
+                                                       hybrid.d_tile_cseg[mode], stream));
+            }
         }
         const uint64_t md = uint64_t(std::max({hybrid.dims[0], hybrid.dims[1], hybrid.dims[2]}));
         const size_t wsb = cptc_tile_operands_bytes(md, R);
         void* ws = nullptr;
         CHECK_HIP(hipMallocAsync(&ws, wsb, stream));
-        const int rc = cptc_mttkrp_dense_tiles3_cws(
-            mode, hybrid.d_tiles4, hybrid.d_tile_cmask, hybrid.d_tile_segoff, hybrid.d_tile_cseg,
-            hybrid.tile_nseg, nt, nullptr, nullptr, 0, d_A, d_B, d_C, d_FtV, R,
-            int(hybrid.dims[0]), int(hybrid.dims[1]), int(hybrid.dims[2]), ws, wsb, stream);
+        const int rc =
+            hybrid.d_tile_cseg[mode]
+                ? cptc_mttkrp_dense_tiles3_cws(
+                      mode, hybrid.d_tiles4, hybrid.d_tile_cmask[mode], hybrid.d_tile_segoff[mode],
+                      hybrid.d_tile_cseg[mode], hybrid.tile_nseg[mode], nt, nullptr, nullptr, 0,
+                      d_A, d_B, d_C, d_FtV, R, int(hybrid.dims[0]), int(hybrid.dims[1]),
+                      int(hybrid.dims[2]), ws, wsb, stream)
+                : cptc_mttkrp_dense_tiles3_ws(mode, hybrid.d_tiles4, t, nt, nullptr, nullptr, 0,
+                                              d_A, d_B, d_C, d_FtV, R, int(hybrid.dims[0]),
+                                              int(hybrid.dims[1]), int(hybrid.dims[2]), ws, wsb,
+                                              stream);
         CHECK_HIP(hipFreeAsync(ws, stream));
         API_TRY("compute_dense_mttkrp_async", rc);
         return;

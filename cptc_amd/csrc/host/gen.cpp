@@ -23,6 +23,7 @@
 #include "hip_util.hpp"
 #include "host_util.hpp"
 #include "layout_nd.hpp"
+#include "split_img.hpp"
 
 namespace {
 
@@ -345,10 +346,7 @@ struct Gen
     void* d_tile_ws = nullptr;
     size_t tile_ws_bytes = 0;
     // compacted unit image (GEN_TILE_COMPACT=0: the dense one)
-    uint32_t* d_cmask = nullptr;
-    uint32_t* d_segoff = nullptr;
-    float* d_cseg = nullptr;
-    uint64_t nseg = 0;
+    cptc::SplitImg uimg[3];   // compacted split unit image per inner slot
     // per-slot unit groups (one target row block each) for the grouped MFMA launch
     uint32_t* d_uorder[3] = {nullptr, nullptr, nullptr};
     uint32_t* d_ugoff[3] = {nullptr, nullptr, nullptr};
@@ -387,9 +385,7 @@ struct Gen
         dfree(d_out2);
         dfree(d_tiles);
         dfree(d_tile_ws);
-        dfree(d_cmask);
-        dfree(d_segoff);
-        dfree(d_cseg);
+        for (cptc::SplitImg& u : uimg) cptc::free_split_img(u);
         dfree(d_W);
         for (int q = 0; q < 3; ++q)
         {
@@ -435,9 +431,10 @@ struct Gen
             }
             const int* in3 = units.inner;
             const int sl = slot_of(n);
-            if (tile_b3 && d_cseg)
+            if (tile_b3 && uimg[sl].ready())
                 CPTC_TRY(cptc_mttkrp_units_nd_cws(
-                    sl, units.d_unit6, units.nunits, d_cmask, d_segoff, d_cseg, nseg, d_W,
+                    sl, units.d_unit6, units.nunits, uimg[sl].cmask, uimg[sl].segoff,
+                    uimg[sl].seg, uimg[sl].nseg, d_W,
                     d_uorder[sl], d_ugoff[sl], ungroups[sl], d_F[in3[0]], d_F[in3[1]],
                     d_F[in3[2]], int(dims[in3[0]]), int(dims[in3[1]]), int(dims[in3[2]]), d_FtV, R,
                     d_tile_ws, tile_ws_bytes, s));
@@ -893,22 +890,12 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
                 const uint64_t md = std::max({g->dims[in[0]], g->dims[in[1]], g->dims[in[2]]});
                 g->tile_ws_bytes = cptc_tile_operands_bytes(md, R);
                 GEN_HIP(hipMalloc(&g->d_tile_ws, g->tile_ws_bytes));
-                // compacted unit image (the order-3 tiles' format)
+                // compacted split unit images, one per inner slot (the order-3
+                // tiles' format)
                 const char* ce = std::getenv("GEN_TILE_COMPACT");
                 if (!(ce && std::strcmp(ce, "0") == 0))
-                {
-                    const size_t nu = g->units.nunits;
-                    GEN_HIP(hipMalloc(&g->d_cmask, nu * 64 * sizeof(uint32_t)));
-                    GEN_HIP(hipMalloc(&g->d_segoff, (nu + 1) * sizeof(uint32_t)));
-                    GEN_TRY(cptc_dense_tiles_compact3_mask(g->d_tiles, nu, g->d_cmask,
-                                                           g->d_segoff, &g->nseg, s));
-                    if (g->nseg * 16u < 0xFFFFFFF0ull)
-                    {
-                        GEN_HIP(hipMalloc(&g->d_cseg, std::max<uint64_t>(g->nseg, 1) * 16));
-                        GEN_TRY(cptc_dense_tiles_compact3_fill(g->d_tiles, nu, g->d_cmask,
-                                                               g->d_segoff, g->d_cseg, s));
-                    }
-                }
+                    for (int sl = 0; sl < 3; ++sl)
+                        GEN_TRY(cptc::build_split_img(g->d_tiles, g->units.nunits, sl, g->uimg[sl], s));
             }
         }
         g->prep_ms[1] = ms_since(t0);

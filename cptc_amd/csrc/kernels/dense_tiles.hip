@@ -58,7 +58,7 @@ template <int MODE, int HDR, bool HAS_W, bool GROUPED, bool COMPACT>
 __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_b3_kernel(
     const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32,
     const uint32_t* __restrict__ cmask, const uint32_t* __restrict__ csegoff,
-    const float4* __restrict__ cseg, size_t ntiles, const uint32_t* __restrict__ order,
+    const cptc_k::u32x4* __restrict__ cseg, size_t ntiles, const uint32_t* __restrict__ order,
     const uint32_t* __restrict__ goff, size_t ngroups, const cptc_k::u32x4* __restrict__ fs_hi,
     const cptc_k::u32x4* __restrict__ fs_lo, const float4* __restrict__ fw,
     const double* __restrict__ W, double* __restrict__ FtV, int R, int Rq, int odim, int S)
@@ -69,10 +69,27 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
         fs_hi, fs_lo, fw, W, FtV, R, Rq, odim, S);
 }
 
-// Compacted tile image, pass 1: per tile the occupancy bits of its 1024
-// 16-byte segments (any nonzero bit in the segment's 4 cells) and the
-// running counts before each 32-bit mask word; counts[t] = occupied segments.
-__global__ __launch_bounds__(256) void compact_tiles_mask_kernel(const float* __restrict__ tiles,
+// Compacted split image of one target slot, the split-bf16 kernel's A
+// operand: tile cell (a, w, c) (target, weight and contracted coordinate of
+// the slot) is image cell (a, c, w) for slot 0, (c, a, w) for slot 1 and
+// (c, w, a) for slot 2 (the image is [i][j][k], k fastest).  Segment
+// s = a * 64 + w * 4 + e holds the cells c = 4e .. 4e + 3 as 4 bf16 hi
+// halves then their 4 bf16 lo halves (16 bytes; the kernel's split of each
+// value, so the products are the same bits); it is occupied when any of its
+// 4 FP32 cells has a nonzero bit.  cmask[64 t + x], x < 32: occupancy bits
+// of segments 32x .. 32x + 31; cmask[64 t + 32 + x]: occupied segments
+// before word x; the occupied segments in order at seg[segoff[t] ..].
+template <int SLOT>
+__device__ __forceinline__ int slot_cell(int a, int w, int c)
+{
+    if constexpr (SLOT == 0) return (a * 16 + c) * 16 + w;
+    if constexpr (SLOT == 1) return (c * 16 + a) * 16 + w;
+    return (c * 16 + w) * 16 + a;
+}
+
+// pass 1: the occupancy words and running counts; counts[t] = occupied segments
+template <int SLOT>
+__global__ __launch_bounds__(256) void compact_split_mask_kernel(const float* __restrict__ tiles,
                                                                  uint32_t* __restrict__ cmask,
                                                                  uint32_t* __restrict__ counts)
 {
@@ -80,42 +97,57 @@ __global__ __launch_bounds__(256) void compact_tiles_mask_kernel(const float* __
     const size_t t = blockIdx.x;
     if (threadIdx.x < 32) wmask[threadIdx.x] = 0u;
     __syncthreads();
-    const uint4* __restrict__ src = reinterpret_cast<const uint4*>(tiles + t * 4096);
+    const uint32_t* __restrict__ src = reinterpret_cast<const uint32_t*>(tiles + t * 4096);
     for (int sg = threadIdx.x; sg < 1024; sg += 256)
     {
-        const uint4 v = src[sg];
-        if ((v.x | v.y | v.z | v.w) != 0u) atomicOr(&wmask[sg >> 5], 1u << (sg & 31));
+        const int a = sg >> 6, w = (sg >> 2) & 15, e = sg & 3;
+        uint32_t any = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) any |= src[slot_cell<SLOT>(a, w, 4 * e + q)];
+        if (any != 0u) atomicOr(&wmask[sg >> 5], 1u << (sg & 31));
     }
     __syncthreads();
     if (threadIdx.x == 0)
     {
         uint32_t run = 0;
-        for (int w = 0; w < 32; ++w)
+        for (int x = 0; x < 32; ++x)
         {
-            cmask[t * 64 + w] = wmask[w];
-            cmask[t * 64 + 32 + w] = run;
-            run += uint32_t(__builtin_popcount(wmask[w]));
+            cmask[t * 64 + x] = wmask[x];
+            cmask[t * 64 + 32 + x] = run;
+            run += uint32_t(__builtin_popcount(wmask[x]));
         }
         counts[t] = run;
     }
 }
 
-// Pass 2: the occupied segments of tile t, in segment order, at segoff[t].
-__global__ __launch_bounds__(256) void compact_tiles_fill_kernel(const float* __restrict__ tiles,
+// pass 2: the occupied segments of tile t, split, in segment order at segoff[t]
+template <int SLOT>
+__global__ __launch_bounds__(256) void compact_split_fill_kernel(const float* __restrict__ tiles,
                                                                  const uint32_t* __restrict__ cmask,
                                                                  const uint32_t* __restrict__ segoff,
-                                                                 float4* __restrict__ cseg)
+                                                                 uint4* __restrict__ seg)
 {
     const size_t t = blockIdx.x;
-    const float4* __restrict__ src = reinterpret_cast<const float4*>(tiles + t * 4096);
+    const float* __restrict__ src = tiles + t * 4096;
     const uint32_t* __restrict__ mp = cmask + t * 64;
     for (int sg = threadIdx.x; sg < 1024; sg += 256)
     {
-        const int w = sg >> 5, b = sg & 31;
-        const uint32_t m = mp[w];
-        if ((m >> b) & 1u)
-            cseg[size_t(segoff[t]) + mp[32 + w] + uint32_t(__builtin_popcount(m & ((1u << b) - 1u)))] =
-                src[sg];
+        const int a = sg >> 6, w = (sg >> 2) & 15, e = sg & 3;
+        const int x = sg >> 5, b = sg & 31;
+        const uint32_t m = mp[x];
+        if (!((m >> b) & 1u)) continue;
+        uint32_t hv[2], lv[2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+        {
+            const float x0 = src[slot_cell<SLOT>(a, w, 4 * e + 2 * d)];
+            const float x1 = src[slot_cell<SLOT>(a, w, 4 * e + 2 * d + 1)];
+            cptc_k::split_bf16x2(x0, x1, hv[d], lv[d],
+                                 __builtin_amdgcn_fmed3f(x0, -cptc_k::BF16_MAX, cptc_k::BF16_MAX),
+                                 __builtin_amdgcn_fmed3f(x1, -cptc_k::BF16_MAX, cptc_k::BF16_MAX));
+        }
+        seg[size_t(segoff[t]) + mp[32 + x] + uint32_t(__builtin_popcount(m & ((1u << b) - 1u)))] =
+            make_uint4(hv[0], hv[1], lv[0], lv[1]);
     }
 }
 
@@ -282,12 +314,13 @@ size_t b3_bytes(uint64_t maxdim, int R)
     return Rq * d16 * 4 /* hi + lo bf16 */ + Rq * d16 * 4 /* FP32 */ + 256;
 }
 
-// compacted tile image (all null: the dense tile_f32 image)
+// compacted split image of the launch's target slot (all null: the dense
+// tile_f32 image)
 struct CompactImg
 {
     const uint32_t* mask = nullptr;
     const uint32_t* segoff = nullptr;
-    const float4* seg = nullptr;
+    const cptc_k::u32x4* seg = nullptr;
 };
 
 template <int MODE, int HDR, bool HAS_W>
@@ -424,20 +457,29 @@ extern "C" int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles,
                                     dimJ, dimK, d_ws, ws_bytes, cptc::as_stream(stream));
 }
 
-extern "C" int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles,
+extern "C" int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles, int slot,
                                               uint32_t* d_cmask, uint32_t* d_segoff,
                                               uint64_t* total_segments, void* stream)
 {
     CPTC_REQUIRE(total_segments, CPTC_ERR_ARG, "cptc_dense_tiles_compact3_mask: null total");
     *total_segments = 0;
+    CPTC_REQUIRE(slot >= 0 && slot < 3, CPTC_ERR_ARG, "cptc_dense_tiles_compact3_mask: slot %d",
+                 slot);
     if (ntiles == 0) return CPTC_OK;
     CPTC_REQUIRE(d_tile_f32 && d_cmask && d_segoff && ntiles < (size_t(1) << 31), CPTC_ERR_ARG,
                  "cptc_dense_tiles_compact3_mask: bad arguments");
     hipStream_t s = cptc::as_stream(stream);
     uint32_t* counts = nullptr;
     CPTC_HIP(hipMallocAsync(reinterpret_cast<void**>(&counts), ntiles * sizeof(uint32_t), s));
-    hipLaunchKernelGGL(compact_tiles_mask_kernel, dim3(unsigned(ntiles)), dim3(256), 0, s,
-                       d_tile_f32, d_cmask, counts);
+    if (slot == 0)
+        hipLaunchKernelGGL(compact_split_mask_kernel<0>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, counts);
+    else if (slot == 1)
+        hipLaunchKernelGGL(compact_split_mask_kernel<1>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, counts);
+    else
+        hipLaunchKernelGGL(compact_split_mask_kernel<2>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, counts);
     hipError_t le = hipGetLastError();
     std::vector<uint32_t> h(ntiles);
     hipError_t ce = hipMemcpyAsync(h.data(), counts, ntiles * sizeof(uint32_t),
@@ -465,25 +507,35 @@ extern "C" int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t nt
     return CPTC_OK;
 }
 
-extern "C" int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles,
+extern "C" int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles, int slot,
                                               const uint32_t* d_cmask, const uint32_t* d_segoff,
-                                              float* d_seg, void* stream)
+                                              void* d_seg, void* stream)
 {
+    CPTC_REQUIRE(slot >= 0 && slot < 3, CPTC_ERR_ARG, "cptc_dense_tiles_compact3_fill: slot %d",
+                 slot);
     if (ntiles == 0) return CPTC_OK;
     CPTC_REQUIRE(d_tile_f32 && d_cmask && d_segoff && d_seg && ntiles < (size_t(1) << 31),
                  CPTC_ERR_ARG, "cptc_dense_tiles_compact3_fill: bad arguments");
     CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_seg) & 15) == 0, CPTC_ERR_ARG,
                  "cptc_dense_tiles_compact3_fill: segments must be 16-byte aligned");
-    hipLaunchKernelGGL(compact_tiles_fill_kernel, dim3(unsigned(ntiles)), dim3(256), 0,
-                       cptc::as_stream(stream), d_tile_f32, d_cmask, d_segoff,
-                       reinterpret_cast<float4*>(d_seg));
+    hipStream_t s = cptc::as_stream(stream);
+    uint4* seg = static_cast<uint4*>(d_seg);
+    if (slot == 0)
+        hipLaunchKernelGGL(compact_split_fill_kernel<0>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, d_segoff, seg);
+    else if (slot == 1)
+        hipLaunchKernelGGL(compact_split_fill_kernel<1>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, d_segoff, seg);
+    else
+        hipLaunchKernelGGL(compact_split_fill_kernel<2>, dim3(unsigned(ntiles)), dim3(256), 0, s,
+                           d_tile_f32, d_cmask, d_segoff, seg);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
 
 extern "C" int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles,
                                             const uint32_t* d_cmask, const uint32_t* d_segoff,
-                                            const float* d_seg, uint64_t nseg, size_t ntiles,
+                                            const void* d_seg, uint64_t nseg, size_t ntiles,
                                             const uint32_t* d_order, const uint32_t* d_group_off,
                                             size_t ngroups, const double* d_A, const double* d_B,
                                             const double* d_C, double* d_FtV, int R, int dimI,
@@ -504,7 +556,7 @@ extern "C" int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles,
     CompactImg ci;
     ci.mask = d_cmask;
     ci.segoff = d_segoff;
-    ci.seg = reinterpret_cast<const float4*>(d_seg);
+    ci.seg = static_cast<const cptc_k::u32x4*>(d_seg);
     return launch_slot_b3<4, false>(mode, d_tiles, nullptr, ci, ntiles, d_order, d_group_off,
                                     ngroups, d_A, d_B, d_C, nullptr, d_FtV, R, dimI, dimJ, dimK,
                                     d_ws, ws_bytes, cptc::as_stream(stream));
@@ -531,7 +583,7 @@ extern "C" int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64
 
 extern "C" int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint64_t nunits,
                                         const uint32_t* d_cmask, const uint32_t* d_segoff,
-                                        const float* d_seg, uint64_t nseg, const double* d_W,
+                                        const void* d_seg, uint64_t nseg, const double* d_W,
                                         const uint32_t* d_order, const uint32_t* d_group_off,
                                         size_t ngroups, const double* d_F0, const double* d_F1,
                                         const double* d_F2, int dim0, int dim1, int dim2,
@@ -551,7 +603,7 @@ extern "C" int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint6
     CompactImg ci;
     ci.mask = d_cmask;
     ci.segoff = d_segoff;
-    ci.seg = reinterpret_cast<const float4*>(d_seg);
+    ci.seg = static_cast<const cptc_k::u32x4*>(d_seg);
     return launch_slot_b3<6, true>(slot, reinterpret_cast<const int32_t*>(d_unit6), nullptr, ci,
                                    size_t(nunits), d_order, d_group_off, ngroups, d_F0, d_F1, d_F2,
                                    d_W, d_FtV, R, dim0, dim1, dim2, d_ws, ws_bytes,

@@ -74,16 +74,18 @@ __device__ __forceinline__ void split_bf16x2(float x0, float x1, uint32_t& hi, u
 // per (row, rank) per group.  S waves share one tile / group, wave s taking
 // the 32-rank blocks s, s + S, ...
 //
-// COMPACT: the tile cells come from the compacted image instead of tile_f32:
-// cmask[64 t .. 64 t + 31] = occupancy bits of the tile's 1024 16-byte
-// segments (4 consecutive cells along the image's fastest axis; bit s % 32
-// of word s / 32), cmask[64 t + 32 + w] = set bits in words 0 .. w - 1, and
-// the occupied segments in order at cseg[csegoff[t] ..].
+// COMPACT: the A operand comes split from the target slot's compacted image
+// instead of tile_f32 (compact_split_*_kernel in dense_tiles.hip): segment
+// a * 64 + w * 4 + e = the bf16 hi then lo halves of cells (a, w,
+// 4e .. 4e + 3) (target, weight, contracted), 16 bytes; cmask[64 t + x] =
+// occupancy bits of the tile's segments 32x .. 32x + 31, cmask[64 t + 32 +
+// x] = occupied segments before word x, the occupied segments in order at
+// cseg[csegoff[t] ..].
 template <int MODE, int HDR, bool HAS_W, bool GROUPED, bool COMPACT = false>
 __device__ __forceinline__ void dense_tiles_b3_body(
     size_t wg, double* gacc_lds, const int32_t* __restrict__ hdr,
     const float* __restrict__ tile_f32, const uint32_t* __restrict__ cmask,
-    const uint32_t* __restrict__ csegoff, const float4* __restrict__ cseg,
+    const uint32_t* __restrict__ csegoff, const u32x4* __restrict__ cseg,
     size_t ntiles, const uint32_t* __restrict__ order,
     const uint32_t* __restrict__ goff, size_t ngroups, const u32x4* __restrict__ fs_hi,
     const u32x4* __restrict__ fs_lo, const float4* __restrict__ fw,
@@ -124,19 +126,19 @@ __device__ __forceinline__ void dense_tiles_b3_body(
 
     auto tile_of = [&](size_t it) -> size_t { return GROUPED ? size_t(order[it]) : it; };
 
-    // the lane's 64 cells: cells[q][p] = T at (target am, contracted 8 h + q,
-    // weight 8 ww + p)
+    // the lane's 64 cells of the dense image: cells[q][p] = T at (target am,
+    // contracted 8 h + q, weight 8 ww + p)
     float cells[8][8];
     // compacted image: buffer loads over the segments (byte offsets below
     // 2^32, checked by the launcher); an unoccupied segment's load takes an
     // offset past the buffer's end, which reads zeros
     const __amdgpu_buffer_rsrc_t rseg = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float4*>(cseg), short(0), int(0xFFFFFFF0u), 0x00020000);
+        const_cast<u32x4*>(cseg), short(0), int(0xFFFFFFF0u), 0x00020000);
     constexpr uint32_t OOB = 0xFFFFFFF0u;
-    // the header of the tile whose cells load next: lane x holds word x of
-    // its 64 (occupancy words 0..31, running counts 32..63), loaded with one
-    // coalesced 256-byte load a tile ahead; the lanes fetch the words they
-    // need from it by lane shuffles
+    // the header of the tile whose operand loads next: lane x holds word x
+    // of its 64 (occupancy words 0..31, running counts 32..63), loaded with
+    // one coalesced 256-byte load a tile ahead; the lanes fetch the words
+    // they need from it by lane shuffles
     uint32_t hdr_w = 0, hdr_so = 0;
     auto load_hdr = [&](size_t tt) {
         if constexpr (COMPACT)
@@ -145,58 +147,41 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             hdr_so = csegoff[tt];
         }
     };
-    // byte offset of segment sgi of the header's tile (OOB when unoccupied)
-    auto seg_off = [&](int sgi) -> uint32_t {
-        const int w = sgi >> 5, b = sgi & 31;
-        const uint32_t m = uint32_t(__shfl(int(hdr_w), w));
-        const uint32_t pre = uint32_t(__shfl(int(hdr_w), 32 + w));
-        const uint32_t idx = hdr_so + pre + uint32_t(__builtin_popcount(m & ((1u << b) - 1u)));
-        return ((m >> b) & 1u) ? idx * 16u : OOB;
+    bf16x8 ahi[8], alo[8];
+    // the A operand halves of the header's tile (compacted image)
+    auto load_a = [&](bf16x8 (&ah)[8], bf16x8 (&al)[8]) {
+        // the lane's 16 segments (w = 8 ww + p, cells 8h .. 8h + 7) are bits
+        // 4 p + 2 h and 4 p + 2 h + 1 of mask word 2 am + ww
+        const uint32_t mw = uint32_t(__shfl(int(hdr_w), 2 * am + ww));
+        const uint32_t base = hdr_so + uint32_t(__shfl(int(hdr_w), 32 + 2 * am + ww));
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+        {
+            const int b = 4 * p + 2 * h;
+            const uint32_t i0 = base + uint32_t(__builtin_popcount(mw & ((1u << b) - 1u)));
+            const uint32_t o0 = ((mw >> b) & 1u) ? i0 * 16u : OOB;
+            const uint32_t o1 = ((mw >> (b + 1)) & 1u) ? (i0 + ((mw >> b) & 1u)) * 16u : OOB;
+            // (the load's vector indexed directly: a __builtin_bit_cast of it
+            // to another 4 x 32-bit vector type compiled to a one-dword load)
+            const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rseg, o0, 0, 0);
+            const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rseg, o1, 0, 0);
+            u32x4 hv, lv;
+            hv[0] = uint32_t(v0[0]);
+            hv[1] = uint32_t(v0[1]);
+            hv[2] = uint32_t(v1[0]);
+            hv[3] = uint32_t(v1[1]);
+            lv[0] = uint32_t(v0[2]);
+            lv[1] = uint32_t(v0[3]);
+            lv[2] = uint32_t(v1[2]);
+            lv[3] = uint32_t(v1[3]);
+            ah[p] = __builtin_bit_cast(bf16x8, hv);
+            al[p] = __builtin_bit_cast(bf16x8, lv);
+        }
     };
     auto load_cells = [&](size_t t) {
         if constexpr (COMPACT)
         {
-#pragma unroll
-            for (int q = 0; q < 8; ++q)
-            {
-                const int c = 8 * h + q;
-                if constexpr (MODE == 0 || MODE == 1)
-                {
-                    const int base = (MODE == 0) ? (am * 16 + c) * 16 : (c * 16 + am) * 16;
-                    const int s0 = (base + 8 * ww) >> 2;
-                    // (the load's vector indexed directly: a __builtin_bit_cast of it
-                    // to another 4 x 32-bit vector type compiled to a one-dword load)
-                    const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rseg, seg_off(s0), 0, 0);
-                    const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rseg, seg_off(s0 + 1), 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                    {
-                        cells[q][e] = __builtin_bit_cast(float, uint32_t(v0[e]));
-                        cells[q][4 + e] = __builtin_bit_cast(float, uint32_t(v1[e]));
-                    }
-                }
-                else
-                {
-                    // the 8 cells (c, 8 ww + p, am) lie in segments
-                    // (c 16 + 8 ww + p) 4 + am / 4 of one mask word (2 c + ww),
-                    // bits 4 p + am / 4
-                    const int w = 2 * c + ww;
-                    const uint32_t m = uint32_t(__shfl(int(hdr_w), w));
-                    const uint32_t base = (hdr_so + uint32_t(__shfl(int(hdr_w), 32 + w))) * 16u +
-                                          uint32_t(am & 3) * 4u;
-#pragma unroll
-                    for (int p = 0; p < 8; ++p)
-                    {
-                        const int b = 4 * p + (am >> 2);
-                        const uint32_t off =
-                            ((m >> b) & 1u)
-                                ? base + uint32_t(__builtin_popcount(m & ((1u << b) - 1u))) * 16u
-                                : OOB;
-                        cells[q][p] = __builtin_bit_cast(
-                            float, __builtin_amdgcn_raw_buffer_load_b32(rseg, off, 0, 0));
-                    }
-                }
-            }
+            load_a(ahi, alo);
             return;
         }
         const float* __restrict__ T = tile_f32 + t * 4096;
@@ -227,8 +212,8 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             }
         }
     };
-    bf16x8 ahi[8], alo[8];
     auto split_cells = [&]() {
+        if constexpr (COMPACT) return;   // the image holds the split halves
 #pragma unroll
         for (int p = 0; p < 8; ++p)
         {

@@ -180,23 +180,31 @@ int cptc_mttkrp_dense_tiles3_ws(int mode, const int32_t* d_tiles, const float* d
                                 int dimI, int dimJ, int dimK, void* d_ws, size_t ws_bytes,
                                 void* stream);
 
-/* Compacted tile image for the split-bf16 kernel: the 1024 16-byte segments
- * of every tile (4 consecutive cells along the image's last axis) with at
- * least one nonzero bit, in order, plus per tile 32 occupancy words and 32
+/* Compacted split image of one target slot for the split-bf16 kernel: its
+ * A operand, stored once instead of split on every launch.  Tile cell
+ * (a, w, c) = (target, weight, contracted coordinate of `slot`) is image
+ * cell (a, c, w) for slot 0, (c, a, w) for slot 1 and (c, w, a) for slot 2.
+ * Segment a * 64 + w * 4 + e of a tile = the bf16 hi halves of cells
+ * (a, w, 4e .. 4e + 3), then their bf16 lo halves (x = hi + lo, round to
+ * nearest even; 16 bytes); only segments with a nonzero bit in one of their
+ * 4 FP32 cells are stored, in order, with per tile 32 occupancy words and 32
  * running counts.  _mask: d_cmask (ntiles x 64 uint32) and d_segoff
  * (ntiles + 1 uint32: first segment of each tile, then the total), the total
  * in *total_segments (host; synchronises the stream).  _fill: the segments
  * into d_seg (total x 16 bytes, 16-byte aligned).  No reference counterpart
  * (the reference builds dense tiles per call, dense.cu:150-190). */
-int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles, uint32_t* d_cmask,
-                                   uint32_t* d_segoff, uint64_t* total_segments, void* stream);
-int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles, const uint32_t* d_cmask,
-                                   const uint32_t* d_segoff, float* d_seg, void* stream);
+int cptc_dense_tiles_compact3_mask(const float* d_tile_f32, size_t ntiles, int slot,
+                                   uint32_t* d_cmask, uint32_t* d_segoff,
+                                   uint64_t* total_segments, void* stream);
+int cptc_dense_tiles_compact3_fill(const float* d_tile_f32, size_t ntiles, int slot,
+                                   const uint32_t* d_cmask, const uint32_t* d_segoff, void* d_seg,
+                                   void* stream);
 
-/* cptc_mttkrp_dense_tiles3_ws over the compacted image (nseg segments,
- * nseg * 16 below 2^32 - 16); the same FP64 contributions per tile. */
+/* cptc_mttkrp_dense_tiles3_ws over the compacted split image of slot `mode`
+ * (nseg segments, nseg * 16 below 2^32 - 16); the same FP64 contributions
+ * per tile. */
 int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles, const uint32_t* d_cmask,
-                                 const uint32_t* d_segoff, const float* d_seg, uint64_t nseg,
+                                 const uint32_t* d_segoff, const void* d_seg, uint64_t nseg,
                                  size_t ntiles, const uint32_t* d_order,
                                  const uint32_t* d_group_off, size_t ngroups, const double* d_A,
                                  const double* d_B, const double* d_C, double* d_FtV, int R,
@@ -598,10 +606,10 @@ int cptc_mttkrp_units_nd_ws(int slot, const uint32_t* d_unit6, uint64_t nunits,
                             const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
                             double* d_FtV, int R, void* d_ws, size_t ws_bytes, void* stream);
 
-/* cptc_mttkrp_units_nd_ws over the units' compacted image
- * (cptc_dense_tiles_compact3_mask / _fill over the unit tiles). */
+/* cptc_mttkrp_units_nd_ws over the units' compacted split image of `slot`
+ * (cptc_dense_tiles_compact3_mask / _fill over the unit tiles, same slot). */
 int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint64_t nunits,
-                             const uint32_t* d_cmask, const uint32_t* d_segoff, const float* d_seg,
+                             const uint32_t* d_cmask, const uint32_t* d_segoff, const void* d_seg,
                              uint64_t nseg, const double* d_W, const uint32_t* d_order,
                              const uint32_t* d_group_off, size_t ngroups, const double* d_F0,
                              const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,

@@ -74,11 +74,12 @@ struct HybridCOOTensor {
     int32_t* d_tiles4 = nullptr;        // num_dense_tiles x {bi, bj, bk, nnz}
     uint64_t* d_pool_off = nullptr;     // num_dense_tiles + 1 pool offsets
     mutable float* d_tile_f32 = nullptr;  // FP32 tile images, packed on first MFMA use
-    // compacted tile image of the split-bf16 kernel, built on its first use
-    mutable uint32_t* d_tile_cmask = nullptr;
-    mutable uint32_t* d_tile_segoff = nullptr;
-    mutable float* d_tile_cseg = nullptr;
-    mutable uint64_t tile_nseg = 0;
+    // compacted split tile images of the split-bf16 kernel, one per target
+    // mode, each built on the mode's first use
+    mutable uint32_t* d_tile_cmask[3] = {nullptr, nullptr, nullptr};
+    mutable uint32_t* d_tile_segoff[3] = {nullptr, nullptr, nullptr};
+    mutable void* d_tile_cseg[3] = {nullptr, nullptr, nullptr};
+    mutable uint64_t tile_nseg[3] = {0, 0, 0};
     size_t dense_nnz = 0;
     int dense_cutoff = 0;
 };

@@ -414,17 +414,17 @@ def test_units_kernel_vs_oracle(ca, orc, dev, N, R, inner, G, kern):
             if kern == "bf16x3":
                 rc = ca.lib.cptc_mttkrp_units_nd_ws(*args, ws.data_ptr(), nb, None)
             else:
-                # the compacted unit image (the order-3 tiles' format)
+                # the slot's compacted split unit image (the order-3 tiles' format)
                 cm = ca.DevBuf.zeros((nu * 64,), np.uint32)
                 so = ca.DevBuf.zeros((nu + 1,), np.uint32)
                 tot = C.c_uint64()
-                assert ca.lib.cptc_dense_tiles_compact3_mask(tiles.data_ptr(), nu, cm.data_ptr(),
-                                                             so.data_ptr(), C.byref(tot),
-                                                             None) == 0
-                sg = ca.DevBuf.zeros((max(tot.value, 1) * 4,), np.float32)
-                assert ca.lib.cptc_dense_tiles_compact3_fill(tiles.data_ptr(), nu, cm.data_ptr(),
-                                                             so.data_ptr(), sg.data_ptr(),
-                                                             None) == 0
+                assert ca.lib.cptc_dense_tiles_compact3_mask(tiles.data_ptr(), nu, slot,
+                                                             cm.data_ptr(), so.data_ptr(),
+                                                             C.byref(tot), None) == 0
+                sg = ca.DevBuf.zeros((max(tot.value, 1) * 4,), np.uint32)
+                assert ca.lib.cptc_dense_tiles_compact3_fill(tiles.data_ptr(), nu, slot,
+                                                             cm.data_ptr(), so.data_ptr(),
+                                                             sg.data_ptr(), None) == 0
                 rc = ca.lib.cptc_mttkrp_units_nd_cws(
                     slot, d6.data_ptr(), nu, cm.data_ptr(), so.data_ptr(), sg.data_ptr(),
                     tot.value, W.data_ptr(), *grp, dF[inner[0]].data_ptr(),

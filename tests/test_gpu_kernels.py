@@ -214,13 +214,38 @@ def test_dense_tiles_mfma_vs_fp64(ca, orc, dev, R, G, kern):
         assert rel_err(out.numpy(), ref) <= 1e-5, (mode, R)
 
 
+def bf16_rne(x):
+    """float32 -> bf16 bits, round to nearest even (finite inputs)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def split_image(img, slot):
+    """numpy restatement of one slot's compacted split image: tile cell
+    (a, w, c) of the [i][j][k] image, 4-cell segments (a, w, e), bf16 hi of
+    the value clamped to the bf16 range, bf16 lo of the float32 remainder."""
+    nt = img.shape[0]
+    t = img.reshape(nt, 16, 16, 16)
+    A = {0: t.transpose(0, 1, 3, 2), 1: t.transpose(0, 2, 3, 1), 2: t.transpose(0, 3, 2, 1)}[slot]
+    cells = np.ascontiguousarray(A).reshape(nt, 1024, 4)
+    occ = cells.view(np.uint32).any(axis=2)
+    bmax = np.float32(3.38953139e38)
+    hi = bf16_rne(np.clip(cells, -bmax, bmax))
+    hif = (hi.astype(np.uint32) << 16).view(np.float32)
+    lo = bf16_rne((cells - hif).astype(np.float32))
+    seg = np.concatenate([hi, lo], axis=2)                    # (nt, 1024, 8) bf16 bits
+    return occ, seg
+
+
 @pytest.mark.parametrize("R,G", [(32, 0), (128, 8), (100, 3), (200, 0)])
 def test_dense_tiles_compact_image(ca, orc, dev, R, G):
-    """The compacted tile image (cptc_dense_tiles_compact3_mask / _fill):
-    occupancy words, running counts, segment offsets and packed segments equal
-    a numpy construction from the dense image; the split-bf16 kernel over it
-    (cptc_mttkrp_dense_tiles3_cws) gives the dense-image kernel's results up
-    to the order of the FP64 atomic adds, every mode, grouped and per tile."""
+    """The compacted split image of each target slot
+    (cptc_dense_tiles_compact3_mask / _fill): occupancy words, running counts,
+    segment offsets and the packed bf16 hi / lo segments equal a numpy
+    construction from the dense image (its own round-to-nearest-even bf16
+    split); the split-bf16 kernel over it (cptc_mttkrp_dense_tiles3_cws) gives
+    the dense-image kernel's results (which split on every launch) up to the
+    order of the FP64 atomic adds, every mode, grouped and per tile."""
     rng = np.random.default_rng(90 + R)
     dims = (40, 45, 37)
     idx, val = block_tensor(rng, dims, fill=0.15)
@@ -234,32 +259,34 @@ def test_dense_tiles_compact_image(ca, orc, dev, R, G):
     pools = [to_dev(ca, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]
     assert ca.lib.cptc_dense_tiles_pack3(*(b.data_ptr() for b in pools), nt, tf.data_ptr(),
                                          stream(ca)) == 0
-    cm = zeros(ca, (nt * 64,), np.uint32)
-    so = zeros(ca, (nt + 1,), np.uint32)
-    tot = C.c_uint64()
-    assert ca.lib.cptc_dense_tiles_compact3_mask(tf.data_ptr(), nt, cm.data_ptr(), so.data_ptr(),
-                                                 C.byref(tot), stream(ca)) == 0
-    nseg = tot.value
-    seg = zeros(ca, (max(nseg, 1) * 4,), np.float32)
-    assert ca.lib.cptc_dense_tiles_compact3_fill(tf.data_ptr(), nt, cm.data_ptr(), so.data_ptr(),
-                                                 seg.data_ptr(), stream(ca)) == 0
     ca.sync()
-    img = tf.numpy().reshape(nt, 1024, 4)
-    occ = img.view(np.uint32).any(axis=2)                     # (nt, 1024)
-    bits = occ.reshape(nt, 32, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)
-    words = bits.sum(axis=2).astype(np.uint32)
-    run = np.concatenate([np.zeros((nt, 1), np.uint32),
-                          np.cumsum(occ.reshape(nt, 32, 32).sum(axis=2), axis=1)[:, :-1]],
-                         axis=1).astype(np.uint32)
-    got_m = cm.numpy().reshape(nt, 64)
-    assert np.array_equal(got_m[:, :32], words) and np.array_equal(got_m[:, 32:], run)
-    cnt = occ.sum(axis=1)
-    assert nseg == int(cnt.sum()) and 0 < nseg < nt * 1024
-    assert np.array_equal(so.numpy(), np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32))
-    assert np.array_equal(seg.numpy()[:nseg * 4].reshape(nseg, 4), img[occ])
+    img = tf.numpy().reshape(nt, 4096)
     nb = ca.lib.cptc_tile_operands_bytes(max(dims), R)
     ws = zeros(ca, (nb,), np.uint8)
     for mode in range(3):
+        cm = zeros(ca, (nt * 64,), np.uint32)
+        so = zeros(ca, (nt + 1,), np.uint32)
+        tot = C.c_uint64()
+        assert ca.lib.cptc_dense_tiles_compact3_mask(tf.data_ptr(), nt, mode, cm.data_ptr(),
+                                                     so.data_ptr(), C.byref(tot), stream(ca)) == 0
+        nseg = tot.value
+        seg = zeros(ca, (max(nseg, 1) * 8,), np.uint16)
+        assert ca.lib.cptc_dense_tiles_compact3_fill(tf.data_ptr(), nt, mode, cm.data_ptr(),
+                                                     so.data_ptr(), seg.data_ptr(),
+                                                     stream(ca)) == 0
+        ca.sync()
+        occ, ref_seg = split_image(img, mode)
+        bits = occ.reshape(nt, 32, 32).astype(np.uint64) << np.arange(32, dtype=np.uint64)
+        words = bits.sum(axis=2).astype(np.uint32)
+        run = np.concatenate([np.zeros((nt, 1), np.uint32),
+                              np.cumsum(occ.reshape(nt, 32, 32).sum(axis=2), axis=1)[:, :-1]],
+                             axis=1).astype(np.uint32)
+        got_m = cm.numpy().reshape(nt, 64)
+        assert np.array_equal(got_m[:, :32], words) and np.array_equal(got_m[:, 32:], run), mode
+        cnt = occ.sum(axis=1)
+        assert nseg == int(cnt.sum()) and 0 < nseg < nt * 1024
+        assert np.array_equal(so.numpy(), np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32))
+        assert np.array_equal(seg.numpy()[:nseg * 8].reshape(nseg, 8), ref_seg[occ]), mode
         grp = (None, None, 0)
         if G:
             go, gf, ng = tile_groups(ca, p["tiles"], 4, mode, G)
