@@ -55,7 +55,13 @@ __global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per
 // Split-bf16 variant (cptc_k::dense_tiles_b3_body in tiles_b3_body.hpp);
 // COMPACT reads the compacted tile image (cmask / csegoff / cseg).
 template <int MODE, int HDR, bool HAS_W, bool GROUPED, bool COMPACT>
-__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(2, 2))) void dense_tiles_b3_kernel(
+#ifndef CPTC_B3_WAVES
+#define CPTC_B3_WAVES 2   // resident waves per SIMD of the split-bf16 kernel
+#endif
+#ifndef CPTC_B3_SMIN
+#define CPTC_B3_SMIN 1    // least waves per tile (rank split) of its grouped form
+#endif
+__global__ __launch_bounds__(WAVE* WAVES_PER_WG) __attribute__((amdgpu_waves_per_eu(CPTC_B3_WAVES, CPTC_B3_WAVES))) void dense_tiles_b3_kernel(
     const int32_t* __restrict__ hdr, const float* __restrict__ tile_f32,
     const uint32_t* __restrict__ cmask, const uint32_t* __restrict__ csegoff,
     const cptc_k::u32x4* __restrict__ cseg, size_t ntiles, const uint32_t* __restrict__ order,
@@ -347,12 +353,15 @@ int launch_tiles_b3(const int32_t* hdr, const float* tiles, CompactImg ci, size_
     const dim3 block{WAVE * WAVES_PER_WG};
     const bool grouped = order && goff && ngroups > 0 && Rq <= GROUP_LDS_MAX_R;
     const size_t items = grouped ? ngroups : ntiles;
-    const int S = rank_split(items, Rq / 2, s);   // 32-rank blocks
+    int S = rank_split(items, Rq / 2, s);   // 32-rank blocks
+    if (grouped) S = std::min(std::max(S, CPTC_B3_SMIN), Rq / 32);
     const size_t wgs = (items * size_t(S) + WAVES_PER_WG - 1) / WAVES_PER_WG;
     CPTC_REQUIRE(wgs < (size_t(1) << 31), CPTC_ERR_ARG, "dense tiles: too many tiles");
     if (grouped)
     {
-        const size_t lds = size_t(WAVES_PER_WG) * 16 * Rq * sizeof(double);   // <= 64 KB
+        // per wave 16 rows x its rank blocks (<= 64 KB per workgroup)
+        const size_t lds = size_t(WAVES_PER_WG) * 16 * size_t((Rq / 32 + S - 1) / S * 32) *
+                           sizeof(double);
         if (compact)
             hipLaunchKernelGGL((dense_tiles_b3_kernel<MODE, HDR, HAS_W, true, true>),
                                dim3(static_cast<unsigned>(wgs)), block, lds, s, hdr, tiles,

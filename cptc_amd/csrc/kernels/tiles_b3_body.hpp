@@ -39,6 +39,10 @@
 
 #include <cstdint>
 
+#ifndef CPTC_B3_PIPE
+#define CPTC_B3_PIPE 4   // MFMA accumulators in flight per wave (2 or 4)
+#endif
+
 namespace cptc_k {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -116,13 +120,17 @@ __device__ __forceinline__ void dense_tiles_b3_body(
     const int h = lane >> 5;   // K group (A, B); row quad parity (D)
     const int m = lane & 31;   // A row: (w half, target row)
     const int ww = m >> 4, am = m & 15;
-    double* gacc = gacc_lds + size_t(threadIdx.x / 64) * 16 * Rq;
+    // the wave's LDS block: 16 rows x (its rank blocks x 32) doubles, rank
+    // block rb at column (rb - rb0) / rstep * 32
+    const int gstride = (Rq / 32 + S - 1) / S * 32;
+    double* gacc = gacc_lds + size_t(threadIdx.x / 64) * 16 * size_t(gstride);
+    auto gcol = [&](int rbx) { return (rbx - rb0) / rstep * 32 + n; };
     // the lane's 8 D rows: target row a(o) = 8 (o / 4) + 4 h + o % 4, o = 0..7
     auto arow = [&](int o) { return 8 * (o >> 2) + 4 * h + (o & 3); };
     if constexpr (GROUPED)
         for (int rb = rb0; rb < Rq; rb += rstep)
 #pragma unroll
-            for (int o = 0; o < 8; ++o) gacc[arow(o) * Rq + rb + n] = 0.0;
+            for (int o = 0; o < 8; ++o) gacc[arow(o) * gstride + gcol(rb)] = 0.0;
 
     auto tile_of = [&](size_t it) -> size_t { return GROUPED ? size_t(order[it]) : it; };
 
@@ -323,6 +331,20 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             for (int o = 0; o < 8; ++o) asm volatile("" : "+v"(out[o]));
             asm volatile("" : "+v"(bh), "+v"(bl));
         };
+#if CPTC_B3_PIPE == 2
+        floatx16 x0, x1;
+        products(0, x0, x1);
+        weigh(0, x0, x1);
+        fence();
+        products(2, x0, x1);
+        weigh(2, x0, x1);
+        fence();
+        products(4, x0, x1);
+        weigh(4, x0, x1);
+        fence();
+        products(6, x0, x1);
+        weigh(6, x0, x1);
+#else
         floatx16 x0, x1, y0, y1;
         products(0, x0, x1);
         products(2, y0, y1);
@@ -335,6 +357,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         weigh(4, x0, x1);
         fence();
         weigh(6, y0, y1);
+#endif
         if (more) load_ops(tn, rbn);
         // unconditional epilogue (ranks >= R hold zeros and are not flushed),
         // so the FMAs above are not sunk into a branch
@@ -347,7 +370,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             if constexpr (HAS_W) tot *= wr;
             if constexpr (GROUPED)
             {
-                gacc[arow(o) * Rq + r] += tot;
+                gacc[arow(o) * gstride + gcol(rb)] += tot;
             }
             else
             {
@@ -376,7 +399,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             for (int o = 0; o < 8; ++o)
             {
                 const int row = ob + arow(o);
-                const double x = gacc[arow(o) * Rq + r];
+                const double x = gacc[arow(o) * gstride + gcol(rb2)];
                 if (row < odim && x != 0.0) atomicAdd(FtV + size_t(row) * R + r, x);
             }
         }
