@@ -45,17 +45,24 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, vendor figure
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, vendor figure
 
 
-def tile_roof(info, R, ntiles, launch_ms, where):
+def tile_roof(info, R, ntiles, launch_ms, where, segments=None):
     """MFMA roofline of the dense-tile kernel over its mean launch time: the
     split-bf16 kernel (three bf16 products per term, 32-rank blocks) against
     the bf16 matrix peak, the FP32 kernel against the FP32 matrix peak; the
-    useful flops (8192 R per tile) and the tile image's bytes beside them."""
+    useful flops (8192 R per tile) and the tile image's bytes beside them
+    (the compacted split images' 16-byte segments plus 64 header words and
+    one offset per tile when `segments` lists them per launch, else the
+    dense FP32 image)."""
     b3 = bool(info.tile_bf16x3)
     rq = (R + 31) // 32 * 32
     useful = 8192.0 * R * ntiles
     executed = 3 * 8192.0 * rq * ntiles if b3 else 8192.0 * ((R + 15) // 16 * 16) * ntiles
     peak = BF16_MFMA_PEAK_TFLOPS if b3 else FP32_MFMA_PEAK_TFLOPS
     mean_s = sum(launch_ms) / len(launch_ms) * 1e-3
+    if segments and all(segments):
+        img_bytes = [int(n) * 16 + ntiles * 260 for n in segments]
+    else:
+        img_bytes = [ntiles * 4096 * 4] * len(launch_ms)
     ach = executed / mean_s / 1e12
     return {
         "kernel": ("dense_tiles_b3_kernel (16^3 tiles, split-bf16 v_mfma_f32_32x32x16_bf16, "
@@ -65,8 +72,8 @@ def tile_roof(info, R, ntiles, launch_ms, where):
         "frac": round(ach / peak, 4),
         "flops_per_launch": executed, "useful_flops_per_launch": useful,
         "useful_TFLOPs": round(useful / mean_s / 1e12, 2),
-        "tile_image_bytes_per_launch": ntiles * 4096 * 4,
-        "tile_image_GBs": round(ntiles * 4096 * 4 / mean_s / 1e9, 1),
+        "tile_image_bytes_per_launch": img_bytes,
+        "tile_image_GBs": round(sum(img_bytes) / len(img_bytes) / mean_s / 1e9, 1),
         "launch_ms": [round(x, 4) for x in launch_ms],
     }
 
@@ -287,7 +294,8 @@ def main() -> int:
         # kernel is the whole MTTKRP
         mt_launch = [float(mt_ms[m]) / kit for m in range(3)]
         if use_mfma and ntiles:
-            roofline = tile_roof(info, R, ntiles, mt_launch, "the whole MTTKRP (no residual)")
+            roofline = tile_roof(info, R, ntiles, mt_launch, "the whole MTTKRP (no residual)",
+                                 list(info.tile_segments) if info.tile_compact else None)
         else:
             roofline = {"kernel": "FP64 dense-view MTTKRP", "bound": "hbm", "achieved": None,
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
@@ -297,7 +305,8 @@ def main() -> int:
     if tiles_timed and snnz:
         where = ("beside the FP64 kernel on a second stream" if info.tiles_beside else
                  "on the main stream before the FP64 kernel")
-        roofline_tiles = tile_roof(info, R, ntiles, tile_ms, where)
+        roofline_tiles = tile_roof(info, R, ntiles, tile_ms, where,
+                                   list(info.tile_segments) if info.tile_compact else None)
 
     line = {
         "metric": BASELINE_METRIC,
@@ -444,7 +453,8 @@ def bench_generic(ca, args, spec, R) -> int:
                               "none for these kernel sources: achieved/frac null",
         },
         "roofline_units": (tile_roof(info, R, int(info.n_units), unit_launch,
-                                     "dense units with FP64 outer weights, per inner mode")
+                                     "dense units with FP64 outer weights, per inner mode",
+                                     list(info.unit_segments))
                            if unit_launch else None),
         "cpu_baseline": cpu,
     }

@@ -70,6 +70,7 @@ class Als3Info(C.Structure):
         ("tile_bf16x3", C.c_int),
         ("tiles_beside", C.c_int),
         ("tile_compact", C.c_int),
+        ("tile_segments", C.c_uint64 * 3),
     ]
 
 
@@ -106,6 +107,7 @@ class GenInfo(C.Structure):
         ("prep_ms", C.c_double * 3),
         ("kernel_nnz", C.c_uint64 * CPTC_MAX_MODES),
         ("tile_bf16x3", C.c_int),
+        ("unit_segments", C.c_uint64 * 3),
     ]
 
 

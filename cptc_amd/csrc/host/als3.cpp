@@ -895,6 +895,7 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->tile_bf16x3 = h->tile_b3 ? 1 : 0;
     info->tile_compact =
         (h->tile_b3 && h->timg[0].ready() && h->timg[1].ready() && h->timg[2].ready()) ? 1 : 0;
+    for (int m = 0; m < 3; ++m) info->tile_segments[m] = h->timg[m].ready() ? h->timg[m].nseg : 0;
     info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }

@@ -436,7 +436,8 @@ typedef struct cptc_als3_info {
     int sparse_blocked;       /* 1 = the residual runs over the blocked layout */
     int tile_bf16x3;          /* 1 = dense tiles on the split-bf16 kernel, 0 = FP32 MFMA */
     int tiles_beside;         /* 1 = tile kernel on a side stream beside the FP64 kernel */
-    int tile_compact;         /* 1 = the split-bf16 kernel reads the compacted tile image */
+    int tile_compact;         /* 1 = the split-bf16 kernel reads the compacted tile images */
+    uint64_t tile_segments[3];  /* 16-byte segments of mode m's compacted split image (0: none) */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
@@ -683,6 +684,7 @@ typedef struct cptc_gen_info {
     uint64_t kernel_nnz[CPTC_MAX_MODES];   /* elements of the MTTKRP kernel's view per mode
                                               (the inner modes' dense elements dropped) */
     int tile_bf16x3;         /* 1 = dense units on the split-bf16 kernel, 0 = FP32 MFMA */
+    uint64_t unit_segments[3];  /* 16-byte segments of inner slot s's compacted split image */
 } cptc_gen_info;
 
 /* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)
