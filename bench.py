@@ -414,7 +414,8 @@ def bench_generic(ca, args, spec, R) -> int:
     workload = f"cfg{args.config}-R{R}"
     prof = load_traffic_seg(workload)
     hbm = (prof["hbm_bytes_per_launch"] / (sum(seg_launch) / N * 1e-3) / 1e9) if prof else None
-    inner = [m for m in range(N) if info.dense_enabled and m in tuple(info.inner)]
+    # the inner modes in slot order (the order of unit_segments)
+    inner = list(tuple(info.inner)) if info.dense_enabled else []
     unit_launch = [float(unit_ms[m]) / kit for m in inner]
 
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter; seg launch ms "
