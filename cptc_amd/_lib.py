@@ -206,6 +206,7 @@ SIGNATURES = {
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,
                                   _I, _P]),
+    "cptc_gen_normalize_gram": (_I, [_P, _Z, _I, _P, _P, _I, _I, _I, _P, _P, _Z, _P]),
     "cptc_mttkrp_units_nd_cws": (_I, [_I, _P, _U64, _P, _P, _P, C.c_uint64, _P, _P, _P, _Z, _P,
                                       _P, _P, _I, _I, _I, _P, _I, _P, _Z, _P]),
     "cptc_mttkrp_units_nd_ws": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I,

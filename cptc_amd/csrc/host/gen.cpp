@@ -412,11 +412,11 @@ struct Gen
 
     const double* const* F() const { return d_F.data(); }
 
-    // FtV = MTTKRP of mode n (zeroed first).  With `timing`, events bracket
-    // the unit kernel (kev 0-1) and the segment kernel (kev 2-3).
-    int mttkrp(int n)
+    // FtV = MTTKRP of mode n (zeroed first, unless `zeroed`).  With `timing`,
+    // events bracket the unit kernel (kev 0-1) and the segment kernel (kev 2-3).
+    int mttkrp(int n, bool zeroed = false)
     {
-        CPTC_HIP(hipMemsetAsync(d_FtV, 0, dims[n] * size_t(R) * sizeof(double), s));
+        if (!zeroed) CPTC_HIP(hipMemsetAsync(d_FtV, 0, dims[n] * size_t(R) * sizeof(double), s));
         const bool in = dense && (inner_mask & (1u << n));
         hipEvent_t* ke = kev_cur + 4 * n;
         if (timing) CPTC_HIP(hipEventRecord(ke[0], s));
@@ -493,11 +493,15 @@ struct Gen
     int enqueue_iteration(double* d_out, int& mk)
     {
         const size_t RR = size_t(R) * R;
+        // a small factor's update (cptc_gen_normalize_gram) also forms the
+        // next mode's FtF and zeroes its FtV
+        bool ftf_ready = false, ftv_zeroed = false;
         for (int n = 0; n < N; ++n)
         {
-            CPTC_TRY(cptc_gram_hadamard(d_grams, N, n, R, d_FtF, s));
+            if (!ftf_ready) CPTC_TRY(cptc_gram_hadamard(d_grams, N, n, R, d_FtF, s));
             mark(mk++);
-            CPTC_TRY(mttkrp(n));
+            CPTC_TRY(mttkrp(n, ftv_zeroed));
+            ftf_ready = ftv_zeroed = false;
             mark(mk++);
             // One stream: factoring FtF on a second stream beside the MTTKRP
             // measured slower (configs 4 and 5: 0.545 -> 0.60 and 1.54 ->
@@ -511,8 +515,25 @@ struct Gen
                 CPTC_TRY(cptc_chol_ridge_apply(d_L, d_FtV, d_F[n], dims[n], R, s));
             }
             mark(mk++);
-            CPTC_TRY(cptc_gen_normalize(d_F[n], dims[n], R, d_lambda, s));
-            CPTC_TRY(cptc_gram(d_F[n], dims[n], R, d_grams + size_t(n) * RR, s));
+            // one workgroup pays while its Gram loop is short: <= 256 rows
+            // per row group (1024 / R^2 groups)
+            if (R <= 32 && dims[n] <= size_t(256) * size_t(1024 / (R * R)) &&
+                dims[n] * size_t(R) <= (size_t(1) << 16))
+            {
+                const int next = n + 1 < N ? n + 1 : -1;
+                const size_t nz = next >= 0 && dims[next] * size_t(R) <= (size_t(1) << 18)
+                                      ? dims[next] * size_t(R)
+                                      : 0;
+                CPTC_TRY(cptc_gen_normalize_gram(d_F[n], dims[n], R, d_lambda, d_grams, N, n, next,
+                                                 d_FtF, d_FtV, nz, s));
+                ftf_ready = next >= 0;
+                ftv_zeroed = nz > 0;
+            }
+            else
+            {
+                CPTC_TRY(cptc_gen_normalize(d_F[n], dims[n], R, d_lambda, s));
+                CPTC_TRY(cptc_gram(d_F[n], dims[n], R, d_grams + size_t(n) * RR, s));
+            }
             if (dense && !(inner_mask & (1u << n))) w_dirty = true;
             mark(mk++);
         }

@@ -514,6 +514,85 @@ __global__ __launch_bounds__(256) void normalize_nd_kernel(double* __restrict__ 
         F[x] /= nrm[x % R];
 }
 
+// A small factor's update tail in one workgroup (rows x R <= SMALL_UPDATE_MAX,
+// R <= 32): the normalisation of normalize_nd_kernel (lambda_r = the column's
+// 2-norm, 1 when it is not finite or below 1e-14; F /= lambda), the Gram
+// G_mode = F^T F of the normalised factor and, when next >= 0, the next
+// mode's FtF = prod_{g != next} G_g in mode order (gram_hadamard_kernel) and
+// its first nzero FtV entries zeroed: one launch instead of six.  Rows are
+// staged in LDS 64 at a time; each Gram entry sums its rows in order.
+constexpr int SMALL_UPDATE_MAX = 1 << 16;
+
+__global__ __launch_bounds__(1024) void small_update_kernel(
+    double* __restrict__ F, int rows, int R, double* __restrict__ lambda, double* __restrict__ grams,
+    int ngram, int mode, int next, double* __restrict__ FtF, double* __restrict__ FtV, int nzero)
+{
+    __shared__ double red[1024];
+    __shared__ double nrm[32];
+    __shared__ double tile[64 * 32];
+    const int tid = threadIdx.x;
+    const int RR = R * R;
+    const int r = tid % R, rl = tid / R, nrl = 1024 / R;
+    double acc = 0.0;
+    if (rl < nrl)
+        for (int i = rl; i < rows; i += nrl)
+        {
+            const double v = F[size_t(i) * R + r];
+            acc += v * v;
+        }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < R)
+    {
+        double sq = 0.0;
+        for (int q = 0; q < nrl; ++q) sq += red[q * R + tid];
+        double n = sqrt(sq);
+        if (!isfinite(n) || n < 1e-14) n = 1.0;
+        nrm[tid] = n;
+        lambda[tid] = n;
+    }
+    __syncthreads();
+    // Gram entry e = tid % RR, row group q = tid / RR of NQ: group q sums the
+    // rows i = q mod NQ, then the groups' sums are added in group order
+    const int NQ = 1024 / RR;
+    const int e = tid % RR, q = tid / RR;
+    const int a = e / R, b = e % R;
+    double g = 0.0;
+    for (int i0 = 0; i0 < rows; i0 += 64)
+    {
+        const int nr = min(64, rows - i0);
+        for (int x = tid; x < nr * R; x += 1024)
+        {
+            const double v = F[size_t(i0) * R + x] / nrm[x % R];
+            F[size_t(i0) * R + x] = v;
+            tile[x] = v;
+        }
+        __syncthreads();
+        if (q < NQ)
+            for (int i = q; i < nr; i += NQ) g += tile[i * R + a] * tile[i * R + b];
+        __syncthreads();
+    }
+    red[tid] = g;
+    __syncthreads();
+    if (tid < RR)
+    {
+        g = 0.0;
+        for (int p = 0; p < NQ; ++p) g += red[p * RR + tid];
+        grams[size_t(mode) * RR + tid] = g;
+    }
+    if (next >= 0)
+    {
+        if (tid < RR)
+        {
+            double v = 1.0;
+            for (int gm = 0; gm < ngram; ++gm)
+                if (gm != next) v *= (gm == mode) ? g : grams[size_t(gm) * RR + tid];
+            FtF[tid] = v;
+        }
+        for (int x = tid; x < nzero; x += 1024) FtV[x] = 0.0;
+    }
+}
+
 // --------------------------------------------------------- exact residual --
 
 __global__ __launch_bounds__(256) void residual_nd_kernel(int nmodes,
@@ -748,6 +827,26 @@ extern "C" int cptc_gen_normalize(double* d_F, size_t rows, int R, double* d_lam
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(normalize_nd_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 1024)),
                        dim3(256), 0, s, d_F, rows, R, part, P, d_lambda);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_normalize_gram(double* d_F, size_t rows, int R, double* d_lambda,
+                                       double* d_grams, int ngram, int mode, int next,
+                                       double* d_FtF, double* d_FtV, size_t nzero, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 32 && rows >= 1 && rows * size_t(R) <= size_t(SMALL_UPDATE_MAX),
+                 CPTC_ERR_ARG, "cptc_gen_normalize_gram: rows %zu x R %d (R <= 32, <= %d values)",
+                 rows, R, SMALL_UPDATE_MAX);
+    CPTC_REQUIRE(ngram >= 1 && mode >= 0 && mode < ngram && next >= -1 && next < ngram &&
+                     nzero <= (size_t(1) << 24),
+                 CPTC_ERR_ARG, "cptc_gen_normalize_gram: ngram %d mode %d next %d nzero %zu",
+                 ngram, mode, next, nzero);
+    CPTC_REQUIRE(d_F && d_lambda && d_grams && (next < 0 || d_FtF) && (nzero == 0 || d_FtV),
+                 CPTC_ERR_ARG, "cptc_gen_normalize_gram: null pointer");
+    hipLaunchKernelGGL(small_update_kernel, dim3(1), dim3(1024), 0, cptc::as_stream(stream), d_F,
+                       int(rows), R, d_lambda, d_grams, ngram, mode, next, d_FtF, d_FtV,
+                       next >= 0 ? int(nzero) : 0);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

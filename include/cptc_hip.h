@@ -616,6 +616,17 @@ int cptc_mttkrp_units_nd_cws(int slot, const uint32_t* d_unit6, uint64_t nunits,
                              const double* d_F1, const double* d_F2, int dim0, int dim1, int dim2,
                              double* d_FtV, int R, void* d_ws, size_t ws_bytes, void* stream);
 
+/* A small factor's update tail in one launch (rows x R <= 65536, R <= 32):
+ * cptc_gen_normalize, then the Gram of the normalised factor into
+ * d_grams + mode * R * R (cptc_gram), then, when next >= 0, the next mode's
+ * d_FtF = prod_{g != next} G_g (cptc_gram_hadamard) and d_FtV[0 .. nzero)
+ * zeroed.  The same values up to the order of the sums.  The generic
+ * driver's update of such factors; no reference counterpart (the reference
+ * launches these steps separately: generic.cu:2040-2060 and 2139-2171). */
+int cptc_gen_normalize_gram(double* d_F, size_t rows, int R, double* d_lambda, double* d_grams,
+                            int ngram, int mode, int next, double* d_FtF, double* d_FtV,
+                            size_t nzero, void* stream);
+
 /* out = prod_{g != skip} G_g over `ngram` consecutive R x R Grams (all ones
  * when none remain): g_fill_kernel + g_mul_kernel, generic.cu:2044-2052. */
 int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double* d_out,

@@ -495,6 +495,54 @@ def test_chol_ridge_singular_pivot(ca, orc, dev):
     assert rel_err(out.numpy(), ref) <= 1e-6
 
 
+@pytest.mark.parametrize("rows,R,next_", [(1, 1, 2), (37, 5, 2), (64, 32, 0), (200, 16, -1),
+                                           (2048, 32, 3), (65, 12, 2)])
+def test_gen_normalize_gram(ca, dev, rows, R, next_):
+    """The fused small-factor update (cptc_gen_normalize_gram): lambda and the
+    normalised factor as numpy's column norms (a zero column keeps norm 1),
+    the Gram of the normalised factor, the next mode's Hadamard product of
+    the other Grams in mode order, FtV zeroed over exactly nzero entries."""
+    rng = np.random.default_rng(rows * 100 + R)
+    F = rng.standard_normal((rows, R))
+    if R > 3:
+        F[:, 3] = 0.0
+    ngram, mode = 4, 1
+    G = rng.standard_normal((ngram, R, R))
+    dF, lam, dG = dbuf(ca, F), ca.DevBuf.zeros(R), dbuf(ca, G)
+    ftf = ca.DevBuf.zeros((R, R))
+    nz = 3 * R + 1
+    ftv0 = rng.standard_normal(nz + 17)
+    ftv = dbuf(ca, ftv0)
+    assert ca.lib.cptc_gen_normalize_gram(dF.data_ptr(), rows, R, lam.data_ptr(), dG.data_ptr(),
+                                          ngram, mode, next_, ftf.data_ptr(), ftv.data_ptr(), nz,
+                                          None) == 0, ca.lib.cptc_last_error()
+    ca.sync()
+    n = np.linalg.norm(F, axis=0)
+    n[~np.isfinite(n) | (n < 1e-14)] = 1.0
+    Fn = F / n
+    assert rel_err(lam.numpy(), n) <= 1e-14
+    assert rel_err(dF.numpy(), Fn) <= 1e-14
+    Gm = Fn.T @ Fn
+    got = dG.numpy().reshape(ngram, R, R)
+    assert rel_err(got[mode], Gm) <= 1e-13
+    for g in range(ngram):
+        if g != mode:
+            assert np.array_equal(got[g], G[g])
+    if next_ >= 0:
+        ref = np.ones((R, R))
+        for g in range(ngram):
+            if g != next_:
+                ref = ref * got[g]
+        assert np.array_equal(ftf.numpy(), ref)   # the kernel's own Gram, in mode order
+        assert np.all(ftv.numpy()[:nz] == 0.0) and np.array_equal(ftv.numpy()[nz:], ftv0[nz:])
+    else:
+        assert np.all(ftf.numpy() == 0.0) and np.array_equal(ftv.numpy(), ftv0)
+    # sizes past the one-workgroup limit are an error, not a launch
+    assert ca.lib.cptc_gen_normalize_gram(dF.data_ptr(), 70000, R, lam.data_ptr(), dG.data_ptr(),
+                                          ngram, mode, next_, ftf.data_ptr(), ftv.data_ptr(), nz,
+                                          None) != 0
+
+
 def test_normalize_hadamard_residual(ca, orc, dev):
     rng = np.random.default_rng(2)
     R = 12
