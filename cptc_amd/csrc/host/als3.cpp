@@ -84,6 +84,7 @@ struct Als3
     double* d_lambda = nullptr;
     double* d_G = nullptr;  // 3 x R x R
     bool gram_ok[3] = {false, false, false};
+    int ftf_for = -1;   // the mode whose FtF (Hadamard of the other Grams) is in d_FtF
     double* d_FtF = nullptr;
     double* d_Ainv = nullptr;  // pinv(FtF) of the mode being updated
     double* d_FtV = nullptr;
@@ -564,8 +565,20 @@ int update_mode(Als3& h, int mode)
     // lambda; column norms, normalise + absorb and this mode's Gram refresh
     // from one Gram of the unnormalised factor (als.cu:480-517)
     CPTC_TRY(cptc_apply_pinv(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.d_lambda, h.s));
-    CPTC_TRY(cptc_gram_normalize_absorb(h.F[mode], dim, R, h.G(mode), h.d_norms, h.d_lambda,
-                                        h.s));
+    // R <= 32: the Gram's sums, norms and normalisation in one workgroup, with
+    // the next mode's FtF (its other Gram is current) from the same launch
+    const int next = (mode + 1) % 3, other = 3 - next - mode;
+    if (R <= 32 && dim >= 1)
+    {
+        const bool fuse = h.gram_ok[other];
+        CPTC_TRY(cptc_gram_normalize_absorb_next(h.F[mode], dim, R, h.G(mode), h.d_norms,
+                                                 h.d_lambda, fuse ? h.G(other) : nullptr,
+                                                 fuse ? h.d_FtF : nullptr, h.s));
+        h.ftf_for = fuse ? next : -1;
+    }
+    else
+        CPTC_TRY(cptc_gram_normalize_absorb(h.F[mode], dim, R, h.G(mode), h.d_norms, h.d_lambda,
+                                            h.s));
     h.gram_ok[mode] = true;
     return CPTC_OK;
 }
@@ -586,7 +599,8 @@ int enqueue_iteration(Als3& h, double* d_out)
                 CPTC_TRY(cptc_gram(h.F[g], h.dims[g], R, h.G(g), h.s));
                 h.gram_ok[g] = true;
             }
-        CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+        if (h.ftf_for != mode) CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+        h.ftf_for = -1;
         CPTC_HIP(hipEventRecord(h.ev_cur[1 + 2 * mode], h.s));
         CPTC_TRY(mttkrp_launch(h, mode, true));
         CPTC_HIP(hipEventRecord(h.ev_cur[2 + 2 * mode], h.s));
@@ -938,6 +952,7 @@ extern "C" int cptc_als3_sgd(void* handle, int iters, double gamma, uint32_t bat
                                  h->dims, h->d_lambda, h->R, iters, gamma, batch, seed,
                                  h->o.verbose, batch_rmse, h->s);
     for (bool& g : h->gram_ok) g = false;   // the factors changed
+    h->ftf_for = -1;
     return rc;
 }
 
@@ -998,6 +1013,7 @@ extern "C" int cptc_als3_set_factor(void* handle, int mode, const double* host_i
                             hipMemcpyHostToDevice, h->s));
     CPTC_HIP(hipStreamSynchronize(h->s));
     h->gram_ok[mode] = false;
+    h->ftf_for = -1;
     return CPTC_OK;
 }
 

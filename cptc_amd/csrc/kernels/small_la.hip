@@ -828,6 +828,39 @@ __global__ __launch_bounds__(FIT_T) void gram_norms_absorb_kernel(double* __rest
     }
 }
 
+// R <= 32, one workgroup: the partial Gram sums of cptc_gram (the same
+// ordered sums), then gram_norms_absorb_kernel's norms, lambda and
+// normalisation, then, when `other` is given, the next mode's FtF = G .*
+// other (hadamard_kernel; the product commutes bit for bit).  Two and, with
+// the product, three launches in one.
+__global__ __launch_bounds__(FIT_T) void gram_finish_small_kernel(
+    const double* __restrict__ part, int P, int R, double* __restrict__ G,
+    double* __restrict__ norms, double* __restrict__ lambda, const double* __restrict__ other,
+    double* __restrict__ FtF)
+{
+    __shared__ double g_l[32 * 32];
+    __shared__ double n_l[32];
+    const int RR = R * R;
+    const int x = threadIdx.x;
+    if (x < RR) g_l[x] = ordered_sum(part, P, size_t(RR), size_t(x));
+    __syncthreads();
+    if (x < R)
+    {
+        const double n = sqrt(g_l[x * R + x]);
+        n_l[x] = n;
+        norms[x] = n;
+        lambda[x] = (n < 1e-14) ? 0.0 : lambda[x] * n;
+    }
+    __syncthreads();
+    if (x < RR)
+    {
+        const double ni = n_l[x / R], nj = n_l[x % R];
+        const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : g_l[x] / (ni * nj);
+        G[x] = v;
+        if (other) FtF[x] = v * other[x];
+    }
+}
+
 // F[:, r] /= n_r (0 when n_r < 1e-14)
 __global__ void scale_columns_kernel(double* __restrict__ F, size_t rows, int R,
                                      const double* __restrict__ norms)
@@ -905,6 +938,36 @@ extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, doubl
                        d_lambda);
     CPTC_LAUNCHED();
     if (rows == 0) return CPTC_OK;
+    hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
+                       dim3(256), 0, s, d_F, rows, R, d_norms);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G,
+                                               double* d_norms, double* d_lambda,
+                                               const double* d_other, double* d_FtF, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 32 && d_F && d_G && d_norms && d_lambda && rows >= 1 &&
+                     (d_other == nullptr) == (d_FtF == nullptr),
+                 CPTC_ERR_ARG, "cptc_gram_normalize_absorb_next: bad arguments (R <= 32)");
+    hipStream_t s = cptc::as_stream(stream);
+    const size_t RR = size_t(R) * R;
+    const int P = partials_for(rows, 64);
+    const size_t rpw = (rows + P - 1) / P;
+    void* part = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(P) * RR * sizeof(double), &part));
+    double* pd = static_cast<double*>(part);
+    if (R <= 16)
+        hipLaunchKernelGGL(gram_partial_kernel<1>, dim3(P, 1), dim3(256), 0, s, d_F, rows, R, rpw,
+                           1, pd);
+    else
+        hipLaunchKernelGGL(gram_partial_kernel<2>, dim3(P, 1), dim3(256), 0, s, d_F, rows, R, rpw,
+                           1, pd);
+    CPTC_LAUNCHED();
+    hipLaunchKernelGGL(gram_finish_small_kernel, dim3(1), dim3(FIT_T), 0, s, pd, P, R, d_G,
+                       d_norms, d_lambda, d_other, d_FtF);
+    CPTC_LAUNCHED();
     hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
                        dim3(256), 0, s, d_F, rows, R, d_norms);
     CPTC_LAUNCHED();

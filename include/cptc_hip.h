@@ -248,6 +248,14 @@ int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, void* stream);
  * R <= 1024. */
 int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G, double* d_norms,
                                double* d_lambda, void* stream);
+/* The same for R <= 32 and rows >= 1 with the Gram's partial sums, the norms
+ * and the normalisation of G in one workgroup launch, and, when d_other is
+ * given (with d_FtF), the next mode's d_FtF = G .* d_other (cptc_hadamard)
+ * from the same launch.  Bit for bit the results of cptc_gram_normalize_absorb
+ * + cptc_hadamard.  No reference counterpart. */
+int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G,
+                                    double* d_norms, double* d_lambda, const double* d_other,
+                                    double* d_FtF, void* stream);
 
 /* C = A o B elementwise over n doubles (C may alias A or B).
  * Replaces elementwise_mult_kernel (als.cu:101-106) and g_mul_kernel

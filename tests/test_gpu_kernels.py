@@ -548,6 +548,45 @@ def test_gram_normalize_absorb_matches_steps(ca, dev, R):
     assert np.all(G2.numpy()[3] == 0.0) and np.all(G2.numpy()[:, 3] == 0.0)
 
 
+@pytest.mark.parametrize("R,rows", [(1, 5), (8, 2003), (17, 64), (32, 512), (32, 1)])
+def test_gram_normalize_absorb_next(ca, dev, R, rows):
+    """The one-workgroup Gram finish for R <= 32 (cptc_gram_normalize_absorb_next)
+    gives cptc_gram_normalize_absorb's factor, norms, lambda and Gram bit for
+    bit, and with d_other the next mode's FtF equal to cptc_hadamard of the
+    new Gram and the other one (zero column included)."""
+    rng = np.random.default_rng(R * 7 + rows)
+    F = rng.standard_normal((rows, R))
+    if R > 3:
+        F[:, 3] = 0.0
+    lam = rng.random(R) + 0.1
+    other = rng.standard_normal((R, R))
+    a_F, a_l = to_dev(ca, F), to_dev(ca, lam)
+    n1, G1, H1 = zeros(ca, (R,)), zeros(ca, (R, R)), zeros(ca, (R, R))
+    assert ca.lib.cptc_gram_normalize_absorb(a_F.data_ptr(), rows, R, G1.data_ptr(),
+                                             n1.data_ptr(), a_l.data_ptr(), stream(ca)) == 0
+    d_o = to_dev(ca, other)
+    assert ca.lib.cptc_hadamard(G1.data_ptr(), d_o.data_ptr(), H1.data_ptr(), R * R,
+                                stream(ca)) == 0
+    for with_next in (True, False):
+        b_F, b_l = to_dev(ca, F), to_dev(ca, lam)
+        n2, G2, H2 = zeros(ca, (R,)), zeros(ca, (R, R)), zeros(ca, (R, R))
+        rc = ca.lib.cptc_gram_normalize_absorb_next(
+            b_F.data_ptr(), rows, R, G2.data_ptr(), n2.data_ptr(), b_l.data_ptr(),
+            d_o.data_ptr() if with_next else None, H2.data_ptr() if with_next else None,
+            stream(ca))
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        for got, ref in ((b_F, a_F), (n2, n1), (b_l, a_l), (G2, G1)):
+            assert np.array_equal(got.numpy(), ref.numpy())
+        if with_next:
+            assert np.array_equal(H2.numpy(), H1.numpy())
+        else:
+            assert np.all(H2.numpy() == 0.0)
+    assert ca.lib.cptc_gram_normalize_absorb_next(b_F.data_ptr(), rows, 33, G2.data_ptr(),
+                                                  n2.data_ptr(), b_l.data_ptr(), None, None,
+                                                  stream(ca)) != 0
+
+
 @pytest.mark.parametrize("R", [1, 7, 32, 100])
 def test_sparse_mttkrp_range(ca, orc, dev, R):
     """compute_sparse_mttkrp_async's sub-range path (sparse.cu:877-955):
