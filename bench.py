@@ -223,7 +223,7 @@ def main() -> int:
     # a queued run records kernel events on every 8th iteration and its last
     assert kit == sum(1 for it in range(args.steps) if it % 8 == 0 or it == args.steps - 1)
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter (host wall), event median "
-        f"{float(np.median(ms_iter)):.3f} ms, MTTKRP median {float(np.median(ms_mtt)):.3f} ms, "
+        f"{float(np.median(ms_iter)):.3f} ms, MTTKRP median {float(np.nanmedian(ms_mtt)) if np.isfinite(ms_mtt).any() else float('nan'):.3f} ms, "
         f"fit {fits[-1]:.6f}")
 
     dims = t.dims

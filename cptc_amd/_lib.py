@@ -71,6 +71,7 @@ class Als3Info(C.Structure):
         ("tiles_beside", C.c_int),
         ("tile_compact", C.c_int),
         ("tile_segments", C.c_uint64 * 3),
+        ("graph_mode", C.c_int),
     ]
 
 
@@ -155,6 +156,7 @@ SIGNATURES = {
     "cptc_dense_tiles_pack3": (_I, [_P, _P, _P, _Z, _P, _P]),
     "cptc_gram": (_I, [_P, _Z, _I, _P, _P]),
     "cptc_gram_normalize_absorb": (_I, [_P, _Z, _I, _P, _P, _P, _P]),
+    "cptc_zero": (_I, [_P, _Z, _P]),
     "cptc_gram_normalize_absorb_next": (_I, [_P, _Z, _I, _P, _P, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),

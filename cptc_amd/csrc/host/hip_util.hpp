@@ -71,5 +71,8 @@ inline unsigned grid_for(size_t n, unsigned block, unsigned cap = 1u << 20)
 // time within one entry point.
 enum ScratchSlot { SCR_GRAM = 0, SCR_PINV, SCR_FLAGS, SCR_REDUCE, SCR_LAYOUT_A, SCR_LAYOUT_B, SCR_NSLOTS };
 int scratch_get(int slot, size_t bytes, void** out);
+// Changes whenever a scratch buffer is (re)allocated: a captured HIP graph
+// that holds scratch addresses is replayed only while it is unchanged.
+uint64_t scratch_generation();
 
 }  // namespace cptc

@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -39,7 +40,11 @@ ScratchTable& table()
     static ScratchTable t;
     return t;
 }
+
+std::atomic<uint64_t> g_scratch_gen{0};
 }  // namespace
+
+uint64_t scratch_generation() { return g_scratch_gen.load(); }
 
 void set_error(const char* fmt, ...)
 {
@@ -73,6 +78,7 @@ int scratch_get(int slot, size_t bytes, void** out)
         want = (want + 4095) & ~size_t(4095);
         CPTC_HIP(hipMalloc(&b.ptr, want));
         b.bytes = want;
+        ++g_scratch_gen;   // captured graphs that hold the old address are stale
     }
     *out = b.ptr;
     return CPTC_OK;

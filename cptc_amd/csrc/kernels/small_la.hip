@@ -861,6 +861,13 @@ __global__ __launch_bounds__(FIT_T) void gram_finish_small_kernel(
     }
 }
 
+__global__ void zero_kernel(double* __restrict__ p, size_t n)
+{
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
+         x += size_t(gridDim.x) * blockDim.x)
+        p[x] = 0.0;
+}
+
 // F[:, r] /= n_r (0 when n_r < 1e-14)
 __global__ void scale_columns_kernel(double* __restrict__ F, size_t rows, int R,
                                      const double* __restrict__ norms)
@@ -970,6 +977,16 @@ extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, 
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
                        dim3(256), 0, s, d_F, rows, R, d_norms);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_zero(double* d_p, size_t n, void* stream)
+{
+    if (n == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_p, CPTC_ERR_ARG, "cptc_zero: null pointer");
+    hipLaunchKernelGGL(zero_kernel, dim3(cptc::grid_for(n, 256, 2048)), dim3(256), 0,
+                       cptc::as_stream(stream), d_p, n);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

@@ -248,6 +248,10 @@ int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, void* stream);
  * R <= 1024. */
 int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G, double* d_norms,
                                double* d_lambda, void* stream);
+/* d_p[0 .. n) = 0 by a kernel (a hipMemsetAsync node in a captured HIP graph
+ * is what the drivers' graph path avoids).  No reference counterpart. */
+int cptc_zero(double* d_p, size_t n, void* stream);
+
 /* The same for R <= 32 and rows >= 1 with the Gram's partial sums, the norms
  * and the normalisation of G in one workgroup launch, and, when d_other is
  * given (with d_FtF), the next mode's d_FtF = G .* d_other (cptc_hadamard)
@@ -446,6 +450,7 @@ typedef struct cptc_als3_info {
     int tiles_beside;         /* 1 = tile kernel on a side stream beside the FP64 kernel */
     int tile_compact;         /* 1 = the split-bf16 kernel reads the compacted tile images */
     uint64_t tile_segments[3];  /* 16-byte segments of mode m's compacted split image (0: none) */
+    int graph_mode;           /* 1 = quiet runs replay one captured iteration (HIP graph) */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
@@ -454,7 +459,12 @@ int cptc_als3_info_get(void* handle, cptc_als3_info* info);
  * als.cu:613, 722-726), ms of MTTKRP per iteration (sum over modes).  With
  * opts.verbose the host waits after every iteration and prints the
  * reference's "[ALS] iter" line; otherwise every iteration is queued and the
- * host waits once at the end. */
+ * host waits once at the end.  In graph mode (cptc_als3_info.graph_mode:
+ * ALS_GRAPH=1, or automatically when nnz x R < 2^30) a queued run replays
+ * one captured steady-state iteration for every iteration except every 8th
+ * and the last (those run eagerly with their events): the same launches and
+ * results, one graph launch instead of ~40 queue operations; a replayed
+ * iteration's MTTKRP time is NaN. */
 int cptc_als3_run(void* handle, int iters, double* fit, float* ms_iter, float* ms_mttkrp);
 
 /* Kernel times accumulated over cptc_als3_run iterations (hipEvents on the
