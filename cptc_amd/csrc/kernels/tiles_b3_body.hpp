@@ -370,7 +370,14 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             if constexpr (HAS_W) tot *= wr;
             if constexpr (GROUPED)
             {
-                gacc[arow(o) * gstride + gcol(rb)] += tot;
+                // LDS atomic add without return (ds_add_f64): the eight
+                // updates do not wait on each other as read-add-write chains
+                // through one register pair do (each entry has one owner
+                // lane, whose LDS operations stay in order, so the sum is
+                // the plain one).  Config 3: 0.37-0.38 -> 0.356-0.367 ms per
+                // launch; config 5 units 0.080-0.091 -> 0.079-0.089 ms.
+                __hip_atomic_fetch_add(&gacc[arow(o) * gstride + gcol(rb)], tot, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             else
             {

@@ -214,8 +214,12 @@ __device__ __forceinline__ void dense_tiles_body(
             }
             if constexpr (GROUPED)
             {
+                // LDS atomic adds without return (ds_add_f64), not
+                // read-add-write chains; one owner lane per entry
 #pragma unroll
-                for (int v = 0; v < 4; ++v) gacc[(4 * hi + v) * Rp + r] += tot[v];
+                for (int v = 0; v < 4; ++v)
+                    __hip_atomic_fetch_add(&gacc[(4 * hi + v) * Rp + r], tot[v], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
             }
             else
             {
