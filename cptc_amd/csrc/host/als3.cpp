@@ -584,7 +584,10 @@ int update_mode(Als3& h, int mode)
     // from one Gram of the unnormalised factor (als.cu:480-517)
     CPTC_TRY(cptc_apply_pinv(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.d_lambda, h.s));
     // R <= 32: the Gram's sums, norms and normalisation in one workgroup, with
-    // the next mode's FtF (its other Gram is current) from the same launch
+    // the next mode's FtF (its other Gram is current) from the same launch.
+    // Above that the FtF product inside the one-workgroup normalisation
+    // measured slower (config 3: 18-20 us per launch against 11-12 us plus a
+    // 4 us Hadamard launch), so the Hadamard stays a grid launch.
     const int next = (mode + 1) % 3, other = 3 - next - mode;
     if (R <= 32 && dim >= 1)
     {

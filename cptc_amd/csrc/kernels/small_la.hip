@@ -686,27 +686,28 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const double* __restri
     for (int rb = 0; rb < R; rb += lanes)
     {
         const int r = rb + rl;
-        // four independent chains over rows i = r_lo + sub + k * rows_per_pass
-        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+        // eight independent chains over rows i = r_lo + sub + k * rows_per_pass
+        // (eight rows' loads in flight per thread)
+        double s8[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
         if (sub < rows_per_pass && r < R)
         {
             size_t i = r_lo + sub;
             const size_t step = size_t(rows_per_pass);
-            for (; i + 3 * step < r_hi; i += 4 * step)
+            for (; i + 7 * step < r_hi; i += 8 * step)
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
+                for (int k = 0; k < 8; ++k)
                 {
                     const size_t ii = i + size_t(k) * step;
                     const double f = F[ii * R + r];
-                    s4[k] += M ? f * M[ii * R + r] : f * f;
+                    s8[k] += M ? f * M[ii * R + r] : f * f;
                 }
             for (int k = 0; i < r_hi; i += step, ++k)
             {
                 const double f = F[i * R + r];
-                s4[k] += M ? f * M[i * R + r] : f * f;
+                s8[k] += M ? f * M[i * R + r] : f * f;
             }
         }
-        red[threadIdx.x] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        red[threadIdx.x] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
         __syncthreads();
         if (threadIdx.x < lanes && rb + threadIdx.x < R)
         {
@@ -772,12 +773,22 @@ __global__ __launch_bounds__(FIT_T) void fit_finalize_kernel(const double* __res
                                                              int ngram, double* __restrict__ out2)
 {
     __shared__ double red[FIT_T];
+    __shared__ double lam[FIT_T];
     const int tid = threadIdx.x;
+    if (tid < R) lam[tid] = lambda[tid];
     const int C = FIT_T / R;   // chunks of partials per rank
     const int r = tid % R, c = tid / R;
-    double d = 0.0;
+    // eight independent accumulators (partials p, p + C, ... loaded together)
+    double d8[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     if (c < C)
-        for (int p = c; p < P; p += C) d += part[size_t(p) * R + r];
+    {
+        int p = c;
+        for (; p + 7 * C < P; p += 8 * C)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) d8[q] += part[size_t(p + q * C) * R + r];
+        for (int q = 0; p < P; p += C, ++q) d8[q] += part[size_t(p) * R + r];
+    }
+    const double d = ((d8[0] + d8[1]) + (d8[2] + d8[3])) + ((d8[4] + d8[5]) + (d8[6] + d8[7]));
     red[tid] = (c < C) ? d : 0.0;
     __syncthreads();
     double ip = 0.0;
@@ -785,18 +796,32 @@ __global__ __launch_bounds__(FIT_T) void fit_finalize_kernel(const double* __res
     {
         double t = 0.0;
         for (int q = 0; q < C; ++q) t += red[q * R + tid];
-        ip = lambda[tid] * t;
+        ip = lam[tid] * t;
     }
     __syncthreads();
     const double iprod = block_sum(ip, red);
-    double md = 0.0;
-    const int RR = R * R;
-    for (int x = tid; x < RR; x += FIT_T)
+    // thread t: column c = t % R of rows t / R, t / R + T / R, ... (no index
+    // division per entry), four independent accumulators
+    double m4[4] = {0.0, 0.0, 0.0, 0.0};
+    const size_t RR = size_t(R) * R;
+    const int rpp = FIT_T / R;
+    const int cc = tid % R, r0 = tid / R;
+    if (r0 < rpp)
     {
-        double v = lambda[x / R] * lambda[x % R];
-        for (int g = 0; g < ngram; ++g) v *= grams[size_t(g) * RR + x];
-        md += v;
+        const double lc = lam[cc];
+        auto term = [&](int i) {
+            const size_t x = size_t(i) * R + cc;
+            double v = lam[i] * lc;
+            for (int g = 0; g < ngram; ++g) v *= grams[size_t(g) * RR + x];
+            return v;
+        };
+        int i = r0;
+        for (; i + 3 * rpp < R; i += 4 * rpp)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) m4[q] += term(i + q * rpp);
+        for (int q = 0; i < R; i += rpp, ++q) m4[q] += term(i);
     }
+    const double md = (m4[0] + m4[1]) + (m4[2] + m4[3]);
     const double model2 = block_sum(md, red);
     if (tid == 0)
     {
@@ -808,24 +833,42 @@ __global__ __launch_bounds__(FIT_T) void fit_finalize_kernel(const double* __res
 // The Gram of the normalised factor from the Gram of the unnormalised one
 // (als.cu:308-342 with the Gram refresh after it): n_r = sqrt(G_rr);
 // lambda_r *= n_r and G_rs /= n_r n_s, with a column of norm < 1e-14 set to
-// zero (its lambda and its Gram row / column too).  One block.
+// zero (its lambda and its Gram row / column too); when `other` is given,
+// also the next mode's FtF = G .* other (hadamard_kernel's product, bit for
+// bit).  One block; thread t keeps column t % R of rows t / R, t / R + T / R,
+// ... (no index division per entry), the norms in LDS.
 __global__ __launch_bounds__(FIT_T) void gram_norms_absorb_kernel(double* __restrict__ G, int R,
                                                                   double* __restrict__ norms,
-                                                                  double* __restrict__ lambda)
+                                                                  double* __restrict__ lambda,
+                                                                  const double* __restrict__ other,
+                                                                  double* __restrict__ FtF)
 {
+    __shared__ double nl[FIT_T];
     for (int r = threadIdx.x; r < R; r += FIT_T)
     {
         const double n = sqrt(G[size_t(r) * R + r]);
         norms[r] = n;
+        nl[r] = n;
         lambda[r] = (n < 1e-14) ? 0.0 : lambda[r] * n;
     }
     __syncthreads();
-    const int RR = R * R;
-    for (int x = threadIdx.x; x < RR; x += FIT_T)
-    {
-        const double ni = norms[x / R], nj = norms[x % R];
-        G[x] = (ni < 1e-14 || nj < 1e-14) ? 0.0 : G[x] / (ni * nj);
-    }
+    const int rpp = FIT_T / R;   // rows per pass (R <= FIT_T)
+    const int c = int(threadIdx.x) % R, r0 = int(threadIdx.x) / R;
+    if (r0 >= rpp) return;
+    const double nj = nl[c];
+    auto one = [&](int i) {
+        const size_t x = size_t(i) * R + c;
+        const double ni = nl[i];
+        const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : G[x] / (ni * nj);
+        G[x] = v;
+        if (other) FtF[x] = v * other[x];
+    };
+    // four rows per round (their loads issued together)
+    int i = r0;
+    for (; i + 3 * rpp < R; i += 4 * rpp)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) one(i + q * rpp);
+    for (; i < R; i += rpp) one(i);
 }
 
 // R <= 32, one workgroup: the partial Gram sums of cptc_gram (the same
@@ -942,7 +985,7 @@ extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, doubl
     hipStream_t s = cptc::as_stream(stream);
     CPTC_TRY(cptc_gram(d_F, rows, R, d_G, s));
     hipLaunchKernelGGL(gram_norms_absorb_kernel, dim3(1), dim3(FIT_T), 0, s, d_G, R, d_norms,
-                       d_lambda);
+                       d_lambda, nullptr, nullptr);
     CPTC_LAUNCHED();
     if (rows == 0) return CPTC_OK;
     hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
@@ -955,10 +998,24 @@ extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, 
                                                double* d_norms, double* d_lambda,
                                                const double* d_other, double* d_FtF, void* stream)
 {
-    CPTC_REQUIRE(R >= 1 && R <= 32 && d_F && d_G && d_norms && d_lambda && rows >= 1 &&
+    CPTC_REQUIRE(R >= 1 && R <= FIT_T && d_F && d_G && d_norms && d_lambda && rows >= 1 &&
                      (d_other == nullptr) == (d_FtF == nullptr),
-                 CPTC_ERR_ARG, "cptc_gram_normalize_absorb_next: bad arguments (R <= 32)");
+                 CPTC_ERR_ARG, "cptc_gram_normalize_absorb_next: bad arguments (R <= %d)", FIT_T);
     hipStream_t s = cptc::as_stream(stream);
+    if (R > 32)
+    {
+        // cptc_gram, then the norms, normalisation and the next mode's FtF in
+        // one launch (cptc_gram_normalize_absorb + cptc_hadamard, same bits)
+        CPTC_TRY(cptc_gram(d_F, rows, R, d_G, s));
+        hipLaunchKernelGGL(gram_norms_absorb_kernel, dim3(1), dim3(FIT_T), 0, s, d_G, R, d_norms,
+                           d_lambda, d_other, d_FtF);
+        CPTC_LAUNCHED();
+        hipLaunchKernelGGL(scale_columns_kernel,
+                           dim3(cptc::grid_for(rows * size_t(R), 256, 4096)), dim3(256), 0, s,
+                           d_F, rows, R, d_norms);
+        CPTC_LAUNCHED();
+        return CPTC_OK;
+    }
     const size_t RR = size_t(R) * R;
     const int P = partials_for(rows, 64);
     const size_t rpw = (rows + P - 1) / P;
@@ -1166,7 +1223,9 @@ namespace {
 int col_reduce(const double* F, const double* M, size_t rows, int R, hipStream_t s, double** part,
                int* P_out)
 {
-    const int P = partials_for(rows, 256);
+    // up to 256 workgroups of >= 64 rows (113 of 256 rows left the column
+    // sums of a 28818-row factor latency-bound at 46 us)
+    const int P = partials_for(rows, 64);
     const size_t rpw = (rows + P - 1) / P;
     void* buf = nullptr;
     CPTC_TRY(cptc::scratch_get(cptc::SCR_REDUCE, size_t(P) * R * sizeof(double), &buf));

@@ -252,11 +252,11 @@ int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G, dou
  * is what the drivers' graph path avoids).  No reference counterpart. */
 int cptc_zero(double* d_p, size_t n, void* stream);
 
-/* The same for R <= 32 and rows >= 1 with the Gram's partial sums, the norms
- * and the normalisation of G in one workgroup launch, and, when d_other is
- * given (with d_FtF), the next mode's d_FtF = G .* d_other (cptc_hadamard)
- * from the same launch.  Bit for bit the results of cptc_gram_normalize_absorb
- * + cptc_hadamard.  No reference counterpart. */
+/* The same for R <= 1024 and rows >= 1, and, when d_other is given (with
+ * d_FtF), the next mode's d_FtF = G .* d_other (cptc_hadamard) from the
+ * launch that normalises G; for R <= 32 the Gram's partial sums, the norms and
+ * the normalisation of G run in one workgroup launch.  Bit for bit the results
+ * of cptc_gram_normalize_absorb + cptc_hadamard.  No reference counterpart. */
 int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G,
                                     double* d_norms, double* d_lambda, const double* d_other,
                                     double* d_FtF, void* stream);

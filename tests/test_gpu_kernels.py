@@ -383,6 +383,28 @@ def test_gram(ca, dev, rows, R):
     assert rel_err(G.numpy(), F.T @ F) < 1e-13 if rows else np.all(G.numpy() == 0)
 
 
+@pytest.mark.parametrize("R,dim", [(64, 100), (65, 1), (65, 77), (100, 1000), (127, 63),
+                                   (128, 28818), (128, 17), (129, 300)])
+def test_apply_pinv_vs_numpy(ca, dev, R, dim):
+    """cptc_apply_pinv: F = Y Ainv / div (the per-entry kernel up to R = 64,
+    the 64 x 64 tiled one above) against numpy, with ragged R and row counts
+    (partial tiles), with and without the divisor."""
+    rng = np.random.default_rng(R * 1000 + dim)
+    Y = rng.standard_normal((dim, R))
+    A = rng.standard_normal((R, R))
+    div = rng.random(R) + 0.5
+    dY, dA, dd = to_dev(ca, Y), to_dev(ca, A), to_dev(ca, div)
+    for use_div in (True, False):
+        out = zeros(ca, (dim, R))
+        assert ca.lib.cptc_apply_pinv(dY.data_ptr(), dA.data_ptr(), out.data_ptr(), dim, R,
+                                      dd.data_ptr() if use_div else None, stream(ca)) == 0
+        ca.sync()
+        ref = Y @ A
+        if use_div:
+            ref = ref / div
+        assert rel_err(out.numpy(), ref) < 1e-13, use_div
+
+
 @pytest.mark.parametrize("R", [1, 5, 16, 17, 32, 33, 63, 64, 65, 100, 128, 129, 200])
 def test_solve_pinv_spd(ca, dev, R):
     rng = np.random.default_rng(R)
@@ -548,12 +570,14 @@ def test_gram_normalize_absorb_matches_steps(ca, dev, R):
     assert np.all(G2.numpy()[3] == 0.0) and np.all(G2.numpy()[:, 3] == 0.0)
 
 
-@pytest.mark.parametrize("R,rows", [(1, 5), (8, 2003), (17, 64), (32, 512), (32, 1)])
+@pytest.mark.parametrize("R,rows", [(1, 5), (8, 2003), (17, 64), (32, 512), (32, 1), (33, 700),
+                                    (100, 3001), (128, 28818), (128, 1)])
 def test_gram_normalize_absorb_next(ca, dev, R, rows):
-    """The one-workgroup Gram finish for R <= 32 (cptc_gram_normalize_absorb_next)
-    gives cptc_gram_normalize_absorb's factor, norms, lambda and Gram bit for
-    bit, and with d_other the next mode's FtF equal to cptc_hadamard of the
-    new Gram and the other one (zero column included)."""
+    """cptc_gram_normalize_absorb_next (one workgroup for R <= 32; above that
+    the Gram launches, then the norms, normalisation and FtF in one) gives
+    cptc_gram_normalize_absorb's factor, norms, lambda and Gram bit for bit,
+    and with d_other the next mode's FtF equal to cptc_hadamard of the new Gram
+    and the other one (zero column included)."""
     rng = np.random.default_rng(R * 7 + rows)
     F = rng.standard_normal((rows, R))
     if R > 3:
@@ -582,7 +606,7 @@ def test_gram_normalize_absorb_next(ca, dev, R, rows):
             assert np.array_equal(H2.numpy(), H1.numpy())
         else:
             assert np.all(H2.numpy() == 0.0)
-    assert ca.lib.cptc_gram_normalize_absorb_next(b_F.data_ptr(), rows, 33, G2.data_ptr(),
+    assert ca.lib.cptc_gram_normalize_absorb_next(b_F.data_ptr(), rows, 1025, G2.data_ptr(),
                                                   n2.data_ptr(), b_l.data_ptr(), None, None,
                                                   stream(ca)) != 0
 
