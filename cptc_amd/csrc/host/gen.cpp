@@ -511,8 +511,7 @@ struct Gen
                 CPTC_TRY(cptc_solve_pinv(d_FtF, d_FtV, d_F[n], dims[n], R, nullptr, s));
             else
             {
-                CPTC_TRY(cptc_chol_ridge_factor(d_FtF, d_L, R, s));
-                CPTC_TRY(cptc_chol_ridge_apply(d_L, d_FtV, d_F[n], dims[n], R, s));
+                CPTC_TRY(cptc_chol_ridge_solve(d_FtF, d_FtV, d_F[n], dims[n], R, s));
             }
             mark(mk++);
             // one workgroup pays while its Gram loop is short: <= 256 rows

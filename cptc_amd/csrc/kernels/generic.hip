@@ -464,6 +464,111 @@ __global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __rest
         if (i < R) out[i] = y[i];
 }
 
+// cptc_chol_ridge_factor + cptc_chol_ridge_apply in one launch, R <= RT <=
+// 32: each 64-lane workgroup (one wave) factors FtF + eps I itself, lane i
+// holding row i in registers and each step's pivot column passing through
+// LDS inside the wave, so no workgroup barrier (chol_factor_kernel's 2 R
+// barriers across four waves are most of its ~17 us at R = 32); every
+// operation is chol_factor_kernel's, in its order, so L is the same bits.
+// Then each lane solves one right-hand-side row as chol_apply_kernel.  The
+// grids are small (one workgroup per 64 rows), so the kernel takes registers
+// over occupancy (the row and the solve vector, 2 x 64 at RT = 32).
+template <int RT>
+__global__ __launch_bounds__(CHOL_T) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+chol_solve_wave_kernel(const double* __restrict__ FtF,
+                                                                 const double* __restrict__ FtV,
+                                                                 double* __restrict__ F,
+                                                                 size_t dim, int R)
+{
+    static_assert(RT <= 32 && CHOL_T == 64, "one wave, one row per lane");
+    __shared__ double L[RT][RT + 1];
+    __shared__ double colv[RT], lcol[RT];
+    __shared__ double trs;
+    const int lane = threadIdx.x;
+    const bool act = lane < RT;
+    const bool mine = lane < R;
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    double a[RT];
+#pragma unroll
+    for (int c = 0; c < RT; ++c) a[c] = (mine && c < R) ? FtF[size_t(lane) * R + c] : 0.0;
+    // eps from the trace, summed in row order (one lane)
+#pragma unroll
+    for (int c = 0; c < RT; ++c)
+        if (act && c == lane) colv[lane] = a[c];
+    wave_sync();
+    if (lane == 0)
+    {
+        double tr = 0.0;
+        for (int i = 0; i < R; ++i) tr += colv[i];
+        trs = tr;
+    }
+    wave_sync();
+    const double tr = trs;
+    const double eps = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
+#pragma unroll
+    for (int c = 0; c < RT; ++c)
+        if (c == lane) a[c] += eps;
+    // (fully unrolled, so the row stays in registers: a partly unrolled
+    // loop indexes it at run time and moves it to scratch memory)
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+    {
+        if (j < R)   // steps j < R only (uniform; no early exit, so the loop unrolls)
+        {
+            if (act) colv[lane] = a[j];
+            wave_sync();
+            const double sp = colv[j];
+            const double d = (sp > 0.0) ? sqrt(sp) : sqrt(eps);
+            const double v = a[j];
+            const double lij = (lane == j) ? d : ((mine && lane > j) ? v / d : v);
+            if (act) lcol[lane] = lij;
+            wave_sync();
+            a[j] = lij;
+#pragma unroll
+            for (int c = j + 1; c < RT; ++c) a[c] -= lij * lcol[c];
+            wave_sync();   // this step's reads before the next step's writes
+        }
+    }
+    // L padded to RT with the identity (chol_apply_kernel's layout)
+    if (act)
+#pragma unroll
+        for (int c = 0; c < RT; ++c)
+            L[lane][c] = (mine && c < R) ? ((c <= lane) ? a[c] : 0.0) : (c == lane ? 1.0 : 0.0);
+    __syncthreads();
+    const size_t row = size_t(blockIdx.x) * CHOL_T + size_t(lane);
+    if (row >= dim) return;
+    const double* b = FtV + row * R;
+    double y[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+    {
+        double sum = y[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) sum -= L[i][k] * y[k];
+        y[i] = sum / L[i][i];
+        asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int i = RT - 1; i >= 0; --i)
+    {
+        double sum = y[i];
+#pragma unroll
+        for (int k = i + 1; k < RT; ++k) sum -= L[k][i] * y[k];
+        y[i] = sum / L[i][i];
+        asm volatile("" ::: "memory");
+    }
+    double* out = F + row * R;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+        if (i < R) out[i] = y[i];
+}
+
 // Column sums of squares: P partials of R each (deterministic).
 __global__ __launch_bounds__(256) void colsq_partial_kernel(const double* __restrict__ F,
                                                             size_t rows, int R,
@@ -806,11 +911,23 @@ extern "C" int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, d
     CPTC_REQUIRE(R >= 1 && R <= CHOL_RM, CPTC_ERR_ARG, "cptc_chol_ridge_solve: R %d (1..32)", R);
     if (dim == 0) return CPTC_OK;
     CPTC_REQUIRE(d_FtF && d_FtV && d_F, CPTC_ERR_ARG, "cptc_chol_ridge_solve: null pointer");
-    void* buf = nullptr;
-    CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, size_t(R) * R * sizeof(double), &buf));
-    double* L = static_cast<double*>(buf);
-    CPTC_TRY(cptc_chol_ridge_factor(d_FtF, L, R, stream));
-    return cptc_chol_ridge_apply(L, d_FtV, d_F, dim, R, stream);
+    CPTC_REQUIRE(dim / CHOL_T < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_chol_ridge_solve: %zu rows", dim);
+    // one launch: every workgroup factors (one wave, ~1-2 us) and solves its
+    // 64 rows; the same bits as cptc_chol_ridge_factor + cptc_chol_ridge_apply
+    const dim3 grid(unsigned((dim + CHOL_T - 1) / CHOL_T));
+    hipStream_t s = cptc::as_stream(stream);
+    if (R <= 8)
+        hipLaunchKernelGGL(chol_solve_wave_kernel<8>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV, d_F,
+                           dim, R);
+    else if (R <= 16)
+        hipLaunchKernelGGL(chol_solve_wave_kernel<16>, grid, dim3(CHOL_T), 0, s, d_FtF, d_FtV,
+                           d_F, dim, R);
+    else
+        hipLaunchKernelGGL(chol_solve_wave_kernel<CHOL_RM>, grid, dim3(CHOL_T), 0, s, d_FtF,
+                           d_FtV, d_F, dim, R);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
 }
 
 extern "C" int cptc_gen_normalize(double* d_F, size_t rows, int R, double* d_lambda, void* stream)

@@ -652,8 +652,10 @@ int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double
 
 /* F = FtV (FtF + eps I)^-1 per row by Cholesky, eps = 1e-12 * tr(FtF) / R +
  * 1e-300 (tr <= 0: 1e-12 + 1e-300); a pivot s <= 0 becomes sqrt(eps).
- * g_chol_solve_kernel, generic.cu:746-819.  R <= 32.  Runs
- * cptc_chol_ridge_factor into library scratch, then cptc_chol_ridge_apply. */
+ * g_chol_solve_kernel, generic.cu:746-819.  R <= 32.  One launch: each
+ * workgroup of 64 rows factors in one wave and solves its rows, with the
+ * same bits as cptc_chol_ridge_factor followed by cptc_chol_ridge_apply; no
+ * scratch memory. */
 int cptc_chol_ridge_solve(const double* d_FtF, const double* d_FtV, double* d_F, size_t dim,
                           int R, void* stream);
 

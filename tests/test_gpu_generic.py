@@ -452,31 +452,37 @@ def test_chol_ridge_solve(ca, orc, dev, R):
 
 
 @pytest.mark.parametrize("R", [1, 7, 16, 17, 32])
-def test_chol_ridge_factor_apply(ca, dev, R):
+@pytest.mark.parametrize("rows,rank_def", [(150, False), (1, False), (64, False), (65, False),
+                                           (1717, False), (150, True)])
+def test_chol_ridge_factor_apply(ca, dev, R, rows, rank_def):
     """The two halves of the ridge solve: L is the Cholesky factor of
     FtF + eps I (eps = 1e-12 tr / R + 1e-300), and factor + apply gives the
-    same bits as cptc_chol_ridge_solve."""
-    rng = np.random.default_rng(100 + R)
-    A = rng.random((3 * R + 5, R))
+    same bits as cptc_chol_ridge_solve (one launch: every 64-row workgroup
+    factors in one wave), for one and several workgroups and for a
+    rank-deficient FtF whose later pivots fall to the eps ridge."""
+    rng = np.random.default_rng(100 + R + rows)
+    A = rng.random(((R + 1) // 2 if rank_def else 3 * R + 5, R))
     FtF = A.T @ A
-    Y = rng.standard_normal((150, R))
+    Y = rng.standard_normal((rows, R))
     dA, dY = dbuf(ca, FtF), dbuf(ca, Y)
     L = ca.DevBuf.zeros((R, R))
-    out = ca.DevBuf.zeros((150, R))
-    ref = ca.DevBuf.zeros((150, R))
+    out = ca.DevBuf.zeros((rows, R))
+    ref = ca.DevBuf.zeros((rows, R))
     assert ca.lib.cptc_chol_ridge_factor(dA.data_ptr(), L.data_ptr(), R, None) == 0
-    assert ca.lib.cptc_chol_ridge_apply(L.data_ptr(), dY.data_ptr(), out.data_ptr(), 150, R,
+    assert ca.lib.cptc_chol_ridge_apply(L.data_ptr(), dY.data_ptr(), out.data_ptr(), rows, R,
                                         None) == 0
-    assert ca.lib.cptc_chol_ridge_solve(dA.data_ptr(), dY.data_ptr(), ref.data_ptr(), 150, R,
+    assert ca.lib.cptc_chol_ridge_solve(dA.data_ptr(), dY.data_ptr(), ref.data_ptr(), rows, R,
                                         None) == 0
     ca.sync()
-    eps = 1e-12 * np.trace(FtF) / R + 1e-300
-    Lref = np.linalg.cholesky(FtF + eps * np.eye(R))
     Lg = L.numpy()
     assert np.all(np.triu(Lg, 1) == 0.0)
-    assert rel_err(Lg, Lref) <= 1e-12
+    if not rank_def:
+        eps = 1e-12 * np.trace(FtF) / R + 1e-300
+        Lref = np.linalg.cholesky(FtF + eps * np.eye(R))
+        assert rel_err(Lg, Lref) <= 1e-12
+        assert rel_err(out.numpy(), np.linalg.solve(FtF + eps * np.eye(R), Y.T).T) <= 1e-10
+    assert np.all(np.isfinite(ref.numpy()))
     assert np.array_equal(out.numpy(), ref.numpy())
-    assert rel_err(out.numpy(), np.linalg.solve(FtF + eps * np.eye(R), Y.T).T) <= 1e-10
 
 
 def test_chol_ridge_singular_pivot(ca, orc, dev):
