@@ -353,8 +353,10 @@ int alloc_buffers(Als3& h);
 
 // Tiles of each mode grouped by target row block (at most TILE_GROUP per
 // wave, fewer when the tiles are few); only for the MFMA path at R <= 128
-// (the grouped kernel's LDS limit).
-constexpr int TILE_GROUP = 8;
+// (the grouped kernel's LDS limit).  Config 3 (split-bf16 tiles, LDS
+// atomic flushes): groups of 4 / 8 / 12 / 16 / 24 measured 0.41-0.42 /
+// 0.35-0.37 / 0.33-0.34 / 0.33-0.34 / 0.32-0.35 ms per launch.
+constexpr int TILE_GROUP = 16;
 
 int build_groups(Als3& h)
 {
