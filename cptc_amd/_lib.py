@@ -215,6 +215,8 @@ SIGNATURES = {
     "cptc_mttkrp_units_nd_ws": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I,
                                      _P, _I, _P, _Z, _P]),
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
+    "cptc_gen_unit_sums": (_I, [_P, _Z, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "cptc_gen_unit_scatter": (_I, [_P, _Z, _I, _I, _P, _P, _I, _Z, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_chol_ridge_factor": (_I, [_P, _P, _I, _P]),
     "cptc_chol_ridge_apply": (_I, [_P, _P, _P, _Z, _I, _P]),

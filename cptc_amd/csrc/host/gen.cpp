@@ -352,6 +352,14 @@ struct Gen
     uint32_t* d_ugoff[3] = {nullptr, nullptr, nullptr};
     size_t ungroups[3] = {0, 0, 0};
     bool w_dirty = true;
+    // every element in a dense unit (config 5): the outer modes' MTTKRP from
+    // per-unit inner sums (cptc_gen_unit_sums, formed once after the inner
+    // factors change) instead of the segment kernel over the same elements;
+    // GEN_UNIT_SUMS=0 keeps the segment kernel
+    bool unit_sums = false;
+    bool usum_ok = false;
+    double* d_usum = nullptr;          // nunits x R
+    double** d_Fo = nullptr;           // the outer modes' factors, device array of pointers
     std::vector<cptc::DevViewN> views;   // kernel views (dense elements dropped, rows sorted)
     std::vector<uint64_t> ref_nseg;      // segments of the reference-layout views
 
@@ -400,6 +408,8 @@ struct Gen
         for (auto& e : ev_pool) (void)hipEventDestroy(e);
         dfree(d_fit_hist);
         dfree(d_L);
+        dfree(d_usum);
+        if (d_Fo) (void)hipFree(d_Fo);
         if (s) (void)hipStreamDestroy(s);
     }
 
@@ -454,6 +464,26 @@ struct Gen
         {
             CPTC_HIP(hipEventRecord(ke[1], s));
             CPTC_HIP(hipEventRecord(ke[2], s));
+        }
+        if (unit_sums && !in)
+        {
+            const int* in3 = units.inner;
+            if (!usum_ok)
+            {
+                CPTC_TRY(cptc_gen_unit_sums(units.d_unit6, units.nunits, units.d_lid, units.d_val,
+                                            d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
+                                            int(dims[in3[0]]), int(dims[in3[1]]),
+                                            int(dims[in3[2]]), R, d_usum, s));
+                usum_ok = true;
+            }
+            int pos = 0;
+            while (units.outer[size_t(pos)] != n) ++pos;
+            CPTC_TRY(cptc_gen_unit_scatter(units.d_outer_coords, units.nunits,
+                                           int(units.outer.size()), pos,
+                                           const_cast<const double* const*>(d_Fo), d_usum, R, dims[n],
+                                           d_FtV, s));
+            if (timing) CPTC_HIP(hipEventRecord(ke[3], s));
+            return CPTC_OK;
         }
         const cptc::DevViewN& v = views[n];
         if (v.key_bytes > 0 && R % 2 == 0)
@@ -534,6 +564,7 @@ struct Gen
                 CPTC_TRY(cptc_gram(d_F[n], dims[n], R, d_grams + size_t(n) * RR, s));
             }
             if (dense && !(inner_mask & (1u << n))) w_dirty = true;
+            if (dense && (inner_mask & (1u << n))) usum_ok = false;
             mark(mk++);
         }
         return cptc_fit_gram(d_F[N - 1], d_FtV, dims[N - 1], d_lambda, d_grams, N, R, d_out, s);
@@ -905,6 +936,19 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
             g->tile_b3 = sw < 0 ? cptc::tile_b3_auto(g->units.nunits, R) : sw == 1;
             GEN_TRY(build_unit_groups(g->units, R, s, g->d_uorder, g->d_ugoff, g->ungroups,
                                       g->tile_b3 ? 32 : 16));
+            // every element in a unit: the outer modes' MTTKRP from per-unit sums
+            const char* us = std::getenv("GEN_UNIT_SUMS");
+            if (g->units.dense_nnz == g->nnz && R <= 32 && !g->units.outer.empty() &&
+                !(us && std::atoi(us) == 0))
+            {
+                GEN_TRY(dmalloc(&g->d_usum, g->units.nunits * size_t(R)));
+                std::vector<const double*> fo;
+                for (int o : g->units.outer) fo.push_back(g->d_F[o]);
+                GEN_HIP(hipMalloc(&g->d_Fo, fo.size() * sizeof(double*)));
+                GEN_HIP(hipMemcpy(g->d_Fo, fo.data(), fo.size() * sizeof(double*),
+                                  hipMemcpyHostToDevice));
+                g->unit_sums = true;
+            }
             if (g->tile_b3)
             {
                 const uint64_t md = std::max({g->dims[in[0]], g->dims[in[1]], g->dims[in[2]]});
@@ -1069,6 +1113,7 @@ extern "C" int cptc_gen_mttkrp(void* handle, int mode, double* host_out)
     Gen* g = as_gen(handle);
     CPTC_REQUIRE(mode >= 0 && mode < g->N, CPTC_ERR_ARG, "cptc_gen_mttkrp: mode %d", mode);
     g->w_dirty = true;
+    g->usum_ok = false;
     CPTC_TRY(g->mttkrp(mode));
     CPTC_HIP(hipMemcpyAsync(host_out, g->d_FtV, g->dims[mode] * size_t(g->R) * sizeof(double),
                             hipMemcpyDeviceToHost, g->s));
@@ -1097,6 +1142,7 @@ extern "C" int cptc_gen_set_factor(void* handle, int mode, const double* host_in
                             hipMemcpyHostToDevice, g->s));
     CPTC_TRY(cptc_gram(g->d_F[mode], g->dims[mode], g->R, g->d_grams + mode * RR, g->s));
     g->w_dirty = true;
+    g->usum_ok = false;
     CPTC_HIP(hipStreamSynchronize(g->s));
     return CPTC_OK;
 }

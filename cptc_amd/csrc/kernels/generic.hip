@@ -569,6 +569,110 @@ chol_solve_wave_kernel(const double* __restrict__ FtF,
         if (i < R) out[i] = y[i];
 }
 
+// Per-unit inner sums, R <= 32: s[u][r] = sum over the unit's elements of
+// v Fa[16 bi + la][r] Fb[16 bj + lb][r] Fc[16 bk + lc][r] (FP64; the unit's
+// contraction over its three inner modes, lid = la 256 + lb 16 + lc).  One
+// wave per unit: its three 16-row factor blocks staged in the wave's LDS
+// (rows past the factor's end as zeros), the elements read 64 at a time
+// (one per lane, coalesced) and handed out by shuffles, the two half-waves
+// taking alternate elements with lane = rank; four independent accumulators.
+constexpr int USUM_R = 32;
+__global__ __launch_bounds__(256) void unit_sums_kernel(const uint32_t* __restrict__ unit6,
+                                                        size_t nunits,
+                                                        const uint32_t* __restrict__ lid,
+                                                        const double* __restrict__ val,
+                                                        const double* __restrict__ Fa,
+                                                        const double* __restrict__ Fb,
+                                                        const double* __restrict__ Fc, int da,
+                                                        int db, int dc, int R,
+                                                        double* __restrict__ sums)
+{
+    __shared__ double blk[4][3][16 * USUM_R];
+    const int w = threadIdx.x / 64;
+    const size_t u = size_t(blockIdx.x) * 4 + size_t(w);
+    if (u >= nunits) return;   // wave-uniform; the LDS below is the wave's own
+    const int lane = threadIdx.x & 63;
+    const uint32_t* h = unit6 + u * 6;
+    const int ra = int(h[0]) * 16, rb = int(h[1]) * 16, rc = int(h[2]) * 16;
+    const uint32_t cnt = h[3], st = h[4];
+    double* fa = blk[w][0];
+    double* fb = blk[w][1];
+    double* fc = blk[w][2];
+    for (int x = lane; x < 16 * R; x += 64)
+    {
+        const int row = x / R, c = x % R;
+        fa[x] = ra + row < da ? Fa[size_t(ra + row) * R + c] : 0.0;
+        fb[x] = rb + row < db ? Fb[size_t(rb + row) * R + c] : 0.0;
+        fc[x] = rc + row < dc ? Fc[size_t(rc + row) * R + c] : 0.0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int r = lane & 31;
+    const uint32_t sub = uint32_t(lane >> 5);
+    const int rr = r < R ? r : 0;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (uint32_t b0 = 0; b0 < cnt; b0 += 64)
+    {
+        const uint32_t e = b0 + uint32_t(lane);
+        const uint32_t l = e < cnt ? lid[st + e] : 0u;
+        const double v = e < cnt ? val[st + e] : 0.0;
+        const uint32_t nb = cnt - b0 < 64u ? cnt - b0 : 64u;
+        auto term = [&](uint32_t k) {
+            const uint32_t lk = uint32_t(__shfl(int(l), int(k)));
+            const double vk = __shfl(v, int(k));
+            return vk * fa[(lk >> 8) * R + rr] * fb[((lk >> 4) & 15) * R + rr] *
+                   fc[(lk & 15) * R + rr];
+        };
+        // both halves take the same (uniform) steps, so every shuffle reads
+        // an active lane: lanes past the batch's end hold v = 0 and lid 0,
+        // so their terms add zero (k <= 56 + 7 < 64)
+        for (uint32_t kk = 0; kk < nb; kk += 8)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[q] += term(kk + 2 * uint32_t(q) + sub);
+    }
+    double t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    t += __shfl_xor(t, 32);
+    if (sub == 0 && r < R) sums[u * size_t(R) + r] = t;
+}
+
+// FtV[i_m(u)][r] += s[u][r] * prod over the other outer modes o of
+// F_o[i_o(u)][r] (outer mode m = outer[pos]); a workgroup takes 256 units,
+// sums them per (row, rank) in LDS when dim_m x R <= 4096 and flushes once;
+// otherwise one atomic add per (unit, rank).
+constexpr int USC_LDS = 4096;
+__global__ __launch_bounds__(256) void unit_scatter_kernel(
+    const uint32_t* __restrict__ outer_coords, size_t nunits, int nouter, int pos,
+    const double* const* __restrict__ Fo, const double* __restrict__ sums, int R, size_t dim_m,
+    double* __restrict__ FtV)
+{
+    __shared__ double acc[USC_LDS];
+    const bool lds = dim_m * size_t(R) <= size_t(USC_LDS);
+    const int n_l = lds ? int(dim_m) * R : 0;
+    for (int x = threadIdx.x; x < n_l; x += 256) acc[x] = 0.0;
+    __syncthreads();
+    const size_t u0 = size_t(blockIdx.x) * 256;
+    for (int x = threadIdx.x; x < 256 * R; x += 256)
+    {
+        const size_t u = u0 + size_t(x / R);
+        const int r = x % R;
+        if (u >= nunits) break;
+        const uint32_t* oc = outer_coords + u * size_t(nouter);
+        double v = sums[u * size_t(R) + r];
+        for (int o = 0; o < nouter; ++o)
+            if (o != pos) v *= Fo[o][size_t(oc[o]) * R + r];
+        const size_t row = oc[pos];
+        if (lds)
+            atomicAdd(&acc[row * R + r], v);
+        else
+            atomicAdd(FtV + row * size_t(R) + r, v);
+    }
+    if (!lds) return;
+    __syncthreads();
+    for (int x = threadIdx.x; x < n_l; x += 256)
+        if (acc[x] != 0.0) atomicAdd(FtV + x, acc[x]);
+}
+
 // Column sums of squares: P partials of R each (deterministic).
 __global__ __launch_bounds__(256) void colsq_partial_kernel(const double* __restrict__ F,
                                                             size_t rows, int R,
@@ -988,6 +1092,41 @@ extern "C" int cptc_residual_nd(int nmodes, const uint32_t* d_coords, const doub
                        F, d_lambda, R, part);
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(finalize_add2_kernel, dim3(1), dim3(64), 0, s, part, P, d_out2);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_unit_sums(const uint32_t* d_unit6, size_t nunits, const uint32_t* d_lid,
+                                  const double* d_val, const double* d_Fa, const double* d_Fb,
+                                  const double* d_Fc, int da, int db, int dc, int R,
+                                  double* d_sums, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= USUM_R && da >= 1 && db >= 1 && dc >= 1, CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums: R %d (1..%d) or dims", R, USUM_R);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_lid && d_val && d_Fa && d_Fb && d_Fc && d_sums, CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums: null pointer");
+    CPTC_REQUIRE((nunits + 3) / 4 < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums: %zu units", nunits);
+    hipLaunchKernelGGL(unit_sums_kernel, dim3(unsigned((nunits + 3) / 4)), dim3(256), 0,
+                       cptc::as_stream(stream), d_unit6, nunits, d_lid, d_val, d_Fa, d_Fb, d_Fc,
+                       da, db, dc, R, d_sums);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_unit_scatter(const uint32_t* d_outer_coords, size_t nunits, int nouter,
+                                     int pos, const double* const* d_Fo, const double* d_sums,
+                                     int R, size_t dim_m, double* d_FtV, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 64 && nouter >= 1 && pos >= 0 && pos < nouter, CPTC_ERR_ARG,
+                 "cptc_gen_unit_scatter: bad arguments");
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_outer_coords && d_Fo && d_sums && d_FtV, CPTC_ERR_ARG,
+                 "cptc_gen_unit_scatter: null pointer");
+    hipLaunchKernelGGL(unit_scatter_kernel, dim3(unsigned((nunits + 255) / 256)), dim3(256), 0,
+                       cptc::as_stream(stream), d_outer_coords, nunits, nouter, pos, d_Fo, d_sums,
+                       R, dim_m, d_FtV);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

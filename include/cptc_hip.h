@@ -650,6 +650,25 @@ int cptc_gen_normalize_gram(double* d_F, size_t rows, int R, double* d_lambda, d
 int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double* d_out,
                        void* stream);
 
+/* Per-unit inner sums for R <= 32: d_sums[u][r] = sum over unit u's dense
+ * elements (d_lid = la 256 + lb 16 + lc, d_val) of v * Fa[16 bi + la][r] *
+ * Fb[16 bj + lb][r] * Fc[16 bk + lc][r] (bi, bj, bk from d_unit6; Fa, Fb, Fc
+ * the three inner modes' factors, of da, db, dc rows), FP64.  With every element in a unit, an
+ * outer mode's MTTKRP is cptc_gen_unit_scatter of these sums: the same sum as
+ * the segment kernel over all elements (generic.cu's path for outer modes),
+ * in another order.  No reference counterpart. */
+int cptc_gen_unit_sums(const uint32_t* d_unit6, size_t nunits, const uint32_t* d_lid,
+                       const double* d_val, const double* d_Fa, const double* d_Fb,
+                       const double* d_Fc, int da, int db, int dc, int R, double* d_sums,
+                       void* stream);
+/* d_FtV[i_m(u)][r] += d_sums[u][r] * prod over the other outer modes o of
+ * d_Fo[o][i_o(u)][r], outer mode m = position pos of nouter; d_outer_coords
+ * nunits x nouter, d_Fo a device array of nouter factor pointers, dim_m rows
+ * of d_FtV.  Adds with FP64 atomics.  No reference counterpart. */
+int cptc_gen_unit_scatter(const uint32_t* d_outer_coords, size_t nunits, int nouter, int pos,
+                          const double* const* d_Fo, const double* d_sums, int R, size_t dim_m,
+                          double* d_FtV, void* stream);
+
 /* F = FtV (FtF + eps I)^-1 per row by Cholesky, eps = 1e-12 * tr(FtF) / R +
  * 1e-300 (tr <= 0: 1e-12 + 1e-300); a pivot s <= 0 becomes sqrt(eps).
  * g_chol_solve_kernel, generic.cu:746-819.  R <= 32.  One launch: each

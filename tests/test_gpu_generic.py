@@ -731,6 +731,46 @@ def test_config4_full_size(ca, orc, dev):
 
 
 @pytest.mark.timeout(600)
+@pytest.mark.parametrize("N,inner,R", [(4, (0, 1, 2), 16), (5, (0, 1, 2), 16), (5, (1, 2, 3), 16),
+                                     (5, (0, 1, 2), 32), (4, (1, 2, 3), 7)])
+def test_unit_sums_outer_modes(ca, orc, dev, N, inner, R, monkeypatch):
+    """Every element in a dense unit (config 5's case): the outer modes'
+    MTTKRP from per-unit inner sums (cptc_gen_unit_sums, then
+    cptc_gen_unit_scatter) against the oracle's FP64 segment sum over all
+    elements (<= 1e-10), and the same with GEN_UNIT_SUMS=0 (the segment
+    kernel); inner modes unchanged (units on the matrix cores, <= 1e-5)."""
+    rng = np.random.default_rng(30 + N + inner[0])
+    dims = (40, 35, 48, 33, 20)[:N]
+    t0 = tensor(ca, clustered(rng, dims, inner, 0.5, 8000), dims, rng)
+    g0 = ca.Gen(t0, R=16, inner=inner)
+    keep = g0.units()["is_dense"].astype(bool)
+    u6 = g0.units()["unit6"].reshape(-1, 6)
+    g0.close()
+    assert keep.sum() > 1000
+    assert u6[:, 3].max() > 100   # units of more than 64 elements (several batches)
+    t = ca.Tensor(dims, np.ascontiguousarray(t0.idx[:, keep]), np.ascontiguousarray(t0.val[keep]))
+    F = [rng.random((d, R)) for d in dims]
+    for flag in ("1", "0"):
+        monkeypatch.setenv("GEN_UNIT_SUMS", flag)
+        g = ca.Gen(t, R=R, inner=inner)
+        assert g.info.dense_enabled and g.units()["is_dense"].all()
+        idx = g.coords()
+        for m in range(N):
+            g.set_factor(m, F[m])
+        u = orc.dense_nd(idx, t.val, dims, 0.03, inner)
+        views = orc.views_nd(idx, t.val, dims, u["is_dense"], True, inner)
+        for n in range(N):
+            got = g.mttkrp(n)
+            ref = np.zeros(dims[n] * R)
+            if n in inner:
+                ref = orc.mttkrp_units_nd(idx, t.val, dims, u, n, [f.ravel() for f in F], R)
+            ref = orc.mttkrp_seg_nd(idx, t.val, dims, views, n, n in inner,
+                                    [f.ravel() for f in F], R, ref)
+            tol = 1e-5 if n in inner else 1e-10
+            assert rel_err(got, ref.reshape(dims[n], R)) <= tol, (flag, n)
+        g.close()
+
+
 def test_config5_full_size(ca, orc, dev):
     """Config 5 (20 M elements, order 5, R = 32, 32 768 dense units): device
     reorder and units bit-exact, 20 iterations' fit against the oracle."""
