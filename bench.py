@@ -412,7 +412,10 @@ def bench_generic(ca, args, spec, R) -> int:
     seg_launch = [float(seg_ms[m]) / kit for m in range(N)]
     achieved = sum(b_seg) / (sum(seg_launch) * 1e-3) / 1e9
     workload = f"cfg{args.config}-R{R}"
-    prof = load_traffic_seg(workload)
+    # outer modes from per-unit sums: the segment kernel's measured traffic
+    # does not describe those launches
+    usums = bool(info.unit_sums)
+    prof = None if usums else load_traffic_seg(workload)
     hbm = (prof["hbm_bytes_per_launch"] / (sum(seg_launch) / N * 1e-3) / 1e9) if prof else None
     # the inner modes in slot order (the order of unit_segments)
     inner = list(tuple(info.inner)) if info.dense_enabled else []
@@ -440,8 +443,12 @@ def bench_generic(ca, args, spec, R) -> int:
                    "tile_kernel": "bf16x3" if info.tile_bf16x3 else "fp32"},
         "fit_last": float(fits[-1]),
         "roofline": {
-            "kernel": "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
-                      "packed level keys), per launch = one mode",
+            "kernel": ("unit_sums_kernel + unit_scatter_kernel for the outer modes (every element "
+                       "in a dense unit: per-unit FP64 inner sums, formed once per iteration), "
+                       "seg_keys kernels for the inner modes' residual views; per launch = one mode"
+                       if usums else
+                       "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
+                       "packed level keys), per launch = one mode"),
             "bound": "hbm", "achieved": round(hbm, 1) if hbm else None, "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4) if hbm else None,
             "traffic": int(prof["hbm_bytes_per_launch"]) if prof else None,
@@ -451,7 +458,8 @@ def bench_generic(ca, args, spec, R) -> int:
             "algorithmic_bytes_per_launch": [int(b) for b in b_seg],
             "traffic_source": (f"profiles/mttkrp_seg_nd_{workload}_pmc.json (kernel sources "
                                f"sha {prof['kernel_src_sha']})") if prof else
-                              "none for these kernel sources: achieved/frac null",
+                              ("no counter profile of the unit-sum kernels: achieved/frac null"
+                               if usums else "none for these kernel sources: achieved/frac null"),
         },
         "roofline_units": (tile_roof(info, R, int(info.n_units), unit_launch,
                                      "dense units with FP64 outer weights, per inner mode",

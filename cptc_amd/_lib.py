@@ -109,6 +109,7 @@ class GenInfo(C.Structure):
         ("kernel_nnz", C.c_uint64 * CPTC_MAX_MODES),
         ("tile_bf16x3", C.c_int),
         ("unit_segments", C.c_uint64 * 3),
+        ("unit_sums", C.c_int),
     ]
 
 

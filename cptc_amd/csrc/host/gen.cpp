@@ -1038,6 +1038,7 @@ extern "C" int cptc_gen_info_get(void* handle, cptc_gen_info* info)
     for (int m = 0; m < g->N; ++m) info->kernel_nnz[m] = g->views[m].nnz;
     info->tile_bf16x3 = (g->dense && g->tile_b3) ? 1 : 0;
     for (int sl = 0; sl < 3; ++sl) info->unit_segments[sl] = g->uimg[sl].ready() ? g->uimg[sl].nseg : 0;
+    info->unit_sums = g->unit_sums ? 1 : 0;
     for (int q = 0; q < 3; ++q) info->prep_ms[q] = g->prep_ms[q];
     return CPTC_OK;
 }

@@ -735,6 +735,8 @@ typedef struct cptc_gen_info {
                                               (the inner modes' dense elements dropped) */
     int tile_bf16x3;         /* 1 = dense units on the split-bf16 kernel, 0 = FP32 MFMA */
     uint64_t unit_segments[3];  /* 16-byte segments of inner slot s's compacted split image */
+    int unit_sums;           /* 1 = outer modes' MTTKRP from per-unit sums (every element in a
+                                unit, R <= 32, GEN_UNIT_SUMS not 0), 0 = segment kernel */
 } cptc_gen_info;
 
 /* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)
