@@ -165,6 +165,8 @@ SIGNATURES = {
                                      C.c_uint64, C.c_uint64, _P]),
     "cptc_mttkrp_merged3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P, _P,
                                  _P, _I, _I, _I, _I, _P]),
+    "cptc_mttkrp_merged3_ex": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P,
+                                    _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "cptc_solve_pinv_noalloc": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_pinv_sym": (_I, [_P, _P, _I, _P, _P]),
     "cptc_apply_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
@@ -216,7 +218,9 @@ SIGNATURES = {
     "cptc_mttkrp_units_nd_ws": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I,
                                      _P, _I, _P, _Z, _P]),
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
-    "cptc_gen_unit_sums": (_I, [_P, _Z, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "cptc_gen_unit_sums": (_I, [_P, _Z, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _P,
+                                _P]),
+    "cptc_gen_unit_sums_plan": (_I, [_P, _Z, _I, _P, _P, _P]),
     "cptc_gen_unit_scatter": (_I, [_P, _Z, _I, _I, _P, _P, _I, _Z, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),
     "cptc_chol_ridge_factor": (_I, [_P, _P, _I, _P]),

@@ -79,6 +79,7 @@ struct Als3
     uint64_t dense_nnz_total = 0;
     bool skip_dense = false, skip_sparse = false;
     bool fused = false;   // merged single-grid MTTKRP (ALS_FUSED)
+    int merged_every = 0, merged_flags = 0;   // ALS_MERGED_STRIDE / _NO_DENSE / _NO_SPARSE
 
     double* d_F = nullptr;  // [A | B | C]
     double* F[3] = {nullptr, nullptr, nullptr};
@@ -92,7 +93,7 @@ struct Als3
     double* d_norms = nullptr;
     double* d_scal = nullptr;  // fit iprod/model2 (2) + residual (2)
     double x_sq = 0.0;
-    hipEvent_t ev[8] = {};
+    hipEvent_t ev[9] = {};
     // around the FP64 residual-view kernel of each mode, accumulated
     hipEvent_t kev[12] = {};   // [2m, 2m+1]: FP64 (or merged) kernel; [6+2m, 7+2m]: tiles
     // the event blocks of the iteration being queued (ev / kev, or a block of
@@ -145,12 +146,11 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     {
         const DevViews3& v = h.views;
         if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode], h.s));
-        CPTC_TRY(cptc_mttkrp_merged3(mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles),
-                                     h.d_order[mode], h.d_goff[mode], h.ngroups[mode],
-                                     v.d_coords[mode], v.d_vals[mode], v.d_blk_row[mode],
-                                     v.d_blk_start[mode], v.d_blk_cnt[mode], v.nseg[mode], A, B,
-                                     C, h.d_FtV, R, int(h.dims[0]), int(h.dims[1]),
-                                     int(h.dims[2]), h.s));
+        CPTC_TRY(cptc_mttkrp_merged3_ex(
+            mode, h.part.d_tiles4, h.d_tile_f32, size_t(h.part.ntiles), h.d_order[mode],
+            h.d_goff[mode], h.ngroups[mode], v.d_coords[mode], v.d_vals[mode], v.d_blk_row[mode],
+            v.d_blk_start[mode], v.d_blk_cnt[mode], v.nseg[mode], A, B, C, h.d_FtV, R,
+            int(h.dims[0]), int(h.dims[1]), int(h.dims[2]), h.merged_every, h.merged_flags, h.s));
         if (h.timing_kernels) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode + 1], h.s));
     }
     else if (dense)
@@ -225,6 +225,7 @@ void choose_fused(Als3& h, int opt)
     const bool want = opt < 0 ? env_flag("ALS_FUSED") != 0 : opt != 0;
     h.fused = want && h.use_mfma && h.part.ntiles > 0 && h.views.ready && !h.dviews.ready &&
               h.R <= 128 && h.R % 2 == 0;
+    cptc::merged_switches(h.merged_every, h.merged_flags);
 }
 
 // Dense tile kernel: the split-bf16 one unless R <= 16 (half of its 32-rank
@@ -629,7 +630,9 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
         if (events) CPTC_HIP(hipEventRecord(h.ev_cur[2 + 2 * mode], h.s));
         CPTC_TRY(update_mode(h, mode));
     }
-    // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP
+    // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP.  ev_cur[8]:
+    // mode C's update done (als.cu's t_solve), for the ALS_PROFILE line
+    if (events) CPTC_HIP(hipEventRecord(h.ev_cur[8], h.s));
     CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, d_out, h.s));
     if (events) CPTC_HIP(hipEventRecord(h.ev_cur[7], h.s));
     return CPTC_OK;
@@ -707,8 +710,20 @@ int collect_iteration(Als3& h, int it, int iters, const double sc[2], double* fi
     if (ms_out) ms_out[it] = ms;
     if (mtt_out) mtt_out[it] = mt;
     if (h.o.verbose) std::printf("[ALS] iter %d/%d time=%g ms fit=%.10g\n", it + 1, iters, ms, fit);
-    if (h.o.verbose && std::getenv("ALS_PROFILE"))
-        std::printf("[ALS][profile] iter %d mttkrp=%g (iter=%g)\n", it + 1, mt, ms);
+    // ALS_PROFILE (als.cu:748-760), eager iterations: gram = iteration start
+    // to mode C's FtF (modes A and B whole, mode C's Grams), mttkrp = mode
+    // C's MTTKRP, solve = mode C's update, fit = the Gram fit
+    if (h.o.verbose && std::getenv("ALS_PROFILE") && !replayed)
+    {
+        float ph[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        CPTC_HIP(hipEventElapsedTime(&ph[0], h.ev_cur[0], h.ev_cur[5]));
+        CPTC_HIP(hipEventElapsedTime(&ph[1], h.ev_cur[5], h.ev_cur[6]));
+        CPTC_HIP(hipEventElapsedTime(&ph[2], h.ev_cur[6], h.ev_cur[8]));
+        CPTC_HIP(hipEventElapsedTime(&ph[3], h.ev_cur[8], h.ev_cur[7]));
+        std::printf("[ALS][profile] iter %d gram=%g mttkrp=%g solve=%g fit=%g (iter=%g)\n",
+                    it + 1, double(ph[0]), double(ph[1]), double(ph[2]), double(ph[3]),
+                    double(ms));
+    }
     return CPTC_OK;
 }
 
@@ -798,7 +813,7 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
         }
         return CPTC_OK;
     }
-    constexpr size_t PER = 20;   // ev (8) + kev (12) per iteration
+    constexpr size_t PER = 21;   // ev (9) + kev (12) per iteration
     while (h.ev_pool.size() < PER * size_t(iters))
     {
         hipEvent_t e = nullptr;
@@ -826,7 +841,7 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
     for (int it = 0; it < iters; ++it)
     {
         h.ev_cur = h.ev_pool.data() + PER * size_t(it);
-        h.kev_cur = h.ev_cur + 8;
+        h.kev_cur = h.ev_cur + 9;
         h.timing_kernels = timed(it);
         if (h.graph_mode && !h.timed_iter && steady(h))
         {
@@ -856,7 +871,7 @@ int run(Als3& h, int iters, double* fit_out, float* ms_out, float* mtt_out)
     for (int it = 0; it < iters; ++it)
     {
         h.ev_cur = h.ev_pool.data() + PER * size_t(it);
-        h.kev_cur = h.ev_cur + 8;
+        h.kev_cur = h.ev_cur + 9;
         h.timing_kernels = timed(it);
         CPTC_TRY(collect_iteration(h, it, iters, sc.data() + 2 * it, fit_out, ms_out, mtt_out,
                                    replayed[size_t(it)] != 0));

@@ -493,8 +493,10 @@ void compute_mttkrp_merged_async(const HybridCOOTensor& hybrid, int mode, double
         const int m = mode;
         const bool views = hybrid.mttkrp_ready && hybrid.sparse_nnz > 0;
         const float* t = hybrid.num_dense_tiles > 0 ? tiles_f32(hybrid, stream) : nullptr;
+        int every = 0, flags = 0;
+        cptc::merged_switches(every, flags);
         API_TRY("compute_mttkrp_merged_async",
-                cptc_mttkrp_merged3(m, hybrid.d_tiles4, t, size_t(std::max<int64_t>(0, hybrid.num_dense_tiles)),
+                cptc_mttkrp_merged3_ex(m, hybrid.d_tiles4, t, size_t(std::max<int64_t>(0, hybrid.num_dense_tiles)),
                                     nullptr, nullptr, 0, views ? hybrid.d_sp2_coords[m] : nullptr,
                                     views ? hybrid.d_sp2_val[m] : nullptr,
                                     views ? hybrid.d_blk_row[m] : nullptr,
@@ -502,7 +504,7 @@ void compute_mttkrp_merged_async(const HybridCOOTensor& hybrid, int mode, double
                                     views ? hybrid.d_blk_cnt[m] : nullptr,
                                     views ? size_t(hybrid.mttkrp_blocks[m]) : 0, d_A, d_B, d_C,
                                     d_FtV, R, int(hybrid.dims[0]), int(hybrid.dims[1]),
-                                    int(hybrid.dims[2]), stream));
+                                    int(hybrid.dims[2]), every, flags, stream));
         return;
     }
     compute_dense_mttkrp_async(hybrid, mode, d_A, d_B, d_C, d_FtV, d_FtF, R, stream);

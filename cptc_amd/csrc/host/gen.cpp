@@ -360,6 +360,9 @@ struct Gen
     bool usum_ok = false;
     double* d_usum = nullptr;          // nunits x R
     double** d_Fo = nullptr;           // the outer modes' factors, device array of pointers
+    uint32_t* d_us_order = nullptr;    // cptc_gen_unit_sums_plan: units by inner block triple
+    uint32_t* d_us_chunk = nullptr;    // chunk offsets into d_us_order
+    size_t us_nchunks = 0;
     std::vector<cptc::DevViewN> views;   // kernel views (dense elements dropped, rows sorted)
     std::vector<uint64_t> ref_nseg;      // segments of the reference-layout views
 
@@ -410,6 +413,8 @@ struct Gen
         dfree(d_L);
         dfree(d_usum);
         if (d_Fo) (void)hipFree(d_Fo);
+        if (d_us_order) (void)hipFree(d_us_order);
+        if (d_us_chunk) (void)hipFree(d_us_chunk);
         if (s) (void)hipStreamDestroy(s);
     }
 
@@ -471,6 +476,7 @@ struct Gen
             if (!usum_ok)
             {
                 CPTC_TRY(cptc_gen_unit_sums(units.d_unit6, units.nunits, units.d_lid, units.d_val,
+                                            d_us_order, d_us_chunk, us_nchunks,
                                             d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
                                             int(dims[in3[0]]), int(dims[in3[1]]),
                                             int(dims[in3[2]]), R, d_usum, s));
@@ -720,6 +726,27 @@ int build_unit_groups(const cptc::DevUnitsN& u, int R, hipStream_t s, uint32_t* 
     return CPTC_OK;
 }
 
+// Units sorted by inner block triple, in chunks of <= 8 (a workgroup of the
+// unit-sum kernel stages the chunk's three factor blocks once; its 4 waves
+// take 2 units each).
+int build_unit_sums_plan(const cptc::DevUnitsN& u, hipStream_t s, uint32_t*& d_order,
+                         uint32_t*& d_chunk, size_t& nchunks)
+{
+    const size_t nu = u.nunits;
+    std::vector<uint32_t> hdr(nu * 6), ord(nu), off(nu + 1);
+    CPTC_HIP(hipMemcpyAsync(hdr.data(), u.d_unit6, hdr.size() * sizeof(uint32_t),
+                            hipMemcpyDeviceToHost, s));
+    CPTC_HIP(hipStreamSynchronize(s));
+    CPTC_TRY(cptc_gen_unit_sums_plan(hdr.data(), nu, 8, ord.data(), off.data(), &nchunks));
+    CPTC_HIP(hipMalloc(&d_order, nu * sizeof(uint32_t)));
+    CPTC_HIP(hipMalloc(&d_chunk, (nchunks + 1) * sizeof(uint32_t)));
+    CPTC_HIP(hipMemcpyAsync(d_order, ord.data(), nu * sizeof(uint32_t), hipMemcpyHostToDevice, s));
+    CPTC_HIP(hipMemcpyAsync(d_chunk, off.data(), (nchunks + 1) * sizeof(uint32_t),
+                            hipMemcpyHostToDevice, s));
+    CPTC_HIP(hipStreamSynchronize(s));
+    return CPTC_OK;
+}
+
 bool env_set(const char* k) { return std::getenv(k) != nullptr; }
 
 // generic.cu:1743-1782: U[0,1) draws in mode order; row a of the data keeps
@@ -942,6 +969,8 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
                 !(us && std::atoi(us) == 0))
             {
                 GEN_TRY(dmalloc(&g->d_usum, g->units.nunits * size_t(R)));
+                GEN_TRY(build_unit_sums_plan(g->units, s, g->d_us_order, g->d_us_chunk,
+                                             g->us_nchunks));
                 std::vector<const double*> fo;
                 for (int o : g->units.outer) fo.push_back(g->d_F[o]);
                 GEN_HIP(hipMalloc(&g->d_Fo, fo.size() * sizeof(double*)));

@@ -6,7 +6,10 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "cptc_hip.h"
 
@@ -65,6 +68,35 @@ inline unsigned grid_for(size_t n, unsigned block, unsigned cap = 1u << 20)
     if (g > cap) g = cap;
     return unsigned(g);
 }
+
+// Raises the dynamic-LDS limit of kernels once per device (the attribute
+// belongs to the device that is current), safe against concurrent first
+// calls:  static cptc::DeviceOnce once;
+//         CPTC_HIP(once.lds_limit({kernel...}, bytes));
+class DeviceOnce
+{
+public:
+    hipError_t lds_limit(std::initializer_list<const void*> kernels, int bytes)
+    {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        std::lock_guard<std::mutex> lk(mu_);
+        if (size_t(dev) >= done_.size()) done_.resize(size_t(dev) + 1, 0);
+        if (done_[size_t(dev)]) return hipSuccess;
+        for (const void* k : kernels)
+        {
+            e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+            if (e != hipSuccess) return e;
+        }
+        done_[size_t(dev)] = 1;
+        return hipSuccess;
+    }
+
+private:
+    std::mutex mu_;
+    std::vector<char> done_;
+};
 
 // Library-owned device scratch, one growing buffer per (device, slot),
 // freed at process exit.  Slots separate buffers that are live at the same

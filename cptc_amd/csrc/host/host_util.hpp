@@ -108,6 +108,19 @@ inline bool tile_b3_auto(size_t ntiles, int R)
     return R > 16 && ntiles * size_t((R + 31) / 32) >= TILE_B3_MIN_ITEMS;
 }
 
+// The merged grid's experiment switches (dense.cu:2277-2283, 2350-2352):
+// ALS_MERGED_STRIDE=<k> makes every k-th workgroup a tile workgroup (unset or
+// <= 0: spread evenly); ALS_MERGED_NO_DENSE / ALS_MERGED_NO_SPARSE, on when
+// set (the reference tests getenv != nullptr), leave the tiles / the
+// residual segments out -> flags bits 0 / 1 of cptc_mttkrp_merged3_ex.
+inline void merged_switches(int& every, int& flags)
+{
+    const char* s = std::getenv("ALS_MERGED_STRIDE");
+    every = s ? std::atoi(s) : 0;
+    flags = (std::getenv("ALS_MERGED_NO_DENSE") ? 1 : 0) |
+            (std::getenv("ALS_MERGED_NO_SPARSE") ? 2 : 0);
+}
+
 inline int tile_group_cap(size_t ntiles, int R, int num_cus, int cap, int rank_block = 16)
 {
     if (const char* e = std::getenv("CPTC_TILE_GROUP"))

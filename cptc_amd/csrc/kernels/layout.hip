@@ -228,13 +228,9 @@ int degrees(const int32_t* d_m, size_t nnz, uint64_t dim, unsigned* d_deg, hipSt
     const unsigned grid = grid_for(nnz, 256, 2048);
     if (dim * sizeof(unsigned) <= 128 * 1024)
     {
-        static bool attr = false;
-        if (!attr)
-        {
-            CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(histogram_lds_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-            attr = true;
-        }
+        static cptc::DeviceOnce attr;
+        CPTC_HIP(attr.lds_limit({reinterpret_cast<const void*>(histogram_lds_kernel)},
+                                128 * 1024));
         hipLaunchKernelGGL(histogram_lds_kernel, dim3(grid), dim3(256), dim * sizeof(unsigned), s,
                            d_m, nnz, int(dim), d_deg);
     }

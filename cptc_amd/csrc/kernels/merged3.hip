@@ -111,19 +111,27 @@ void launch_m(int mode, bool grouped, dim3 grid, size_t lds, hipStream_t st, con
 
 }  // namespace
 
-extern "C" int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float* d_tile_f32,
-                                   size_t ntiles, const uint32_t* d_order,
-                                   const uint32_t* d_group_off, size_t ngroups,
-                                   const uint64_t* d_coords, const double* d_vals,
-                                   const uint32_t* d_blk_row, const uint32_t* d_blk_start,
-                                   const uint32_t* d_blk_cnt, size_t nblocks, const double* d_A,
-                                   const double* d_B, const double* d_C, double* d_FtV, int R,
-                                   int dimI, int dimJ, int dimK, void* stream)
+// dense_every > 0 fixes the interleave (every dense_every-th workgroup a
+// tile workgroup, ALS_MERGED_STRIDE, dense.cu:2350-2381); flags bit 0 drops
+// the tile role (ALS_MERGED_NO_DENSE), bit 1 the segment role
+// (ALS_MERGED_NO_SPARSE) (dense.cu:2277-2283, 2326-2336).
+extern "C" int cptc_mttkrp_merged3_ex(int mode, const int32_t* d_tiles, const float* d_tile_f32,
+                                      size_t ntiles, const uint32_t* d_order,
+                                      const uint32_t* d_group_off, size_t ngroups,
+                                      const uint64_t* d_coords, const double* d_vals,
+                                      const uint32_t* d_blk_row, const uint32_t* d_blk_start,
+                                      const uint32_t* d_blk_cnt, size_t nblocks, const double* d_A,
+                                      const double* d_B, const double* d_C, double* d_FtV, int R,
+                                      int dimI, int dimJ, int dimK, int dense_every, int flags,
+                                      void* stream)
 {
     CPTC_REQUIRE(mode >= 0 && mode < 3 && R >= 1, CPTC_ERR_ARG,
                  "cptc_mttkrp_merged3: mode %d R %d", mode, R);
     CPTC_REQUIRE(R <= 128 && R % 2 == 0, CPTC_ERR_UNSUPPORTED,
                  "cptc_mttkrp_merged3: R %d (even R <= 128 only)", R);
+    CPTC_REQUIRE((flags & ~3) == 0, CPTC_ERR_ARG, "cptc_mttkrp_merged3: flags %d", flags);
+    if (flags & 1) ntiles = 0;
+    if (flags & 2) nblocks = 0;
     if (ntiles == 0 && nblocks == 0) return CPTC_OK;
     CPTC_REQUIRE(d_A && d_B && d_C && d_FtV, CPTC_ERR_ARG, "cptc_mttkrp_merged3: null factor");
     CPTC_REQUIRE(ntiles == 0 || (d_tiles && d_tile_f32), CPTC_ERR_ARG,
@@ -133,12 +141,25 @@ extern "C" int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float
     for (const double* p : {d_A, d_B, d_C})
         CPTC_REQUIRE((reinterpret_cast<uintptr_t>(p) & 15) == 0, CPTC_ERR_UNSUPPORTED,
                      "cptc_mttkrp_merged3: factors must be 16-byte aligned");
-    const bool grouped = d_order && d_group_off && ngroups > 0;
+    const bool grouped = ntiles > 0 && d_order && d_group_off && ngroups > 0;
     const size_t items = ntiles == 0 ? 0 : (grouped ? ngroups : ntiles);
     const size_t dwg = (items + WAVES - 1) / WAVES;
-    const size_t grid = dwg + nblocks;
+    // the automatic interleave spreads the D tile workgroups evenly over the
+    // grid of D + segments; a fixed stride k places tile workgroup d at
+    // position d k, so the grid must reach k (D - 1) (every other position
+    // before the end is a segment, later ones too: D + segments suffices)
+    size_t grid = dwg + nblocks;
+    uint32_t every;
+    if (dwg == 0)
+        every = uint32_t(std::min<size_t>(grid + 1, 0xFFFFFFFFu));
+    else if (dense_every > 0 && nblocks > 0)
+    {
+        every = uint32_t(dense_every);
+        grid = std::max(grid, size_t(every) * (dwg - 1) + 1);
+    }
+    else
+        every = uint32_t(std::max<size_t>(1, grid / dwg));
     CPTC_REQUIRE(grid < (size_t(1) << 31), CPTC_ERR_ARG, "cptc_mttkrp_merged3: grid too large");
-    const uint32_t every = dwg ? uint32_t(std::max<size_t>(1, grid / dwg)) : uint32_t(grid + 1);
     const int Rp = (R + 15) / 16 * 16;
     const size_t lds = grouped ? size_t(WAVES) * 16 * Rp * sizeof(double) : 0;
     hipStream_t st = cptc::as_stream(stream);
@@ -146,17 +167,12 @@ extern "C" int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float
     if (lds > 48 * 1024)
     {
         // the grouped tile role's accumulators (64 KB at R = 128)
-        static bool attr_set = false;
-        if (!attr_set)
-        {
-            for (const void* k :
-                 {reinterpret_cast<const void*>(mttkrp3_merged_kernel<0, 128, true>),
-                  reinterpret_cast<const void*>(mttkrp3_merged_kernel<1, 128, true>),
-                  reinterpret_cast<const void*>(mttkrp3_merged_kernel<2, 128, true>)})
-                CPTC_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             64 * 1024));
-            attr_set = true;
-        }
+        static cptc::DeviceOnce attr;
+        CPTC_HIP(attr.lds_limit(
+            {reinterpret_cast<const void*>(mttkrp3_merged_kernel<0, 128, true>),
+             reinterpret_cast<const void*>(mttkrp3_merged_kernel<1, 128, true>),
+             reinterpret_cast<const void*>(mttkrp3_merged_kernel<2, 128, true>)},
+            64 * 1024));
     }
     const int dI = dimI, dJ = dimJ, dK = dimK;
 #define CPTC_MERGED_ARGS                                                                       \
@@ -176,4 +192,18 @@ extern "C" int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float
 #undef CPTC_MERGED_ARGS
     CPTC_LAUNCHED();
     return CPTC_OK;
+}
+
+extern "C" int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float* d_tile_f32,
+                                   size_t ntiles, const uint32_t* d_order,
+                                   const uint32_t* d_group_off, size_t ngroups,
+                                   const uint64_t* d_coords, const double* d_vals,
+                                   const uint32_t* d_blk_row, const uint32_t* d_blk_start,
+                                   const uint32_t* d_blk_cnt, size_t nblocks, const double* d_A,
+                                   const double* d_B, const double* d_C, double* d_FtV, int R,
+                                   int dimI, int dimJ, int dimK, void* stream)
+{
+    return cptc_mttkrp_merged3_ex(mode, d_tiles, d_tile_f32, ntiles, d_order, d_group_off,
+                                  ngroups, d_coords, d_vals, d_blk_row, d_blk_start, d_blk_cnt,
+                                  nblocks, d_A, d_B, d_C, d_FtV, R, dimI, dimJ, dimK, 0, 0, stream);
 }

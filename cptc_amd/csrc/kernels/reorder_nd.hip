@@ -359,14 +359,9 @@ int cadr_device(int N, const uint64_t* dims, const uint32_t* d_coords, uint64_t 
         const uint32_t* c = d_coords + uint64_t(m) * nnz;
         if (dims[m] <= DEG_LDS_MAX)
         {
-            static bool attr = false;
-            if (!attr)
-            {
-                CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(degree_lds_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             int(DEG_LDS_MAX * sizeof(uint32_t))));
-                attr = true;
-            }
+            static cptc::DeviceOnce attr;
+            CPTC_HIP(attr.lds_limit({reinterpret_cast<const void*>(degree_lds_kernel)},
+                                    int(DEG_LDS_MAX * sizeof(uint32_t))));
             // one block per CU: each flushes at most dims[m] counts
             hipLaunchKernelGGL(degree_lds_kernel, dim3(std::min(grid1(nnz), 256u)), dim3(256),
                                dims[m] * sizeof(uint32_t), s, c, nnz, uint32_t(dims[m]), deg.p);

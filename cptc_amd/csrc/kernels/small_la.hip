@@ -1069,15 +1069,10 @@ int pinv_launch_ws(const double* d_FtF, double* d_Ainv, int R, int* flag, double
     const size_t RR = size_t(R) * R;
     const bool use_lds = RR * sizeof(double) <= 128 * 1024;
     const size_t lds = use_lds ? RR * sizeof(double) : 0;
-    static bool attr_set = false;
-    if (!attr_set)
-    {
-        CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(chol_inverse_kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-        CPTC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(jacobi_pinv_kernel),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024));
-        attr_set = true;
-    }
+    static cptc::DeviceOnce attr;
+    CPTC_HIP(attr.lds_limit({reinterpret_cast<const void*>(chol_inverse_kernel),
+                             reinterpret_cast<const void*>(jacobi_pinv_kernel)},
+                            128 * 1024));
     if (R <= 16)
         hipLaunchKernelGGL(sweep_inverse_kernel<16>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
                            flag);

@@ -325,6 +325,19 @@ int cptc_mttkrp_merged3(int mode, const int32_t* d_tiles, const float* d_tile_f3
                         const double* d_A, const double* d_B, const double* d_C, double* d_FtV,
                         int R, int dimI, int dimJ, int dimK, void* stream);
 
+/* cptc_mttkrp_merged3 with the reference's experiment switches of the merged
+ * grid (dense.cu:2277-2283, 2326-2336, 2350-2381): dense_every > 0 makes
+ * every dense_every-th workgroup a tile workgroup (ALS_MERGED_STRIDE; 0 =
+ * spread evenly), flags bit 0 leaves the tiles out (ALS_MERGED_NO_DENSE),
+ * bit 1 the residual segments (ALS_MERGED_NO_SPARSE). */
+int cptc_mttkrp_merged3_ex(int mode, const int32_t* d_tiles, const float* d_tile_f32,
+                           size_t ntiles, const uint32_t* d_order, const uint32_t* d_group_off,
+                           size_t ngroups, const uint64_t* d_coords, const double* d_vals,
+                           const uint32_t* d_blk_row, const uint32_t* d_blk_start,
+                           const uint32_t* d_blk_cnt, size_t nblocks, const double* d_A,
+                           const double* d_B, const double* d_C, double* d_FtV, int R, int dimI,
+                           int dimJ, int dimK, int dense_every, int flags, void* stream);
+
 /* CP-SGD on the order-3 sparse residual (sgd.cu:51-467; ALS_SGD,
  * main.cu:467-501).  cptc_sgd3_sample: d_idx[b] = SplitMix64-finalised
  * (seed + b * 0x9E3779B97F4A7C15) mod nnz (cpsgd_sample_kernel).
@@ -656,11 +669,19 @@ int cptc_gram_hadamard(const double* d_grams, int ngram, int skip, int R, double
  * the three inner modes' factors, of da, db, dc rows), FP64.  With every element in a unit, an
  * outer mode's MTTKRP is cptc_gen_unit_scatter of these sums: the same sum as
  * the segment kernel over all elements (generic.cu's path for outer modes),
- * in another order.  No reference counterpart. */
+ * in another order.  d_order / d_chunk_off / nchunks: the plan of
+ * cptc_gen_unit_sums_plan for these units (every chunk's units share their
+ * (bi, bj, bk), which the kernel relies on).  No reference counterpart. */
 int cptc_gen_unit_sums(const uint32_t* d_unit6, size_t nunits, const uint32_t* d_lid,
-                       const double* d_val, const double* d_Fa, const double* d_Fb,
-                       const double* d_Fc, int da, int db, int dc, int R, double* d_sums,
-                       void* stream);
+                       const double* d_val, const uint32_t* d_order, const uint32_t* d_chunk_off,
+                       size_t nchunks, const double* d_Fa, const double* d_Fb, const double* d_Fc,
+                       int da, int db, int dc, int R, double* d_sums, void* stream);
+/* Host: the plan of cptc_gen_unit_sums.  h_order (nunits entries) = the
+ * units sorted stably by (bi, bj, bk); chunk c = h_order[h_chunk_off[c] ..
+ * h_chunk_off[c + 1]), at most max_chunk units of one (bi, bj, bk);
+ * h_chunk_off holds up to nunits + 1 entries; *nchunks = the chunk count. */
+int cptc_gen_unit_sums_plan(const uint32_t* h_unit6, size_t nunits, int max_chunk,
+                            uint32_t* h_order, uint32_t* h_chunk_off, size_t* nchunks);
 /* d_FtV[i_m(u)][r] += d_sums[u][r] * prod over the other outer modes o of
  * d_Fo[o][i_o(u)][r], outer mode m = position pos of nouter; d_outer_coords
  * nunits x nouter, d_Fo a device array of nouter factor pointers, dim_m rows

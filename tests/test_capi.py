@@ -130,6 +130,37 @@ def test_dense_groups(ca, hdr_words, slot, G):
             assert off[g] - off[g - 1] == G
 
 
+@pytest.mark.parametrize("chunk", [1, 3, 8])
+def test_unit_sums_plan(ca, chunk):
+    """Host plan of the unit-sum kernel: the units sorted stably by their
+    inner block triple (words 0..2 of the 6-word header), cut into maximal
+    chunks of <= `chunk` units that share one triple, covering every unit."""
+    import ctypes as C
+    rng = np.random.default_rng(chunk)
+    n = 700
+    hdr = rng.integers(0, 3, (n, 6)).astype(np.uint32)
+    hdr[:, 3:] = rng.integers(0, 1000, (n, 3))
+    order = np.zeros(n, np.uint32)
+    off = np.zeros(n + 1, np.uint32)
+    nc = C.c_size_t()
+    assert ca.lib.cptc_gen_unit_sums_plan(hdr.ctypes.data, n, chunk, order.ctypes.data,
+                                          off.ctypes.data, C.byref(nc)) == 0
+    nc = nc.value
+    ref = sorted(range(n), key=lambda u: tuple(hdr[u, :3]))   # Python's sort is stable
+    assert np.array_equal(order, np.array(ref, np.uint32))
+    assert off[0] == 0 and off[nc] == n
+    for c in range(nc):
+        a, b = off[c], off[c + 1]
+        assert 1 <= b - a <= chunk
+        assert len({tuple(hdr[u, :3]) for u in order[a:b]}) == 1
+    for c in range(1, nc):
+        a = off[c]
+        if tuple(hdr[order[a], :3]) == tuple(hdr[order[a - 1], :3]):
+            assert off[c] - off[c - 1] == chunk
+    assert ca.lib.cptc_gen_unit_sums_plan(hdr.ctypes.data, n, 0, order.ctypes.data,
+                                          off.ctypes.data, C.byref(C.c_size_t())) == -1
+
+
 @pytest.mark.parametrize("bits,nbytes", [((6, 6, 6, 4), 4), ((16, 16), 4), ((17, 16), 8),
                                          ((1,), 4), ((32, 32), 8), ((32, 32, 1), 0),
                                          ((0, 5), 0), ((33,), 0)])

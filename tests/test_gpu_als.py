@@ -405,3 +405,84 @@ def test_cli_cpp_flow_matches_driver(ca, dev, tmp_path, env_path, path):
     assert np.max(np.abs(fits[:3] - ref[:3])) <= 1e-10, (fits, ref)
     cli_lam = [l for l in lines if l.startswith("[Main] Final CP weights:")][0].split(":")[1]
     assert np.allclose(np.array([float(x) for x in cli_lam.split()]), lam, rtol=1e-5)
+
+
+@pytest.mark.parametrize("switch,value", [("ALS_MERGED_NO_SPARSE", "1"),
+                                          ("ALS_MERGED_NO_DENSE", "1"),
+                                          ("ALS_MERGED_STRIDE", "2"),
+                                          ("ALS_MERGED_STRIDE", "7"),
+                                          ("ALS_MERGED_STRIDE", "100000")])
+def test_merged_switches(ca, orc, dev, tmp_path, switch, value, monkeypatch):
+    """The merged grid's experiment switches (dense.cu:2277-2283, 2350-2352)
+    on ALS_FUSED: ALS_MERGED_NO_SPARSE leaves only the tile workgroups (the
+    MTTKRP is the tiles' alone, MFMA bound 1e-5), ALS_MERGED_NO_DENSE only the
+    residual segments (FP64, 1e-10), ALS_MERGED_STRIDE=k puts a tile workgroup
+    at every k-th grid position (the whole MTTKRP, 1e-5; k past the grid puts
+    the tiles after every segment).  Then the CLI (main.cu's flow on the C++
+    interface, compute_mttkrp_merged_async) under the same switch reproduces
+    the C-ABI driver's fits."""
+    t = clustered(ca, 9)
+    perms, p, v = oracle_layout(orc, t, 0.03)
+    assert len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
+    R = 16
+    monkeypatch.setenv(switch, value)
+    with ca.Als3(t, R=R, threshold=0.03, path=1, fused=1) as h:
+        assert int(h.info.fused) == 1
+        F = [h.factor(m).ravel() for m in range(3)]
+        for mode in range(3):
+            ref = np.zeros(t.dims[mode] * R)
+            if switch != "ALS_MERGED_NO_SPARSE":
+                ref = ref + orc.mttkrp3_view(v, mode, *F, R, t.dims[mode])
+            if switch != "ALS_MERGED_NO_DENSE":
+                ref = ref + orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+            tol = 1e-10 if switch == "ALS_MERGED_NO_DENSE" else 1e-5
+            err = rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R))
+            assert err <= tol, (mode, err)
+    fpath = str(tmp_path / "t.tns")
+    ca.write_tns(fpath, t)
+    env = dict(os.environ, ALS_FUSED="1", ALS_FORCE_WMMA="1")
+    env[switch] = value
+    env.pop("ALS_FORCE_CUDA", None)
+    out = subprocess.run([ca.CLI_PATH, fpath, "4", str(R)], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.splitlines()
+    assert any(l.startswith("[ALS] FUSED path active") for l in lines)
+    fits = np.array([float(l.split("fit=")[1]) for l in lines if l.startswith("[ALS] iter ")])
+    t2 = ca.load_tns3(fpath)
+    with ca.Als3(t2, R=R, path=1, fused=1) as h:
+        ref, _, _ = h.run(4)
+    # the same layout, factors and launches; FP64 atomic order only (see
+    # test_cli_cpp_flow_matches_driver), the CLI prints 10 significant digits
+    assert len(fits) == 4 and np.max(np.abs(fits - ref)) <= 1e-8, (fits, ref)
+
+
+def test_cli_profile_line(ca, dev, tmp_path):
+    """ALS_PROFILE (als.cu:748-760): after each '[ALS] iter' line,
+    '[ALS][profile] iter k gram=.. mttkrp=.. solve=.. fit=.. (iter=..)' with
+    the reference's phases: gram = iteration start to mode C's Hadamard
+    (modes A and B whole), mttkrp = mode C's MTTKRP, solve = mode C's update,
+    fit = the Gram fit; consecutive event spans, so they add up to at most
+    the iteration's time."""
+    t = make(ca, "zipf", 5)
+    fpath = str(tmp_path / "t.tns")
+    ca.write_tns(fpath, t)
+    env = dict(os.environ, ALS_PROFILE="1")
+    out = subprocess.run([ca.CLI_PATH, fpath, "3", "8"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    lines = out.stdout.splitlines()
+    prof = [l for l in lines if l.startswith("[ALS][profile] iter ")]
+    assert len(prof) == 3
+    for k, l in enumerate(prof):
+        head, rest = l.split(" gram=")
+        assert head == f"[ALS][profile] iter {k + 1}"
+        vals = {}
+        for part in ("gram=" + rest).replace("(", "").replace(")", "").split():
+            key, val = part.split("=")
+            vals[key] = float(val)
+        assert list(vals) == ["gram", "mttkrp", "solve", "fit", "iter"]
+        assert all(x >= 0 for x in vals.values()) and vals["mttkrp"] > 0
+        parts = vals["gram"] + vals["mttkrp"] + vals["solve"] + vals["fit"]
+        assert parts <= vals["iter"] * 1.0001 + 1e-3, vals
+        assert lines[lines.index(l) - 1].startswith(f"[ALS] iter {k + 1}/3 ")

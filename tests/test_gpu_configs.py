@@ -4,7 +4,9 @@ Configs 1 (256^3, 15.1 M nnz, every nonzero in a dense tile) and 2 (512^3
 clustered, 3.0 M nnz, fill below the MFMA threshold): the device layout is
 bit-exact with the oracle's (CADR permutations, tiles, pools, views), the
 fill-rate rule picks the reference's path (main.cu:334-426, MI355X: fill_min
-0.08), and 20 ALS iterations reach the oracle's fits.
+0.08), every mode's MTTKRP on the driver's initial factors matches the oracle
+(config 1: MFMA tiles only, 1e-5; config 2: FP64 views, 1e-10), and 20 ALS
+iterations reach the oracle's fits.
 
 Config 3 (12092 x 9184 x 28818, 76.9 M nnz, R = 128, the headline workload):
 the device layout is byte-for-byte the oracle's (CADR permutations, whose
@@ -13,8 +15,14 @@ pools; the three residual views; about a minute of oracle time), and it also
 satisfies the invariants (every nonzero in exactly one tile or the residual,
 tile counts against the cutoff, view keys sorted, segments <= 1024 elements
 covering each row).  The FP64 sparse MTTKRP alone (MFMA tiles skipped) is held
-to 1e-10 per mode, sparse + MFMA tiles to 1e-5, and 20 ALS iterations reach the
-oracle's fits.
+to 1e-10 per mode, the MFMA tiles alone (residual skipped) and sparse + MFMA
+tiles to 1e-5, and 20 ALS iterations reach the oracle's fits.
+
+Bounds: 1e-10 relative (Frobenius) for FP64 MTTKRP and 1e-5 for the matrix-core
+path are the task's parity bounds, measured with the reference's relative-L2
+metric (generic.cu:1619-1629).  The fit bound is the task's 1e-4 (1e-6 where no
+matrix core is involved: FP64 paths differ from the oracle only in the order
+of additions), capped at 1e-3 of the fit.
 """
 import numpy as np
 import pytest
@@ -24,6 +32,13 @@ from conftest import rel_err
 pytestmark = pytest.mark.gpu
 
 FILL_MIN_MI355X = 0.08      # max(0.08, 0.11 / sqrt(256 / 24)), main.cu:369-381
+
+
+def fit_tol(fit, cap):
+    """Fit bound after 20 iterations: the task's 1e-4 (or `cap`), but never
+    more than 1e-3 of the fit itself, so a small fit (config 5's is about
+    0.0023) is held as tightly relative to its size as a large one."""
+    return min(cap, 1e-3 * abs(fit))
 
 
 def oracle_layout(orc, t, thr):
@@ -71,11 +86,23 @@ def test_baseline_config_full_size(ca, orc, dev, cfg):
                 for k in ("coords", "vals", "blk_row", "blk_start", "blk_cnt"):
                     assert np.array_equal(got[k], np.asarray(dv[m][k])), ("dense", m, k)
         F = [h.factor(m).ravel() for m in range(3)]
+        # every mode's MTTKRP on the driver's initial factors: config 1 is
+        # tiles only (MFMA, 1e-5), config 2 the FP64 residual + dense views
+        # (1e-10); the reference's relative-L2 metric (generic.cu:1619-1629)
+        for mode in range(3):
+            if expect_mfma:
+                ref = orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+            else:
+                ref = orc.mttkrp3_view(v, mode, *F, R, t.dims[mode]) \
+                    + orc.mttkrp3_view(dv, mode, *F, R, t.dims[mode])
+            err = rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R))
+            print(f"[cfg{cfg}] mode {mode} MTTKRP rel err {err:.3e}", flush=True)
+            assert err <= (1e-5 if expect_mfma else 1e-10), mode
         o = orc.Als3(v, dv, p if expect_mfma else None, float(np.sum(t.val ** 2)), t.dims, R,
                      *F, None)
         fit, _, _ = h.run(20)
         ofit, _, _ = o.iterate(20)
-        tol = 1e-4 if expect_mfma else 1e-6
+        tol = fit_tol(ofit[-1], 1e-4 if expect_mfma else 1e-6)
         print(f"[cfg{cfg}] fit {fit[-1]:.10f} oracle {ofit[-1]:.10f}", flush=True)
         assert np.max(np.abs(fit - ofit)) <= tol, (fit[-3:], ofit[-3:])
 
@@ -152,7 +179,7 @@ def test_config3_full_size(ca, orc, dev):
         fit, _, _ = h.run(20)
     ofit, _, _ = o.iterate(20)
     print(f"[cfg3] fit {fit[-1]:.10f} oracle {ofit[-1]:.10f}", flush=True)
-    assert np.max(np.abs(fit - ofit)) <= 1e-4, (fit[-3:], ofit[-3:])
+    assert np.max(np.abs(fit - ofit)) <= fit_tol(ofit[-1], 1e-4), (fit[-3:], ofit[-3:])
     del o
     # the FP64 sparse kernel alone at the sparse path's bound
     with ca.Als3(t, R=R, threshold=thr, skip_dense=1) as h:
@@ -162,3 +189,12 @@ def test_config3_full_size(ca, orc, dev):
             err = rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R))
             print(f"[cfg3] mode {mode} sparse-only MTTKRP rel err {err:.3e}", flush=True)
             assert err <= 1e-10, mode
+    # the MFMA tiles alone (the FP64 residual skipped) at the MFMA bound
+    with ca.Als3(t, R=R, threshold=thr, skip_sparse=1) as h:
+        assert bool(h.info.use_mfma)
+        for mode in range(3):
+            assert np.array_equal(h.factor(mode).ravel(), F[mode])
+            ref = orc.mttkrp3_tiles(p, mode, *F, R, t.dims)
+            err = rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R))
+            print(f"[cfg3] mode {mode} tiles-only MTTKRP rel err {err:.3e}", flush=True)
+            assert err <= 1e-5, mode
