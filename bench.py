@@ -130,6 +130,23 @@ def load_traffic(workload: str, sources=SPARSE3_SOURCES):
 
 
 SEG_ND_SOURCES = ("cptc_amd/csrc/kernels/seg_keys.hip",)
+UNIT_SUMS_SOURCES = ("cptc_amd/csrc/kernels/unit_sums.hip",)
+LDS_PEAK_TBS = 78.6   # 256 CUs x 128 B/clk x 2.4 GHz
+
+
+def load_traffic_named(name: str, sources, workload: str):
+    """A kernel's measured traffic summary profiles/<name>_pmc.json, or None
+    when absent or measured on other kernel sources."""
+    path = os.path.join(ROOT, "profiles", f"{name}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != workload or d.get("kernel_src_sha") != sources_sha(sources):
+        return None
+    return d
 
 
 def load_traffic_seg(workload: str):
@@ -267,27 +284,30 @@ def main() -> int:
                        if 64 < R <= 128 else
                        "mttkrp3_seg_kernel (FP64 residual view)") + ", per launch = one mode",
             "bound": "hbm",
-            "achieved": round(dram, 1) if dram else None,
+            "achieved": round(gather_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(dram / HBM_PEAK_GBS, 4) if dram else None,
+            "frac": round(gather_gbs / HBM_PEAK_GBS, 4),
             "traffic": int(traffic) if traffic else None,
             "launch_ms": [round(x, 4) for x in launch_ms],
-            "gather_model_GBs": round(gather_gbs, 1),
-            "gather_model_frac": round(gather_gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
+            "traffic_GBs": round(dram, 1) if dram else None,
+            "traffic_frac": round(dram / HBM_PEAK_GBS, 4) if dram else None,
             "compulsory_GBs": round(comp_gbs, 1),
             "compulsory_frac": round(comp_gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_launch": [int(b) for b in b_launch],
             "compulsory_bytes_per_launch": [int(b) for b in compulsory],
             "traffic_source": (f"profiles/mttkrp_sparse3_{workload}_pmc.json "
                                f"(kernel sources sha {prof['kernel_src_sha']})") if prof else
-                              "none for these kernel sources: achieved/frac null",
-            "note": "achieved = HBM bytes per launch measured by rocprofv3 --pmc (L2-to-fabric "
-                    "read + write bytes, calibrated on a copy kernel; MALL hits count as "
-                    "fabric traffic, so this bounds the DRAM bytes from above) over the launch "
-                    "time measured here; gather_model = the no-reuse gather model (every "
-                    "factor row read per nonzero, L1/L2/MALL hits included, so it exceeds the "
-                    "HBM peak); compulsory = view stream + every factor row once + output.",
+                              "none for these kernel sources: traffic null",
+            "note": "achieved = algorithmic bytes per launch (no-reuse gather model: per residual "
+                    "nonzero its 20-byte COO entry and one R-wide FP64 row of each of the two "
+                    "other factors, plus the output rows) over the launch time measured here "
+                    "with hipEvents; L1, L2 and the 256 MB MALL serve most of those row "
+                    "gathers, so frac exceeds 1. traffic = bytes per launch between L2 and "
+                    "memory measured by rocprofv3 --pmc (read + write, calibrated on a copy "
+                    "kernel; MALL hits count, so it bounds the DRAM bytes from above); "
+                    "traffic_GBs = traffic over the same launch time. compulsory = view "
+                    "stream + every factor row once + output rows.",
         }
     else:
         # no sparse residual (every nonzero in a dense tile): the MFMA tile
@@ -412,14 +432,75 @@ def bench_generic(ca, args, spec, R) -> int:
     seg_launch = [float(seg_ms[m]) / kit for m in range(N)]
     achieved = sum(b_seg) / (sum(seg_launch) * 1e-3) / 1e9
     workload = f"cfg{args.config}-R{R}"
-    # outer modes from per-unit sums: the segment kernel's measured traffic
-    # does not describe those launches
     usums = bool(info.unit_sums)
-    prof = None if usums else load_traffic_seg(workload)
-    hbm = (prof["hbm_bytes_per_launch"] / (sum(seg_launch) / N * 1e-3) / 1e9) if prof else None
     # the inner modes in slot order (the order of unit_segments)
     inner = list(tuple(info.inner)) if info.dense_enabled else []
+    outer = [m for m in range(N) if m not in inner]
     unit_launch = [float(unit_ms[m]) / kit for m in inner]
+    if usums:
+        # outer modes from per-unit sums: one unit_sums_kernel launch per
+        # iteration (its time is reported under the first outer mode's unit
+        # kernel), then one scatter per outer mode
+        us_ms = sum(float(unit_ms[m]) for m in outer) / kit
+        n_el = int(info.dense_nnz)
+        # algorithmic bytes: every element's 12-byte (lid, value) record and
+        # its three R-wide FP64 inner factor rows, plus the unit sums written
+        b_us = n_el * 12 + n_el * 3 * R * 8 + int(info.n_units) * R * 8
+        ach_us = b_us / (us_ms * 1e-3) / 1e9
+        prof = load_traffic_named(f"unit_sums_{workload}", UNIT_SUMS_SOURCES, workload)
+        traffic = prof["hbm_bytes_per_launch"] if prof else None
+        # the kernel reads RT >= R ranks per row (RT = 8, 16 or 32)
+        rt = 8 if R <= 8 else 16 if R <= 16 else 32
+        lds_b = n_el * 3 * rt * 8
+        roofline = {
+            "kernel": "unit_sums_kernel (per-unit FP64 inner sums for the outer modes: every "
+                      "element lies in a dense unit), one launch per iteration",
+            "bound": "hbm", "achieved": round(ach_us, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach_us / HBM_PEAK_GBS, 4),
+            "traffic": int(traffic) if traffic else None,
+            "launch_ms": [round(us_ms, 4)],
+            "algorithmic_bytes_per_launch": [int(b_us)],
+            "traffic_GBs": round(traffic / (us_ms * 1e-3) / 1e9, 1) if traffic else None,
+            "traffic_frac": round(traffic / (us_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            if traffic else None,
+            "lds_bytes_per_launch": int(lds_b),
+            "lds_TBs": round(lds_b / (us_ms * 1e-3) / 1e12, 2),
+            "lds_peak_TBs": LDS_PEAK_TBS,
+            "lds_frac": round(lds_b / (us_ms * 1e-3) / 1e12 / LDS_PEAK_TBS, 4),
+            "scatter_launch_ms": [round(float(seg_ms[m]) / kit, 4) for m in outer],
+            "traffic_source": (f"profiles/unit_sums_{workload}_pmc.json (kernel sources sha "
+                               f"{prof['kernel_src_sha']})") if prof else
+                              "none for these kernel sources: traffic null",
+            "note": "achieved = algorithmic bytes per launch (per element its (lid, value) "
+                    "record and three R-wide FP64 inner factor rows, plus the unit sums) over "
+                    "the launch time measured with hipEvents; the rows come from LDS (each "
+                    "workgroup stages its units' three 16-row factor blocks once), so frac "
+                    "exceeds 1 and the kernel is bound by the LDS reads: lds_bytes = 3 "
+                    "FP64 row values per element and rank, against 256 CUs x 128 B/clk x 2.4 "
+                    "GHz.",
+        }
+    else:
+        prof = load_traffic_seg(workload)
+        traffic = prof["hbm_bytes_per_launch"] if prof else None
+        mean_s = sum(seg_launch) / N * 1e-3
+        roofline = {
+            "kernel": "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
+                      "packed level keys), per launch = one mode",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": int(traffic) if traffic else None,
+            "launch_ms": [round(x, 4) for x in seg_launch],
+            "algorithmic_bytes_per_launch": [int(b) for b in b_seg],
+            "traffic_GBs": round(traffic / mean_s / 1e9, 1) if traffic else None,
+            "traffic_frac": round(traffic / mean_s / 1e9 / HBM_PEAK_GBS, 4) if traffic else None,
+            "traffic_source": (f"profiles/mttkrp_seg_nd_{workload}_pmc.json (kernel sources "
+                               f"sha {prof['kernel_src_sha']})") if prof else
+                              "none for these kernel sources: traffic null",
+            "note": "achieved = algorithmic bytes per launch (no-reuse gather model over the "
+                    "kernel view's elements) over the launch time measured with hipEvents; "
+                    "L1/L2 serve the gathers, so frac exceeds 1; traffic = L2-to-memory bytes "
+                    "per launch (rocprofv3 --pmc).",
+        }
 
     log(f"timed {args.steps} iterations: {ms_per_step:.3f} ms/iter; seg launch ms "
         f"{[round(x, 4) for x in seg_launch]}; unit launch ms {[round(x, 4) for x in unit_launch]}")
@@ -442,25 +523,8 @@ def bench_generic(ca, args, spec, R) -> int:
                    "path": "generic N-order", "parallelism": "single GPU",
                    "tile_kernel": "bf16x3" if info.tile_bf16x3 else "fp32"},
         "fit_last": float(fits[-1]),
-        "roofline": {
-            "kernel": ("unit_sums_kernel + unit_scatter_kernel for the outer modes (every element "
-                       "in a dense unit: per-unit FP64 inner sums, formed once per iteration), "
-                       "seg_keys kernels for the inner modes' residual views; per launch = one mode"
-                       if usums else
-                       "seg_keys_kernel / seg_keys_leaf_lds_kernel (FP64 segment MTTKRP over "
-                       "packed level keys), per launch = one mode"),
-            "bound": "hbm", "achieved": round(hbm, 1) if hbm else None, "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4) if hbm else None,
-            "traffic": int(prof["hbm_bytes_per_launch"]) if prof else None,
-            "launch_ms": [round(x, 4) for x in seg_launch],
-            "gather_model_GBs": round(achieved, 1),
-            "gather_model_frac": round(achieved / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_launch": [int(b) for b in b_seg],
-            "traffic_source": (f"profiles/mttkrp_seg_nd_{workload}_pmc.json (kernel sources "
-                               f"sha {prof['kernel_src_sha']})") if prof else
-                              ("no counter profile of the unit-sum kernels: achieved/frac null"
-                               if usums else "none for these kernel sources: achieved/frac null"),
-        },
+        "mttkrp_launch_ms": [round(x, 4) for x in seg_launch],
+        "roofline": roofline,
         "roofline_units": (tile_roof(info, R, int(info.n_units), unit_launch,
                                      "dense units with FP64 outer weights, per inner mode",
                                      list(info.unit_segments))
@@ -547,17 +611,23 @@ def calib() -> int:
 
 def host_info() -> dict:
     """nproc, the OpenMP thread count and the CPU model of this host."""
-    model = None
+    fields = {}
+    sockets = set()
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "physical id":
+                    sockets.add(val)
+                if key in ("model name", "cpu family", "model", "stepping", "cpu MHz",
+                           "cache size", "cpu cores", "siblings") and key not in fields:
+                    fields[key] = val
     except OSError:
         pass
     return {"nproc": os.cpu_count(), "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
-            "cpu_model": model}
+            "cpu_model": fields.get("model name"),
+            "cpuinfo": dict(fields, sockets=len(sockets) or None)}
 
 
 def summarize_cpu(ms, extra: dict) -> dict:

@@ -430,7 +430,9 @@ class Gen:
     def kernel_times(self, reset: bool = True):
         """(segment-kernel ms per mode, unit-kernel ms per mode, iterations
         timed).  Queued runs time the kernels on every 8th iteration and on
-        the last one; verbose or profiled runs on every iteration."""
+        the last one; verbose or profiled runs on every iteration.  Outer
+        modes on the per-unit-sum path report the scatter as their segment
+        kernel and the per-unit sums (where formed) as their unit kernel."""
         out = np.zeros(16, np.float64)
         it = C.c_int()
         check(lib.cptc_gen_kernel_times(self._h, out.ctypes.data, C.byref(it), int(reset)),

@@ -465,13 +465,15 @@ struct Gen
                                               int(dims[in3[0]]), int(dims[in3[1]]),
                                               int(dims[in3[2]]), d_FtV, R, s));
         }
-        if (timing)
+        const bool usum_path = unit_sums && !in;
+        if (timing && !usum_path)
         {
             CPTC_HIP(hipEventRecord(ke[1], s));
             CPTC_HIP(hipEventRecord(ke[2], s));
         }
-        if (unit_sums && !in)
+        if (usum_path)
         {
+            // events: kev 0-1 the per-unit sums (when formed), kev 2-3 the scatter
             const int* in3 = units.inner;
             if (!usum_ok)
             {
@@ -481,6 +483,11 @@ struct Gen
                                             int(dims[in3[0]]), int(dims[in3[1]]),
                                             int(dims[in3[2]]), R, d_usum, s));
                 usum_ok = true;
+            }
+            if (timing)
+            {
+                CPTC_HIP(hipEventRecord(ke[1], s));
+                CPTC_HIP(hipEventRecord(ke[2], s));
             }
             int pos = 0;
             while (units.outer[size_t(pos)] != n) ++pos;

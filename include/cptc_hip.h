@@ -783,7 +783,10 @@ int cptc_gen_profile(void* handle, double* out5, int* iters, int reset);
 
 /* Kernel times summed over cptc_gen_run iterations (hipEvents on the
  * driver's stream): out[m] = ms of mode m's segment MTTKRP kernel,
- * out[CPTC_MAX_MODES + m] = ms of its dense-unit kernel (0 when none);
+ * out[CPTC_MAX_MODES + m] = ms of its dense-unit kernel (0 when none); an
+ * outer mode on the per-unit-sum path (cptc_gen_info.unit_sums) has its
+ * scatter in out[m] and the per-unit sums, when this mode formed them, in
+ * out[CPTC_MAX_MODES + m];
  * *iters = iterations summed; reset != 0 zeroes the sums.  A queued
  * (quiet) run times every 8th iteration and its last one; a verbose or
  * profiled run times every iteration.  Measurement
