@@ -252,6 +252,11 @@ class Als3:
     def __exit__(self, *a):
         self.close()
 
+    def refresh_info(self):
+        """Re-reads cptc_als3_info (graph captures change as runs proceed)."""
+        check(lib.cptc_als3_info_get(self._h, C.byref(self.info)), "cptc_als3_info_get")
+        return self.info
+
     def run(self, iters: int):
         fit = np.zeros(iters, np.float64)
         ms = np.zeros(iters, np.float32)

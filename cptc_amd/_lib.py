@@ -72,6 +72,7 @@ class Als3Info(C.Structure):
         ("tile_compact", C.c_int),
         ("tile_segments", C.c_uint64 * 3),
         ("graph_mode", C.c_int),
+        ("graph_captures", C.c_int),
     ]
 
 

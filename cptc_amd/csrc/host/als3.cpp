@@ -107,6 +107,7 @@ struct Als3
     int graph_mode = 0;                  // 1: replay untimed iterations (ALS_GRAPH / automatic)
     hipGraphExec_t gexec = nullptr;      // the captured steady-state iteration
     uint64_t g_gen = 0;                  // scratch generation it was captured at
+    int n_captures = 0;                  // successful captures (cptc_als3_info.graph_captures)
     double k_sparse_ms[3] = {0, 0, 0}, k_mttkrp_ms[3] = {0, 0, 0}, k_tile_ms[3] = {0, 0, 0};
     bool tile_timed[3] = {false, false, false};
     int k_iters = 0;
@@ -672,6 +673,7 @@ int capture_iteration(Als3& h, double* d_out)
     (void)hipGraphDestroy(g);
     CPTC_HIP(ie);
     h.g_gen = scratch_generation();
+    ++h.n_captures;
     return CPTC_OK;
 }
 
@@ -1013,6 +1015,7 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
         (h->tile_b3 && h->timg[0].ready() && h->timg[1].ready() && h->timg[2].ready()) ? 1 : 0;
     for (int m = 0; m < 3; ++m) info->tile_segments[m] = h->timg[m].ready() ? h->timg[m].nseg : 0;
     info->graph_mode = h->graph_mode;
+    info->graph_captures = h->n_captures;
     info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }

@@ -665,7 +665,23 @@ extern "C" int cptc_dense_groups(const int32_t* hdr, int hdr_words, size_t ntile
         group_off_out[++ng] = uint32_t(j);
         i = j;
     }
-    for (size_t t = 0; t < ntiles; ++t) order_out[t] = ord[t];
+    // longest groups first (ties in block order): the launch's last waves
+    // are the short groups, so the SIMDs run out of work together
+    std::vector<uint32_t> gi(ng);
+    for (size_t g = 0; g < ng; ++g) gi[g] = uint32_t(g);
+    std::stable_sort(gi.begin(), gi.end(), [&](uint32_t a, uint32_t b) {
+        return group_off_out[a + 1] - group_off_out[a] > group_off_out[b + 1] - group_off_out[b];
+    });
+    std::vector<uint32_t> off2(ng + 1);
+    size_t pos = 0;
+    for (size_t g = 0; g < ng; ++g)
+    {
+        off2[g] = uint32_t(pos);
+        for (uint32_t i = group_off_out[gi[g]]; i < group_off_out[gi[g] + 1]; ++i)
+            order_out[pos++] = ord[i];
+    }
+    off2[ng] = uint32_t(pos);
+    for (size_t g = 0; g <= ng; ++g) group_off_out[g] = off2[g];
     *ngroups_out = ng;
     return CPTC_OK;
 }

@@ -535,9 +535,40 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
                 const double arp = A[r * R + p], arq = A[r * R + q];
                 A[r * R + p] = c * arp - s * arq;
                 A[r * R + q] = s * arp + c * arq;
-                const double vrp = V[r * R + p], vrq = V[r * R + q];
-                V[r * R + p] = c * vrp - s * vrq;
-                V[r * R + q] = s * vrp + c * vrq;
+            }
+            // V <- V J, V in global memory: a thread's VB column pairs are
+            // loaded together, then rotated and stored, so a round waits on
+            // one memory round trip per VB pairs instead of one per pair
+            // (the same operations on every entry as a pair-at-a-time loop)
+            constexpr int VB = 8;
+            for (int x0 = 0; x0 < npairs * R; x0 += VB * PINV_THREADS)
+            {
+                double vp[VB], vq[VB], cc[VB], ss[VB];
+                int ip[VB], iq[VB];
+                bool on[VB];
+#pragma unroll
+                for (int j = 0; j < VB; ++j)
+                {
+                    const int x = x0 + j * PINV_THREADS + tid;
+                    const int k = x / R, r = x % R;
+                    on[j] = x < npairs * R;
+                    const int kk = on[j] ? k : 0;
+                    const int p = pair_p[kk], q = pair_q[kk];
+                    on[j] = on[j] && q < R && rot_s[kk] != 0.0;
+                    cc[j] = rot_c[kk];
+                    ss[j] = rot_s[kk];
+                    ip[j] = on[j] ? r * R + p : 0;
+                    iq[j] = on[j] ? r * R + q : 0;
+                    vp[j] = on[j] ? V[ip[j]] : 0.0;
+                    vq[j] = on[j] ? V[iq[j]] : 0.0;
+                }
+#pragma unroll
+                for (int j = 0; j < VB; ++j)
+                    if (on[j])
+                    {
+                        V[ip[j]] = cc[j] * vp[j] - ss[j] * vq[j];
+                        V[iq[j]] = ss[j] * vp[j] + cc[j] * vq[j];
+                    }
             }
             __syncthreads();
             // A <- J^T A (rows p, q)

@@ -214,10 +214,12 @@ int cptc_mttkrp_dense_tiles3_cws(int mode, const int32_t* d_tiles, const uint32_
 /* Tile groups for the grouped MFMA launches (no reference counterpart; the
  * reference issues one atomic per (row, rank, tile)).  hdr: ntiles x
  * hdr_words int32 on the host ({bi, bj, bk, ...}: 4 words for order-3 tiles,
- * 6 for generic units).  order_out (ntiles) = tile indices sorted by (block
- * of `slot`, then the other two blocks); group_off_out (ntiles + 1) cuts
- * them into runs of <= max_group tiles with one target block; *ngroups_out
- * = number of runs.  Passing d_order / d_group_off / ngroups (device copies)
+ * 6 for generic units).  The tiles sorted by (block of `slot`, then the
+ * other two blocks) are cut into runs of <= max_group tiles with one target
+ * block; the runs are then ordered longest first (equal lengths keep that
+ * order), so a launch ends on its shortest groups.  order_out (ntiles) =
+ * the tile indices run after run; group_off_out (ntiles + 1) = run
+ * boundaries; *ngroups_out = number of runs.  Passing d_order / d_group_off / ngroups (device copies)
  * to cptc_mttkrp_dense_tiles3 or cptc_mttkrp_units_nd makes one wave sum
  * a group in LDS and issue one atomic per (row, rank) per group (R <= 128;
  * NULL / larger R: one atomic per tile).  Host code. */
@@ -464,6 +466,8 @@ typedef struct cptc_als3_info {
     int tile_compact;         /* 1 = the split-bf16 kernel reads the compacted tile images */
     uint64_t tile_segments[3];  /* 16-byte segments of mode m's compacted split image (0: none) */
     int graph_mode;           /* 1 = quiet runs replay one captured iteration (HIP graph) */
+    int graph_captures;       /* iterations captured so far (a capture is redone after the
+                                 library's scratch buffers were reallocated) */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 

@@ -102,8 +102,9 @@ def test_cadr3_rejects_out_of_range_index(ca):
 
 @pytest.mark.parametrize("hdr_words,slot,G", [(4, 0, 8), (4, 1, 8), (4, 2, 3), (6, 1, 16)])
 def test_dense_groups(ca, hdr_words, slot, G):
-    """Host group builder: a permutation sorted by (target block, others),
-    runs of <= G tiles with one target block covering every tile."""
+    """Host group builder: the tiles sorted by (target block, others) cut into
+    maximal runs of <= G tiles with one target block, the runs ordered
+    longest first (stable), covering every tile."""
     import ctypes as C
     rng = np.random.default_rng(slot + G)
     n = 500
@@ -116,18 +117,22 @@ def test_dense_groups(ca, hdr_words, slot, G):
     ng = ng.value
     assert np.array_equal(np.sort(order), np.arange(n))
     p, q = (slot + 1) % 3, (slot + 2) % 3
-    keys = [tuple(hdr[t, [slot, p, q]]) for t in order]
-    assert keys == sorted(keys)
-    assert off[0] == 0 and off[ng] == n
+    # the reference partition: maximal runs of <= G over the sorted tiles
+    srt = sorted(range(n), key=lambda t: tuple(hdr[t, [slot, p, q]]))
+    runs, i = [], 0
+    while i < n:
+        j = i + 1
+        while j < n and j - i < G and hdr[srt[j], slot] == hdr[srt[i], slot]:
+            j += 1
+        runs.append(srt[i:j])
+        i = j
+    runs = sorted(runs, key=lambda r: -len(r))   # stable: equal lengths keep block order
+    assert off[0] == 0 and off[ng] == n and ng == len(runs)
     for g in range(ng):
         a, b = off[g], off[g + 1]
-        assert 1 <= b - a <= G
-        assert len(set(hdr[order[a:b], slot])) == 1
-    # maximal runs: a new group starts only at a block change or a full group
-    for g in range(1, ng):
-        a = off[g]
-        if hdr[order[a], slot] == hdr[order[a - 1], slot]:
-            assert off[g] - off[g - 1] == G
+        assert list(order[a:b]) == runs[g]
+        assert 1 <= b - a <= G and len(set(hdr[order[a:b], slot])) == 1
+    assert all(off[g + 1] - off[g] >= off[g + 2] - off[g + 1] for g in range(ng - 1))
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 8])

@@ -300,6 +300,53 @@ def test_graph_replay_matches_eager(ca, dev, kind, R, path, fused, monkeypatch):
             h.close()
 
 
+def test_graph_recaptured_after_scratch_growth(ca, dev, monkeypatch):
+    """A captured iteration holds the addresses of the library's scratch
+    buffers (Gram partials, pseudoinverse workspace, reduction partials).
+    When another entry point grows one of them (cptc_gram on a wider
+    factor reallocates the Gram partials), the next graph-mode run must
+    capture the iteration again (cptc_als3_info.graph_captures counts the
+    captures) and still match the eager driver from the same factors, within
+    the bounds of test_graph_replay_matches_eager."""
+    t = make(ca, "clustered", 6)
+    R = 32
+    hs = {}
+    for g in ("1", "0"):
+        monkeypatch.setenv("ALS_GRAPH", g)
+        hs[g] = ca.Als3(t, R=R, threshold=0.03, path=1)
+    try:
+        assert int(hs["1"].refresh_info().graph_captures) == 0
+        F = [hs["0"].factor(m) for m in range(3)]
+
+        def both():
+            out = {}
+            for g, h in hs.items():
+                for m in range(3):
+                    h.set_factor(m, F[m])
+                fit, _, _ = h.run(3)
+                out[g] = (fit, [h.factor(m) for m in range(3)])
+            assert np.max(np.abs(out["1"][0] - out["0"][0])) <= 1e-8
+            for a_, b_ in zip(out["1"][1], out["0"][1]):
+                assert rel_err(a_, b_) <= 1e-6
+
+        both()
+        assert int(hs["1"].refresh_info().graph_captures) == 1
+        both()   # the cached graph is replayed: no new capture
+        assert int(hs["1"].refresh_info().graph_captures) == 1
+        # grow the Gram-partials scratch: 256 partials of 320 x 320 doubles
+        rows, Rb = 16384, 320
+        Fb = ca.DevBuf.from_numpy(np.random.default_rng(0).random((rows, Rb)))
+        Gb = ca.DevBuf.zeros((Rb, Rb))
+        assert ca.lib.cptc_gram(Fb.data_ptr(), rows, Rb, Gb.data_ptr(), None) == 0
+        ca.sync()
+        del Fb, Gb
+        both()
+        assert int(hs["1"].refresh_info().graph_captures) == 2
+    finally:
+        for h in hs.values():
+            h.close()
+
+
 def test_cli_runs_and_exports(ca, dev, tmp_path):
     t = make(ca, "zipf", 5)
     path = str(tmp_path / "t.tns")
