@@ -691,6 +691,25 @@ int blk_views3_device(const DevViews3& v, const uint64_t dims[3], int lg_tb, int
             ctv.push_back(stb[x]);
             tot = sc[x];
         }
+        {
+            // chunks ordered by their first run-level block, then target block
+            std::vector<uint32_t> ci(c0v.size());
+            for (size_t x = 0; x < c0v.size(); ++x) ci[x] = uint32_t(x);
+            std::stable_sort(ci.begin(), ci.end(), [&](uint32_t a, uint32_t b) {
+                const uint32_t ka = sk[c0v[a]] & 0x7FFFFFFFu, kb = sk[c0v[b]] & 0x7FFFFFFFu;
+                return ka < kb;
+            });
+            std::vector<uint32_t> a0(c0v.size()), an(c0v.size()), at(c0v.size());
+            for (size_t x = 0; x < ci.size(); ++x)
+            {
+                a0[x] = c0v[ci[x]];
+                an[x] = cnv[ci[x]];
+                at[x] = ctv[ci[x]];
+            }
+            c0v.swap(a0);
+            cnv.swap(an);
+            ctv.swap(at);
+        }
         out.nspan[mode] = ss.size();
         out.nchunk[mode] = c0v.size();
         auto up = [&](uint32_t** dst, const std::vector<uint32_t>& src) -> int {

@@ -114,6 +114,13 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 
         const uint32_t lo = st + min(cnt, uint32_t(wave) * wchunk);
         const uint32_t hi = st + min(cnt, uint32_t(wave + 1) * wchunk);
 
+        // The span's body, instantiated separately for staged and unstaged
+        // spans: with one body for both, the compiler gives the run-level row
+        // one register block whether it comes from LDS or from a global load,
+        // and before each LDS read into it waits for every global load in
+        // flight (s_waitcnt vmcnt(0)), the element gathers included.
+        auto run_span = [&](auto staged_t) {
+        constexpr bool STAGED = decltype(staged_t)::value;
         double acc0 = 0.0, acc1 = 0.0, t0 = 0.0, t1 = 0.0;
         uint32_t cur = NONE;      // run key (target row in block << 15 | o1) of the open run
         uint32_t cur_f2 = 0;      // byte offset of its F2 row (LDS when staged)
@@ -128,7 +135,10 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 
             acc0 = acc1 = 0.0;
         };
         auto f2_row = [&](uint32_t off) {
-            return staged ? lds_row(stg, off) : row_load(rs2, off);
+            if constexpr (STAGED)
+                return lds_row(stg, off);
+            else
+                return row_load(rs2, off);
         };
 
         uint64_t pc = 0;
@@ -198,7 +208,7 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 
             const uint32_t o1 = uint32_t(pc >> sh1) & 0x7FFFu;
             const uint32_t off1_l = (uint32_t(pc >> sh0) & 0x7FFFu) * rowb;
             const uint32_t key_l = ((t & uint32_t(TB - 1)) << 15) | o1;
-            const uint32_t off2_l = staged ? (o1 - kb0) * uint32_t(RT * 8) : o1 * rowb;
+            const uint32_t off2_l = STAGED ? (o1 - kb0) * uint32_t(RT * 8) : o1 * rowb;
             asm volatile("" ::: "memory");   // the previous window's reads come first
             vw[lane] = v;
             asm volatile("" ::: "memory");
@@ -224,7 +234,12 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 
             acc1 += t1 * f2.y;
             flush(cur);
         }
-    }
+        };
+        if (staged)
+            run_span(std::true_type{});
+        else
+            run_span(std::false_type{});
+}
     __syncthreads();
     for (int x = tid; x < TB * RT; x += WAVE * WAVES)
     {
