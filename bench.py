@@ -99,7 +99,8 @@ def gather_bytes(nnz: int, dim_n: int, R: int, N: int = 3) -> float:
 
 
 SPARSE3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_sparse.hip", "cptc_amd/csrc/kernels/seg3_body.hpp")
-BLK3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_blk.hip",)
+BLK3_SOURCES = ("cptc_amd/csrc/kernels/mttkrp_blk.hip", "cptc_amd/csrc/host/blk3_params.hpp",
+                "cptc_amd/csrc/kernels/layout.hip")
 
 
 def sources_sha(paths) -> str:

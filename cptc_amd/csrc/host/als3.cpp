@@ -28,6 +28,7 @@
 #include <string>
 #include <vector>
 
+#include "blk3_params.hpp"
 #include "cptc_hip.h"
 #include "hip_util.hpp"
 #include "host_util.hpp"
@@ -270,7 +271,8 @@ int build_blk(Als3& h)
     const bool beside_tiles = h.use_mfma && h.part.ntiles > 0 && h.dense_beside && !h.skip_dense;
     const bool want = e ? std::strcmp(e, "0") != 0 : !beside_tiles;
     if (!want) return CPTC_OK;
-    return blk_views3_device(h.views, h.dims, 5, 4, 2048, 64, h.blk, h.s);
+    return blk_views3_device(h.views, h.dims, CPTC_BLK3_LG_TB, CPTC_BLK3_LG_KB, CPTC_BLK3_CHUNK,
+                             CPTC_BLK3_STAGE_MIN, h.blk, h.s);
 }
 
 // Quiet runs of small problems are paced by the host's ~40 queue operations

@@ -6,17 +6,14 @@
 // (layout.hip) builds the layout.
 #include <hip/hip_runtime.h>
 
+#include "../host/blk3_params.hpp"
 #include "../host/hip_util.hpp"
 
-// Target rows per block and run-level rows per staged block, as log2.
-#ifndef CPTC_BLK3_LG_TB
-#define CPTC_BLK3_LG_TB 5
-#endif
-#ifndef CPTC_BLK3_LG_KB
-#define CPTC_BLK3_LG_KB 4
-#endif
 #ifndef CPTC_BLK3_UNROLL
 #define CPTC_BLK3_UNROLL 4   // gathers in flight per wave
+#endif
+#ifndef CPTC_BLK3_WPE
+#define CPTC_BLK3_WPE 6      // resident waves per SIMD the registers are sized for
 #endif
 
 namespace {
@@ -41,7 +38,7 @@ constexpr int BLK_WAVES = 8;
 // global atomic per (row, rank) per chunk.  Same sum as mttkrp3_seg_kernel,
 // reassociated: sum over runs of F2[o1] * sum over the run of v F1[o0].
 template <int MODE, int LG_TB, int LG_KB, int WAVES, int UNROLL>
-__global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 6))) void mttkrp3_blk_kernel(
+__global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(CPTC_BLK3_WPE, CPTC_BLK3_WPE))) void mttkrp3_blk_kernel(
     const uint64_t* __restrict__ coords, const double* __restrict__ vals,
     const uint32_t* __restrict__ span_start, const uint32_t* __restrict__ span_cnt,
     const uint32_t* __restrict__ span_kb, const uint32_t* __restrict__ chunk_span0,
@@ -53,6 +50,7 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(6, 
     constexpr int TB = 1 << LG_TB;
     constexpr int KB = 1 << LG_KB;
     constexpr int U = UNROLL;
+    static_assert(WAVE % U == 0, "a full window is whole batches of U elements");
     constexpr uint32_t NONE = 0xFFFFFFFFu;
     constexpr int sh_t = (MODE == 0) ? 30 : (MODE == 1) ? 15 : 0;
     constexpr int sh0 = (MODE == 0) ? 15 : 30;
