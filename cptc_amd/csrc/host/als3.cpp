@@ -252,12 +252,14 @@ void choose_tiles(Als3& h)
 }
 
 // Blocked residual views for R in (64, 128] (the one-element-per-wave
-// kernels): 32 target rows x 16 run-level rows per block pair (the kernel's
-// CPTC_BLK3_LG_TB / CPTC_BLK3_LG_KB), 2048 elements per workgroup, run-level
-// rows staged from 64 elements of a block pair on (config 3, per launch:
-// 16 x 8 blocks 2.45-2.71, 32 x 8 2.46-2.52, 32 x 32 2.93-3.00; chunks of
-// 8192 / 4096 / 1024 elements 2.48-2.69 / 2.46-2.55 / 2.43-2.52; staging
-// from 32 / 128 elements 2.54-2.58 / 2.43-2.54 ms).  Used when the FP64
+// kernels): 32 target rows x 16 run-level rows per block pair, 1024 elements
+// per workgroup, run-level rows staged from 64 elements of a block pair on
+// (blk3_params.hpp; config 3, per launch, with the chunks in run-level order:
+// chunks of 512 / 768 / 1024 / 1536 / 2048 / 4096 elements 2.19-2.26 /
+// 2.16-2.21 / 2.12-2.20 / 2.15-2.19 / 2.20-2.25 / 2.27-2.37 ms; 16-row target
+// blocks 2.19-2.27; staging from 32 / 96 / 128 elements 2.26-2.31 / equal /
+// equal; before that, in target-block order: 16 x 8 blocks 2.45-2.71, 32 x 8
+// 2.46-2.52, 32 x 32 2.93-3.00).  Used when the FP64
 // residual kernel runs without the MFMA tile kernel beside it: alone it is
 // faster than the row-segment kernel (config 3: 2.45 against 3.1-3.4 ms per
 // launch), beside the FP32 tile kernel it is not (its LDS keeps tile
