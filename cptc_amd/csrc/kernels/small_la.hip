@@ -449,6 +449,9 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
 // pseudoinverse of a symmetric matrix (solver.cu:764-775, 900-1002).
 // A in LDS (R <= 128) or global scratch; V in global scratch.
 // ---------------------------------------------------------------------------
+constexpr int JACOBI_SWEEPS = 15;
+constexpr double JACOBI_TOL = 1e-14;
+
 __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double* __restrict__ Ain,
                                                                    int R, double* work,
                                                                    double* V,
@@ -489,7 +492,9 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         if (tid == 0) s_fro = sqrt(f);
     }
     __syncthreads();
-    for (int sweep = 0; sweep < 100; ++sweep)
+    // gesvdj's settings in the reference (solver.cu:837-838): at most 15
+    // sweeps, stop once the off-diagonal norm is <= 1e-14 of the Frobenius norm
+    for (int sweep = 0; sweep < JACOBI_SWEEPS; ++sweep)
     {
         double o = 0.0;
         for (int x = tid; x < n2; x += PINV_THREADS)
@@ -497,7 +502,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         o = block_sum(o);
         if (tid == 0) s_off = sqrt(o);
         __syncthreads();
-        if (!(s_off > 1e-15 * s_fro)) break;
+        if (!(s_off > JACOBI_TOL * s_fro)) break;
         for (int round = 0; round < Rp - 1; ++round)
         {
             // round-robin: index 0 fixed, others rotate
@@ -525,16 +530,46 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
                 rot_s[k] = s;
             }
             __syncthreads();
-            // A <- A J (columns p, q)
-            for (int x = tid; x < npairs * R; x += PINV_THREADS)
+            // A <- J^T A J, one 2 x 2 block (rows of pair a, columns of pair
+            // b) per item, in place: the column rotation of pair b, then the
+            // row rotation of pair a on the column-rotated values, the same
+            // operations on every entry as a pass over all columns followed
+            // by a pass over all rows, with one barrier per round fewer
+            for (int x = tid; x < npairs * npairs; x += PINV_THREADS)
             {
-                const int k = x / R, r = x % R;
-                const int p = pair_p[k], q = pair_q[k];
-                if (q >= R || rot_s[k] == 0.0) continue;
-                const double c = rot_c[k], s = rot_s[k];
-                const double arp = A[r * R + p], arq = A[r * R + q];
-                A[r * R + p] = c * arp - s * arq;
-                A[r * R + q] = s * arp + c * arq;
+                const int a = x / npairs, b = x % npairs;
+                const int i0 = pair_p[a], i1 = pair_q[a], j0 = pair_p[b], j1 = pair_q[b];
+                const bool ra = i1 < R && rot_s[a] != 0.0, rb = j1 < R && rot_s[b] != 0.0;
+                if (!ra && !rb) continue;
+                const bool has_i1 = i1 < R, has_j1 = j1 < R;
+                double a00 = A[i0 * R + j0];
+                double a01 = has_j1 ? A[i0 * R + j1] : 0.0;
+                double a10 = has_i1 ? A[i1 * R + j0] : 0.0;
+                double a11 = (has_i1 && has_j1) ? A[i1 * R + j1] : 0.0;
+                if (rb)
+                {
+                    const double c = rot_c[b], sn = rot_s[b];
+                    const double t00 = c * a00 - sn * a01, t01 = sn * a00 + c * a01;
+                    const double t10 = c * a10 - sn * a11, t11 = sn * a10 + c * a11;
+                    a00 = t00;
+                    a01 = t01;
+                    a10 = t10;
+                    a11 = t11;
+                }
+                if (ra)
+                {
+                    const double c = rot_c[a], sn = rot_s[a];
+                    const double t00 = c * a00 - sn * a10, t10 = sn * a00 + c * a10;
+                    const double t01 = c * a01 - sn * a11, t11 = sn * a01 + c * a11;
+                    a00 = t00;
+                    a01 = t01;
+                    a10 = t10;
+                    a11 = t11;
+                }
+                A[i0 * R + j0] = a00;
+                if (has_j1) A[i0 * R + j1] = a01;
+                if (has_i1) A[i1 * R + j0] = a10;
+                if (has_i1 && has_j1) A[i1 * R + j1] = a11;
             }
             // V <- V J, V in global memory: a thread's VB column pairs are
             // loaded together, then rotated and stored, so a round waits on
@@ -569,18 +604,6 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
                         V[ip[j]] = cc[j] * vp[j] - ss[j] * vq[j];
                         V[iq[j]] = ss[j] * vp[j] + cc[j] * vq[j];
                     }
-            }
-            __syncthreads();
-            // A <- J^T A (rows p, q)
-            for (int x = tid; x < npairs * R; x += PINV_THREADS)
-            {
-                const int k = x / R, r = x % R;
-                const int p = pair_p[k], q = pair_q[k];
-                if (q >= R || rot_s[k] == 0.0) continue;
-                const double c = rot_c[k], s = rot_s[k];
-                const double apr = A[p * R + r], aqr = A[q * R + r];
-                A[p * R + r] = c * apr - s * aqr;
-                A[q * R + r] = s * apr + c * aqr;
             }
             __syncthreads();
         }

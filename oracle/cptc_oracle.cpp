@@ -446,13 +446,15 @@ int pinv_sym(const double* Ain, int R, double* Ainv)
     double fro = 0.0;
     for (double x : a) fro += x * x;
     fro = std::sqrt(fro);
+    // gesvdj's settings (solver.cu:837-838): at most 15 sweeps, tolerance
+    // 1e-14 on the off-diagonal norm relative to the Frobenius norm
     int sweep = 0;
-    for (; sweep < 100; ++sweep)
+    for (; sweep < 15; ++sweep)
     {
         double off = 0.0;
         for (size_t p = 0; p < n; ++p)
             for (size_t q = p + 1; q < n; ++q) off += a[p * n + q] * a[p * n + q];
-        if (std::sqrt(2.0 * off) <= 1e-15 * fro || fro == 0.0) break;
+        if (std::sqrt(2.0 * off) <= 1e-14 * fro || fro == 0.0) break;
         for (size_t p = 0; p + 1 < n; ++p)
             for (size_t q = p + 1; q < n; ++q)
             {
