@@ -133,6 +133,7 @@ def load_traffic(workload: str, sources=SPARSE3_SOURCES):
 SEG_ND_SOURCES = ("cptc_amd/csrc/kernels/seg_keys.hip",)
 UNIT_SUMS_SOURCES = ("cptc_amd/csrc/kernels/unit_sums.hip",)
 LDS_PEAK_TBS = 78.6   # 256 CUs x 128 B/clk x 2.4 GHz
+L1_PEAK_TBS = 39.3    # vector L1 / texture path: 256 CUs x 64 B/clk x 2.4 GHz
 
 
 def load_traffic_named(name: str, sources, workload: str):
@@ -297,6 +298,13 @@ def main() -> int:
             "compulsory_GBs": round(comp_gbs, 1),
             "compulsory_frac": round(comp_gbs / HBM_PEAK_GBS, 4),
             "compulsory_bytes_per_launch": [int(b) for b in compulsory],
+            # the floor that every row an L1 hit would leave: each residual
+            # nonzero loads one R-wide FP64 row of its element-level factor
+            # through the vector L1 (the run-level rows come once per run,
+            # from LDS when staged)
+            "element_gather_floor_ms": round(snnz * R * 8 / (L1_PEAK_TBS * 1e12) * 1e3, 4),
+            "element_gather_floor_basis": "residual nnz x R x 8 B through the vector L1 at "
+                                          "64 B/clk/CU, 256 CUs, 2.4 GHz",
             "traffic_source": (f"profiles/mttkrp_sparse3_{workload}_pmc.json "
                                f"(kernel sources sha {prof['kernel_src_sha']})") if prof else
                               "none for these kernel sources: traffic null",

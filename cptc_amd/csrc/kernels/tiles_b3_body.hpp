@@ -156,23 +156,41 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         }
     };
     bf16x8 ahi[8], alo[8];
-    // the A operand halves of the header's tile (compacted image)
-    auto load_a = [&](bf16x8 (&ah)[8], bf16x8 (&al)[8]) {
+    // The A operand of the compacted image in two steps, so that the loads
+    // of the next tile are in flight while the current rank block computes:
+    // issue_a loads the header's tile's 16 segments of the lane into araw
+    // (raw 16-byte segments: hi halves then lo halves of 4 cells each),
+    // assemble_a moves them into the operand registers.
+    using raw4 = decltype(__builtin_amdgcn_raw_buffer_load_b128(rseg, 0u, 0, 0));
+    raw4 araw[16];
+    auto issue_a = [&]() {
         // the lane's 16 segments (w = 8 ww + p, cells 8h .. 8h + 7) are bits
         // 4 p + 2 h and 4 p + 2 h + 1 of mask word 2 am + ww
+        // (shifted by 2 h once, so the per-p masks and bit positions are
+        // constants rather than per-lane registers)
         const uint32_t mw = uint32_t(__shfl(int(hdr_w), 2 * am + ww));
-        const uint32_t base = hdr_so + uint32_t(__shfl(int(hdr_w), 32 + 2 * am + ww));
+        const uint32_t sh = 2u * uint32_t(h);
+        const uint32_t mwh = mw >> sh;
+        const uint32_t base = hdr_so + uint32_t(__shfl(int(hdr_w), 32 + 2 * am + ww)) +
+                              uint32_t(__builtin_popcount(mw & ((1u << sh) - 1u)));
 #pragma unroll
         for (int p = 0; p < 8; ++p)
         {
-            const int b = 4 * p + 2 * h;
-            const uint32_t i0 = base + uint32_t(__builtin_popcount(mw & ((1u << b) - 1u)));
-            const uint32_t o0 = ((mw >> b) & 1u) ? i0 * 16u : OOB;
-            const uint32_t o1 = ((mw >> (b + 1)) & 1u) ? (i0 + ((mw >> b) & 1u)) * 16u : OOB;
+            const uint32_t i0 = base + uint32_t(__builtin_popcount(mwh & ((1u << (4 * p)) - 1u)));
+            const uint32_t b0 = (mwh >> (4 * p)) & 1u, b1 = (mwh >> (4 * p + 1)) & 1u;
+            const uint32_t o0 = b0 ? i0 * 16u : OOB;
+            const uint32_t o1 = b1 ? (i0 + b0) * 16u : OOB;
+            araw[2 * p] = __builtin_amdgcn_raw_buffer_load_b128(rseg, o0, 0, 0);
+            araw[2 * p + 1] = __builtin_amdgcn_raw_buffer_load_b128(rseg, o1, 0, 0);
+        }
+    };
+    auto assemble_a = [&]() {
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+        {
             // (the load's vector indexed directly: a __builtin_bit_cast of it
             // to another 4 x 32-bit vector type compiled to a one-dword load)
-            const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rseg, o0, 0, 0);
-            const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rseg, o1, 0, 0);
+            const raw4 v0 = araw[2 * p], v1 = araw[2 * p + 1];
             u32x4 hv, lv;
             hv[0] = uint32_t(v0[0]);
             hv[1] = uint32_t(v0[1]);
@@ -182,14 +200,15 @@ __device__ __forceinline__ void dense_tiles_b3_body(
             lv[1] = uint32_t(v0[3]);
             lv[2] = uint32_t(v1[2]);
             lv[3] = uint32_t(v1[3]);
-            ah[p] = __builtin_bit_cast(bf16x8, hv);
-            al[p] = __builtin_bit_cast(bf16x8, lv);
+            ahi[p] = __builtin_bit_cast(bf16x8, hv);
+            alo[p] = __builtin_bit_cast(bf16x8, lv);
         }
     };
     auto load_cells = [&](size_t t) {
         if constexpr (COMPACT)
         {
-            load_a(ahi, alo);
+            issue_a();
+            assemble_a();
             return;
         }
         const float* __restrict__ T = tile_f32 + t * 4096;
@@ -245,6 +264,9 @@ __device__ __forceinline__ void dense_tiles_b3_body(
 
     u32x4 bh, bl;
     float4 cw4[4];
+    // the item's FP64 outer weight (HAS_W), loaded by every lane at a
+    // clamped rank (no path skips the load, so the waits can count it)
+    double wop = 1.0;
     auto load_ops = [&](size_t t, int rb) {
         const int cb = hdr[HDR * t + CS];   // contracted block (16 rows)
         const int wb = hdr[HDR * t + WS];   // weight block
@@ -254,6 +276,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         const float4* pw = fw + (size_t(wb) * size_t(Rq) + size_t(rb + n)) * 4;
 #pragma unroll
         for (int s = 0; s < 4; ++s) cw4[s] = pw[s];
+        if constexpr (HAS_W) wop = W[t * size_t(R) + size_t(rb + n < R ? rb + n : R - 1)];
     };
 
     size_t it = it0;
@@ -278,6 +301,9 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         }
         ob = hdr[HDR * t + MODE] * 16;
         const int r = rb + n;
+        // (the operands below were loaded with the previous item's; the
+        // next item's overwrite them before this item's epilogue)
+        const double wr = (r < R) ? wop : 0.0;
         size_t itn = it;
         int rbn = rb + rstep;
         if (rbn >= Rq)
@@ -290,10 +316,34 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         // modes 0 / 1 of the dense image: the next tile's cells load while
         // this rank block computes (the raw cell registers are free once the
         // current tile is split; mode 2's 64 scalar loads leave no room for
-        // that, and the compacted image prefetches the tile header instead)
+        // that); the compacted image's next A operand likewise (issue_a)
         const bool next_tile = more && itn != it;
         constexpr bool PF_CELLS = MODE != 2 && !COMPACT;
         if (PF_CELLS && next_tile) load_cells(tn);
+        if constexpr (COMPACT)
+        {
+            // this rank block's B and weight operands are waited for here,
+            // before the next tile's loads are issued: the wait for them
+            // below would otherwise count those loads too (the two paths
+            // into the products merge with different loads in flight, and
+            // the merged wait is the stricter one)
+            asm volatile("" ::"v"(bh), "v"(bl), "v"(wop));
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                asm volatile("" ::"v"(cw4[s].x), "v"(cw4[s].y), "v"(cw4[s].z), "v"(cw4[s].w));
+        }
+        // the next tile's A operand loads during this rank block (its
+        // address arithmetic placed after the first products are issued, so
+        // it runs while the matrix cores work); the header after it loads
+        // once its words have been read
+        auto prefetch_a = [&]() {
+            if constexpr (COMPACT)
+                if (next_tile)
+                {
+                    issue_a();
+                    if (itn + 1 < it1) load_hdr(tile_of(itn + 1));
+                }
+        };
 
         // Software pipeline over the four w pairs: the products of pair
         // pp + 1 are issued before the FMAs of pair pp consume theirs, so
@@ -334,6 +384,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
 #if CPTC_B3_PIPE == 2
         floatx16 x0, x1;
         products(0, x0, x1);
+        prefetch_a();
         weigh(0, x0, x1);
         fence();
         products(2, x0, x1);
@@ -348,6 +399,7 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         floatx16 x0, x1, y0, y1;
         products(0, x0, x1);
         products(2, y0, y1);
+        prefetch_a();
         weigh(0, x0, x1);
         fence();
         products(4, x0, x1);
@@ -358,11 +410,12 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         fence();
         weigh(6, y0, y1);
 #endif
-        if (more) load_ops(tn, rbn);
+        // unconditional (the last item reloads its own operands), so the
+        // loads land in the registers the next rank block reads instead of
+        // being copied there, with a wait, at the end of the iteration
+        load_ops(tn, more ? rbn : rb);
         // unconditional epilogue (ranks >= R hold zeros and are not flushed),
         // so the FMAs above are not sunk into a branch
-        double wr = 1.0;
-        if constexpr (HAS_W) wr = (r < R) ? W[t * size_t(R) + r] : 0.0;
 #pragma unroll
         for (int o = 0; o < 8; ++o)
         {
@@ -388,9 +441,14 @@ __device__ __forceinline__ void dense_tiles_b3_body(
         if (!more) break;
         if (next_tile)
         {
-            if (!PF_CELLS) load_cells(tn);
-            split_cells();
-            if (itn + 1 < it1) load_hdr(tile_of(itn + 1));
+            if constexpr (COMPACT)
+                assemble_a();
+            else
+            {
+                if (!PF_CELLS) load_cells(tn);
+                split_cells();
+                if (itn + 1 < it1) load_hdr(tile_of(itn + 1));
+            }
         }
         it = itn;
         rb = rbn;
