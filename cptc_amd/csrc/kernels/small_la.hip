@@ -20,7 +20,10 @@ constexpr int WAVE = 64;
 // partial[p] (one RT x RT output tile per grid.y); stage 2 sums partials in
 // p order.  16 x 16 threads, TPT x TPT outputs per thread (RT = 16 * TPT).
 // ---------------------------------------------------------------------------
-template <int TPT>
+// TRI: grid.y runs over the upper-triangle tile pairs (bi <= bj) only; the
+// partial's other tiles are left unwritten and sum_partials_sym_kernel reads
+// their mirror images (the same products, so the same bits).
+template <int TPT, bool TRI = false>
 __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restrict__ F,
                                                            size_t rows, int R, size_t rpw,
                                                            int ntile, double* __restrict__ part)
@@ -30,7 +33,18 @@ __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restr
     __shared__ double sa[CH][RT + 1];
     __shared__ double sb[CH][RT + 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int bi = int(blockIdx.y) / ntile, bj = int(blockIdx.y) % ntile;
+    int bi = int(blockIdx.y) / ntile, bj = int(blockIdx.y) % ntile;
+    if constexpr (TRI)
+    {
+        int rem = int(blockIdx.y);
+        bi = 0;
+        while (rem >= ntile - bi)
+        {
+            rem -= ntile - bi;
+            ++bi;
+        }
+        bj = bi + rem;
+    }
     const int ci = bi * RT, cj = bj * RT;
     const size_t r_lo = size_t(blockIdx.x) * rpw;
     const size_t r_hi = (r_lo + rpw < rows) ? r_lo + rpw : rows;
@@ -98,6 +112,26 @@ __global__ void sum_partials_kernel(const double* __restrict__ part, int P, size
     for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
          x += size_t(gridDim.x) * blockDim.x)
         out[x] = ordered_sum(part, P, n, x);
+}
+
+// sum_partials_kernel over upper-triangle partials (gram_partial_kernel<., true>
+// with tiles of `tile` ranks): the upper tiles' entries are summed (partials
+// read in order, coalesced) and written to their own place and, above the
+// diagonal tiles, to their mirror's (the one scattered access, once per
+// entry rather than once per partial).
+__global__ void sum_partials_sym_kernel(const double* __restrict__ part, int P, int R, int tile,
+                                        double* __restrict__ out)
+{
+    const size_t n = size_t(R) * R;
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
+         x += size_t(gridDim.x) * blockDim.x)
+    {
+        const int r = int(x / size_t(R)), c = int(x % size_t(R));
+        if (r / tile > c / tile) continue;
+        const double v = ordered_sum(part, P, n, x);
+        out[x] = v;
+        if (r / tile < c / tile) out[size_t(c) * R + r] = v;
+    }
 }
 
 __global__ void hadamard_kernel(const double* A, const double* B, double* C, size_t n)
@@ -1020,9 +1054,18 @@ extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, voi
     }
     else
     {
-        const int nt = (R + 127) / 128;
-        hipLaunchKernelGGL(gram_partial_kernel<8>, dim3(P, nt * nt), dim3(256), 0, s, d_F, rows,
-                           R, rpw, nt, pd);
+        // 64 x 64 tiles, the upper triangle only: at R = 128 three tiles of
+        // 16 accumulators per thread (three workgroups per CU) instead of one
+        // 128 x 128 tile of 64 (one per CU); each entry the same ordered sum
+        // as before.  Config 3: 37 -> 26.5 us per launch on average.
+        const int nt = (R + 63) / 64;
+        hipLaunchKernelGGL((gram_partial_kernel<4, true>), dim3(P, nt * (nt + 1) / 2), dim3(256),
+                           0, s, d_F, rows, R, rpw, nt, pd);
+        CPTC_LAUNCHED();
+        hipLaunchKernelGGL(sum_partials_sym_kernel, dim3(cptc::grid_for(RR, 256, 1024)),
+                           dim3(256), 0, s, pd, P, R, 64, d_G);
+        CPTC_LAUNCHED();
+        return CPTC_OK;
     }
     CPTC_LAUNCHED();
     hipLaunchKernelGGL(sum_partials_kernel, dim3(cptc::grid_for(RR, 256, 1024)), dim3(256), 0, s,

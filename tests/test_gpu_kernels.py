@@ -373,14 +373,18 @@ def test_dense_tile_pack_last_write_wins(ca, orc, dev):
     assert np.array_equal(tf.numpy(), X.ravel().astype(np.float32))
 
 
-@pytest.mark.parametrize("rows,R", [(1, 1), (1000, 7), (28818, 128), (5000, 200), (0, 16)])
+@pytest.mark.parametrize("rows,R", [(1, 1), (1000, 7), (28818, 128), (5000, 200), (0, 16),
+                                    (300, 65), (9184, 100)])
 def test_gram(ca, dev, rows, R):
+    """cptc_gram against numpy; above R = 64 only the upper-triangle tiles are
+    summed and the rest mirrored, so G must also be exactly symmetric."""
     F = np.random.default_rng(rows + R).standard_normal((rows, R))
     dF = to_dev(ca, F)
     G = zeros(ca, (R, R))
     assert ca.lib.cptc_gram(dF.data_ptr(), rows, R, G.data_ptr(), stream(ca)) == 0
     ca.sync()
     assert rel_err(G.numpy(), F.T @ F) < 1e-13 if rows else np.all(G.numpy() == 0)
+    assert np.array_equal(G.numpy(), G.numpy().T)
 
 
 @pytest.mark.parametrize("R,dim", [(64, 100), (65, 1), (65, 77), (100, 1000), (127, 63),
