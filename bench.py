@@ -13,11 +13,13 @@ on the same row-sorted views, copied from the device, from the same initial
 factors, for --cpu-iters iterations on the full tensor; the first iteration
 is dropped and the median and mean of the rest are reported.
 
-roofline (the FP64 sparse kernel, per launch): achieved = HBM bytes per
-launch measured by rocprofv3 --pmc (profiles/mttkrp_sparse3_<workload>_pmc.json,
-valid only while the kernel's sources hash to the value recorded there) over
-the launch time measured here with hipEvents; the no-reuse gather model and
-the compulsory bytes over the same time are reported beside it.
+roofline (the FP64 sparse kernel, per launch): achieved = the algorithmic
+bytes of the no-reuse gather model over the launch time measured here with
+hipEvents; traffic = the bytes per launch between L2 and memory measured by
+rocprofv3 --pmc (profiles/mttkrp_sparse3_<workload>_pmc.json, valid only while
+the kernel's sources hash to the value recorded there); the compulsory bytes
+and the element-gather floor (a probe kernel that runs the blocked kernel's
+element-level row gathers alone, after the timed region) beside them.
 --fused runs the merged single-grid MTTKRP (ALS_FUSED).
 
 --config 4 / 5 run the generic N-order path on BASELINE configs 4 and 5
@@ -268,6 +270,8 @@ def main() -> int:
     tile_ms = [float(x) / kit for x in tile_ms_acc]
     tiles_timed = use_mfma and ntiles and all(x > 0 for x in tile_ms)
 
+    probe_ms = h.gather_probe(3) if blocked else None
+
     cpu = None
     if not args.no_cpu and args.cpu_iters > 0:
         cpu = cpu_baseline(ca, h, t, R, args.cpu_iters, use_mfma, F_init)
@@ -298,13 +302,19 @@ def main() -> int:
             "compulsory_GBs": round(comp_gbs, 1),
             "compulsory_frac": round(comp_gbs / HBM_PEAK_GBS, 4),
             "compulsory_bytes_per_launch": [int(b) for b in compulsory],
-            # the floor that every row an L1 hit would leave: each residual
-            # nonzero loads one R-wide FP64 row of its element-level factor
-            # through the vector L1 (the run-level rows come once per run,
-            # from LDS when staged)
-            "element_gather_floor_ms": round(snnz * R * 8 / (L1_PEAK_TBS * 1e12) * 1e3, 4),
-            "element_gather_floor_basis": "residual nnz x R x 8 B through the vector L1 at "
-                                          "64 B/clk/CU, 256 CUs, 2.4 GHz",
+            # the element-level row gathers alone, measured: the probe kernel
+            # runs them in the blocked kernel's order and occupancy (None
+            # when the layout is not blocked)
+            "element_gather_floor_ms": ([round(float(x), 4) for x in probe_ms]
+                                        if probe_ms is not None else None),
+            "element_gather_floor_basis": "cptc_gather_probe3_blk on the same blocked view and "
+                                          "factors: each residual nonzero's R-wide FP64 row of "
+                                          "its element-level factor, same chunks, waves and rows "
+                                          "in flight, nothing else (mean of 3 launches per mode, "
+                                          "after the timed region)",
+            # the same rows if every one were an L1 hit: R x 8 B per residual
+            # nonzero through the vector L1 at its 64 B per clock per CU
+            "l1_floor_model_ms": round(snnz * R * 8 / (L1_PEAK_TBS * 1e12) * 1e3, 4),
             "traffic_source": (f"profiles/mttkrp_sparse3_{workload}_pmc.json "
                                f"(kernel sources sha {prof['kernel_src_sha']})") if prof else
                               "none for these kernel sources: traffic null",

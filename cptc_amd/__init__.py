@@ -279,6 +279,15 @@ class Als3:
         check(lib.cptc_als3_tile_times(self._h, out.ctypes.data), "cptc_als3_tile_times")
         return out
 
+    def gather_probe(self, reps: int = 3) -> np.ndarray:
+        """ms per launch, per mode, of the element-gather probe on the blocked
+        residual view (the blocked kernel's element-level row gathers alone,
+        same order and occupancy): the floor those gathers set."""
+        out = np.zeros(3, np.float64)
+        check(lib.cptc_als3_gather_probe(self._h, int(reps), out.ctypes.data),
+              "cptc_als3_gather_probe")
+        return out
+
     def sgd(self, iters: int, gamma: float = 1e-9, batch: int = 1 << 20,
             seed: int = 42) -> np.ndarray:
         """CP-SGD on the residual (ALS_SGD); batch RMSE per iteration (-1 where

@@ -164,6 +164,7 @@ SIGNATURES = {
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_mttkrp_sparse3_blk": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I,
                                      C.c_uint64, C.c_uint64, _P]),
+    "cptc_gather_probe3_blk": (_I, [_I, _P, _P, _P, _P, _P, _Z, _P, _I, _P, _P]),
     "cptc_mttkrp_merged3": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P, _P,
                                  _P, _I, _I, _I, _I, _P]),
     "cptc_mttkrp_merged3_ex": (_I, [_I, _P, _P, _Z, _P, _P, _Z, _P, _P, _P, _P, _P, _Z, _P, _P,
@@ -184,6 +185,7 @@ SIGNATURES = {
     "cptc_als3_mttkrp": (_I, [_P, _I, _P]),
     "cptc_als3_kernel_times": (_I, [_P, _P, C.POINTER(_I), _I]),
     "cptc_als3_tile_times": (_I, [_P, _P]),
+    "cptc_als3_gather_probe": (_I, [_P, _I, _P]),
     "cptc_als3_sgd": (_I, [_P, _I, _D, C.c_uint32, C.c_uint64, _P]),
     "cptc_sgd3_sample": (_I, [_P, C.c_uint32, C.c_uint64, C.c_uint64, _P]),
     "cptc_sgd3_update": (_I, [_P, _P, _P, C.c_uint32, _P, _P, _P, _P, _I, _D, _P]),

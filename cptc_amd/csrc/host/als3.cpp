@@ -1074,6 +1074,58 @@ extern "C" int cptc_als3_tile_times(void* handle, double* out3)
     return CPTC_OK;
 }
 
+extern "C" int cptc_als3_gather_probe(void* handle, int reps, double* out3)
+{
+    Als3* h = cptc::as_h(handle);
+    CPTC_REQUIRE(h && out3 && reps >= 1, CPTC_ERR_ARG, "cptc_als3_gather_probe: bad arguments");
+    CPTC_REQUIRE(h->blk.ready, CPTC_ERR_STATE,
+                 "cptc_als3_gather_probe: no blocked residual view (R in (64, 128] with MFMA "
+                 "tiles, or ALS_SPARSE_BLOCKED=1)");
+    const cptc::DevBlk3& b = h->blk;
+    double* sink = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = CPTC_OK;
+    auto fail = [&](hipError_t e) {
+        cptc::set_error("cptc_als3_gather_probe: %s", hipGetErrorString(e));
+        rc = CPTC_ERR_HIP;
+    };
+    hipError_t e = hipMalloc(&sink, sizeof(double));
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e != hipSuccess) fail(e);
+    for (int m = 0; m < 3 && rc == CPTC_OK; ++m)
+    {
+        // the element-level factor of mttkrp_launch: F_j for mode 0, F_i otherwise
+        const double* F1 = m == 0 ? h->F[1] : h->F[0];
+        if ((e = hipEventRecord(e0, h->s)) != hipSuccess)
+        {
+            fail(e);
+            break;
+        }
+        for (int r = 0; r < reps && rc == CPTC_OK; ++r)
+            rc = cptc_gather_probe3_blk(m, b.d_coords[m], b.d_span_start[m], b.d_span_cnt[m],
+                                        b.d_chunk_span0[m], b.d_chunk_nspan[m], b.nchunk[m], F1,
+                                        h->R, sink, h->s);
+        if (rc != CPTC_OK) break;
+        float ms = 0.0f;
+        if ((e = hipEventRecord(e1, h->s)) != hipSuccess || (e = hipEventSynchronize(e1)) != hipSuccess ||
+            (e = hipEventElapsedTime(&ms, e0, e1)) != hipSuccess)
+        {
+            fail(e);
+            break;
+        }
+        out3[m] = double(ms) / reps;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (sink)
+    {
+        (void)hipStreamSynchronize(h->s);
+        (void)hipFree(sink);
+    }
+    return rc;
+}
+
 extern "C" int cptc_als3_mttkrp(void* handle, int mode, double* host_out)
 {
     Als3* h = cptc::as_h(handle);

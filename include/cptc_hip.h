@@ -312,6 +312,18 @@ int cptc_mttkrp_sparse3_blk(int mode, const uint64_t* d_coords, const double* d_
                             size_t nchunk, const double* d_F1, const double* d_F2, double* d_FtV,
                             int R, uint64_t dim_target, uint64_t dim_f2, void* stream);
 
+/* Measurement probe, no reference counterpart: the element-level row
+ * gathers of cptc_mttkrp_sparse3_blk alone (the same chunks, spans, per-wave
+ * element ranges, rows in flight and resident waves; no run-level rows, LDS
+ * accumulation or atomics), i.e. the floor those gathers set on the same
+ * blocked view.  d_F1 is the mode's element-level factor (F_j for mode 0,
+ * F_i otherwise); d_sink (one double) is written only if the row sums hit a
+ * sentinel no finite factor produces. */
+int cptc_gather_probe3_blk(int mode, const uint64_t* d_coords, const uint32_t* d_span_start,
+                           const uint32_t* d_span_cnt, const uint32_t* d_chunk_span0,
+                           const uint32_t* d_chunk_nspan, size_t nchunk, const double* d_F1,
+                           int R, double* d_sink, void* stream);
+
 /* One launch for both halves of an order-3 mode's MTTKRP: the MFMA dense
  * tiles (as cptc_mttkrp_dense_tiles3; grouped when d_order / d_group_off are
  * given) and the FP64 residual segments (as cptc_mttkrp_sparse3) in one grid
@@ -499,6 +511,11 @@ int cptc_als3_kernel_times(void* handle, double* out6, int* iters, int reset);
  * with it; 0 for modes whose tiles ran in the merged grid or not at all.
  * Measurement helper, no reference counterpart. */
 int cptc_als3_tile_times(void* handle, double* out3);
+/* ms per launch of cptc_gather_probe3_blk on the handle's blocked residual
+ * view and current factors, per mode (mean of `reps` launches between
+ * hipEvents on the driver's stream; waits for them).  CPTC_ERR_STATE without
+ * a blocked view.  Measurement helper, no reference counterpart. */
+int cptc_als3_gather_probe(void* handle, int reps, double* out3);
 
 /* CP-SGD (cptc_sgd3_run) on the handle's mode-0 residual view, factors and
  * lambda (main.cu:467-501 starts it with lambda = 1, which a fresh handle
