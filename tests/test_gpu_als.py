@@ -531,6 +531,24 @@ def test_merged_switches(ca, orc, dev, tmp_path, switch, value, monkeypatch):
     assert len(fits) == 4 and np.max(np.abs(fits - ref)) <= 1e-8, (fits, ref)
 
 
+@pytest.mark.parametrize("fm,path", [("0.99", "FP64 only"), ("0", "MFMA tiles + FP64 residual")])
+def test_cli_fill_min(ca, dev, tmp_path, fm, path):
+    """ALS_FILL_MIN (main.cu:370-391) replaces the CU-scaled fill_min in the
+    density check: a threshold above every fill keeps the tiles in FP64 views,
+    0 sends them to the matrix cores."""
+    t = make(ca, "clustered", 3)
+    fpath = str(tmp_path / "t.tns")
+    ca.write_tns(fpath, t)
+    env = dict(os.environ, ALS_FILL_MIN=fm)
+    out = subprocess.run([ca.CLI_PATH, fpath, "2", "8"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    line = [l for l in out.stdout.splitlines() if l.startswith("[Main] density check:")]
+    assert len(line) == 1 and f"(threshold {float(fm):g}) -> {path}" in line[0], line
+    assert "tiles=0 " not in line[0]
+    assert "[Main] device=" not in out.stdout   # the CU-scaled default was not consulted
+
+
 def test_cli_profile_line(ca, dev, tmp_path):
     """ALS_PROFILE (als.cu:748-760): after each '[ALS] iter' line,
     '[ALS][profile] iter k gram=.. mttkrp=.. solve=.. fit=.. (iter=..)' with

@@ -926,6 +926,53 @@ def test_dump_input_order(ca, dev, tmp_path):
     assert abs(np.sum((t.val - xhat) ** 2) - res) <= 1e-9 * x2
 
 
+def cli_fit(out):
+    """Fit of the last '[GEN] iter' line."""
+    it = [l for l in out.splitlines() if l.startswith("[GEN] iter ")]
+    return float(it[-1].split("fit=")[1].split()[0])
+
+
+def test_cli_generic_switches(ca, dev, tmp_path):
+    """The generic driver's switches through the CLI (generic.cu:1647-1663,
+    1796-1840, 2114-2116; main.cu:102-130): GEN_REORDER (none / an unknown
+    name falls back to cadr), GEN_REORDER_T, GEN_DENSE=0, a GEN_DENSE_INNER
+    that is not three distinct modes (the dense path is disabled),
+    GEN_SOLVER=svd (pseudoinverse instead of the ridge Cholesky: the same fit
+    on a well-conditioned problem), GEN_SEED (another start), and
+    ALS_GENERIC_FORCE=1, which sends an order-3 file down the generic path."""
+    rng = np.random.default_rng(9)
+    dims = (40, 35, 48, 3)
+    t = tensor(ca, clustered(rng, dims, (0, 1, 2), 0.5, 3000), dims, rng)
+    path = str(tmp_path / "t4.tns")
+    ca.write_tns(path, t)
+
+    def run(p=path, **env):
+        r = subprocess.run([ca.CLI_PATH, p, "3", "8"], capture_output=True, text=True,
+                           env=dict(os.environ, **env), timeout=120)
+        assert r.returncode == 0, (env, r.stderr)
+        return r.stdout
+
+    base = run()
+    assert "[GEN] reorder=hits(T=3)" in base and "[GEN] dense: units=" in base
+    out = run(GEN_REORDER="none", GEN_DENSE="0")
+    assert "[GEN] reorder=none" in out and "[GEN] dense: units=" not in out
+    out = run(GEN_REORDER="bogus")
+    assert "[GEN] unknown GEN_REORDER=bogus -> falling back to cadr" in out
+    assert "[GEN] reorder=cadr" in out
+    assert "[GEN] reorder=hits(T=1)" in run(GEN_REORDER_T="1")
+    out = run(GEN_DENSE_INNER="0,0,1")
+    assert "[GEN] dense path disabled: GEN_DENSE_INNER=0,0,1" in out
+    assert "[GEN] dense: units=" not in out
+    assert abs(cli_fit(run(GEN_SOLVER="svd")) - cli_fit(base)) <= 1e-6
+    assert cli_fit(run(GEN_SEED="7")) != cli_fit(base)
+    t3 = tensor(ca, clustered(rng, (40, 35, 48), (0, 1, 2), 0.5, 2000), (40, 35, 48), rng)
+    p3 = str(tmp_path / "t3.tns")
+    ca.write_tns(p3, t3)
+    out = run(p3, ALS_GENERIC_FORCE="1")
+    assert "[Main] order-3 tensor -> generic" in out and "[GEN] reorder=cadr" in out
+    assert "[GEN] iter 3/3" in out
+
+
 def test_cli_generic_and_selftest(ca, dev, tmp_path):
     rng = np.random.default_rng(8)
     dims = (40, 35, 48, 3)
