@@ -341,7 +341,8 @@ __global__ void gram_hadamard_kernel(const double* __restrict__ G, int ngram, in
 //
 // chol_apply_kernel stages L in LDS and solves one right-hand-side row per
 // lane with its y / x vector in registers (loops unrolled to RT >= R): the
-// reference's k-ascending forward and backward substitutions.
+// reference's k-ascending forward and backward substitutions, each pivot's
+// division a multiplication by its reciprocal (chol_substitute).
 constexpr int CHOL_RM = 32;
 constexpr int CHOL_T = 64;     // chol_apply_kernel: one right-hand side per thread
 constexpr int CHOL_FT = 256;   // chol_factor_kernel
@@ -417,6 +418,63 @@ __global__ __launch_bounds__(CHOL_FT) void chol_factor_kernel(const double* __re
             if (c0 + c < R) Lout[size_t(row) * R + c0 + c] = (c0 + c <= row) ? a[c] : 0.0;
 }
 
+// L y' = y, then L^T x = y', with the Cholesky factor in LDS (RT x RT, padded
+// with the identity, so padding entries stay exact zeros) and the reciprocals
+// of its diagonal (dinv): row by row, each row's sum in ascending k as the
+// reference's substitutions, the division by the pivot done as a
+// multiplication by its reciprocal (one correctly rounded division per pivot
+// per workgroup instead of one per pivot and right-hand side; the row's
+// result differs from the division's by at most an ulp).  The next row's
+// entries of L (and its reciprocal) load into a second register set while
+// the current row's sum runs; the empty asm with a memory clobber keeps a
+// later row's loads from being hoisted further, which would not fit the
+// registers.
+template <int RT>
+__device__ __forceinline__ void chol_substitute(const double (*L)[RT + 1],
+                                                const double* __restrict__ dinv,
+                                                double (&y)[RT])
+{
+    double cur[RT], nxt[RT], cd = dinv[0], nd = 0.0;
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+    {
+        if (i + 1 < RT)
+        {
+#pragma unroll
+            for (int k = 0; k <= i; ++k) nxt[k] = L[i + 1][k];
+            nd = dinv[i + 1];
+        }
+        double s = y[i];
+#pragma unroll
+        for (int k = 0; k < i; ++k) s -= cur[k] * y[k];
+        y[i] = s * cd;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k <= i; ++k) cur[k] = nxt[k];
+        cd = nd;
+    }
+    // L^T x = y': row i takes column i of L below the diagonal
+    cd = dinv[RT - 1];
+#pragma unroll
+    for (int i = RT - 1; i >= 0; --i)
+    {
+        if (i > 0)
+        {
+#pragma unroll
+            for (int k = i; k < RT; ++k) nxt[k] = L[k][i - 1];
+            nd = dinv[i - 1];
+        }
+        double s = y[i];
+#pragma unroll
+        for (int k = i + 1; k < RT; ++k) s -= cur[k] * y[k];
+        y[i] = s * cd;   // x[i]
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = i; k < RT; ++k) cur[k] = nxt[k];
+        cd = nd;
+    }
+}
+
 template <int RT>
 __global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __restrict__ Lg,
                                                             const double* __restrict__ FtV,
@@ -427,10 +485,13 @@ __global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __rest
     // only exact zeros are subtracted from the others, so the unrolled loops
     // below need no condition on R
     __shared__ double L[RT][RT + 1];
+    __shared__ double dinv[RT];
     for (int x = threadIdx.x; x < RT * RT; x += CHOL_T)
     {
         const int i = x / RT, k = x % RT;
-        L[i][k] = (i < R && k < R) ? Lg[size_t(i) * R + k] : (i == k ? 1.0 : 0.0);
+        const double v = (i < R && k < R) ? Lg[size_t(i) * R + k] : (i == k ? 1.0 : 0.0);
+        L[i][k] = v;
+        if (i == k) dinv[i] = 1.0 / v;
     }
     __syncthreads();
     const size_t row = size_t(blockIdx.x) * CHOL_T + threadIdx.x;
@@ -439,26 +500,7 @@ __global__ __launch_bounds__(CHOL_T) void chol_apply_kernel(const double* __rest
     double y[RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
-    // (the empty asm with a memory clobber keeps each step's LDS reads of L
-    // inside that step; hoisted, all of L would not fit the registers)
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-    {
-        double s = y[i];
-#pragma unroll
-        for (int k = 0; k < i; ++k) s -= L[i][k] * y[k];
-        y[i] = s / L[i][i];
-        asm volatile("" ::: "memory");
-    }
-#pragma unroll
-    for (int i = RT - 1; i >= 0; --i)
-    {
-        double s = y[i];
-#pragma unroll
-        for (int k = i + 1; k < RT; ++k) s -= L[k][i] * y[k];
-        y[i] = s / L[i][i];   // x[i]
-        asm volatile("" ::: "memory");
-    }
+    chol_substitute<RT>(L, dinv, y);
     double* out = F + row * R;
 #pragma unroll
     for (int i = 0; i < RT; ++i)
@@ -483,8 +525,8 @@ chol_solve_wave_kernel(const double* __restrict__ FtF,
 {
     static_assert(RT <= 32 && CHOL_T == 64, "one wave, one row per lane");
     __shared__ double L[RT][RT + 1];
-    __shared__ double colv[RT], lcol[RT];
-    __shared__ double trs;
+    __shared__ double dinv[RT];
+    __shared__ double lcol[2][RT];   // column j of L, alternating buffers by step
     const int lane = threadIdx.x;
     const bool act = lane < RT;
     const bool mine = lane < R;
@@ -493,52 +535,58 @@ chol_solve_wave_kernel(const double* __restrict__ FtF,
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
+    // lane l's value of x (a wave-uniform result)
+    auto lane_f64 = [](double x, int l) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, x);
+        const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u)), l));
+        const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u >> 32)), l));
+        return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
+    };
     double a[RT];
 #pragma unroll
     for (int c = 0; c < RT; ++c) a[c] = (mine && c < R) ? FtF[size_t(lane) * R + c] : 0.0;
-    // eps from the trace, summed in row order (one lane)
+    // eps from the trace, summed in row order (the diagonal entry of row i is
+    // lane i's a[i])
+    double tr = 0.0;
 #pragma unroll
-    for (int c = 0; c < RT; ++c)
-        if (act && c == lane) colv[lane] = a[c];
-    wave_sync();
-    if (lane == 0)
-    {
-        double tr = 0.0;
-        for (int i = 0; i < R; ++i) tr += colv[i];
-        trs = tr;
-    }
-    wave_sync();
-    const double tr = trs;
+    for (int i = 0; i < RT; ++i)
+        if (i < R) tr += lane_f64(a[i], i);
     const double eps = 1e-12 * ((tr > 0.0) ? tr / double(R) : 1.0) + 1e-300;
 #pragma unroll
     for (int c = 0; c < RT; ++c)
         if (c == lane) a[c] += eps;
     // (fully unrolled, so the row stays in registers: a partly unrolled
-    // loop indexes it at run time and moves it to scratch memory)
+    // loop indexes it at run time and moves it to scratch memory).  The
+    // pivot is lane j's a[j], read across lanes; column j of L goes through
+    // LDS, in the buffer the step after next reuses (a wave's LDS operations
+    // are in order, so the next step's writes to the other buffer need no
+    // barrier behind this step's reads).
 #pragma unroll
     for (int j = 0; j < RT; ++j)
     {
         if (j < R)   // steps j < R only (uniform; no early exit, so the loop unrolls)
         {
-            if (act) colv[lane] = a[j];
-            wave_sync();
-            const double sp = colv[j];
+            const double sp = lane_f64(a[j], j);
             const double d = (sp > 0.0) ? sqrt(sp) : sqrt(eps);
             const double v = a[j];
             const double lij = (lane == j) ? d : ((mine && lane > j) ? v / d : v);
-            if (act) lcol[lane] = lij;
+            double* lc = lcol[j & 1];
+            if (act) lc[lane] = lij;
             wave_sync();
             a[j] = lij;
 #pragma unroll
-            for (int c = j + 1; c < RT; ++c) a[c] -= lij * lcol[c];
-            wave_sync();   // this step's reads before the next step's writes
+            for (int c = j + 1; c < RT; ++c) a[c] -= lij * lc[c];
         }
     }
     // L padded to RT with the identity (chol_apply_kernel's layout)
     if (act)
 #pragma unroll
         for (int c = 0; c < RT; ++c)
-            L[lane][c] = (mine && c < R) ? ((c <= lane) ? a[c] : 0.0) : (c == lane ? 1.0 : 0.0);
+        {
+            const double v = (mine && c < R) ? ((c <= lane) ? a[c] : 0.0) : (c == lane ? 1.0 : 0.0);
+            L[lane][c] = v;
+            if (c == lane) dinv[lane] = 1.0 / v;
+        }
     __syncthreads();
     const size_t row = size_t(blockIdx.x) * CHOL_T + size_t(lane);
     if (row >= dim) return;
@@ -546,24 +594,7 @@ chol_solve_wave_kernel(const double* __restrict__ FtF,
     double y[RT];
 #pragma unroll
     for (int i = 0; i < RT; ++i) y[i] = (i < R) ? b[i] : 0.0;
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-    {
-        double sum = y[i];
-#pragma unroll
-        for (int k = 0; k < i; ++k) sum -= L[i][k] * y[k];
-        y[i] = sum / L[i][i];
-        asm volatile("" ::: "memory");
-    }
-#pragma unroll
-    for (int i = RT - 1; i >= 0; --i)
-    {
-        double sum = y[i];
-#pragma unroll
-        for (int k = i + 1; k < RT; ++k) sum -= L[k][i] * y[k];
-        y[i] = sum / L[i][i];
-        asm volatile("" ::: "memory");
-    }
+    chol_substitute<RT>(L, dinv, y);
     double* out = F + row * R;
 #pragma unroll
     for (int i = 0; i < RT; ++i)
