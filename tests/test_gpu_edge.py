@@ -69,6 +69,28 @@ def test_empty_tensor(ca, dev):
         assert np.all(np.isnan(h.factor(1))) and np.all(np.isnan(h.factor(2)))
 
 
+@pytest.mark.parametrize("big", [0, 1, 2])
+def test_dim_beyond_packed_coordinates(ca, dev, big):
+    """A mode of 32768 or more indices does not fit the views' 15-bit packed
+    coordinate.  The reference then skips building the views and computes a
+    zero sparse MTTKRP (partition.cu:1896-1906, sparse.cu:839-843); here
+    creating the driver fails with an error that names the limit, whichever
+    mode is too long (32767 still works)."""
+    dims = [20, 30, 40]
+    dims[big] = 32768
+    rng = np.random.default_rng(big)
+    idx = np.stack([rng.integers(0, d, 500) for d in dims]).astype(np.uint32)
+    idx[big, 0] = 32767
+    t = ca.Tensor(tuple(dims), idx, rng.random(500) + 0.5)
+    with pytest.raises(ca.CptcError, match="32768"):
+        ca.Als3(t, R=8)
+    dims[big] = 32767
+    idx[big, 0] = 32766
+    t = ca.Tensor(tuple(dims), idx, rng.random(500) + 0.5)
+    with ca.Als3(t, R=8) as h:
+        assert int(h.info.sparse_nnz) + int(h.info.dense_nnz) == 500
+
+
 def test_single_nonzero(ca, orc, dev):
     t = ca.Tensor((3, 4, 5), np.array([[1], [2], [3]], np.uint32), np.array([2.5]))
     check_against_oracle(ca, orc, t, R=4, thr=0.03, iters=10, fit_tol=1e-8)

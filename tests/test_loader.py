@@ -97,6 +97,25 @@ def test_probe_nmodes_missing_and_order3(tmp_path, ca):
     assert ca.probe_nmodes(_write(tmp_path, "\n# c\n1 2 3 4.0\n")) == 3
 
 
+def test_long_lines(tmp_path, ca):
+    """The N-order loader reads through a 4 MiB line buffer and aborts on a
+    longer line (generic.cu:1132-1138); the order-3 loader reads lines of any
+    length (std::getline, tensor.cu)."""
+    pad = " " * (5 << 20)
+    path = str(tmp_path / "long.tns")
+    with open(path, "w") as f:
+        f.write("1 2 3 4.0\n2" + pad + " 1 1 2.5\n")
+    with pytest.raises(ca.CptcError, match="line longer than read buffer"):
+        ca.load_tns_generic(path)
+    t = ca.load_tns3(path)
+    assert t.dims == (2, 2, 3) and list(t.val) == [4.0, 2.5]
+    short = str(tmp_path / "short.tns")
+    with open(short, "w") as f:
+        f.write("1 2 3 4.0\n2" + " " * (3 << 20) + " 1 1 2.5\n")
+    g = ca.load_tns_generic(short)
+    assert g.dims == (2, 2, 3) and list(g.val) == [4.0, 2.5]
+
+
 def test_generic_rejects_order1(tmp_path, ca):
     with pytest.raises(ca.CptcError):
         ca.load_tns_generic(_write(tmp_path, "1 2.0\n2 3.0\n"))
