@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <initializer_list>
@@ -67,6 +68,21 @@ inline unsigned grid_for(size_t n, unsigned block, unsigned cap = 1u << 20)
     if (g == 0) g = 1;
     if (g > cap) g = cap;
     return unsigned(g);
+}
+
+// Compute units of device `dev`, queried once per device (0..63; others are
+// queried every time) and kept in atomics, so concurrent first calls are
+// safe; 256 if the query fails.
+inline int cu_count(int dev)
+{
+    static std::atomic<int> cache[64];
+    if (dev >= 0 && dev < 64)
+        if (const int c = cache[dev].load(std::memory_order_relaxed); c > 0) return c;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 // Raises the dynamic-LDS limit of kernels once per device (the attribute

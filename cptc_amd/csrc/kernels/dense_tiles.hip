@@ -265,18 +265,9 @@ int rank_split(size_t items, int R, hipStream_t s)
         return e ? std::atoi(e) : 0;
     }();
     if (fixed > 0) return std::min(fixed, nrb);
-    static int simds[64] = {};
     int dev = 0;
-    if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (simds[dev] == 0)
-    {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            n <= 0)
-            n = 256;
-        simds[dev] = 4 * n;
-    }
-    const size_t want = size_t(simds[dev]);
+    if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0) dev = 0;
+    const size_t want = size_t(4) * size_t(cptc::cu_count(dev));   // SIMDs
     if (items >= want) return 1;
     return int(std::min<size_t>((want + items - 1) / items, size_t(nrb)));
 }

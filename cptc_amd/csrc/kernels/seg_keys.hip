@@ -534,17 +534,9 @@ extern "C" int cptc_mttkrp_seg_nd_keys_dims(int nmodes, int mode, const void* d_
         // the key field bounds every leaf coordinate by its width, the dims by rows
         if (rows >= 1 && rows <= lv.mask[nlev - 1] + 1 && bytes <= LEAF_LDS_MAX)
         {
-            // CU count per device, queried once (every caller stores the same value)
-            static int cu_count[64] = {};
             int dev = 0;
             CPTC_HIP(hipGetDevice(&dev));
-            int cus = (dev >= 0 && dev < 64) ? cu_count[dev] : 0;
-            if (cus <= 0)
-            {
-                CPTC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-                if (cus <= 0) cus = 256;
-                if (dev >= 0 && dev < 64) cu_count[dev] = cus;
-            }
+            const int cus = cptc::cu_count(dev);
             const uint64_t grid = uint64_t(LEAF_LDS_WG_PER_CU) * uint64_t(cus);
             if (nseg >= LEAF_LDS_MIN_SEGS * grid)
             {
