@@ -10,6 +10,7 @@
 
 #include <cstdint>
 
+#include "../host/blk3_params.hpp"
 #include "../host/hip_util.hpp"
 
 namespace {
@@ -18,11 +19,14 @@ constexpr int WAVE = 64;
 constexpr int PROBE_WAVES = 8;   // as mttkrp3_blk_kernel
 constexpr int PROBE_U = 4;       // rows in flight per wave, as mttkrp3_blk_kernel
 #define CPTC_PROBE_WPE 6         // resident waves per SIMD, as mttkrp3_blk_kernel
-// the LDS of mttkrp3_blk_kernel<., 5, 4, 8, 4> (32 x 128 FP64 accumulator, 16
-// staged rows, the waves' value buffers), reserved and unused, so that as
-// many workgroups are resident per CU as for the kernel (more would widen the
-// set of rows in flight and change the L2 hits the probe is there to see)
-constexpr size_t PROBE_LDS = (32 * 128 + 16 * 128 + PROBE_WAVES * WAVE) * sizeof(double);
+// the LDS of mttkrp3_blk_kernel (TB x 128 FP64 accumulator, KB staged rows,
+// the waves' value buffers; TB, KB from blk3_params.hpp), reserved and
+// unused, so that as many workgroups are resident per CU as for the kernel
+// (more would widen the set of rows in flight and change the L2 hits the
+// probe is there to see)
+constexpr size_t PROBE_LDS =
+    ((size_t(1) << CPTC_BLK3_LG_TB) * 128 + (size_t(1) << CPTC_BLK3_LG_KB) * 128 +
+     PROBE_WAVES * WAVE) * sizeof(double);
 
 template <int MODE>
 __global__ __launch_bounds__(WAVE* PROBE_WAVES) __attribute__((amdgpu_waves_per_eu(CPTC_PROBE_WPE, CPTC_PROBE_WPE))) void gather_probe_kernel(
