@@ -650,7 +650,8 @@ def host_info() -> dict:
 
 
 def summarize_cpu(ms, extra: dict) -> dict:
-    """BASELINE.md's plan: drop iteration 1, median and mean of the rest."""
+    """The CPU timing rule: drop iteration 1 (first-touch and warm-up), report the
+    median and mean of the rest."""
     kept = ms[1:] if len(ms) > 1 else ms
     out = {
         "value": round(float(np.median(kept)), 1),
