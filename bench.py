@@ -253,14 +253,17 @@ def main() -> int:
     b_iter = sum(gather_bytes(nnz, dims[m], R) for m in range(3))
     mtt_ms_iter = float(np.sum(mt_ms)) / kit
     mtt_gbs = b_iter / (mtt_ms_iter * 1e-3) / 1e9
-    # dominant kernel: the FP64 residual-view sparse MTTKRP, per launch (one mode)
-    snnz = int(info.sparse_nnz)
+    # dominant kernel: the FP64 residual-view sparse MTTKRP, per launch (one
+    # mode); on the FP64-only path with a merged view it reads every nonzero
+    merged_fp64 = bool(info.fp64_merged)
+    snnz = int(info.nnz) if merged_fp64 else int(info.sparse_nnz)
     b_launch = [gather_bytes(snnz, dims[m], R) for m in range(3)]
     launch_ms = [float(sp_ms[m]) / kit for m in range(3)]
     mean_ms = sum(launch_ms) / 3
     gather_gbs = sum(b_launch) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
     blocked = bool(info.sparse_blocked) and not args.fused
-    workload = f"cfg{args.config}-R{R}" + ("-fused" if args.fused else "-blocked" if blocked else "")
+    workload = f"cfg{args.config}-R{R}" + ("-fused" if args.fused else "-blocked" if blocked else
+                                          "-merged" if merged_fp64 else "")
     # compulsory traffic per launch: the view stream + every factor row once + output rows
     compulsory = [snnz * 20 + sum(dims) * R * 8 + dims[m] * R * 8 for m in range(3)]
     comp_gbs = sum(compulsory) / (sum(launch_ms) * 1e-3) / 1e9 if snnz else 0.0
@@ -288,6 +291,8 @@ def main() -> int:
                        if blocked else
                        "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128])"
                        if 64 < R <= 128 else
+                       "mttkrp3_seg_kernel (FP64 view of every nonzero: residual + dense pool)"
+                       if merged_fp64 else
                        "mttkrp3_seg_kernel (FP64 residual view)") + ", per launch = one mode",
             "bound": "hbm",
             "achieved": round(gather_gbs, 1),
@@ -366,7 +371,8 @@ def main() -> int:
             "workload": spec["name"] if R == spec["R"] else f"{spec['name']} (R={R})",
             "R": R, "nnz": nnz, "dims": list(dims), "dense_threshold": thr,
             "dense_tiles": int(info.num_dense_tiles), "dense_nnz": int(info.dense_nnz),
-            "sparse_nnz": snnz, "path": "mfma+fp64" if use_mfma else "fp64",
+            "sparse_nnz": int(info.sparse_nnz), "fp64_kernel_nnz": snnz,
+            "fp64_merged_view": merged_fp64, "path": "mfma+fp64" if use_mfma else "fp64",
             "fused": bool(info.fused), "sparse_blocked": bool(info.sparse_blocked),
             "tile_kernel": "bf16x3" if info.tile_bf16x3 else "fp32",
             "tiles_beside": bool(info.tiles_beside),

@@ -329,9 +329,11 @@ class Als3:
         return out
 
     def view(self, which: int, mode: int) -> dict:
-        """Row-sorted view `which` (0 residual, 1 FP64 dense view) of `mode`."""
-        nnz = int(self.info.sparse_nnz) if which == 0 else int(self.info.dense_nnz)
-        nseg = int(self.info.segments[mode] if which == 0 else self.info.dense_view_segments[mode])
+        """Row-sorted view `which` of `mode`: 0 residual, 1 FP64 dense view, 2
+        the FP64-only path's merged view over every nonzero (info.fp64_merged)."""
+        i = self.info
+        nnz = (int(i.sparse_nnz), int(i.dense_nnz), int(i.nnz))[which]
+        nseg = int((i.segments, i.dense_view_segments, i.merged_segments)[which][mode])
         if nseg == 0:
             nnz = 0
         d = {

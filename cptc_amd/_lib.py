@@ -73,6 +73,8 @@ class Als3Info(C.Structure):
         ("tile_segments", C.c_uint64 * 3),
         ("graph_mode", C.c_int),
         ("graph_captures", C.c_int),
+        ("fp64_merged", C.c_int),
+        ("merged_segments", C.c_uint64 * 3),
     ]
 
 

@@ -61,6 +61,10 @@ struct Als3
     int32_t* d_perm[3] = {nullptr, nullptr, nullptr};
     DevPartition3 part;
     DevViews3 views, dviews;
+    // FP64-only path: one row-sorted view over residual and dense-pool
+    // nonzeros together (want_fp64_merge); the kernels then read it
+    // instead of views + dviews, which stay for the layout getters
+    DevViews3 aviews;
     DevBlk3 blk;   // blocked residual views (R in (64, 128]), for the FP64 kernel
     float* d_tile_f32 = nullptr;
     // split-bf16 tile kernel (choose_tiles) and its per-launch operand images
@@ -185,12 +189,15 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     {
         const double* F1 = mode == 0 ? B : A;
         const double* F2 = mode == 2 ? B : C;
-        for (const DevViews3* v : {&h.views, &h.dviews})
+        // the merged FP64 view, when built, stands for both
+        const DevViews3* first = h.aviews.ready ? &h.aviews : &h.views;
+        const DevViews3* second = h.aviews.ready ? nullptr : &h.dviews;
+        for (const DevViews3* v : {first, second})
         {
-            if (!v->ready) continue;
-            const bool timed = h.timing_kernels && v == &h.views;
+            if (!v || !v->ready) continue;
+            const bool timed = h.timing_kernels && v == first;
             if (timed) CPTC_HIP(hipEventRecord(h.kev_cur[2 * mode], h.s));
-            if (v == &h.views && h.blk.ready)
+            if (v == first && h.blk.ready)
             {
                 const DevBlk3& b = h.blk;
                 CPTC_TRY(cptc_mttkrp_sparse3_blk(
@@ -210,6 +217,20 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
     if (h.overlap && with_pinv) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_pinv, 0));
     if (dense_side) CPTC_HIP(hipStreamWaitEvent(h.s, h.e_dense, 0));
     return CPTC_OK;
+}
+
+// The FP64-only path (tiles below fill_min) has two FP64 views of one
+// tensor: the residual and the dense pool re-sorted by row (the reference's
+// two launches per mode, partition.cu:2387-2517).  Here both are one view
+// over all nonzeros, sorted by target row: one launch per mode, and each
+// output row's nonzeros from the two sets accumulate in one segment instead
+// of two flushes.  The same products summed in another order (FP64
+// reassociation, ~1e-16 relative per row).  ALS_FP64_MERGE=0 keeps two.
+bool want_fp64_merge(const Als3& h)
+{
+    const char* e = std::getenv("ALS_FP64_MERGE");
+    if (e && std::strcmp(e, "0") == 0) return false;
+    return !h.use_mfma && h.part.ntiles > 0 && h.part.sparse_nnz > 0;
 }
 
 // Side streams only pay when both sides of the fork run long: each fork /
@@ -267,13 +288,15 @@ void choose_tiles(Als3& h)
 // ALS_SPARSE_BLOCKED=1 / 0 forces it on / off.
 int build_blk(Als3& h)
 {
-    if (!h.views.ready || h.views.nnz == 0 || h.R <= 64 || h.R > 128 || h.R % 2 != 0)
+    // over the view the FP64 kernel reads first (mttkrp_launch)
+    const DevViews3& v = h.aviews.ready ? h.aviews : h.views;
+    if (!v.ready || v.nnz == 0 || h.R <= 64 || h.R > 128 || h.R % 2 != 0)
         return CPTC_OK;
     const char* e = std::getenv("ALS_SPARSE_BLOCKED");
     const bool beside_tiles = h.use_mfma && h.part.ntiles > 0 && h.dense_beside && !h.skip_dense;
     const bool want = e ? std::strcmp(e, "0") != 0 : !beside_tiles;
     if (!want) return CPTC_OK;
-    return blk_views3_device(h.views, h.dims, CPTC_BLK3_LG_TB, CPTC_BLK3_LG_KB, CPTC_BLK3_CHUNK,
+    return blk_views3_device(v, h.dims, CPTC_BLK3_LG_TB, CPTC_BLK3_LG_KB, CPTC_BLK3_CHUNK,
                              CPTC_BLK3_STAGE_MIN, h.blk, h.s);
 }
 
@@ -312,8 +335,9 @@ int residual_launch(Als3& h, bool with_lambda)
     double* out = h.d_scal + 2;
     CPTC_HIP(hipMemsetAsync(out, 0, 2 * sizeof(double), h.s));
     const double* lam = with_lambda ? h.d_lambda : nullptr;
-    for (const DevViews3* v : {&h.views, &h.dviews})
-        if (v->ready)
+    const bool all = h.aviews.ready;
+    for (const DevViews3* v : {all ? &h.aviews : &h.views, all ? nullptr : &h.dviews})
+        if (v && v->ready)
             CPTC_TRY(cptc_residual3_view(v->d_coords[0], v->d_vals[0], v->nnz, h.F[0], h.F[1],
                                          h.F[2], lam, h.R, out, h.s));
     if (h.use_mfma && h.part.ntiles > 0)
@@ -331,6 +355,7 @@ void destroy(Als3* h)
     free_partition(h->part);
     free_views(h->views);
     free_views(h->dviews);
+    free_views(h->aviews);
     free_blk(h->blk);
     for (auto& p : h->d_perm)
         if (p) (void)hipFree(p);
@@ -426,16 +451,15 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
 
     // 1. COO -> device, CADR (main.cu:176-192)
     DevCoo3 c;
+    // released once the FP64 views are built, or on any early return
+    struct CooGuard
+    {
+        DevCoo3& c;
+        ~CooGuard() { free_coo(c); }
+    } c_guard{c};
     CPTC_TRY(upload_coo3(coo->idx, coo->val, coo->nnz, coo->dims, c, h->s));
     if (o.cadr)
-    {
-        const int rc = cadr3_device(c, h->perm, h->d_perm, 1, h->s);
-        if (rc != CPTC_OK)
-        {
-            free_coo(c);
-            return rc;
-        }
-    }
+        CPTC_TRY(cadr3_device(c, h->perm, h->d_perm, 1, h->s));
     else
     {
         for (int m = 0; m < 3; ++m)
@@ -464,11 +488,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     }
 
     // 3. hybrid partition, then the COO is released (main.cu:268-301)
-    {
-        const int rc = partition3_device(c, o.threshold, h->num_cus, h->part, h->s);
-        free_coo(c);
-        CPTC_TRY(rc);
-    }
+    CPTC_TRY(partition3_device(c, o.threshold, h->num_cus, h->part, h->s));
     h->tiles_total = h->part.ntiles;
     h->dense_nnz_total = h->part.dense_nnz;
 
@@ -505,6 +525,13 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     int path = o.path;
     if (path < 0) path = env_flag("ALS_FORCE_WMMA") ? 1 : env_flag("ALS_FORCE_CUDA") ? 2 : 0;
     h->use_mfma = (path == 1) ? true : (path == 2) ? false : (h->avg_fill >= h->fill_min);
+    // the FP64-only path reads every nonzero from one view (want_fp64_merge)
+    if (want_fp64_merge(*h))
+        CPTC_TRY(views3_device(reinterpret_cast<const uint32_t*>(c.d_m[0]),
+                               reinterpret_cast<const uint32_t*>(c.d_m[1]),
+                               reinterpret_cast<const uint32_t*>(c.d_m[2]), c.d_val, c.nnz,
+                               h->dims, h->aviews, h->s));
+    free_coo(c);
     h->skip_dense = o.skip_dense < 0 ? env_flag("ALS_NO_DENSE") != 0 : o.skip_dense != 0;
     h->skip_sparse = o.skip_sparse < 0 ? env_flag("ALS_NO_SPARSE") != 0 : o.skip_sparse != 0;
     if (h->part.ntiles > 0)
@@ -1020,6 +1047,8 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     for (int m = 0; m < 3; ++m) info->tile_segments[m] = h->timg[m].ready() ? h->timg[m].nseg : 0;
     info->graph_mode = h->graph_mode;
     info->graph_captures = h->n_captures;
+    info->fp64_merged = h->aviews.ready ? 1 : 0;
+    for (int m = 0; m < 3; ++m) info->merged_segments[m] = h->aviews.ready ? h->aviews.nseg[m] : 0;
     info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }
@@ -1215,9 +1244,9 @@ extern "C" int cptc_als3_view(void* handle, int which, int mode, uint64_t* coord
                               uint32_t* blk_row, uint32_t* blk_start, uint32_t* blk_cnt)
 {
     Als3* h = cptc::as_h(handle);
-    CPTC_REQUIRE(h && mode >= 0 && mode < 3 && (which == 0 || which == 1), CPTC_ERR_ARG,
+    CPTC_REQUIRE(h && mode >= 0 && mode < 3 && which >= 0 && which <= 2, CPTC_ERR_ARG,
                  "cptc_als3_view: bad arguments");
-    const cptc::DevViews3& v = which == 0 ? h->views : h->dviews;
+    const cptc::DevViews3& v = which == 0 ? h->views : which == 1 ? h->dviews : h->aviews;
     if (!v.ready) return CPTC_OK;
     auto cp = [&](void* dst, const void* src, size_t bytes) -> int {
         if (dst && src && bytes)

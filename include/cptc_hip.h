@@ -480,6 +480,10 @@ typedef struct cptc_als3_info {
     int graph_mode;           /* 1 = quiet runs replay one captured iteration (HIP graph) */
     int graph_captures;       /* iterations captured so far (a capture is redone after the
                                  library's scratch buffers were reallocated) */
+    int fp64_merged;          /* 1 = FP64-only path with residual and dense-pool nonzeros in
+                                 one row-sorted view: one FP64 launch per mode, and the
+                                 per-mode sparse kernel time covers every nonzero */
+    uint64_t merged_segments[3];  /* segments of that view per mode (0: none) */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 
@@ -540,7 +544,7 @@ int cptc_als3_residual(void* handle, double* res_sq, double* x_sq);
 
 /* Copies of the layout for bit-exactness tests.  Sizes via *_info first. */
 int cptc_als3_perm(void* handle, int mode, int32_t* host_out);
-int cptc_als3_view(void* handle, int which /*0 residual, 1 dense-fp64*/, int mode,
+int cptc_als3_view(void* handle, int which /*0 residual, 1 dense-fp64, 2 merged fp64*/, int mode,
                    uint64_t* coords, double* vals, uint32_t* blk_row, uint32_t* blk_start,
                    uint32_t* blk_cnt);
 int cptc_als3_tiles(void* handle, int32_t* tiles4, uint64_t* pool_off, int32_t* pool_lid,

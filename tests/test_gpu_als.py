@@ -66,6 +66,43 @@ def test_layout_bit_exact(ca, orc, dev, kind, thr):
                     assert np.array_equal(got[k], np.asarray(dv[m][k])), ("dense", m, k)
 
 
+@pytest.mark.parametrize("kind,thr", [("blocks", 0.03), ("blocks", 0.001), ("zipf", 0.03)])
+def test_fp64_merged_view(ca, orc, dev, kind, thr, monkeypatch):
+    """FP64-only path with dense tiles and a residual: the kernels read one
+    row-sorted view of every nonzero (bit-exact with the oracle's views3 of
+    the whole relabelled tensor), its MTTKRP of every mode is within 1e-10 of
+    the reference's two views (residual + dense pool, partition.cu:2387-2517),
+    and 20 iterations' fits are within 1e-6 of ALS_FP64_MERGE=0, which keeps
+    the two launches.  Without tiles or without a residual there is nothing
+    to merge."""
+    t = make(ca, kind)
+    perms, p, v = oracle_layout(orc, t, thr)
+    both = len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
+    R = 16
+    monkeypatch.delenv("ALS_FP64_MERGE", raising=False)
+    with ca.Als3(t, R=R, threshold=thr, path=2) as h:
+        assert int(h.info.fp64_merged) == int(both)
+        if both:
+            idx = np.stack([perms[m][t.idx[m]] for m in range(3)]).astype(np.int32)
+            av = orc.views3(idx[0], idx[1], idx[2], t.val, t.dims)
+            for m in range(3):
+                got = h.view(2, m)
+                for k in ("coords", "vals", "blk_row", "blk_start", "blk_cnt"):
+                    assert np.array_equal(got[k], np.asarray(av[m][k])), (m, k)
+            F = [h.factor(m).ravel() for m in range(3)]
+            dv = orc.dense_views3(p, t.dims)
+            for mode in range(3):
+                ref = (orc.mttkrp3_view(v, mode, *F, R, t.dims[mode]) +
+                       orc.mttkrp3_view(dv, mode, *F, R, t.dims[mode]))
+                assert rel_err(h.mttkrp(mode), ref.reshape(t.dims[mode], R)) <= 1e-10, mode
+        fit, _, _ = h.run(20)
+    monkeypatch.setenv("ALS_FP64_MERGE", "0")
+    with ca.Als3(t, R=R, threshold=thr, path=2) as h2:
+        assert int(h2.info.fp64_merged) == 0
+        fit2, _, _ = h2.run(20)
+    assert np.max(np.abs(fit - fit2)) <= 1e-6, (fit[-3:], fit2[-3:])
+
+
 def test_cadr_entry_point_matches_oracle(ca, orc, dev):
     t = ca.synth_zipf((300, 256, 999), (1.1, 0.0, 1.3), 50000, 0, 2)
     perms, idx = ca.cadr3(t)
