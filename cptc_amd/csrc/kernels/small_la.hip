@@ -664,74 +664,146 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
 }
 
 // ---------------------------------------------------------------------------
-// F = FtV * Ainv (row-major dim x R times R x R), then F[:, r] /= div[r].
-// 64 x 64 output tile per workgroup, 4 x 4 per thread, K in chunks of 16.
+// F = FtV * Ainv (row-major dim x R times R x R), then F[:, r] /= div[r],
+// for R > 64, on the FP64 matrix cores (v_mfma_f64_16x16x4f64).
+//
+// A workgroup of 4 waves takes 16 rows x 128 columns (grid.y walks 128-wide
+// column blocks when R > 128); wave w takes columns 32w .. 32w + 31 of the
+// block as two 16 x 16 tiles.  K advances 4 per step.  Operand layout of the
+// instruction: lane l holds A[l % 16][l / 16] = Y[row0 + l % 16][k + l / 16]
+// and B[l / 16][l % 16] = Ainv[k + l / 16][col + l % 16]; the accumulator's
+// element v of lane l is D[l / 16 + 4 v][l % 16] (measured: the FP32
+// instructions' 4 (l / 16) + v order does not hold for this one).
+//
+// On this GPU the FP64 matrix rate equals the FP64 vector rate; the matrix
+// form pays because each operand in a register feeds 16 products.  The
+// workgroup's 16 rows of Y are staged in LDS, 128 columns of K at a time
+// (an A operand read from global memory touches 16 rows, i.e. 16 cache
+// lines, per instruction, and the four waves would each read it), zero
+// from R to the pass's 128 columns; batches never run past them.  Steps run in batches of 8 (16 B-operand
+// loads, 8 LDS reads, 16 MFMAs), two register sets in turn: a batch's loads
+// are issued before the previous batch's MFMAs.  The B loads are
+// unconditional (a column past R reads column R - 1 and is not stored; a K
+// step past R reads row R - 1 and meets a zero A), so no branch sits
+// between a load and its use.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void apply_kernel(const double* __restrict__ Y,
-                                                    const double* __restrict__ Ainv,
-                                                    double* __restrict__ F, size_t dim, int R,
-                                                    const double* __restrict__ div)
+typedef double apply_d4 __attribute__((ext_vector_type(4)));
+constexpr int APPLY_B = 8;            // K steps (of 4) per batch
+constexpr int APPLY_KC = 128;         // K columns of Y staged per pass
+constexpr int APPLY_LD = APPLY_KC + 1;   // LDS row stride (odd: rows on distinct banks)
+
+__global__ __launch_bounds__(256) void apply_mfma_kernel(const double* __restrict__ Y,
+                                                         const double* __restrict__ Ainv,
+                                                         double* __restrict__ F, size_t dim, int R,
+                                                         const double* __restrict__ div)
 {
-    constexpr int TM = 64, TN = 64, TK = 16;
-    __shared__ double sy[TK][TM + 1];
-    __shared__ double sa[TK][TN + 1];
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const size_t i0 = size_t(blockIdx.x) * TM;
-    const int c0 = int(blockIdx.y) * TN;
-    double acc[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
-    for (int k0 = 0; k0 < R; k0 += TK)
+    __shared__ double sA[16 * APPLY_LD];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    const size_t row0 = size_t(blockIdx.x) * 16;
+    const int cb = int(blockIdx.y) * 128 + wave * 32;
+    const bool active = cb < R;   // wave-uniform: waves past R stage and wait only
+    const int c0 = cb + li, c1 = cb + 16 + li;
+    const bool c0_ok = c0 < R, c1_ok = c1 < R;
+    const int c0c = c0_ok ? c0 : R - 1, c1c = c1_ok ? c1 : R - 1;
+    apply_d4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+
+    struct Batch
     {
-        for (int x = threadIdx.x; x < TM * TK; x += 256)
+        double b0[APPLY_B], b1[APPLY_B];
+    };
+    // B operands of batch bt of the pass at K offset kc (K rows clamped to R)
+    auto load = [&](int kc, int bt, Batch& x) {
+#pragma unroll
+        for (int u = 0; u < APPLY_B; ++u)
         {
-            const int rr = x / TK, kk = x % TK;
-            const size_t i = i0 + rr;
-            sy[kk][rr] = (i < dim && k0 + kk < R) ? Y[i * R + k0 + kk] : 0.0;
+            const int k = kc + 4 * (APPLY_B * bt + u) + lk;
+            const double* __restrict__ ak = Ainv + size_t(k < R ? k : R - 1) * size_t(R);
+            x.b0[u] = ak[c0c];
+            x.b1[u] = ak[c1c];
         }
-        for (int x = threadIdx.x; x < TK * TN; x += 256)
+    };
+    auto compute = [&](int bt, const Batch& x) {
+        const double* __restrict__ arow = sA + li * APPLY_LD + 4 * APPLY_B * bt + lk;
+#pragma unroll
+        for (int u = 0; u < APPLY_B; ++u)
         {
-            const int kk = x / TN, cc = x % TN;
-            sa[kk][cc] = (k0 + kk < R && c0 + cc < R) ? Ainv[size_t(k0 + kk) * R + c0 + cc] : 0.0;
+            const double a = arow[4 * u];
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, x.b0[u], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, x.b1[u], acc1, 0, 0, 0);
+        }
+    };
+
+    for (int kc = 0; kc < R; kc += APPLY_KC)
+    {
+        const int kn = R - kc < APPLY_KC ? R - kc : APPLY_KC;
+        if (kc > 0) __syncthreads();   // the previous pass's LDS reads are done
+        // the first batch's B operands load while Y is staged (inactive
+        // waves load them too, from clamped addresses, and never use them)
+        Batch P, Q;
+        load(kc, 0, P);
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            // 16 x 128 entries, 8 per thread: row 2j + tid / 128, column
+            // tid % 128; loads from clamped addresses, all issued before
+            // the first store
+            constexpr int PER = 16 * APPLY_KC / 256;
+            const int c = tid & (APPLY_KC - 1);
+            const int cc = kc + (c < kn ? c : kn - 1);
+            double v[PER];
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+            {
+                const size_t i = row0 + size_t(2 * j + (tid >> 7));
+                v[j] = Y[(i < dim ? i : dim - 1) * size_t(R) + cc];
+            }
+#pragma unroll
+            for (int j = 0; j < PER; ++j)
+            {
+                const int r = 2 * j + (tid >> 7);
+                const bool ok = c < kn && row0 + size_t(r) < dim;
+                sA[r * APPLY_LD + c] = ok ? v[j] : 0.0;
+            }
         }
         __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < TK; ++kk)
+        if (!active) continue;
+        // batches of this pass, taken in pairs; an odd count (kn <= 96) runs
+        // one more batch, over the staged zeros between kn and 128
+        const int nb = (kn + 4 * APPLY_B - 1) / (4 * APPLY_B);
+        // the scheduling barriers keep each batch's loads ahead of the other
+        // batch's MFMAs (left alone, the scheduler sinks every load to its use)
+        for (int bt = 0; bt < nb; bt += 2)
         {
-            double y[4], a[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] = sy[kk][ty + 16 * q];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) a[q] = sa[kk][tx + 16 * q];
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[p][q] += y[p] * a[q];
+            load(kc, bt + 1, Q);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(bt, P);
+            __builtin_amdgcn_sched_barrier(0);
+            load(kc, bt + 2 < nb ? bt + 2 : bt, P);   // the last pass's reload is not used
+            __builtin_amdgcn_sched_barrier(0);
+            compute(bt + 1, Q);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
     }
+    if (!active) return;
+
+    const double d0 = (div && c0_ok) ? div[c0] : 1.0;
+    const double d1 = (div && c1_ok) ? div[c1] : 1.0;
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int v = 0; v < 4; ++v)
     {
-        const size_t i = i0 + ty + 16 * p;
+        const size_t i = row0 + size_t(lk + 4 * v);
         if (i >= dim) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-        {
-            const int c = c0 + tx + 16 * q;
-            if (c >= R) continue;
-            const double v = acc[p][q];
-            F[i * R + c] = div ? v / div[c] : v;
-        }
+        double* __restrict__ out = F + i * size_t(R);
+        if (c0_ok) out[c0] = div ? acc0[v] / d0 : acc0[v];
+        if (c1_ok) out[c1] = div ? acc1[v] / d1 : acc1[v];
     }
 }
 
 // F = FtV * Ainv for R <= 64: Ainv staged in LDS, one thread per output
 // entry (row x / R, column x % R); the R threads of a row read the same FtV
-// row.  Each entry is the same k-ascending FMA chain as apply_kernel's, so
-// the two give identical results.
+// row; each entry is one k-ascending FMA chain.
 constexpr int APPLY_SMALL_R = 64;
 __global__ __launch_bounds__(256) void apply_small_kernel(const double* __restrict__ Y,
                                                           const double* __restrict__ Ainv,
@@ -1213,8 +1285,9 @@ int apply_launch(const double* d_FtV, const double* d_Ainv, double* d_F, size_t 
     }
     else
     {
-        dim3 grid(unsigned((dim + 63) / 64), unsigned((R + 63) / 64));
-        hipLaunchKernelGGL(apply_kernel, grid, dim3(256), 0, s, d_FtV, d_Ainv, d_F, dim, R,
+        CPTC_REQUIRE((dim + 15) / 16 < (size_t(1) << 31), CPTC_ERR_ARG, "apply: %zu rows", dim);
+        const dim3 grid{unsigned((dim + 15) / 16), unsigned((R + 127) / 128)};
+        hipLaunchKernelGGL(apply_mfma_kernel, grid, dim3(256), 0, s, d_FtV, d_Ainv, d_F, dim, R,
                            d_div);
     }
     CPTC_LAUNCHED();
