@@ -20,10 +20,7 @@ constexpr int WAVE = 64;
 // partial[p] (one RT x RT output tile per grid.y); stage 2 sums partials in
 // p order.  16 x 16 threads, TPT x TPT outputs per thread (RT = 16 * TPT).
 // ---------------------------------------------------------------------------
-// TRI: grid.y runs over the upper-triangle tile pairs (bi <= bj) only; the
-// partial's other tiles are left unwritten and sum_partials_sym_kernel reads
-// their mirror images (the same products, so the same bits).
-template <int TPT, bool TRI = false>
+template <int TPT>
 __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restrict__ F,
                                                            size_t rows, int R, size_t rpw,
                                                            int ntile, double* __restrict__ part)
@@ -33,18 +30,7 @@ __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restr
     __shared__ double sa[CH][RT + 1];
     __shared__ double sb[CH][RT + 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    int bi = int(blockIdx.y) / ntile, bj = int(blockIdx.y) % ntile;
-    if constexpr (TRI)
-    {
-        int rem = int(blockIdx.y);
-        bi = 0;
-        while (rem >= ntile - bi)
-        {
-            rem -= ntile - bi;
-            ++bi;
-        }
-        bj = bi + rem;
-    }
+    const int bi = int(blockIdx.y) / ntile, bj = int(blockIdx.y) % ntile;
     const int ci = bi * RT, cj = bj * RT;
     const size_t r_lo = size_t(blockIdx.x) * rpw;
     const size_t r_hi = (r_lo + rpw < rows) ? r_lo + rpw : rows;
@@ -90,6 +76,117 @@ __global__ __launch_bounds__(256) void gram_partial_kernel(const double* __restr
         }
 }
 
+// Gram partials for R > 64 on the FP64 matrix cores (v_mfma_f64_16x16x4f64):
+// grid.x = row range p (rows [p rpw, (p + 1) rpw)), grid.y = one upper-
+// triangle pair (bi <= bj) of 64-rank tiles.  Wave w takes tile rows
+// 16w .. 16w + 15 against the tile's four 16-column blocks t (all four, so
+// the MFMA sequence has no branch) and stores t >= w in diagonal tiles: the
+// partials hold every entry r <= c, which is what sum_partials_sym_kernel
+// reads.  K runs over the range's rows, 4 per
+// step: lane l holds A[l % 16][l / 16] = F[i + l / 16][ci + 16w + l % 16]
+// and B_t[l / 16][l % 16] = F[i + l / 16][cj + 16t + l % 16]; the
+// accumulator's element v of lane l is D[l / 16 + 4 v][l % 16].  Steps run
+// in batches of 8 (40 loads, up to 32 MFMAs), two register sets in turn,
+// with scheduling barriers so a batch's loads issue before the previous
+// batch's MFMAs.  Loads are unconditional: rows past the range read its
+// last row and their A is zeroed when the batch is used; columns past R
+// read column R - 1 and are not stored.
+typedef double gram_d4 __attribute__((ext_vector_type(4)));
+constexpr int GRAM_B = 8;   // K steps (of 4 rows) per batch
+#ifndef CPTC_GRAM_MFMA_ROWS
+#define CPTC_GRAM_MFMA_ROWS 64   // at least this many rows per partial
+#endif
+
+__global__ __launch_bounds__(256) void gram_mfma_partial_kernel(const double* __restrict__ F,
+                                                                size_t rows, int R, size_t rpw,
+                                                                int ntile,
+                                                                double* __restrict__ part)
+{
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    int rem = int(blockIdx.y), bi = 0;
+    while (rem >= ntile - bi)
+    {
+        rem -= ntile - bi;
+        ++bi;
+    }
+    const int bj = bi + rem;
+    const int ca = bi * 64 + 16 * w;          // this wave's 16 G rows
+    if (ca >= R) return;                      // wave-uniform; no barrier in the kernel
+    const int t0 = (bi == bj) ? w : 0;        // first column block at or above the diagonal
+    const size_t r_lo = size_t(blockIdx.x) * rpw;
+    const size_t r_hi = (r_lo + rpw < rows) ? r_lo + rpw : rows;
+    if (r_lo >= r_hi) return;
+    const int colA = (ca + li < R) ? ca + li : R - 1;
+    int colB[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+    {
+        const int c = bj * 64 + 16 * t + li;
+        colB[t] = c < R ? c : R - 1;
+    }
+    gram_d4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = gram_d4{0.0, 0.0, 0.0, 0.0};
+
+    struct Batch
+    {
+        double a[GRAM_B], b[4][GRAM_B];
+    };
+    const size_t last = r_hi - 1;
+    auto load = [&](size_t i0, Batch& x) {
+#pragma unroll
+        for (int u = 0; u < GRAM_B; ++u)
+        {
+            const size_t i = i0 + size_t(4 * u + lk);
+            const double* __restrict__ row = F + (i < r_hi ? i : last) * size_t(R);
+            x.a[u] = row[colA];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) x.b[t][u] = row[colB[t]];
+        }
+    };
+    auto compute = [&](size_t i0, const Batch& x) {
+#pragma unroll
+        for (int u = 0; u < GRAM_B; ++u)
+        {
+            const size_t i = i0 + size_t(4 * u + lk);
+            const double a = (i < r_hi) ? x.a[u] : 0.0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, x.b[t][u], acc[t], 0, 0, 0);
+        }
+    };
+    constexpr size_t STEP = 4 * GRAM_B;   // rows per batch
+    Batch P, Q;
+    load(r_lo, P);
+    for (size_t i0 = r_lo; i0 < r_hi; i0 += 2 * STEP)
+    {
+        load(i0 + STEP, Q);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(i0, P);
+        __builtin_amdgcn_sched_barrier(0);
+        load(i0 + 2 * STEP, P);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(i0 + STEP, Q);   // all-zero A past the range
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    double* __restrict__ out = part + size_t(blockIdx.x) * size_t(R) * R;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+    {
+        if (t < t0) continue;
+        const int c = bj * 64 + 16 * t + li;
+        if (c >= R) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+        {
+            const int r = ca + lk + 4 * v;
+            if (r < R) out[size_t(r) * R + c] = acc[t][v];
+        }
+    }
+}
+
 // sum over p of part[p * n + x], in a fixed order: eight interleaved
 // accumulators (partials p = k mod 8), combined pairwise, so the loads of
 // eight partials are in flight at once and the result is the same on every
@@ -114,12 +211,12 @@ __global__ void sum_partials_kernel(const double* __restrict__ part, int P, size
         out[x] = ordered_sum(part, P, n, x);
 }
 
-// sum_partials_kernel over upper-triangle partials (gram_partial_kernel<., true>
-// with tiles of `tile` ranks): the upper tiles' entries are summed (partials
+// sum_partials_kernel over upper-triangle partials (gram_mfma_partial_kernel:
+// the partials hold the entries r <= c): those entries are summed (partials
 // read in order, coalesced) and written to their own place and, above the
-// diagonal tiles, to their mirror's (the one scattered access, once per
-// entry rather than once per partial).
-__global__ void sum_partials_sym_kernel(const double* __restrict__ part, int P, int R, int tile,
+// diagonal, to their mirror's (the one scattered access, once per entry
+// rather than once per partial), so the result is symmetric by construction.
+__global__ void sum_partials_sym_kernel(const double* __restrict__ part, int P, int R,
                                         double* __restrict__ out)
 {
     const size_t n = size_t(R) * R;
@@ -127,10 +224,10 @@ __global__ void sum_partials_sym_kernel(const double* __restrict__ part, int P, 
          x += size_t(gridDim.x) * blockDim.x)
     {
         const int r = int(x / size_t(R)), c = int(x % size_t(R));
-        if (r / tile > c / tile) continue;
+        if (r > c) continue;
         const double v = ordered_sum(part, P, n, x);
         out[x] = v;
-        if (r / tile < c / tile) out[size_t(c) * R + r] = v;
+        if (r < c) out[size_t(c) * R + r] = v;
     }
 }
 
@@ -1104,7 +1201,7 @@ extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, voi
         CPTC_HIP(hipMemsetAsync(d_G, 0, RR * sizeof(double), s));
         return CPTC_OK;
     }
-    const int P = partials_for(rows, 64);
+    const int P = partials_for(rows, R > 64 ? CPTC_GRAM_MFMA_ROWS : 64);
     const size_t rpw = (rows + P - 1) / P;
     void* part = nullptr;
     CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(P) * RR * sizeof(double), &part));
@@ -1126,16 +1223,13 @@ extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, voi
     }
     else
     {
-        // 64 x 64 tiles, the upper triangle only: at R = 128 three tiles of
-        // 16 accumulators per thread (three workgroups per CU) instead of one
-        // 128 x 128 tile of 64 (one per CU); each entry the same ordered sum
-        // as before.  Config 3: 37 -> 26.5 us per launch on average.
+        // the FP64 matrix cores over 64 x 64 tiles, upper triangle only
         const int nt = (R + 63) / 64;
-        hipLaunchKernelGGL((gram_partial_kernel<4, true>), dim3(P, nt * (nt + 1) / 2), dim3(256),
-                           0, s, d_F, rows, R, rpw, nt, pd);
+        hipLaunchKernelGGL(gram_mfma_partial_kernel, dim3(P, nt * (nt + 1) / 2), dim3(256), 0, s,
+                           d_F, rows, R, rpw, nt, pd);
         CPTC_LAUNCHED();
         hipLaunchKernelGGL(sum_partials_sym_kernel, dim3(cptc::grid_for(RR, 256, 1024)),
-                           dim3(256), 0, s, pd, P, R, 64, d_G);
+                           dim3(256), 0, s, pd, P, R, d_G);
         CPTC_LAUNCHED();
         return CPTC_OK;
     }
@@ -1186,7 +1280,7 @@ extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, 
         return CPTC_OK;
     }
     const size_t RR = size_t(R) * R;
-    const int P = partials_for(rows, 64);
+    const int P = partials_for(rows, R > 64 ? CPTC_GRAM_MFMA_ROWS : 64);
     const size_t rpw = (rows + P - 1) / P;
     void* part = nullptr;
     CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(P) * RR * sizeof(double), &part));

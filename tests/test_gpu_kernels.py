@@ -374,10 +374,13 @@ def test_dense_tile_pack_last_write_wins(ca, orc, dev):
 
 
 @pytest.mark.parametrize("rows,R", [(1, 1), (1000, 7), (28818, 128), (5000, 200), (0, 16),
-                                    (300, 65), (9184, 100)])
+                                    (300, 65), (9184, 100), (1, 128), (37, 96), (64, 66),
+                                    (12092, 128), (129, 512)])
 def test_gram(ca, dev, rows, R):
-    """cptc_gram against numpy; above R = 64 only the upper-triangle tiles are
-    summed and the rest mirrored, so G must also be exactly symmetric."""
+    """cptc_gram against numpy; above R = 64 (the FP64 matrix-core partials)
+    only the entries on and above the diagonal are summed and the rest
+    mirrored, so G must also be exactly symmetric.  Ragged row ranges (rows
+    not a multiple of a batch, fewer rows than one partial) and ragged R."""
     F = np.random.default_rng(rows + R).standard_normal((rows, R))
     dF = to_dev(ca, F)
     G = zeros(ca, (R, R))
