@@ -22,6 +22,9 @@
 #ifndef CPTC_SPARSE3_UNROLL
 #define CPTC_SPARSE3_UNROLL 8   // gathers in flight per element slot
 #endif
+#ifndef CPTC_SPARSE3_LANES_UNROLL
+#define CPTC_SPARSE3_LANES_UNROLL 2   // elements per batch and slot, R <= 64
+#endif
 
 namespace {
 
@@ -217,6 +220,194 @@ __global__ __launch_bounds__(WAVE* WAVES) __attribute__((amdgpu_waves_per_eu(1, 
     }
 }
 
+// R <= 64 with 16-byte rows: EPW = 128 / RT element slots per wave (RT = 8,
+// 16, 32, 64 -> 16, 8, 4, 2 slots of LPE = RT / 2 lanes), with the sum and
+// run logic of mttkrp3_seg_kernel; the per-element work is cut, because at
+// these R a lane's two ranks per element leave that kernel bound by
+// instruction issue and by the latency of its window stream (config 2 at
+// R = 32: 21 VALU, 12 SALU and 4 LDS instructions per element and slot):
+//   * the mode is a template parameter (constant field shifts);
+//   * a wave loads its whole range of the segment (up to CH elements) at
+//     once, each lane decodes its elements into the byte offsets of their
+//     F1 and F2 rows and writes {off1, off2, value} as 16-byte records to a
+//     per-wave LDS array; no stream load is then left to wait behind the
+//     row gathers (the hardware waits for loads in issue order);
+//   * slot s takes a contiguous share of the range (runs of equal o1 are
+//     cut only at share boundaries, not every 64 elements) and reads each
+//     of its elements with one broadcast ds_read_b128;
+//   * rows are buffer loads at voffset = the lane's rank offset + the row's
+//     byte offset (o * R * 8 < 2^31);
+//   * when every share holds the same multiple of U elements the batches
+//     run without per-element guards; otherwise each element is guarded
+//     (records past the range hold row 0 and value 0, so every load stays
+//     in bounds).
+constexpr int LANES_CH = 256;             // elements per wave and pass (a 1024-element segment / 4 waves)
+constexpr int LANES_REC = LANES_CH + 32;  // records per wave: reads run past the range by < EPW + U
+
+template <int MODE, int RT, int WAVES, int U>
+__global__ __launch_bounds__(WAVE* WAVES) void mttkrp3_seg_lanes_kernel(
+    const uint64_t* __restrict__ coords, const double* __restrict__ vals,
+    const uint32_t* __restrict__ blk_row, const uint32_t* __restrict__ blk_start,
+    const uint32_t* __restrict__ blk_cnt, const double* __restrict__ F1,
+    const double* __restrict__ F2, double* __restrict__ FtV, int R)
+{
+    constexpr int LPE = RT / 2;           // lanes per element
+    constexpr int EPW = WAVE / LPE;       // element slots per wave
+    static_assert(RT <= 64 && LPE % U == 0 && EPW + U <= LANES_REC - LANES_CH,
+                  "records must cover the reads past the range");
+    constexpr uint32_t NONE = 0xFFFFFFFFu;   // no open run (row offsets are < 2^31)
+    const uint32_t seg = blockIdx.x;
+    const uint32_t row = blk_row[seg];
+    const uint32_t start = blk_start[seg];
+    const uint32_t cnt = blk_cnt[seg];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    const int slot = lane / LPE;
+    const int r0 = (lane % LPE) * 2;
+    const bool rank_ok = r0 < R;
+    const uint32_t voff = uint32_t(rank_ok ? r0 : 0) * 8u;
+    constexpr int sh0 = (MODE == 0) ? 15 : 30;
+    constexpr int sh1 = (MODE == 2) ? 15 : 0;
+    const __amdgpu_buffer_rsrc_t rs1 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(F1), short(0), 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs2 =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<double*>(F2), short(0), 0x7FFFFFFF, 0x00020000);
+    const uint32_t rowb = uint32_t(R) * 8u;
+    auto row_load = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + off, 0u, 0);
+        return make_double2(
+            __longlong_as_double((long long)((uint64_t(uint32_t(w[1])) << 32) | uint32_t(w[0]))),
+            __longlong_as_double((long long)((uint64_t(uint32_t(w[3])) << 32) | uint32_t(w[2]))));
+    };
+
+    const uint32_t wchunk = (cnt + WAVES - 1) / WAVES;
+    const uint32_t lo = start + min(cnt, uint32_t(wave) * wchunk);
+    const uint32_t hi = start + min(cnt, uint32_t(wave + 1) * wchunk);
+
+    double acc0 = 0.0, acc1 = 0.0, t0 = 0.0, t1 = 0.0;
+    uint32_t cur = NONE;
+
+    struct alignas(16) Rec
+    {
+        uint32_t off1, off2;
+        double v;
+    };
+    // the records, reused for the cross-wave sums at the end; a wave's LDS
+    // operations are processed in order, so its own record writes are
+    // visible to its later reads
+    __shared__ Rec recs[WAVES][LANES_REC];
+    static_assert(sizeof(recs) >= sizeof(double) * WAVES * RT, "reduction space");
+    Rec* const rw = recs[wave];
+
+    // one batch of U elements at share position i; FULL: all exist
+    auto batch = [&](auto full, const Rec* rsl, int i, int n_slot) {
+        constexpr bool FULL = decltype(full)::value;
+        Rec e[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) e[u] = rsl[i + u];
+        double2 f1[U], f2[U];
+        bool closes[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            const bool live = FULL || i + u < n_slot;
+            const uint32_t prev = (u == 0) ? cur : e[u - 1].off2;
+            closes[u] = live && e[u].off2 != prev && prev != NONE;
+            f1[u] = row_load(rs1, e[u].off1);   // records hold valid offsets
+            if (closes[u]) f2[u] = row_load(rs2, prev);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+        {
+            if (FULL || i + u < n_slot)
+            {
+                if (closes[u])
+                {
+                    acc0 += t0 * f2[u].x;
+                    acc1 += t1 * f2[u].y;
+                    t0 = t1 = 0.0;
+                }
+                cur = e[u].off2;
+                t0 += e[u].v * f1[u].x;
+                t1 += e[u].v * f1[u].y;
+            }
+        }
+    };
+    for (uint32_t cb = lo; cb < hi; cb += LANES_CH)
+    {
+        const uint32_t m = min(uint32_t(LANES_CH), hi - cb);
+        // every position of the pass at once: unconditional loads from
+        // clamped positions, zeroed past the range
+        constexpr int K = LANES_CH / WAVE;
+        uint64_t pc[K];
+        double v[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+        {
+            const uint32_t e = min(uint32_t(lane + WAVE * k), m - 1);
+            pc[k] = __builtin_nontemporal_load(coords + cb + e);
+            v[k] = __builtin_nontemporal_load(vals + cb + e);
+        }
+        asm volatile("" ::: "memory");   // the previous pass's reads come first
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+        {
+            const bool ok = uint32_t(lane + WAVE * k) < m;
+            const uint64_t p = ok ? pc[k] : uint64_t(0);
+            rw[lane + WAVE * k] = Rec{(uint32_t(p >> sh0) & 0x7FFFu) * rowb,
+                                      (uint32_t(p >> sh1) & 0x7FFFu) * rowb, ok ? v[k] : 0.0};
+        }
+        if (lane < LANES_REC - LANES_CH) rw[LANES_CH + lane] = Rec{0u, 0u, 0.0};
+        asm volatile("" ::: "memory");
+        const int q = int(m + EPW - 1) / EPW;   // share per slot
+        const Rec* const rsl = rw + slot * q;
+        if (int(m) == EPW * q && q % U == 0)
+        {
+#pragma nounroll
+            for (int i = 0; i < q; i += U) batch(std::true_type{}, rsl, i, q);
+        }
+        else
+        {
+            const int left = int(m) - slot * q;
+            const int n_slot = left < 0 ? 0 : (left > q ? q : left);
+#pragma nounroll
+            for (int i = 0; i < q; i += U) batch(std::false_type{}, rsl, i, n_slot);
+        }
+    }
+    if (cur != NONE)
+    {
+        const double2 f2 = row_load(rs2, cur);
+        acc0 += t0 * f2.x;
+        acc1 += t1 * f2.y;
+    }
+    if (!rank_ok) acc0 = acc1 = 0.0;
+    // reduce the slots of the wave (lanes l, l ^ LPE, l ^ 2 LPE, ...)
+#pragma unroll
+    for (int off = LPE; off < WAVE; off <<= 1)
+    {
+        acc0 += __shfl_xor(acc0, off, WAVE);
+        acc1 += __shfl_xor(acc1, off, WAVE);
+    }
+    __syncthreads();   // every wave's record reads are done
+    double* const red = reinterpret_cast<double*>(&recs[0][0]);   // [WAVES][RT]
+    if (slot == 0)
+    {
+        red[wave * RT + r0] = acc0;
+        red[wave * RT + r0 + 1] = acc1;
+    }
+    __syncthreads();
+    for (int x = tid; x < RT; x += WAVE * WAVES)
+    {
+        if (x >= R) continue;
+        double tot = 0.0;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += red[w * RT + x];
+        if (tot != 0.0) atomicAdd(FtV + size_t(row) * R + x, tot);
+    }
+}
+
 template <int RT, int VEC>
 hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const uint32_t* br,
                      const uint32_t* bs, const uint32_t* bc, size_t nblocks, const double* F1,
@@ -228,7 +419,22 @@ hipError_t launch_rt(int mode, const uint64_t* coords, const double* vals, const
     dim3 grid(unsigned(nblocks), ry);
     // the wave-uniform kernel addresses rows by 32-bit byte offsets o * R * 8
     // (o < 2^15), so it needs R * 8 * 2^15 < 2^31
-    if (RT == 128 && VEC == 2 && R <= 8000)
+    if (RT <= 64 && VEC == 2)
+    {
+        constexpr int RL = RT <= 64 ? RT : 64;   // (the branch is dead for RT = 128)
+        constexpr int UL = CPTC_SPARSE3_LANES_UNROLL;
+        const dim3 block(WAVE * WAVES);
+        if (mode == 0)
+            hipLaunchKernelGGL((mttkrp3_seg_lanes_kernel<0, RL, WAVES, UL>), grid, block, 0, s,
+                               coords, vals, br, bs, bc, F1, F2, FtV, R);
+        else if (mode == 1)
+            hipLaunchKernelGGL((mttkrp3_seg_lanes_kernel<1, RL, WAVES, UL>), grid, block, 0, s,
+                               coords, vals, br, bs, bc, F1, F2, FtV, R);
+        else
+            hipLaunchKernelGGL((mttkrp3_seg_lanes_kernel<2, RL, WAVES, UL>), grid, block, 0, s,
+                               coords, vals, br, bs, bc, F1, F2, FtV, R);
+    }
+    else if (RT == 128 && VEC == 2 && R <= 8000)
     {
         const dim3 block(WAVE * WAVES);
         if (mode == 0)

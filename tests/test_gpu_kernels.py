@@ -62,6 +62,52 @@ def test_sparse_mttkrp_vs_oracle(ca, orc, dev, R):
         assert rel_err(out.numpy(), ref) <= 1e-10, (mode, R)
 
 
+@pytest.mark.parametrize("R", [8, 16, 30, 32, 64, 128])
+@pytest.mark.parametrize("split", ["rows", "random"])
+def test_sparse_mttkrp_free_segment_tables(ca, orc, dev, R, split):
+    """The C ABI takes any segment table over a row-sorted view: whole rows
+    as one segment (hot rows far beyond the 1024 elements of the reference's
+    table, so a wave takes several passes) and rows cut at random lengths
+    (1 to 3000: ragged shares of the wave's range and of its element slots).
+    Every mode within 1e-10 of the oracle."""
+    dims = (400, 300, 700)
+    t, views = zipf_views(ca, orc, dims, 80000, R + 7)
+    rng = np.random.default_rng(R)
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    for mode in range(3):
+        v = views[mode]
+        ref = orc.mttkrp3_view(views, mode, F[0].ravel(), F[1].ravel(), F[2].ravel(), R,
+                               dims[mode]).reshape(dims[mode], R)
+        # rows of the view from its reference segment table
+        rows = np.repeat(v["blk_row"], v["blk_cnt"]).astype(np.int64)
+        starts = np.flatnonzero(np.r_[True, rows[1:] != rows[:-1]])
+        ends = np.r_[starts[1:], len(rows)]
+        br, bs, bc = [], [], []
+        for a, b in zip(starts, ends):
+            if split == "rows":
+                cuts = [a, b]
+            else:
+                cuts = [a]
+                while cuts[-1] < b:
+                    cuts.append(min(b, cuts[-1] + int(rng.integers(1, 3001))))
+            for x, y in zip(cuts[:-1], cuts[1:]):
+                br.append(rows[a]); bs.append(x); bc.append(y - x)
+        assert max(bc) > 1024
+        seg = [to_dev(ca, np.asarray(a, np.uint32)) for a in (br, bs, bc)]
+        dc, dv = to_dev(ca, v["coords"]), to_dev(ca, v["vals"])
+        out = zeros(ca, (dims[mode], R))
+        F1 = dF[1] if mode == 0 else dF[0]
+        F2 = dF[1] if mode == 2 else dF[2]
+        rc = ca.lib.cptc_mttkrp_sparse3(mode, dc.data_ptr(), dv.data_ptr(), seg[0].data_ptr(),
+                                        seg[1].data_ptr(), seg[2].data_ptr(), len(br),
+                                        F1.data_ptr(), F2.data_ptr(), out.data_ptr(), R,
+                                        stream(ca))
+        assert rc == 0, ca.lib.cptc_last_error()
+        ca.sync()
+        assert rel_err(out.numpy(), ref) <= 1e-10, (mode, R, split)
+
+
 def test_sparse_mttkrp_misaligned_factor_base(ca, orc, dev):
     """Factor bases that are only 8-byte aligned take the scalar path."""
     R, dims = 16, (200, 150, 300)
