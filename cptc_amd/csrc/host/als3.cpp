@@ -33,6 +33,7 @@
 #include "hip_util.hpp"
 #include "host_util.hpp"
 #include "layout.hpp"
+#include "small_la.hpp"
 #include "split_img.hpp"
 
 namespace cptc {
@@ -92,6 +93,7 @@ struct Als3
     double* d_G = nullptr;  // 3 x R x R
     bool gram_ok[3] = {false, false, false};
     int ftf_for = -1;   // the mode whose FtF (Hadamard of the other Grams) is in d_FtF
+    int ftv_zero_for = -1;   // the mode whose MTTKRP finds d_FtV already cleared
     double* d_FtF = nullptr;
     double* d_Ainv = nullptr;  // pinv(FtF) of the mode being updated
     double* d_FtV = nullptr;
@@ -130,8 +132,10 @@ int mttkrp_launch(Als3& h, int mode, bool with_pinv)
 {
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
-    // a kernel, not hipMemsetAsync: the iteration may be captured in a HIP graph
-    CPTC_TRY(cptc_zero(h.d_FtV, dim * size_t(R), h.s));
+    // a kernel, not hipMemsetAsync: the iteration may be captured in a HIP
+    // graph; skipped when the previous mode's update cleared it (TailJobs)
+    if (h.ftv_zero_for != mode) CPTC_TRY(cptc_zero(h.d_FtV, dim * size_t(R), h.s));
+    h.ftv_zero_for = -1;
     const double* A = h.F[0];
     const double* B = h.F[1];
     const double* C = h.F[2];
@@ -618,23 +622,41 @@ int update_mode(Als3& h, int mode)
     // lambda; column norms, normalise + absorb and this mode's Gram refresh
     // from one Gram of the unnormalised factor (als.cu:480-517)
     CPTC_TRY(cptc_apply_pinv(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.d_lambda, h.s));
+    // The update's last launch (the column scaling) also clears FtV for the
+    // next mode of the iteration (the apply above was its last reader; after
+    // mode C the fit still reads it) and, above R = 32, forms the next
+    // mode's FtF when its other Gram is current: two launches fewer per mode.
     // R <= 32: the Gram's sums, norms and normalisation in one workgroup, with
-    // the next mode's FtF (its other Gram is current) from the same launch.
-    // Above that the FtF product inside the one-workgroup normalisation
-    // measured slower (config 3: 18-20 us per launch against 11-12 us plus a
-    // 4 us Hadamard launch), so the Hadamard stays a grid launch.
+    // the next mode's FtF from the same launch.
     const int next = (mode + 1) % 3, other = 3 - next - mode;
+    TailJobs tj;
+    if (mode < 2)
+    {
+        tj.zero = h.d_FtV;
+        tj.nzero = h.dims[next] * size_t(R);
+    }
     if (R <= 32 && dim >= 1)
     {
         const bool fuse = h.gram_ok[other];
-        CPTC_TRY(cptc_gram_normalize_absorb_next(h.F[mode], dim, R, h.G(mode), h.d_norms,
+        CPTC_TRY(gram_normalize_absorb_next_tail(h.F[mode], dim, R, h.G(mode), h.d_norms,
                                                  h.d_lambda, fuse ? h.G(other) : nullptr,
-                                                 fuse ? h.d_FtF : nullptr, h.s));
+                                                 fuse ? h.d_FtF : nullptr, &tj, h.s));
         h.ftf_for = fuse ? next : -1;
     }
     else
-        CPTC_TRY(cptc_gram_normalize_absorb(h.F[mode], dim, R, h.G(mode), h.d_norms, h.d_lambda,
-                                            h.s));
+    {
+        const bool fuse = h.gram_ok[other];
+        if (fuse)
+        {
+            tj.ga = h.G(mode);   // normalised by the launch before the scaling
+            tj.gb = h.G(other);
+            tj.ftf = h.d_FtF;
+        }
+        CPTC_TRY(gram_normalize_absorb_tail(h.F[mode], dim, R, h.G(mode), h.d_norms, h.d_lambda,
+                                            &tj, h.s));
+        h.ftf_for = fuse ? next : -1;
+    }
+    h.ftv_zero_for = mode < 2 ? next : -1;
     h.gram_ok[mode] = true;
     return CPTC_OK;
 }
@@ -670,13 +692,14 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
     return CPTC_OK;
 }
 
-// The state an iteration leaves behind and finds: every Gram current and,
-// for R <= 32, mode 0's FtF formed by mode 2's update.  Only an iteration
-// that starts there has the captured iteration's launches.
+// The state an iteration leaves behind and finds: every Gram current, mode
+// 0's FtF formed by mode 2's update and FtV not yet cleared for mode 0 (the
+// fit reads it).  Only an iteration that starts there has the captured
+// iteration's launches.
 bool steady(const Als3& h)
 {
     return h.gram_ok[0] && h.gram_ok[1] && h.gram_ok[2] &&
-           h.ftf_for == ((h.R <= 32 && h.dims[1] >= 1 && h.dims[2] >= 1) ? 0 : -1);
+           h.ftf_for == 0 && h.ftv_zero_for == -1;
 }
 
 // Captures one steady-state iteration (no events, kernel timing off, the
@@ -697,6 +720,7 @@ int capture_iteration(Als3& h, double* d_out)
     {
         if (g) (void)hipGraphDestroy(g);
         h.ftf_for = -1;   // nothing ran: the next iteration forms its FtF itself
+        h.ftv_zero_for = -1;
         return rc;
     }
     CPTC_HIP(ee);
@@ -1092,6 +1116,7 @@ extern "C" int cptc_als3_sgd(void* handle, int iters, double gamma, uint32_t bat
                                  h->o.verbose, batch_rmse, h->s);
     for (bool& g : h->gram_ok) g = false;   // the factors changed
     h->ftf_for = -1;
+    h->ftv_zero_for = -1;
     return rc;
 }
 
@@ -1205,6 +1230,7 @@ extern "C" int cptc_als3_set_factor(void* handle, int mode, const double* host_i
     CPTC_HIP(hipStreamSynchronize(h->s));
     h->gram_ok[mode] = false;
     h->ftf_for = -1;
+    h->ftv_zero_for = -1;
     return CPTC_OK;
 }
 

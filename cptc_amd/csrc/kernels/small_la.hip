@@ -5,11 +5,13 @@
 // then one ordered sum), so every result is bit-reproducible run to run.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <mutex>
 
 #include "../host/hip_util.hpp"
+#include "../host/small_la.hpp"
 
 namespace {
 
@@ -1168,17 +1170,46 @@ __global__ void zero_kernel(double* __restrict__ p, size_t n)
         p[x] = 0.0;
 }
 
-// F[:, r] /= n_r (0 when n_r < 1e-14)
+// F[:, r] /= n_r (0 when n_r < 1e-14).  The driver's update tail also
+// hands this last launch of a mode's update two jobs for the next mode
+// (cptc::TailJobs): zero z[0, nz) (the next MTTKRP's output, once the apply
+// has read it) and form C = A .* B over n2 entries (the next mode's FtF,
+// hadamard_kernel's product bit for bit), so neither needs a launch.
 __global__ void scale_columns_kernel(double* __restrict__ F, size_t rows, int R,
-                                     const double* __restrict__ norms)
+                                     const double* __restrict__ norms, double* __restrict__ z,
+                                     size_t nz, const double* __restrict__ A,
+                                     const double* __restrict__ B, double* __restrict__ C,
+                                     size_t n2)
 {
     const size_t total = rows * size_t(R);
-    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < total;
+    const size_t n = total > nz ? (total > n2 ? total : n2) : (nz > n2 ? nz : n2);
+    for (size_t x = size_t(blockIdx.x) * blockDim.x + threadIdx.x; x < n;
          x += size_t(gridDim.x) * blockDim.x)
     {
-        const double n = norms[x % size_t(R)];
-        F[x] = (n < 1e-14) ? 0.0 : F[x] / n;
+        if (x < total)
+        {
+            const double nr = norms[x % size_t(R)];
+            F[x] = (nr < 1e-14) ? 0.0 : F[x] / nr;
+        }
+        if (x < nz) z[x] = 0.0;
+        if (x < n2) C[x] = A[x] * B[x];
     }
+}
+
+int scale_launch(double* F, size_t rows, int R, const double* norms, const cptc::TailJobs* t,
+                 hipStream_t s)
+{
+    double* z = t ? t->zero : nullptr;
+    const size_t nz = z ? t->nzero : 0;
+    const bool had = t && t->ftf;
+    const size_t n2 = had ? size_t(R) * R : 0;
+    const size_t n = std::max({rows * size_t(R), nz, n2});
+    if (n == 0) return CPTC_OK;
+    hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(n, 256, 4096)), dim3(256), 0, s,
+                       F, rows, R, norms, z, nz, had ? t->ga : nullptr, had ? t->gb : nullptr,
+                       had ? t->ftf : nullptr, n2);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
 }
 
 int partials_for(size_t rows, size_t min_rows)
@@ -1240,31 +1271,27 @@ extern "C" int cptc_gram(const double* d_F, size_t rows, int R, double* d_G, voi
     return CPTC_OK;
 }
 
-extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G,
-                                          double* d_norms, double* d_lambda, void* stream)
+namespace cptc {
+
+int gram_normalize_absorb_tail(double* d_F, size_t rows, int R, double* d_G, double* d_norms,
+                               double* d_lambda, const TailJobs* t, hipStream_t s)
 {
     CPTC_REQUIRE(R >= 1 && R <= FIT_T && d_F && d_G && d_norms && d_lambda, CPTC_ERR_ARG,
                  "cptc_gram_normalize_absorb: bad arguments");
-    hipStream_t s = cptc::as_stream(stream);
     CPTC_TRY(cptc_gram(d_F, rows, R, d_G, s));
     hipLaunchKernelGGL(gram_norms_absorb_kernel, dim3(1), dim3(FIT_T), 0, s, d_G, R, d_norms,
                        d_lambda, nullptr, nullptr);
     CPTC_LAUNCHED();
-    if (rows == 0) return CPTC_OK;
-    hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
-                       dim3(256), 0, s, d_F, rows, R, d_norms);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    return scale_launch(d_F, rows, R, d_norms, t, s);
 }
 
-extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G,
-                                               double* d_norms, double* d_lambda,
-                                               const double* d_other, double* d_FtF, void* stream)
+int gram_normalize_absorb_next_tail(double* d_F, size_t rows, int R, double* d_G,
+                                    double* d_norms, double* d_lambda, const double* d_other,
+                                    double* d_FtF, const TailJobs* t, hipStream_t s)
 {
     CPTC_REQUIRE(R >= 1 && R <= FIT_T && d_F && d_G && d_norms && d_lambda && rows >= 1 &&
                      (d_other == nullptr) == (d_FtF == nullptr),
                  CPTC_ERR_ARG, "cptc_gram_normalize_absorb_next: bad arguments (R <= %d)", FIT_T);
-    hipStream_t s = cptc::as_stream(stream);
     if (R > 32)
     {
         // cptc_gram, then the norms, normalisation and the next mode's FtF in
@@ -1273,14 +1300,10 @@ extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, 
         hipLaunchKernelGGL(gram_norms_absorb_kernel, dim3(1), dim3(FIT_T), 0, s, d_G, R, d_norms,
                            d_lambda, d_other, d_FtF);
         CPTC_LAUNCHED();
-        hipLaunchKernelGGL(scale_columns_kernel,
-                           dim3(cptc::grid_for(rows * size_t(R), 256, 4096)), dim3(256), 0, s,
-                           d_F, rows, R, d_norms);
-        CPTC_LAUNCHED();
-        return CPTC_OK;
+        return scale_launch(d_F, rows, R, d_norms, t, s);
     }
     const size_t RR = size_t(R) * R;
-    const int P = partials_for(rows, R > 64 ? CPTC_GRAM_MFMA_ROWS : 64);
+    const int P = partials_for(rows, 64);
     const size_t rpw = (rows + P - 1) / P;
     void* part = nullptr;
     CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(P) * RR * sizeof(double), &part));
@@ -1295,10 +1318,24 @@ extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, 
     hipLaunchKernelGGL(gram_finish_small_kernel, dim3(1), dim3(FIT_T), 0, s, pd, P, R, d_G,
                        d_norms, d_lambda, d_other, d_FtF);
     CPTC_LAUNCHED();
-    hipLaunchKernelGGL(scale_columns_kernel, dim3(cptc::grid_for(rows * size_t(R), 256, 4096)),
-                       dim3(256), 0, s, d_F, rows, R, d_norms);
-    CPTC_LAUNCHED();
-    return CPTC_OK;
+    return scale_launch(d_F, rows, R, d_norms, t, s);
+}
+
+}  // namespace cptc
+
+extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G,
+                                          double* d_norms, double* d_lambda, void* stream)
+{
+    return cptc::gram_normalize_absorb_tail(d_F, rows, R, d_G, d_norms, d_lambda, nullptr,
+                                            cptc::as_stream(stream));
+}
+
+extern "C" int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G,
+                                               double* d_norms, double* d_lambda,
+                                               const double* d_other, double* d_FtF, void* stream)
+{
+    return cptc::gram_normalize_absorb_next_tail(d_F, rows, R, d_G, d_norms, d_lambda, d_other,
+                                                 d_FtF, nullptr, cptc::as_stream(stream));
 }
 
 extern "C" int cptc_zero(double* d_p, size_t n, void* stream)
