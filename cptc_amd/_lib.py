@@ -113,6 +113,7 @@ class GenInfo(C.Structure):
         ("tile_bf16x3", C.c_int),
         ("unit_segments", C.c_uint64 * 3),
         ("unit_sums", C.c_int),
+        ("unit_sums_img", C.c_int),
     ]
 
 
@@ -214,6 +215,7 @@ SIGNATURES = {
     "cptc_mttkrp_seg_nd_keys_dims": (_I, [_I, _I, _P, _I, _P, _P, _P, _U64, _P, _P, _P, _P,
                                           _U64, _P, _P, _P, _I, _P]),
     "cptc_units_pack_nd": (_I, [_P, _U64, _P, _P, _P, _P]),
+    "cptc_units_pack_nd_f64": (_I, [_P, _U64, _P, _P, _P, _P]),
     "cptc_units_weights_nd": (_I, [_P, _U64, _P, _I, _P, _P, _I, _P, _P]),
     "cptc_mttkrp_units_nd": (_I, [_I, _P, _U64, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _P,
                                   _I, _P]),
@@ -225,6 +227,8 @@ SIGNATURES = {
     "cptc_gram_hadamard": (_I, [_P, _I, _I, _I, _P, _P]),
     "cptc_gen_unit_sums": (_I, [_P, _Z, _P, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _P,
                                 _P]),
+    "cptc_gen_unit_sums_img": (_I, [_P, _Z, _P, _P, _P, _Z, _P, _P, _P, _I, _I, _I, _I, _P,
+                                   _P]),
     "cptc_gen_unit_sums_plan": (_I, [_P, _Z, _I, _P, _P, _P]),
     "cptc_gen_unit_scatter": (_I, [_P, _Z, _I, _I, _P, _P, _I, _Z, _P, _P]),
     "cptc_chol_ridge_solve": (_I, [_P, _P, _P, _Z, _I, _P]),

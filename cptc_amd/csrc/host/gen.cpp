@@ -359,6 +359,7 @@ struct Gen
     bool unit_sums = false;
     bool usum_ok = false;
     double* d_usum = nullptr;          // nunits x R
+    double* d_uimg64 = nullptr;        // the units' FP64 images for cptc_gen_unit_sums_img
     double** d_Fo = nullptr;           // the outer modes' factors, device array of pointers
     uint32_t* d_us_order = nullptr;    // cptc_gen_unit_sums_plan: units by inner block triple
     uint32_t* d_us_chunk = nullptr;    // chunk offsets into d_us_order
@@ -412,6 +413,7 @@ struct Gen
         dfree(d_fit_hist);
         dfree(d_L);
         dfree(d_usum);
+        dfree(d_uimg64);
         if (d_Fo) (void)hipFree(d_Fo);
         if (d_us_order) (void)hipFree(d_us_order);
         if (d_us_chunk) (void)hipFree(d_us_chunk);
@@ -477,11 +479,18 @@ struct Gen
             const int* in3 = units.inner;
             if (!usum_ok)
             {
-                CPTC_TRY(cptc_gen_unit_sums(units.d_unit6, units.nunits, units.d_lid, units.d_val,
-                                            d_us_order, d_us_chunk, us_nchunks,
-                                            d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
-                                            int(dims[in3[0]]), int(dims[in3[1]]),
-                                            int(dims[in3[2]]), R, d_usum, s));
+                if (d_uimg64)
+                    CPTC_TRY(cptc_gen_unit_sums_img(units.d_unit6, units.nunits, d_uimg64,
+                                                    d_us_order, d_us_chunk, us_nchunks,
+                                                    d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
+                                                    int(dims[in3[0]]), int(dims[in3[1]]),
+                                                    int(dims[in3[2]]), R, d_usum, s));
+                else
+                    CPTC_TRY(cptc_gen_unit_sums(units.d_unit6, units.nunits, units.d_lid,
+                                                units.d_val, d_us_order, d_us_chunk, us_nchunks,
+                                                d_F[in3[0]], d_F[in3[1]], d_F[in3[2]],
+                                                int(dims[in3[0]]), int(dims[in3[1]]),
+                                                int(dims[in3[2]]), R, d_usum, s));
                 usum_ok = true;
             }
             if (timing)
@@ -978,6 +987,23 @@ extern "C" int cptc_gen_create(const cptc_coo* coo, const cptc_gen_opts* opts, v
                 GEN_TRY(dmalloc(&g->d_usum, g->units.nunits * size_t(R)));
                 GEN_TRY(build_unit_sums_plan(g->units, s, g->d_us_order, g->d_us_chunk,
                                              g->us_nchunks));
+                // the sums from FP64 unit images on the matrix cores (32 KB
+                // per unit, up to 8 GiB) when the units are at least a fifth
+                // full: the image path streams every cell (HBM bound, ~6.7 ns
+                // per unit) whatever the fill, the pool path reads three
+                // factor rows from LDS per element (LDS bound, ~10 ps per
+                // element).  Config 5 (fill 0.149): 0.220 against 0.203 ms
+                // per call.  GEN_UNIT_SUMS_IMG=1 / 0 forces the choice.
+                const char* ui = std::getenv("GEN_UNIT_SUMS_IMG");
+                const double fill = double(g->units.dense_nnz) /
+                                    (double(g->units.nunits) * 4096.0);
+                const bool img = ui ? std::strcmp(ui, "0") != 0 : fill >= 0.2;
+                if (img && g->units.nunits <= (size_t(8) << 30) / (4096 * sizeof(double)))
+                {
+                    GEN_TRY(dmalloc(&g->d_uimg64, g->units.nunits * 4096));
+                    GEN_TRY(cptc_units_pack_nd_f64(g->units.d_unit6, g->units.nunits,
+                                                   g->units.d_lid, g->units.d_val, g->d_uimg64, s));
+                }
                 std::vector<const double*> fo;
                 for (int o : g->units.outer) fo.push_back(g->d_F[o]);
                 GEN_HIP(hipMalloc(&g->d_Fo, fo.size() * sizeof(double*)));
@@ -1075,6 +1101,7 @@ extern "C" int cptc_gen_info_get(void* handle, cptc_gen_info* info)
     info->tile_bf16x3 = (g->dense && g->tile_b3) ? 1 : 0;
     for (int sl = 0; sl < 3; ++sl) info->unit_segments[sl] = g->uimg[sl].ready() ? g->uimg[sl].nseg : 0;
     info->unit_sums = g->unit_sums ? 1 : 0;
+    info->unit_sums_img = (g->unit_sums && g->d_uimg64) ? 1 : 0;
     for (int q = 0; q < 3; ++q) info->prep_ms[q] = g->prep_ms[q];
     return CPTC_OK;
 }

@@ -291,6 +291,24 @@ __global__ __launch_bounds__(256) void units_pack_kernel(const uint32_t* __restr
                              float(T[4 * c + 3]));
 }
 
+// The same cells in FP64 (the per-unit sums' operand): one workgroup per
+// unit, FP64 accumulation in LDS (duplicates summed), written as doubles.
+__global__ __launch_bounds__(256) void units_pack_f64_kernel(const uint32_t* __restrict__ unit6,
+                                                             const uint32_t* __restrict__ lid,
+                                                             const double* __restrict__ val,
+                                                             double* __restrict__ img)
+{
+    __shared__ double T[4096];
+    const size_t u = blockIdx.x;
+    for (int c = threadIdx.x; c < 4096; c += 256) T[c] = 0.0;
+    __syncthreads();
+    const uint32_t n = unit6[6 * u + 3], st = unit6[6 * u + 4];
+    for (uint32_t e = threadIdx.x; e < n; e += 256) atomicAdd(&T[lid[st + e] & 4095u], val[st + e]);
+    __syncthreads();
+    double2* out = reinterpret_cast<double2*>(img + u * 4096);
+    for (int c = threadIdx.x; c < 2048; c += 256) out[c] = make_double2(T[2 * c], T[2 * c + 1]);
+}
+
 __global__ void units_weights_kernel(const uint32_t* __restrict__ unit6, uint64_t nunits,
                                      const uint32_t* __restrict__ oc, int nouter, Factors Fo,
                                      int R, double* __restrict__ W)
@@ -860,6 +878,23 @@ extern "C" int cptc_units_pack_nd(const uint32_t* d_unit6, uint64_t nunits, cons
     CPTC_REQUIRE(nunits < (uint64_t(1) << 31), CPTC_ERR_ARG, "cptc_units_pack_nd: too many units");
     hipLaunchKernelGGL(units_pack_kernel, dim3(unsigned(nunits)), dim3(256), 0,
                        cptc::as_stream(stream), d_unit6, d_lid, d_val, d_tiles);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_units_pack_nd_f64(const uint32_t* d_unit6, uint64_t nunits,
+                                      const uint32_t* d_lid, const double* d_val, double* d_img,
+                                      void* stream)
+{
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_lid && d_val && d_img, CPTC_ERR_ARG,
+                 "cptc_units_pack_nd_f64: null pointer");
+    CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_img) & 15) == 0, CPTC_ERR_ARG,
+                 "cptc_units_pack_nd_f64: the image must be 16-byte aligned");
+    CPTC_REQUIRE(nunits < (uint64_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_units_pack_nd_f64: too many units");
+    hipLaunchKernelGGL(units_pack_f64_kernel, dim3(unsigned(nunits)), dim3(256), 0,
+                       cptc::as_stream(stream), d_unit6, d_lid, d_val, d_img);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

@@ -136,6 +136,144 @@ __global__ __launch_bounds__(64 * USUM_WAVES) void unit_sums_kernel(
     }
 }
 
+// The same sums on the FP64 matrix cores (v_mfma_f64_16x16x4f64) from the
+// units' dense FP64 images (cptc_units_pack_nd_f64, cell la 256 + lb 16 +
+// lc): s_u[r] = sum_la Fa[la][r] sum_lb Fb[lb][r] X_la[lb][r] with X_la =
+// T_la Fc_blk, T_la the unit's 16 x 16 (lb x lc) slab at la.  unit_sums_kernel
+// reads three factor rows from LDS per element and rank pair and is bound by
+// the LDS; here each element meets its Fc row inside the matrix product, and
+// the Fb and Fa weights are applied once per (la, lb) and per la.
+//
+// Chunks and staging as unit_sums_kernel; each wave takes every 4th unit.
+// Per la and 16-rank tile c: four MFMA steps over lc, where lane l = 16 q +
+// j holds A = T_la[lb = j][lc = 4 q + s] (the lane's four cells are one
+// 32-byte load; the 64 lanes read the 2 KB slab contiguously) and B =
+// Fc[4 q + s][16 c + j]; the result's element v of lane l is X_la[lb = q +
+// 4 v][16 c + j] (this instruction's output layout).  The lane then adds
+// Fa[la][16 c + j] * sum_v Fb[q + 4 v][16 c + j] X[v] to its sum, and the
+// four lane groups q are added at the end.  The B operands and Fb weights
+// are fixed per chunk and held in registers.  Rows past a factor's end and
+// ranks past R are staged as zeros (image cells there are zero).
+typedef double usum_d4 __attribute__((ext_vector_type(4)));
+template <int NT>   // 16-rank tiles
+__global__ __launch_bounds__(64 * USUM_WAVES) void unit_sums_mfma_kernel(
+    const uint32_t* __restrict__ unit6, const uint32_t* __restrict__ order,
+    const uint32_t* __restrict__ chunk_off, const double* __restrict__ img,
+    const double* __restrict__ Fa, const double* __restrict__ Fb, const double* __restrict__ Fc,
+    int da, int db, int dc, int R, double* __restrict__ sums)
+{
+    constexpr int RT = 16 * NT;
+    __shared__ double blk[3][16][RT];
+    const uint32_t i0 = chunk_off[blockIdx.x], i1 = chunk_off[blockIdx.x + 1];
+    {
+        const uint32_t* h = unit6 + size_t(order[i0]) * 6;
+        const int r0[3] = {int(h[0]) * 16, int(h[1]) * 16, int(h[2]) * 16};
+        const int dim[3] = {da, db, dc};
+        const double* F[3] = {Fa, Fb, Fc};
+        for (int x = threadIdx.x; x < 3 * 16 * RT; x += 64 * USUM_WAVES)
+        {
+            const int f = x / (16 * RT), rem = x % (16 * RT);
+            const int row = rem / RT, c = rem % RT;
+            const int g = r0[f] + row;
+            blk[f][row][c] = (g < dim[f] && c < R) ? F[f][size_t(g) * R + c] : 0.0;
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    double bfr[NT][4], fbw[NT][4];
+#pragma unroll
+    for (int c = 0; c < NT; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            bfr[c][k] = blk[2][4 * q + k][16 * c + j];
+            fbw[c][k] = blk[1][q + 4 * k][16 * c + j];
+        }
+    // the wave's units are i0 + w, i0 + w + 4, ...; each in four steps of
+    // four la slabs (8 KB), the next step's slabs loaded during this one's
+    // MFMAs (two register sets in turn, kept in that order by scheduling
+    // barriers), across unit boundaries
+    const uint32_t n_unit = (i1 - i0 > uint32_t(w)) ? (i1 - i0 - uint32_t(w) + USUM_WAVES - 1) / USUM_WAVES : 0u;
+    const uint32_t n_step = 4 * n_unit;
+    struct Slabs
+    {
+        double2 a[4][2];
+    };
+    auto load = [&](uint32_t k, Slabs& x) {
+        const uint32_t kk = k < n_step ? k : n_step - 1;   // past the end: a reload, never used
+        const uint32_t u = order[i0 + uint32_t(w) + USUM_WAVES * (kk >> 2)];
+        const double* __restrict__ T = img + size_t(u) * 4096 + (kk & 3u) * 1024u + 16 * j + 4 * q;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+        {
+            x.a[b][0] = *reinterpret_cast<const double2*>(T + b * 256);
+            x.a[b][1] = *reinterpret_cast<const double2*>(T + b * 256 + 2);
+        }
+    };
+    double acc[NT];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) acc[c] = 0.0;
+    auto compute = [&](uint32_t k, const Slabs& x) {
+        const int la0 = int(k & 3u) * 4;
+        usum_d4 xs[4][NT];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int c = 0; c < NT; ++c)
+            {
+                usum_d4 y = {0.0, 0.0, 0.0, 0.0};
+                y = __builtin_amdgcn_mfma_f64_16x16x4f64(x.a[b][0].x, bfr[c][0], y, 0, 0, 0);
+                y = __builtin_amdgcn_mfma_f64_16x16x4f64(x.a[b][0].y, bfr[c][1], y, 0, 0, 0);
+                y = __builtin_amdgcn_mfma_f64_16x16x4f64(x.a[b][1].x, bfr[c][2], y, 0, 0, 0);
+                y = __builtin_amdgcn_mfma_f64_16x16x4f64(x.a[b][1].y, bfr[c][3], y, 0, 0, 0);
+                xs[b][c] = y;
+            }
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int c = 0; c < NT; ++c)
+            {
+                double t = xs[b][c][0] * fbw[c][0];
+                t = __builtin_fma(xs[b][c][1], fbw[c][1], t);
+                t = __builtin_fma(xs[b][c][2], fbw[c][2], t);
+                t = __builtin_fma(xs[b][c][3], fbw[c][3], t);
+                acc[c] = __builtin_fma(blk[0][la0 + b][16 * c + j], t, acc[c]);
+            }
+        if ((k & 3u) == 3u)   // the unit's last step: its sums
+        {
+            const uint32_t u = order[i0 + uint32_t(w) + USUM_WAVES * (k >> 2)];
+#pragma unroll
+            for (int c = 0; c < NT; ++c)
+            {
+                double v = acc[c];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                const int r = 16 * c + j;
+                if (q == 0 && r < R) sums[size_t(u) * R + r] = v;
+                acc[c] = 0.0;
+            }
+        }
+    };
+    if (n_step > 0)
+    {
+        Slabs P, Q;
+        load(0, P);
+        for (uint32_t k = 0; k < n_step; k += 2)   // n_step is a multiple of 4
+        {
+            load(k + 1, Q);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(k, P);
+            __builtin_amdgcn_sched_barrier(0);
+            load(k + 2, P);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(k + 1, Q);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 // FtV[i_m(u)][r] += s[u][r] * prod over the other outer modes o of
 // F_o[i_o(u)][r] (outer mode m = outer[pos]); a workgroup takes 256 units,
 // sums them per (row, rank) in LDS when dim_m x R <= 4096 and flushes once;
@@ -228,6 +366,34 @@ extern "C" int cptc_gen_unit_sums(const uint32_t* d_unit6, size_t nunits, const 
     else
         hipLaunchKernelGGL(unit_sums_kernel<32>, grid, block, 0, s, d_unit6, d_order, d_chunk_off,
                            d_lid, d_val, d_Fa, d_Fb, d_Fc, da, db, dc, R, d_sums);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
+extern "C" int cptc_gen_unit_sums_img(const uint32_t* d_unit6, size_t nunits, const double* d_img,
+                                      const uint32_t* d_order, const uint32_t* d_chunk_off,
+                                      size_t nchunks, const double* d_Fa, const double* d_Fb,
+                                      const double* d_Fc, int da, int db, int dc, int R,
+                                      double* d_sums, void* stream)
+{
+    CPTC_REQUIRE(R >= 1 && R <= USUM_R && da >= 1 && db >= 1 && dc >= 1, CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums_img: R %d (1..%d) or dims", R, USUM_R);
+    if (nunits == 0) return CPTC_OK;
+    CPTC_REQUIRE(d_unit6 && d_img && d_order && d_chunk_off && d_Fa && d_Fb && d_Fc && d_sums &&
+                     nchunks >= 1,
+                 CPTC_ERR_ARG, "cptc_gen_unit_sums_img: null pointer or no chunks");
+    CPTC_REQUIRE((reinterpret_cast<uintptr_t>(d_img) & 15) == 0, CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums_img: the image must be 16-byte aligned");
+    CPTC_REQUIRE(nchunks <= nunits && nchunks < (size_t(1) << 31), CPTC_ERR_ARG,
+                 "cptc_gen_unit_sums_img: %zu chunks for %zu units", nchunks, nunits);
+    hipStream_t s = cptc::as_stream(stream);
+    const dim3 grid{unsigned(nchunks)}, block{64 * USUM_WAVES};
+    if (R <= 16)
+        hipLaunchKernelGGL(unit_sums_mfma_kernel<1>, grid, block, 0, s, d_unit6, d_order,
+                           d_chunk_off, d_img, d_Fa, d_Fb, d_Fc, da, db, dc, R, d_sums);
+    else
+        hipLaunchKernelGGL(unit_sums_mfma_kernel<2>, grid, block, 0, s, d_unit6, d_order,
+                           d_chunk_off, d_img, d_Fa, d_Fb, d_Fc, da, db, dc, R, d_sums);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }

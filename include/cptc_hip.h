@@ -636,6 +636,11 @@ int cptc_mttkrp_seg_nd_keys_dims(int nmodes, int mode, const void* d_keys, int k
  * with FP32 shared-memory atomics, generic.cu:447-466). */
 int cptc_units_pack_nd(const uint32_t* d_unit6, uint64_t nunits, const uint32_t* d_lid,
                        const double* d_val, float* d_tiles, void* stream);
+/* The same cells kept in FP64 (nunits x 4096 doubles, d_img 16-byte
+ * aligned; duplicates summed in FP64): the operand of
+ * cptc_gen_unit_sums_img.  No reference counterpart. */
+int cptc_units_pack_nd_f64(const uint32_t* d_unit6, uint64_t nunits, const uint32_t* d_lid,
+                           const double* d_val, double* d_img, void* stream);
 
 /* Per-unit FP64 weights W[u, r] = prod_{k < nouter} F_{outer[k]}[
  * outer_coords[outer_off(u) + k], r] (generic.cu:470-490); W = 1 when
@@ -701,6 +706,14 @@ int cptc_gen_unit_sums(const uint32_t* d_unit6, size_t nunits, const uint32_t* d
                        const double* d_val, const uint32_t* d_order, const uint32_t* d_chunk_off,
                        size_t nchunks, const double* d_Fa, const double* d_Fb, const double* d_Fc,
                        int da, int db, int dc, int R, double* d_sums, void* stream);
+/* cptc_gen_unit_sums from the units' dense FP64 images instead of their
+ * pools (d_img: nunits x 4096 doubles, cell la 256 + lb 16 + lc, as
+ * cptc_units_pack_nd_f64 builds them; 16-byte aligned), on the FP64 matrix
+ * cores: the same sums in another order.  No reference counterpart. */
+int cptc_gen_unit_sums_img(const uint32_t* d_unit6, size_t nunits, const double* d_img,
+                           const uint32_t* d_order, const uint32_t* d_chunk_off, size_t nchunks,
+                           const double* d_Fa, const double* d_Fb, const double* d_Fc, int da,
+                           int db, int dc, int R, double* d_sums, void* stream);
 /* Host: the plan of cptc_gen_unit_sums.  h_order (nunits entries) = the
  * units sorted stably by (bi, bj, bk); chunk c = h_order[h_chunk_off[c] ..
  * h_chunk_off[c + 1]), at most max_chunk units of one (bi, bj, bk);
@@ -783,6 +796,8 @@ typedef struct cptc_gen_info {
     uint64_t unit_segments[3];  /* 16-byte segments of inner slot s's compacted split image */
     int unit_sums;           /* 1 = outer modes' MTTKRP from per-unit sums (every element in a
                                 unit, R <= 32, GEN_UNIT_SUMS not 0), 0 = segment kernel */
+    int unit_sums_img;       /* 1 = those sums from FP64 unit images on the matrix cores
+                                (cptc_gen_unit_sums_img; GEN_UNIT_SUMS_IMG=0: from the pools) */
 } cptc_gen_info;
 
 /* Reorders a copy of `coo`, initialises the factors (mt19937(seed) U[0,1)

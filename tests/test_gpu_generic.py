@@ -768,13 +768,15 @@ def test_config4_full_size(ca, orc, dev):
 
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("N,inner,R", [(4, (0, 1, 2), 16), (5, (0, 1, 2), 16), (5, (1, 2, 3), 16),
-                                     (5, (0, 1, 2), 32), (4, (1, 2, 3), 7)])
+                                     (5, (0, 1, 2), 32), (4, (1, 2, 3), 7), (5, (1, 2, 3), 20)])
 def test_unit_sums_outer_modes(ca, orc, dev, N, inner, R, monkeypatch):
     """Every element in a dense unit (config 5's case): the outer modes'
-    MTTKRP from per-unit inner sums (cptc_gen_unit_sums, then
-    cptc_gen_unit_scatter) against the oracle's FP64 segment sum over all
-    elements (<= 1e-10), and the same with GEN_UNIT_SUMS=0 (the segment
-    kernel); inner modes unchanged (units on the matrix cores, <= 1e-5)."""
+    MTTKRP from per-unit inner sums (from the FP64 unit images on the matrix
+    cores, cptc_gen_unit_sums_img, and with GEN_UNIT_SUMS_IMG=0 from the pools,
+    cptc_gen_unit_sums; then cptc_gen_unit_scatter) against the oracle's FP64
+    segment sum over all elements (<= 1e-10), and the same with
+    GEN_UNIT_SUMS=0 (the segment kernel); inner modes unchanged (units on the
+    matrix cores, <= 1e-5).  R = 7 and 20 pad the rank tiles."""
     rng = np.random.default_rng(30 + N + inner[0])
     dims = (40, 35, 48, 33, 20)[:N]
     t0 = tensor(ca, clustered(rng, dims, inner, 0.5, 8000), dims, rng)
@@ -786,10 +788,13 @@ def test_unit_sums_outer_modes(ca, orc, dev, N, inner, R, monkeypatch):
     assert u6[:, 3].max() > 100   # units of more than 64 elements (several batches)
     t = ca.Tensor(dims, np.ascontiguousarray(t0.idx[:, keep]), np.ascontiguousarray(t0.val[keep]))
     F = [rng.random((d, R)) for d in dims]
-    for flag in ("1", "0"):
+    for flag, img in (("1", "1"), ("1", "0"), ("0", "1")):
         monkeypatch.setenv("GEN_UNIT_SUMS", flag)
+        monkeypatch.setenv("GEN_UNIT_SUMS_IMG", img)
         g = ca.Gen(t, R=R, inner=inner)
         assert g.info.dense_enabled and g.units()["is_dense"].all()
+        assert int(g.info.unit_sums) == int(flag)
+        assert int(g.info.unit_sums_img) == int(flag == "1" and img == "1")
         idx = g.coords()
         for m in range(N):
             g.set_factor(m, F[m])
