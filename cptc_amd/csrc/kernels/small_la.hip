@@ -470,12 +470,20 @@ __global__ __launch_bounds__(PINV_THREADS) void chol_inverse_kernel(const double
 // ---------------------------------------------------------------------------
 constexpr int SWEEP_T = 256;
 
+template <int T>
+__device__ void jacobi_pinv_body(const double* __restrict__ Ain, int R, double* work, double* V,
+                                 double* __restrict__ Ainv, int use_lds, double* lds);
+
+// When the fast path declines, the same workgroup runs the Jacobi
+// pseudoinverse (jacobi_pinv_body with its 256 threads, A in this kernel's
+// LDS, V in `V`), so R <= 64 needs one launch per solve, not two.
 template <int RT>
 __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __restrict__ Ain,
                                                                 int R,
                                                                 double* __restrict__ Ainv,
-                                                                int* fallback)
+                                                                int* fallback, double* V)
 {
+    __shared__ double jA[RT * RT];   // the Jacobi path's A
     constexpr int LPR = SWEEP_T / RT;
     constexpr int C = RT / LPR;
     static_assert(C >= 1 && C <= 16, "sweep layout");
@@ -553,9 +561,11 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
             __syncthreads();
         }
     }
+    // both declines below are uniform over the workgroup
     if (!ok)
     {
         if (tid == 0) *fallback = 1;
+        jacobi_pinv_body<SWEEP_T>(Ain, R, nullptr, V, Ainv, 1, jA);
         return;
     }
     // condition check (fast_inverse_ok); padding entries are 0
@@ -566,6 +576,7 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
     if (!fast_inverse_ok(fro2_A, fro2_inv, R))
     {
         if (tid == 0) *fallback = 1;
+        jacobi_pinv_body<SWEEP_T>(Ain, R, nullptr, V, Ainv, 1, jA);
         return;
     }
     if (tid == 0) *fallback = 0;
@@ -585,17 +596,12 @@ __global__ __launch_bounds__(SWEEP_T) void sweep_inverse_kernel(const double* __
 constexpr int JACOBI_SWEEPS = 15;
 constexpr double JACOBI_TOL = 1e-14;
 
-__global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double* __restrict__ Ain,
-                                                                   int R, double* work,
-                                                                   double* V,
-                                                                   double* __restrict__ Ainv,
-                                                                   const int* fallback,
-                                                                   int use_lds)
+template <int T>
+__device__ void jacobi_pinv_body(const double* __restrict__ Ain, int R, double* work, double* V,
+                                 double* __restrict__ Ainv, int use_lds, double* lds)
 {
-    if (*fallback == 0) return;
-    extern __shared__ double lds[];
     double* A = use_lds ? lds : work;
-    __shared__ double red[PINV_THREADS / WAVE];
+    __shared__ double red[T / WAVE];
     __shared__ double s_off, s_fro;
     __shared__ int pair_p[256], pair_q[256];
     __shared__ double rot_c[256], rot_s[256];
@@ -603,7 +609,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
     const int n2 = R * R;
     const int Rp = R + (R & 1);  // even with a dummy index R when R is odd
     const int npairs = Rp / 2;
-    for (int x = tid; x < n2; x += PINV_THREADS)
+    for (int x = tid; x < n2; x += T)
     {
         A[x] = Ain[x];
         V[x] = ((x / R) == (x % R)) ? 1.0 : 0.0;
@@ -614,13 +620,13 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         if ((tid & (WAVE - 1)) == 0) red[tid / WAVE] = v;
         __syncthreads();
         double t = 0.0;
-        for (int w = 0; w < PINV_THREADS / WAVE; ++w) t += red[w];
+        for (int w = 0; w < T / WAVE; ++w) t += red[w];
         __syncthreads();
         return t;
     };
     {
         double f = 0.0;
-        for (int x = tid; x < n2; x += PINV_THREADS) f += A[x] * A[x];
+        for (int x = tid; x < n2; x += T) f += A[x] * A[x];
         f = block_sum(f);
         if (tid == 0) s_fro = sqrt(f);
     }
@@ -630,7 +636,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
     for (int sweep = 0; sweep < JACOBI_SWEEPS; ++sweep)
     {
         double o = 0.0;
-        for (int x = tid; x < n2; x += PINV_THREADS)
+        for (int x = tid; x < n2; x += T)
             if ((x / R) != (x % R)) o += A[x] * A[x];
         o = block_sum(o);
         if (tid == 0) s_off = sqrt(o);
@@ -639,7 +645,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         for (int round = 0; round < Rp - 1; ++round)
         {
             // round-robin: index 0 fixed, others rotate
-            for (int k = tid; k < npairs; k += PINV_THREADS)
+            for (int k = tid; k < npairs; k += T)
             {
                 auto at = [&](int pos) { return pos == 0 ? 0 : 1 + (pos - 1 + round) % (Rp - 1); };
                 int p = at(k), q = at(Rp - 1 - k);
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
             // row rotation of pair a on the column-rotated values, the same
             // operations on every entry as a pass over all columns followed
             // by a pass over all rows, with one barrier per round fewer
-            for (int x = tid; x < npairs * npairs; x += PINV_THREADS)
+            for (int x = tid; x < npairs * npairs; x += T)
             {
                 const int a = x / npairs, b = x % npairs;
                 const int i0 = pair_p[a], i1 = pair_q[a], j0 = pair_p[b], j1 = pair_q[b];
@@ -709,7 +715,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
             // one memory round trip per VB pairs instead of one per pair
             // (the same operations on every entry as a pair-at-a-time loop)
             constexpr int VB = 8;
-            for (int x0 = 0; x0 < npairs * R; x0 += VB * PINV_THREADS)
+            for (int x0 = 0; x0 < npairs * R; x0 += VB * T)
             {
                 double vp[VB], vq[VB], cc[VB], ss[VB];
                 int ip[VB], iq[VB];
@@ -717,7 +723,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
 #pragma unroll
                 for (int j = 0; j < VB; ++j)
                 {
-                    const int x = x0 + j * PINV_THREADS + tid;
+                    const int x = x0 + j * T + tid;
                     const int k = x / R, r = x % R;
                     on[j] = x < npairs * R;
                     const int kk = on[j] ? k : 0;
@@ -749,7 +755,7 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         s_tol = double(R) * (nextafter(smax, smax + 1.0) - smax);
     }
     __syncthreads();
-    for (int x = tid; x < n2; x += PINV_THREADS)
+    for (int x = tid; x < n2; x += T)
     {
         const int r = x / R, c = x % R;
         double s = 0.0;
@@ -760,6 +766,18 @@ __global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double*
         }
         Ainv[x] = s;
     }
+}
+
+__global__ __launch_bounds__(PINV_THREADS) void jacobi_pinv_kernel(const double* __restrict__ Ain,
+                                                                   int R, double* work,
+                                                                   double* V,
+                                                                   double* __restrict__ Ainv,
+                                                                   const int* fallback,
+                                                                   int use_lds)
+{
+    if (*fallback == 0) return;
+    extern __shared__ double lds[];
+    jacobi_pinv_body<PINV_THREADS>(Ain, R, work, V, Ainv, use_lds, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1373,21 +1391,24 @@ int pinv_launch_ws(const double* d_FtF, double* d_Ainv, int R, int* flag, double
     CPTC_HIP(attr.lds_limit({reinterpret_cast<const void*>(chol_inverse_kernel),
                              reinterpret_cast<const void*>(jacobi_pinv_kernel)},
                             128 * 1024));
+    // R <= 64: the sweep kernel runs its own Jacobi fallback (one launch)
     if (R <= 16)
         hipLaunchKernelGGL(sweep_inverse_kernel<16>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
-                           flag);
+                           flag, V);
     else if (R <= 32)
         hipLaunchKernelGGL(sweep_inverse_kernel<32>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
-                           flag);
+                           flag, V);
     else if (R <= 64)
         hipLaunchKernelGGL(sweep_inverse_kernel<64>, dim3(1), dim3(SWEEP_T), 0, s, d_FtF, R, d_Ainv,
-                           flag);
+                           flag, V);
     else
+    {
         hipLaunchKernelGGL(chol_inverse_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R,
                            work, d_Ainv, flag, int(use_lds));
-    CPTC_LAUNCHED();
-    hipLaunchKernelGGL(jacobi_pinv_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work, V,
-                       d_Ainv, flag, int(use_lds));
+        CPTC_LAUNCHED();
+        hipLaunchKernelGGL(jacobi_pinv_kernel, dim3(1), dim3(PINV_THREADS), lds, s, d_FtF, R, work,
+                           V, d_Ainv, flag, int(use_lds));
+    }
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
