@@ -291,9 +291,10 @@ def main() -> int:
                        if blocked else
                        "mttkrp3_seg_wave_kernel (FP64 residual view, R in (64,128])"
                        if 64 < R <= 128 else
-                       "mttkrp3_seg_kernel (FP64 view of every nonzero: residual + dense pool)"
-                       if merged_fp64 else
-                       "mttkrp3_seg_kernel (FP64 residual view)") + ", per launch = one mode",
+                       ("mttkrp3_seg_lanes_kernel" if R % 2 == 0 and R <= 64
+                        else "mttkrp3_seg_kernel") +
+                       (" (FP64 view of every nonzero: residual + dense pool)" if merged_fp64
+                        else " (FP64 residual view)")) + ", per launch = one mode",
             "bound": "hbm",
             "achieved": round(gather_gbs, 1),
             "peak": HBM_PEAK_GBS,
