@@ -66,22 +66,24 @@ def test_layout_bit_exact(ca, orc, dev, kind, thr):
                     assert np.array_equal(got[k], np.asarray(dv[m][k])), ("dense", m, k)
 
 
-@pytest.mark.parametrize("kind,thr", [("blocks", 0.03), ("blocks", 0.001), ("zipf", 0.03)])
-def test_fp64_merged_view(ca, orc, dev, kind, thr, monkeypatch):
+@pytest.mark.parametrize("kind,thr,R", [("blocks", 0.03, 16), ("blocks", 0.001, 16),
+                                        ("zipf", 0.03, 16), ("blocks", 0.03, 100)])
+def test_fp64_merged_view(ca, orc, dev, kind, thr, R, monkeypatch):
     """FP64-only path with dense tiles and a residual: the kernels read one
     row-sorted view of every nonzero (bit-exact with the oracle's views3 of
     the whole relabelled tensor), its MTTKRP of every mode is within 1e-10 of
     the reference's two views (residual + dense pool, partition.cu:2387-2517),
     and 20 iterations' fits are within 1e-6 of ALS_FP64_MERGE=0, which keeps
     the two launches.  Without tiles or without a residual there is nothing
-    to merge."""
+    to merge.  At R = 100 the FP64 kernel reads the blocked layout built over
+    the merged view."""
     t = make(ca, kind)
     perms, p, v = oracle_layout(orc, t, thr)
     both = len(p["tiles"]) > 0 and len(p["sp_val"]) > 0
-    R = 16
     monkeypatch.delenv("ALS_FP64_MERGE", raising=False)
     with ca.Als3(t, R=R, threshold=thr, path=2) as h:
         assert int(h.info.fp64_merged) == int(both)
+        assert int(h.info.sparse_blocked) == int(R > 64)
         if both:
             idx = np.stack([perms[m][t.idx[m]] for m in range(3)]).astype(np.int32)
             av = orc.views3(idx[0], idx[1], idx[2], t.val, t.dims)

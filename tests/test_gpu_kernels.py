@@ -37,7 +37,7 @@ def zipf_views(ca, orc, dims, nnz, seed, dup=False):
     return t, v
 
 
-@pytest.mark.parametrize("R", [1, 3, 8, 16, 31, 32, 64, 100, 128, 200])
+@pytest.mark.parametrize("R", [1, 2, 3, 6, 8, 10, 16, 31, 32, 48, 64, 100, 128, 200])
 def test_sparse_mttkrp_vs_oracle(ca, orc, dev, R):
     dims = (500, 300, 900)
     t, views = zipf_views(ca, orc, dims, 60000, R, dup=True)
