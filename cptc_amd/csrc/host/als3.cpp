@@ -111,6 +111,9 @@ struct Als3
     double* d_fit_hist = nullptr;
     size_t fit_hist_cap = 0;
     // quiet runs of launch-bound problems replay one captured iteration
+    // bit m: mode m's update is one launch (update3_small); bit 3:
+    // mode C's also forms the fit scalars and clears FtV for mode A
+    int small_upd = 0;
     int graph_mode = 0;                  // 1: replay untimed iterations (ALS_GRAPH / automatic)
     hipGraphExec_t gexec = nullptr;      // the captured steady-state iteration
     uint64_t g_gen = 0;                  // scratch generation it was captured at
@@ -312,6 +315,23 @@ void choose_graph(Als3& h)
     const char* e = std::getenv("ALS_GRAPH");
     if (e) h.graph_mode = std::strcmp(e, "0") != 0 ? 1 : 0;
     else h.graph_mode = double(h.nnz) * double(h.R) < double(1u << 30) ? 1 : 0;
+}
+
+// Small factors (R <= 32, at most UPDATE3_SMALL_MAX_ROWS rows): a mode's
+// apply, Gram, norms, normalisation, scaling and the next mode's FtF in one
+// launch instead of five, and mode C's with the Gram fit and the
+// clearing of FtV for mode A (two launches fewer again).  Config 1 (256^3,
+// R = 32): 0.198 ms per iteration with the separate launches.  The ALS_DEBUG
+// dump reads mode C's MTTKRP after the iteration, so it keeps the separate
+// fit.  ALS_SMALL_UPDATE=0 keeps the separate launches.
+void choose_small_update(Als3& h)
+{
+    h.small_upd = 0;
+    const char* e = std::getenv("ALS_SMALL_UPDATE");
+    if ((e && std::strcmp(e, "0") == 0) || h.R > 32) return;
+    for (int m = 0; m < 3; ++m)
+        if (h.dims[m] >= 1 && h.dims[m] <= UPDATE3_SMALL_MAX_ROWS) h.small_upd |= 1 << m;
+    if ((h.small_upd & 4) && !(h.o.verbose && std::getenv("ALS_DEBUG"))) h.small_upd |= 8;
 }
 
 void choose_overlap(Als3& h)
@@ -562,6 +582,7 @@ int create(const cptc_coo* coo, const cptc_als3_opts* opts, Als3* h)
     CPTC_TRY(build_blk(*h));
     CPTC_TRY(alloc_buffers(*h));
     choose_graph(*h);
+    choose_small_update(*h);
     if (o.verbose && h->fused)
         std::printf("[ALS] FUSED path active: one load-balanced grid (dense MFMA + sparse FP64, "
                     "R=%d)\n", h->R);
@@ -614,10 +635,29 @@ int alloc_buffers(Als3& hr)
     return CPTC_OK;
 }
 
-int update_mode(Als3& h, int mode)
+// d_fit: where the iteration's fit scalars go; *fit_done is set when this
+// update formed them (mode C on the one-launch path).
+int update_mode(Als3& h, int mode, double* d_fit = nullptr, bool* fit_done = nullptr)
 {
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
+    const int next = (mode + 1) % 3, other = 3 - next - mode;
+    if (h.small_upd & (1 << mode))
+    {
+        // one launch: apply, Gram, norms, normalisation, scaling, the next
+        // FtF, the next MTTKRP's cleared FtV and, for mode C, the fit
+        const bool fuse = h.gram_ok[other];
+        const bool fit = mode == 2 && d_fit && (h.small_upd & 8);
+        const size_t nz = (mode < 2 || fit) ? h.dims[next] * size_t(R) : 0;
+        CPTC_TRY(update3_small(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.G(mode), h.d_norms,
+                               h.d_lambda, fuse ? h.G(other) : nullptr, fuse ? h.d_FtF : nullptr,
+                               nz, fit ? h.d_G : nullptr, fit ? d_fit : nullptr, h.s));
+        h.ftf_for = fuse ? next : -1;
+        h.ftv_zero_for = nz ? next : -1;
+        h.gram_ok[mode] = true;
+        if (fit_done) *fit_done = fit;
+        return CPTC_OK;
+    }
     // F = FtV * pinv(FtF) (pinv computed beside the MTTKRP) and divide by
     // lambda; column norms, normalise + absorb and this mode's Gram refresh
     // from one Gram of the unnormalised factor (als.cu:480-517)
@@ -628,7 +668,6 @@ int update_mode(Als3& h, int mode)
     // mode's FtF when its other Gram is current: two launches fewer per mode.
     // R <= 32: the Gram's sums, norms and normalisation in one workgroup, with
     // the next mode's FtF from the same launch.
-    const int next = (mode + 1) % 3, other = 3 - next - mode;
     TailJobs tj;
     if (mode < 2)
     {
@@ -668,6 +707,7 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
     const int R = h.R;
     const size_t RR = size_t(R) * R;
     if (events) CPTC_HIP(hipEventRecord(h.ev_cur[0], h.s));
+    bool fit_done = false;
     for (int mode = 0; mode < 3; ++mode)
     {
         const int p = mode == 0 ? 1 : 0, q = mode == 2 ? 1 : 2;
@@ -682,24 +722,26 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
         if (events) CPTC_HIP(hipEventRecord(h.ev_cur[1 + 2 * mode], h.s));
         CPTC_TRY(mttkrp_launch(h, mode, true));
         if (events) CPTC_HIP(hipEventRecord(h.ev_cur[2 + 2 * mode], h.s));
-        CPTC_TRY(update_mode(h, mode));
+        CPTC_TRY(update_mode(h, mode, d_out, &fit_done));
     }
     // Gram fit (als.cu:659-715); FtV holds mode C's MTTKRP.  ev_cur[8]:
     // mode C's update done (als.cu's t_solve), for the ALS_PROFILE line
     if (events) CPTC_HIP(hipEventRecord(h.ev_cur[8], h.s));
-    CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, d_out, h.s));
+    if (!fit_done)
+        CPTC_TRY(cptc_fit_gram(h.F[2], h.d_FtV, h.dims[2], h.d_lambda, h.d_G, 3, R, d_out, h.s));
     if (events) CPTC_HIP(hipEventRecord(h.ev_cur[7], h.s));
     return CPTC_OK;
 }
 
 // The state an iteration leaves behind and finds: every Gram current, mode
 // 0's FtF formed by mode 2's update and FtV not yet cleared for mode 0 (the
-// fit reads it).  Only an iteration that starts there has the captured
+// fit reads it), or already cleared when mode C's one-launch update formed
+// the fit.  Only an iteration that starts there has the captured
 // iteration's launches.
 bool steady(const Als3& h)
 {
-    return h.gram_ok[0] && h.gram_ok[1] && h.gram_ok[2] &&
-           h.ftf_for == 0 && h.ftv_zero_for == -1;
+    return h.gram_ok[0] && h.gram_ok[1] && h.gram_ok[2] && h.ftf_for == 0 &&
+           h.ftv_zero_for == ((h.small_upd & 8) ? 0 : -1);
 }
 
 // Captures one steady-state iteration (no events, kernel timing off, the
@@ -984,6 +1026,7 @@ int als3_execute(const uint64_t dims[3], const DevPartition3& part, const DevVie
                     "R=%d)\n", R);
     if (rc == CPTC_OK) step(alloc_buffers(*h));
     choose_graph(*h);
+    choose_small_update(*h);
     std::vector<double> fits(static_cast<size_t>(iters > 0 ? iters : 1), 0.0);
     if (rc == CPTC_OK) step(run(*h, iters, fits.data(), nullptr, nullptr));
     if (rc == CPTC_OK)
@@ -1073,6 +1116,7 @@ extern "C" int cptc_als3_info_get(void* handle, cptc_als3_info* info)
     info->graph_captures = h->n_captures;
     info->fp64_merged = h->aviews.ready ? 1 : 0;
     for (int m = 0; m < 3; ++m) info->merged_segments[m] = h->aviews.ready ? h->aviews.nseg[m] : 0;
+    info->small_update = h->small_upd;
     info->tiles_beside = (h->dense_beside && h->use_mfma && h->part.ntiles > 0 && !h->fused) ? 1 : 0;
     return CPTC_OK;
 }

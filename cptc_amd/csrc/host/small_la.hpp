@@ -29,4 +29,12 @@ int gram_normalize_absorb_next_tail(double* d_F, size_t rows, int R, double* d_G
                                     double* d_norms, double* d_lambda, const double* d_other,
                                     double* d_FtF, const TailJobs* t, hipStream_t s);
 
+// cptc_update_small3: a small mode's whole update in one launch
+// (rows <= UPDATE3_SMALL_MAX_ROWS, R <= 32)
+constexpr size_t UPDATE3_SMALL_MAX_ROWS = 4096;
+int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
+                  double* d_G, double* d_norms, double* d_lambda, const double* d_other,
+                  double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
+                  hipStream_t s);
+
 }  // namespace cptc

@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
+#include <cstdlib>
 #include <mutex>
 
 #include "../host/hip_util.hpp"
@@ -1230,6 +1231,593 @@ int scale_launch(double* F, size_t rows, int R, const double* norms, const cptc:
     return CPTC_OK;
 }
 
+// ---------------------------------------------------------------------------
+// A small factor's whole update in one launch (rows <= UPD3_MAX_ROWS, R <=
+// 16 NT <= 32) on the FP64 matrix cores (v_mfma_f64_16x16x4f64), the six
+// launches of apply + Gram + norms + scaling (+ fit) in one:
+//   F = (FtV Ainv) / lambda                      (apply_small_kernel)
+//   G = F^T F; n_r = sqrt(G_rr); lambda_r *= n_r, 0 when n_r < 1e-14;
+//   G_rs /= n_r n_s (0 at a tiny norm); FtF = G .* other when other is given
+//                                                (gram_finish_small_kernel)
+//   F[:, r] /= n_r (0 at a tiny norm)            (scale_columns_kernel)
+// With fit_out (the iteration's last mode), also the Gram fit scalars of
+// fit_finalize_kernel: fit_out[0] = sum_r lambda_r <F[:, r], FtV[:, r]>,
+// fit_out[1] = sum_{r,s} lambda_r lambda_s G_0 G_1 G_2 [r][s] (grams holds
+// G_0 and G_1; G_2 is this launch's G).  Last, Z[0, nz) is cleared (Z is
+// FtV).
+// Stage 1, every workgroup: wave w takes the 16-row block 4 blockIdx + w
+// (and every 4 gridDim-th after it); the apply's accumulator element v of
+// lane l is F[16 b + l / 16 + 4 v][16 t + l % 16], stored unscaled, and it
+// is also the Gram's A operand (F^T, ranks 16 t .. + 15 against rows 16 b +
+// 4 v .. + 3) and B operand, so the Gram partial needs no data movement;
+// the workgroup's Gram (and, for the fit, per-rank <F, FtV>) partial goes
+// to part[blockIdx] after the four waves' sums in wave order.  Stage 2, the
+// workgroup that finishes last (a device counter taken after a release
+// fence; no workgroup waits for another): the partials in workgroup order,
+// the norms, lambda, G, FtF and the fit, then the factor scaled in place
+// and FtV cleared (every workgroup's reads of FtV precede its count).  The
+// last workgroup resets the counter, so launches on one device must not
+// overlap (the library's scratch buffers have the same rule).  The sums run
+// in the matrix cores' order, not the separate kernels'.
+// ---------------------------------------------------------------------------
+// Loads that may be padding are zeroed by an AND with a mask made opaque
+// by an empty asm, not by a select: the compiler turns `cond ? load : 0`
+// into a branch around the load, with a wait of its own per load.
+__device__ __forceinline__ long long upd3_mask(bool keep)
+{
+    long long m = keep ? -1LL : 0LL;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ double upd3_and(double v, long long m)
+{
+    return __longlong_as_double(__double_as_longlong(v) & m);
+}
+// A value as an operand of an empty asm: a load before it cannot be moved
+// past this point (placed where the load has completed anyway).
+__device__ __forceinline__ double upd3_keep(double v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+constexpr int UPD3_T = 256;
+constexpr int UPD3_WAVES = UPD3_T / WAVE;
+constexpr int UPD3_MAX_ROWS = 4096;
+constexpr int UPD3_MAX_P = UPD3_MAX_ROWS / (16 * UPD3_WAVES);   // 64 workgroups
+__device__ unsigned int upd3_count;   // zero at load; the last workgroup resets it
+
+template <int NT>
+__global__ __launch_bounds__(UPD3_T) void update3_small_kernel(
+    const double* Y, const double* __restrict__ Ainv, double* F, int rows, int R,
+    double* __restrict__ G, double* __restrict__ norms, double* lambda,
+    const double* __restrict__ other, double* __restrict__ FtF, double* Z, int nz,
+    const double* __restrict__ grams, double* __restrict__ fit_out, double* part)
+{
+    constexpr int NP = NT * (NT + 1) / 2;   // tile pairs (a <= c) of the Gram
+    constexpr int KS = 4 * NT;              // K steps of 4 over R padded to 16 NT
+    __shared__ double gl[UPD3_WAVES][NP][256];
+    __shared__ double g_s[32][33];
+    __shared__ double n_s[32], lamn_s[32], fit_s[UPD3_WAVES][32];
+    __shared__ double red2[2][UPD3_WAVES];
+    __shared__ int last_s;
+    const int tid = threadIdx.x, w = tid / WAVE, l = tid % WAVE;
+    const int lr = l % 16, lk = l / 16;
+    const int RR = R * R;
+    const int P = int(gridDim.x);
+    const int stride = R * (R + 1);   // one partial: RR Gram entries, then R fit sums
+    // ---- stage 1 -------------------------------------------------------
+    double bop[KS][NT];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            const int k = 4 * kk + lk, c = 16 * t + lr;
+            bop[kk][t] = upd3_and(Ainv[min(k, R - 1) * R + min(c, R - 1)],
+                                  upd3_mask(k < R && c < R));
+        }
+    // (padding columns: any divisor; their entries are not kept)
+    double dv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dv[t] = lambda[min(16 * t + lr, R - 1)];
+    const int nb = (rows + 15) / 16;
+    gram_d4 gacc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) gacc[p] = gram_d4{0.0, 0.0, 0.0, 0.0};
+    double sp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) sp[t] = 0.0;
+    for (int blk = UPD3_WAVES * int(blockIdx.x) + w; blk < nb; blk += UPD3_WAVES * P)
+    {
+        const int row0 = 16 * blk;
+        const int ar = min(row0 + lr, rows - 1);
+        double aop[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+        {
+            const int k = 4 * kk + lk;
+            aop[kk] = upd3_and(Y[size_t(ar) * R + min(k, R - 1)],
+                               upd3_mask(row0 + lr < rows && k < R));
+        }
+        // the fit's FtV entries at the accumulator's positions (loaded on
+        // every path, pinned after the products; used only with fit_out)
+        double ym[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ym[t][v] = Y[size_t(min(row0 + lk + 4 * v, rows - 1)) * R +
+                             min(16 * t + lr, R - 1)];
+        gram_d4 f[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            gram_d4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(aop[kk], bop[kk][t], acc, 0, 0, 0);
+            const int c = 16 * t + lr;
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+            {
+                const int row = row0 + lk + 4 * v;
+                const bool in = row < rows && c < R;
+                const double x = in ? acc[v] / dv[t] : 0.0;
+                f[t][v] = x;
+                if (in) F[size_t(row) * R + c] = x;
+                const double y = upd3_keep(ym[t][v]);
+                if (fit_out) sp[t] += in ? x * y : 0.0;
+            }
+        }
+        int p = 0;
+#pragma unroll
+        for (int a = 0; a < NT; ++a)
+#pragma unroll
+            for (int c = a; c < NT; ++c, ++p)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    gacc[p] = __builtin_amdgcn_mfma_f64_16x16x4f64(f[a][v], f[c][v], gacc[p], 0,
+                                                                   0, 0);
+    }
+    // the workgroup's partial: Gram tiles summed in wave order, the upper
+    // triangle mirrored (exactly symmetric), then the fit's per-rank sums
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gl[w][p][(lk + 4 * v) * 16 + lr] = gacc[p][v];
+    if (fit_out)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            sp[t] += __shfl_xor(sp[t], 16);
+            sp[t] += __shfl_xor(sp[t], 32);
+            if (lk == 0) fit_s[w][16 * t + lr] = sp[t];
+        }
+    __syncthreads();
+    double* my = part + size_t(blockIdx.x) * stride;
+    for (int x = tid; x < NP * 256; x += UPD3_T)
+    {
+        const int p = x / 256, e = x % 256, m = e / 16, n = e % 16;
+        const int a = (p == 2) ? 1 : 0, c = (p == 0) ? 0 : 1;
+        double s = 0.0;
+#pragma unroll
+        for (int q = 0; q < UPD3_WAVES; ++q) s += gl[q][p][e];
+        const int i = 16 * a + m, j = 16 * c + n;
+        if ((a != c || m <= n) && i < R && j < R)
+        {
+            my[i * R + j] = s;
+            my[j * R + i] = s;
+        }
+    }
+    if (fit_out && tid < R)
+    {
+        double s = 0.0;
+#pragma unroll
+        for (int q = 0; q < UPD3_WAVES; ++q) s += fit_s[q][tid];
+        my[RR + tid] = s;
+    }
+    // every thread's stores (factor and partial) visible device-wide, then
+    // one count per workgroup
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last_s = (atomicAdd(&upd3_count, 1u) == unsigned(P - 1)) ? 1 : 0;
+    __syncthreads();
+    if (!last_s) return;
+    // ---- stage 2: the last workgroup --------------------------------------
+    __threadfence();   // acquire: the other workgroups' stores are seen
+    // every load that does not depend on the sums is issued first: the
+    // factor's first SB entries of this thread's column (thread t: column
+    // t % R, rows t / R + k rpp), the next FtF's other Gram and the fit's
+    // two Grams (entries tid + q T, RR <= 4 T)
+    constexpr int SB = 32;
+    const int c0 = tid % R, rpp = UPD3_T / R, r0 = tid / R;
+    double fv[SB];
+#pragma unroll
+    for (int k = 0; k < SB; ++k) fv[k] = F[size_t(min(r0 + k * rpp, rows - 1)) * R + c0];
+    // (a null operand reads the partials instead: valid memory, unused)
+    const double* osrc = other ? other : part;
+    const double* gsrc = fit_out ? grams : part;
+    double ot[4], ga[4], gb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+    {
+        const int xc = min(tid + q * UPD3_T, RR - 1);
+        ot[q] = osrc[xc];
+        ga[q] = gsrc[xc];
+        gb[q] = gsrc[(fit_out ? size_t(RR) : 0) + xc];
+    }
+    // partial sums in workgroup order: the thread's Gram entries tid + q T
+    // (q < 4) and, for tid < R, the fit sum of rank tid; all loads of eight
+    // partials issued together
+    double gs[4] = {0.0, 0.0, 0.0, 0.0}, fsum = 0.0;
+    for (int q0 = 0; q0 < P; q0 += 8)
+    {
+        double v[8][5];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+        {
+            const double* pp = part + size_t(min(q0 + u, P - 1)) * stride;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[u][q] = pp[min(tid + q * UPD3_T, RR - 1)];
+            v[u][4] = pp[RR + min(tid, R - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (q0 + u < P)
+            {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) gs[q] += v[u][q];
+                fsum += fit_out ? v[u][4] : 0.0;
+            }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+    {
+        const int x = tid + q * UPD3_T;
+        if (x < RR) g_s[x / R][x % R] = gs[q];
+    }
+    // the early loads, issued before the partials', have landed: pin them here
+#pragma unroll
+    for (int k = 0; k < SB; ++k) fv[k] = upd3_keep(fv[k]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+    {
+        ot[q] = upd3_keep(ot[q]);
+        ga[q] = upd3_keep(ga[q]);
+        gb[q] = upd3_keep(gb[q]);
+    }
+    __syncthreads();
+    if (tid < R)
+    {
+        const double n = sqrt(g_s[tid][tid]);
+        n_s[tid] = n;
+        norms[tid] = n;
+        const double lm = (n < 1e-14) ? 0.0 : lambda[tid] * n;
+        lamn_s[tid] = lm;
+        lambda[tid] = lm;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+    {
+        const int x = tid + q * UPD3_T;
+        if (x < RR)
+        {
+            const int i = x / R, j = x % R;
+            const double ni = n_s[i], nj = n_s[j];
+            const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : g_s[i][j] / (ni * nj);
+            g_s[i][j] = v;   // each entry read and written by its own thread only
+            G[x] = v;
+            if (other) FtF[x] = v * ot[q];
+        }
+    }
+    // the factor scaled in place, SB rows of the thread's column at a time
+    if (r0 < rpp)
+    {
+        const double n = n_s[c0];
+        const bool zero = n < 1e-14;
+#pragma unroll
+        for (int k = 0; k < SB; ++k)
+        {
+            const int i = r0 + k * rpp;
+            if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
+        }
+        for (int i0 = r0 + SB * rpp; i0 < rows; i0 += SB * rpp)
+        {
+#pragma unroll
+            for (int k = 0; k < SB; ++k) fv[k] = F[size_t(min(i0 + k * rpp, rows - 1)) * R + c0];
+#pragma unroll
+            for (int k = 0; k < SB; ++k)
+            {
+                const int i = i0 + k * rpp;
+                if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
+            }
+        }
+    }
+    if (fit_out)   // uniform (a kernel argument)
+    {
+        // <F[:, r], FtV[:, r]> = <F_unscaled[:, r], FtV[:, r]> / n_r
+        const double ip =
+            (tid < R) ? lamn_s[tid] * (n_s[tid] < 1e-14 ? 0.0 : fsum / n_s[tid]) : 0.0;
+        double md = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const int x = tid + q * UPD3_T;
+            if (x < RR)
+            {
+                const int i = x / R, j = x % R;
+                md += lamn_s[i] * lamn_s[j] * ga[q] * gb[q] * g_s[i][j];
+            }
+        }
+        double ipw = ip, mdw = md;
+#pragma unroll
+        for (int o = WAVE / 2; o >= 1; o >>= 1)
+        {
+            ipw += __shfl_xor(ipw, o);
+            mdw += __shfl_xor(mdw, o);
+        }
+        if (l == 0)
+        {
+            red2[0][w] = ipw;
+            red2[1][w] = mdw;
+        }
+        __syncthreads();
+        if (tid == 0)
+        {
+            double a = 0.0, m2 = 0.0;
+#pragma unroll
+            for (int q = 0; q < UPD3_WAVES; ++q)
+            {
+                a += red2[0][q];
+                m2 += red2[1][q];
+            }
+            fit_out[0] = a;
+            fit_out[1] = m2;
+        }
+    }
+    for (int x = tid; x < nz; x += UPD3_T) Z[x] = 0.0;
+    if (tid == 0) upd3_count = 0u;
+}
+
+// The same update in one workgroup of UPD1_T threads for rows <= 16
+// UPD1_WAVES MAXB: no partials, counter or rescaling pass.  Wave w owns the
+// blocks w, w + UPD1_WAVES, ... and keeps their factor entries in registers
+// from the product to the scaled store; the waves' Gram tiles are summed in
+// wave order.  All matrix-core work runs on one CU, so it is the form for a
+// few hundred rows (two memory round trips instead of five).
+constexpr int UPD1_T = 512;
+constexpr int UPD1_WAVES = UPD1_T / WAVE;
+
+template <int NT, int MAXB>
+__global__ __launch_bounds__(UPD1_T) void update3_one_kernel(
+    const double* Y, const double* __restrict__ Ainv, double* __restrict__ F, int rows, int R,
+    double* __restrict__ G, double* __restrict__ norms, double* __restrict__ lambda,
+    const double* __restrict__ other, double* __restrict__ FtF, double* Z, int nz,
+    const double* __restrict__ grams, double* __restrict__ fit_out)
+{
+    constexpr int NP = NT * (NT + 1) / 2;
+    constexpr int KS = 4 * NT;
+    __shared__ double gl[UPD1_WAVES][NP][256];
+    __shared__ double g_s[32][33];
+    __shared__ double n_s[32], lamn_s[32], fit_s[UPD1_WAVES][32];
+    __shared__ double red2[2][UPD1_WAVES];
+    const int tid = threadIdx.x, w = tid / WAVE, l = tid % WAVE;
+    const int lr = l % 16, lk = l / 16;
+    const int RR = R * R;
+    const int nb = (rows + 15) / 16;
+    double bop[KS][NT];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            const int k = 4 * kk + lk, c = 16 * t + lr;
+            bop[kk][t] = upd3_and(Ainv[min(k, R - 1) * R + min(c, R - 1)],
+                                  upd3_mask(k < R && c < R));
+        }
+    double dv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dv[t] = lambda[min(16 * t + lr, R - 1)];
+    // the next FtF's other Gram and the fit's two Grams (entries tid + q T,
+    // RR <= 2 T); a null operand reads Ainv instead (valid, unused)
+    const double* osrc = other ? other : Ainv;
+    const double* gsrc = fit_out ? grams : Ainv;
+    double ot[2], ga[2], gb[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+    {
+        const int xc = min(tid + q * UPD1_T, RR - 1);
+        ot[q] = osrc[xc];
+        ga[q] = gsrc[xc];
+        gb[q] = gsrc[(fit_out ? size_t(RR) : 0) + xc];
+    }
+    gram_d4 f[MAXB][NT];
+    gram_d4 gacc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) gacc[p] = gram_d4{0.0, 0.0, 0.0, 0.0};
+    // A operands of every block the wave owns, loaded together
+    double aop[MAXB][KS];
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b)
+    {
+        const int row0 = 16 * (w + UPD1_WAVES * b);
+        const int ar = max(0, min(row0 + lr, rows - 1));
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+        {
+            const int k = 4 * kk + lk;
+            aop[b][kk] = upd3_and(Y[size_t(ar) * R + min(k, R - 1)],
+                                  upd3_mask(row0 + lr < rows && k < R));
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b)
+    {
+        const int row0 = 16 * (w + UPD1_WAVES * b);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) f[b][t] = gram_d4{0.0, 0.0, 0.0, 0.0};
+        if (row0 >= rows) continue;   // uniform over the wave
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            gram_d4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(aop[b][kk], bop[kk][t], acc, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                f[b][t][v] =
+                    (row0 + lk + 4 * v < rows && 16 * t + lr < R) ? acc[v] / dv[t] : 0.0;
+        }
+        int p = 0;
+#pragma unroll
+        for (int a = 0; a < NT; ++a)
+#pragma unroll
+            for (int c = a; c < NT; ++c, ++p)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    gacc[p] = __builtin_amdgcn_mfma_f64_16x16x4f64(f[b][a][v], f[b][c][v],
+                                                                   gacc[p], 0, 0, 0);
+    }
+    // the fit's FtV entries at the accumulator positions, in flight during
+    // the Gram's reduction (used only with fit_out)
+    double ym[MAXB][NT][4];
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                ym[b][t][v] = Y[size_t(max(0, min(16 * (w + UPD1_WAVES * b) + lk + 4 * v,
+                                                  rows - 1))) * R +
+                                min(16 * t + lr, R - 1)];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gl[w][p][(lk + 4 * v) * 16 + lr] = gacc[p][v];
+    __syncthreads();
+    for (int x = tid; x < NP * 256; x += UPD1_T)
+    {
+        const int p = x / 256, e = x % 256, m = e / 16, n = e % 16;
+        const int a = (p == 2) ? 1 : 0, c = (p == 0) ? 0 : 1;
+        double s = 0.0;
+#pragma unroll
+        for (int q = 0; q < UPD1_WAVES; ++q) s += gl[q][p][e];
+        if (a != c || m <= n)
+        {
+            g_s[16 * a + m][16 * c + n] = s;
+            g_s[16 * c + n][16 * a + m] = s;
+        }
+    }
+    __syncthreads();
+    if (tid < R)
+    {
+        const double n = sqrt(g_s[tid][tid]);
+        n_s[tid] = n;
+        norms[tid] = n;
+        const double lm = (n < 1e-14) ? 0.0 : lambda[tid] * n;
+        lamn_s[tid] = lm;
+        lambda[tid] = lm;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+    {
+        const int x = tid + q * UPD1_T;
+        if (x < RR)
+        {
+            const int i = x / R, j = x % R;
+            const double ni = n_s[i], nj = n_s[j];
+            const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : g_s[i][j] / (ni * nj);
+            g_s[i][j] = v;   // each entry read and written by its own thread only
+            G[x] = v;
+            if (other) FtF[x] = v * ot[q];
+        }
+    }
+    double nr[NT], sp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+    {
+        nr[t] = (16 * t + lr < R) ? n_s[16 * t + lr] : 1.0;
+        sp[t] = 0.0;
+    }
+#pragma unroll
+    for (int b = 0; b < MAXB; ++b)
+    {
+        const int row0 = 16 * (w + UPD1_WAVES * b);
+        if (row0 >= rows) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+            {
+                const int row = row0 + lk + 4 * v, c = 16 * t + lr;
+                const double x = (nr[t] < 1e-14) ? 0.0 : f[b][t][v] / nr[t];
+                const bool in = row < rows && c < R;
+                if (in) F[size_t(row) * R + c] = x;
+                if (fit_out) sp[t] += in ? x * ym[b][t][v] : 0.0;
+            }
+    }
+    if (fit_out)   // uniform (a kernel argument)
+    {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+        {
+            sp[t] += __shfl_xor(sp[t], 16);
+            sp[t] += __shfl_xor(sp[t], 32);
+            if (lk == 0) fit_s[w][16 * t + lr] = sp[t];
+        }
+        __syncthreads();
+        double ip = 0.0;
+        if (tid < R)
+        {
+            double s = 0.0;
+#pragma unroll
+            for (int q = 0; q < UPD1_WAVES; ++q) s += fit_s[q][tid];
+            ip = lamn_s[tid] * s;
+        }
+        double md = 0.0;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+        {
+            const int x = tid + q * UPD1_T;
+            if (x < RR)
+            {
+                const int i = x / R, j = x % R;
+                md += lamn_s[i] * lamn_s[j] * ga[q] * gb[q] * g_s[i][j];
+            }
+        }
+#pragma unroll
+        for (int o = WAVE / 2; o >= 1; o >>= 1)
+        {
+            ip += __shfl_xor(ip, o);
+            md += __shfl_xor(md, o);
+        }
+        if (l == 0)
+        {
+            red2[0][w] = ip;
+            red2[1][w] = md;
+        }
+        __syncthreads();
+        if (tid == 0)
+        {
+            double a = 0.0, m2 = 0.0;
+#pragma unroll
+            for (int q = 0; q < UPD1_WAVES; ++q)
+            {
+                a += red2[0][q];
+                m2 += red2[1][q];
+            }
+            fit_out[0] = a;
+            fit_out[1] = m2;
+        }
+    }
+    __syncthreads();   // every wave's FtV loads are consumed
+    for (int x = tid; x < nz; x += UPD1_T) Z[x] = 0.0;
+}
+
 int partials_for(size_t rows, size_t min_rows)
 {
     size_t p = (rows + min_rows - 1) / min_rows;
@@ -1339,7 +1927,68 @@ int gram_normalize_absorb_next_tail(double* d_F, size_t rows, int R, double* d_G
     return scale_launch(d_F, rows, R, d_norms, t, s);
 }
 
+int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
+                  double* d_G, double* d_norms, double* d_lambda, const double* d_other,
+                  double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
+                  hipStream_t s)
+{
+    CPTC_REQUIRE(R >= 1 && R <= 32 && rows >= 1 && rows <= UPDATE3_SMALL_MAX_ROWS,
+                 CPTC_ERR_ARG, "cptc_update_small3: rows %zu R %d (1..%zu rows, R <= 32)", rows,
+                 R, UPDATE3_SMALL_MAX_ROWS);
+    CPTC_REQUIRE(d_FtV && d_Ainv && d_F && d_G && d_norms && d_lambda &&
+                     (d_other == nullptr) == (d_FtF == nullptr) && (!d_fit || d_grams) &&
+                     nzero < (size_t(1) << 31),
+                 CPTC_ERR_ARG, "cptc_update_small3: bad arguments");
+    static_assert(UPDATE3_SMALL_MAX_ROWS == size_t(UPD3_MAX_ROWS), "row limit");
+    const int nb = int((rows + 15) / 16);
+    const int P = (nb + UPD3_WAVES - 1) / UPD3_WAVES;   // one 16-row block per wave
+    void* buf = nullptr;
+    CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(UPD3_MAX_P) * 32 * (32 + 1) * sizeof(double),
+                               &buf));
+    double* part = static_cast<double*>(buf);
+    const int nr = int(rows), nz = int(nzero);
+    // one workgroup up to 256 rows, the multi-workgroup form above that
+    // (CPTC_UPD3_ONE_ROWS overrides the limit, at most 512; 0 = never).
+    // Per launch at R = 32: 256 rows 13.0 us in one workgroup against 15.0
+    // in four; 512 rows 22.0 us against 19.2 in eight.
+    static const int one_rows = [] {
+        const char* e = std::getenv("CPTC_UPD3_ONE_ROWS");
+        return e ? std::atoi(e) : 256;
+    }();
+    if (nr <= one_rows && nr <= 16 * UPD1_WAVES * 4)
+    {
+        const bool two = nr <= 16 * UPD1_WAVES * 2;
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, dim3(1), dim3(UPD1_T), 0, s, d_FtV, d_Ainv, d_F, nr, R, d_G,
+                               d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams, d_fit);
+        };
+        if (R <= 16) two ? go(update3_one_kernel<1, 2>) : go(update3_one_kernel<1, 4>);
+        else two ? go(update3_one_kernel<2, 2>) : go(update3_one_kernel<2, 4>);
+        CPTC_LAUNCHED();
+        return CPTC_OK;
+    }
+    if (R <= 16)
+        hipLaunchKernelGGL(update3_small_kernel<1>, dim3(P), dim3(UPD3_T), 0, s, d_FtV, d_Ainv,
+                           d_F, nr, R, d_G, d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams,
+                           d_fit, part);
+    else
+        hipLaunchKernelGGL(update3_small_kernel<2>, dim3(P), dim3(UPD3_T), 0, s, d_FtV, d_Ainv,
+                           d_F, nr, R, d_G, d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams,
+                           d_fit, part);
+    CPTC_LAUNCHED();
+    return CPTC_OK;
+}
+
 }  // namespace cptc
+
+extern "C" int cptc_update_small3(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows,
+                                  int R, double* d_G, double* d_norms, double* d_lambda,
+                                  const double* d_other, double* d_FtF, size_t nzero,
+                                  const double* d_grams, double* d_fit, void* stream)
+{
+    return cptc::update3_small(d_FtV, d_Ainv, d_F, rows, R, d_G, d_norms, d_lambda, d_other,
+                               d_FtF, nzero, d_grams, d_fit, cptc::as_stream(stream));
+}
 
 extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G,
                                           double* d_norms, double* d_lambda, void* stream)

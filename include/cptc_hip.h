@@ -263,6 +263,24 @@ int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G
                                     double* d_norms, double* d_lambda, const double* d_other,
                                     double* d_FtF, void* stream);
 
+/* One mode's whole update for a small factor in one launch (1 <= rows <=
+ * 4096, R <= 32; FP64 matrix cores): F = (d_FtV * d_Ainv) /
+ * lambda (cptc_apply_pinv's product with d_Ainv = pinv(FtF) given), then
+ * cptc_gram_normalize_absorb_next on it (G, norms, lambda, F scaled, the
+ * next FtF = G .* d_other when d_other / d_FtF are given), then
+ * d_FtV[0, nzero) = 0 (the next MTTKRP's output; d_FtV is read before).
+ * With d_fit (and d_grams = G_0, G_1 of an order-3 model, this call's G
+ * being G_2), also the Gram fit scalars of cptc_fit_gram over the new
+ * factor and d_FtV: d_fit[0] = iprod, d_fit[1] = model^2.  Results equal
+ * the separate calls' up to summation order (als.cu:480-517, 659-715).
+ * Uses the library's Gram scratch and a device counter: calls that overlap
+ * on one GPU race.  No reference counterpart: the reference runs these as
+ * separate kernels. */
+int cptc_update_small3(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
+                       double* d_G, double* d_norms, double* d_lambda, const double* d_other,
+                       double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
+                       void* stream);
+
 /* C = A o B elementwise over n doubles (C may alias A or B).
  * Replaces elementwise_mult_kernel (als.cu:101-106) and g_mul_kernel
  * (generic.cu:50-88). */
@@ -484,6 +502,9 @@ typedef struct cptc_als3_info {
                                  one row-sorted view: one FP64 launch per mode, and the
                                  per-mode sparse kernel time covers every nonzero */
     uint64_t merged_segments[3];  /* segments of that view per mode (0: none) */
+    int small_update;         /* bit m: mode m's update runs as one launch
+                                 (cptc_update_small3; R <= 32, at most 4096 rows); bit 3:
+                                 mode C's launch also forms the Gram fit scalars */
 } cptc_als3_info;
 int cptc_als3_info_get(void* handle, cptc_als3_info* info);
 

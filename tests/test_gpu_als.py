@@ -366,6 +366,50 @@ def test_graph_replay_matches_eager(ca, dev, kind, R, path, fused, monkeypatch):
             h.close()
 
 
+@pytest.mark.parametrize("kind,R,bits", [("clustered", 32, 15), ("clustered", 5, 15),
+                                         ("zipf", 16, 15), ("zipf_wide", 16, 3),
+                                         ("zipf", 33, 0)])
+def test_small_update_matches_separate_launches(ca, dev, kind, R, bits, monkeypatch):
+    """The one-launch update (cptc_update_small3: every mode of at most 4096
+    rows at R <= 32, bit 3 = mode C's launch also forms the fit) against
+    ALS_SMALL_UPDATE=0, which runs the separate apply, Gram, scaling and fit
+    launches, from the same factors: 3 iterations, eager and replayed from
+    the captured graph, within test_graph_replay_matches_eager's bounds
+    (fits 1e-8, factors 1e-6: the MTTKRP's atomic order and the new sums'
+    order differ at 1e-16 and ALS amplifies that; a missing clear of FtV or
+    a stale FtF shows at 1e-3 and more).  zipf_wide's mode C has 5000 rows,
+    so modes A and B take the one launch and mode C the separate ones."""
+    if kind == "zipf_wide":
+        t = ca.synth_zipf((700, 400, 5000), (1.1, 1.1, 1.1), 120000, 0, 5)
+    else:
+        t = make(ca, kind, 5)
+    hs = {}
+    for key, small, g in (("base", "0", "0"), ("eager", "1", "0"), ("graph", "1", "1")):
+        monkeypatch.setenv("ALS_SMALL_UPDATE", small)
+        monkeypatch.setenv("ALS_GRAPH", g)
+        hs[key] = ca.Als3(t, R=R, threshold=0.03, path=1)
+        assert int(hs[key].info.small_update) == (0 if small == "0" else bits)
+    monkeypatch.delenv("ALS_SMALL_UPDATE")
+    try:
+        F = [hs["base"].factor(m) for m in range(3)]
+        for rnd in range(2):
+            out = {}
+            for key, h in hs.items():
+                for m in range(3):
+                    h.set_factor(m, F[m])
+                fit, _, _ = h.run(3)
+                out[key] = (fit, [h.factor(m) for m in range(3)])
+                h.mttkrp(2)
+            for key in ("eager", "graph"):
+                assert np.max(np.abs(out[key][0] - out["base"][0])) <= 1e-8, (key, rnd)
+                for a_, b_ in zip(out[key][1], out["base"][1]):
+                    assert rel_err(a_, b_) <= 1e-6, (key, rnd)
+            F = [f * 0.9 for f in out["base"][1]]
+    finally:
+        for h in hs.values():
+            h.close()
+
+
 def test_graph_recaptured_after_scratch_growth(ca, dev, monkeypatch):
     """A captured iteration holds the addresses of the library's scratch
     buffers (Gram partials, pseudoinverse workspace, reduction partials).

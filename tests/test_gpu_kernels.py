@@ -664,6 +664,87 @@ def test_gram_normalize_absorb_next(ca, dev, R, rows):
                                                   stream(ca)) != 0
 
 
+@pytest.mark.parametrize("R,rows", [(1, 1), (5, 17), (16, 256), (17, 15), (20, 513),
+                                    (31, 1000), (32, 256), (32, 257), (32, 512), (32, 1024),
+                                    (3, 129), (32, 4096), (7, 3001), (24, 70), (9, 200)])
+def test_update_small3_matches_steps(ca, dev, R, rows):
+    """cptc_update_small3 (FP64 matrix cores; up to 256 rows one workgroup
+    keeps the factor in registers, above that one 16-row block per wave and
+    the last workgroup to finish sums the partials and scales) against the
+    separate calls it replaces: cptc_apply_pinv with lambda, then
+    cptc_gram_normalize_absorb_next with the next FtF, then cptc_fit_gram on
+    the new factor with grams (G_0, G_1, this G).  Factor, norms, lambda, G
+    and FtF within 1e-13 (relative, 2-norm), the fit scalars within 1e-12:
+    the sums run in another order; a dropped block, column or rank term
+    shows at 1e-2 and more.  A zero column of Ainv gives a zero column of F
+    (norm < 1e-14): F, lambda and the Gram's row and column are exactly 0.
+    FtV[0, nzero) is cleared after its reads and the rest is untouched; a
+    second call without the fit and the next FtF leaves fit and FtF alone.
+    Sizes past 4096 rows or R = 33 are refused.  Two calls in a row check
+    that the workgroup counter is left at zero."""
+    rng = np.random.default_rng(R * 1000 + rows)
+    Y = rng.standard_normal((rows, R))
+    A = rng.standard_normal((R, R))
+    A = A + A.T
+    zc = 2 if R > 2 else None
+    if zc is not None:
+        A[:, zc] = 0.0
+    lam = rng.random(R) + 0.1
+    other = rng.standard_normal((R, R))
+    g01 = rng.random((2, R, R))
+    dY, dA, do = to_dev(ca, Y), to_dev(ca, A), to_dev(ca, other)
+    # the separate calls
+    a_F, a_l = zeros(ca, (rows, R)), to_dev(ca, lam)
+    n1, G1, H1, out1 = zeros(ca, (R,)), zeros(ca, (R, R)), zeros(ca, (R, R)), zeros(ca, (2,))
+    assert ca.lib.cptc_apply_pinv(dY.data_ptr(), dA.data_ptr(), a_F.data_ptr(), rows, R,
+                                  a_l.data_ptr(), stream(ca)) == 0
+    assert ca.lib.cptc_gram_normalize_absorb_next(a_F.data_ptr(), rows, R, G1.data_ptr(),
+                                                  n1.data_ptr(), a_l.data_ptr(), do.data_ptr(),
+                                                  H1.data_ptr(), stream(ca)) == 0
+    ca.sync()
+    g3 = to_dev(ca, np.concatenate([g01.ravel(), G1.numpy().ravel()]))
+    assert ca.lib.cptc_fit_gram(a_F.data_ptr(), dY.data_ptr(), rows, a_l.data_ptr(),
+                                g3.data_ptr(), 3, R, out1.data_ptr(), stream(ca)) == 0
+    # one launch; FtV in a longer buffer, cleared over nzero entries
+    extra = 40
+    Yb = np.concatenate([Y.ravel(), np.full(extra, 7.0)])
+    nzero = rows * R + extra // 2
+    dYb = to_dev(ca, Yb)
+    b_F, b_l = zeros(ca, (rows, R)), to_dev(ca, lam)
+    n2, G2, H2, out2 = zeros(ca, (R,)), zeros(ca, (R, R)), zeros(ca, (R, R)), zeros(ca, (2,))
+    g01d = to_dev(ca, g01)
+    rc = ca.lib.cptc_update_small3(dYb.data_ptr(), dA.data_ptr(), b_F.data_ptr(), rows, R,
+                                   G2.data_ptr(), n2.data_ptr(), b_l.data_ptr(), do.data_ptr(),
+                                   H2.data_ptr(), nzero, g01d.data_ptr(), out2.data_ptr(),
+                                   stream(ca))
+    assert rc == 0, ca.lib.cptc_last_error()
+    ca.sync()
+    for got, ref in ((b_F, a_F), (n2, n1), (b_l, a_l), (G2, G1), (H2, H1)):
+        assert rel_err(got.numpy(), ref.numpy()) <= 1e-13
+    o1, o2 = out1.numpy(), out2.numpy()
+    assert abs(o2[0] - o1[0]) <= 1e-12 * abs(o1[0]) and abs(o2[1] - o1[1]) <= 1e-12 * abs(o1[1])
+    if zc is not None:
+        assert np.all(b_F.numpy()[:, zc] == 0.0) and b_l.numpy()[zc] == 0.0
+        assert np.all(G2.numpy()[zc] == 0.0) and np.all(G2.numpy()[:, zc] == 0.0)
+    assert np.array_equal(G2.numpy(), G2.numpy().T)
+    yb = dYb.numpy()
+    assert np.all(yb[:nzero] == 0.0) and np.all(yb[nzero:] == 7.0)
+    # without fit, next FtF or clearing: those outputs are left alone
+    dY2 = to_dev(ca, Y)
+    c_l = to_dev(ca, lam)
+    n3, G3 = zeros(ca, (R,)), zeros(ca, (R, R))
+    assert ca.lib.cptc_update_small3(dY2.data_ptr(), dA.data_ptr(), b_F.data_ptr(), rows, R,
+                                     G3.data_ptr(), n3.data_ptr(), c_l.data_ptr(), None, None, 0,
+                                     None, None, stream(ca)) == 0
+    ca.sync()
+    assert rel_err(b_F.numpy(), a_F.numpy()) <= 1e-13
+    assert np.array_equal(G3.numpy(), G2.numpy()) and np.array_equal(dY2.numpy(), Y)
+    for bad_rows, bad_R in ((4097, R), (rows, 33), (0, R)):
+        assert ca.lib.cptc_update_small3(dY2.data_ptr(), dA.data_ptr(), b_F.data_ptr(), bad_rows,
+                                         bad_R, G3.data_ptr(), n3.data_ptr(), c_l.data_ptr(),
+                                         None, None, 0, None, None, stream(ca)) != 0
+
+
 @pytest.mark.parametrize("R", [1, 7, 32, 100])
 def test_sparse_mttkrp_range(ca, orc, dev, R):
     """compute_sparse_mttkrp_async's sub-range path (sparse.cu:877-955):
