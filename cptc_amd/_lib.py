@@ -165,7 +165,7 @@ SIGNATURES = {
     "cptc_zero": (_I, [_P, _Z, _P]),
     "cptc_gram_normalize_absorb_next": (_I, [_P, _Z, _I, _P, _P, _P, _P, _P, _P]),
     "cptc_hadamard": (_I, [_P, _P, _P, _Z, _P]),
-    "cptc_update_small3": (_I, [_P, _P, _P, _Z, _I, _P, _P, _P, _P, _P, _Z, _P, _P, _P]),
+    "cptc_update_small3": (_I, [_P, _P, _P, _Z, _I, _P, _P, _P, _P, _P, _Z, _P, _P, _I, _P]),
     "cptc_solve_pinv": (_I, [_P, _P, _P, _Z, _I, _P, _P]),
     "cptc_mttkrp_sparse3_blk": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _P, _P, _I,
                                      C.c_uint64, C.c_uint64, _P]),

@@ -93,6 +93,7 @@ struct Als3
     double* d_G = nullptr;  // 3 x R x R
     bool gram_ok[3] = {false, false, false};
     int ftf_for = -1;   // the mode whose FtF (Hadamard of the other Grams) is in d_FtF
+    int ainv_for = -1;  // the mode whose pinv(FtF) is already in d_Ainv
     int ftv_zero_for = -1;   // the mode whose MTTKRP finds d_FtV already cleared
     double* d_FtF = nullptr;
     double* d_Ainv = nullptr;  // pinv(FtF) of the mode being updated
@@ -129,12 +130,14 @@ struct Als3
 };
 
 // FtV = MTTKRP of `mode`; with_pinv also writes pinv(FtF) to d_Ainv (FtF
-// must already hold the mode's Hadamard product).  Everything is ordered
-// on the main stream when this returns.
+// must already hold the mode's Hadamard product) unless the previous mode's
+// one-launch update formed it already.  Everything is ordered on the main
+// stream when this returns.
 int mttkrp_launch(Als3& h, int mode, bool with_pinv)
 {
     const int R = h.R;
     const uint64_t dim = h.dims[mode];
+    if (with_pinv && h.ainv_for == mode) with_pinv = false;
     // a kernel, not hipMemsetAsync: the iteration may be captured in a HIP
     // graph; skipped when the previous mode's update cleared it (TailJobs)
     if (h.ftv_zero_for != mode) CPTC_TRY(cptc_zero(h.d_FtV, dim * size_t(R), h.s));
@@ -651,8 +654,10 @@ int update_mode(Als3& h, int mode, double* d_fit = nullptr, bool* fit_done = nul
         const size_t nz = (mode < 2 || fit) ? h.dims[next] * size_t(R) : 0;
         CPTC_TRY(update3_small(h.d_FtV, h.d_Ainv, h.F[mode], dim, R, h.G(mode), h.d_norms,
                                h.d_lambda, fuse ? h.G(other) : nullptr, fuse ? h.d_FtF : nullptr,
-                               nz, fit ? h.d_G : nullptr, fit ? d_fit : nullptr, h.s));
+                               nz, fit ? h.d_G : nullptr, fit ? d_fit : nullptr, fuse ? 1 : 0,
+                               h.s));
         h.ftf_for = fuse ? next : -1;
+        h.ainv_for = fuse ? next : -1;   // the launch also formed pinv(FtF)
         h.ftv_zero_for = nz ? next : -1;
         h.gram_ok[mode] = true;
         if (fit_done) *fit_done = fit;
@@ -668,6 +673,7 @@ int update_mode(Als3& h, int mode, double* d_fit = nullptr, bool* fit_done = nul
     // mode's FtF when its other Gram is current: two launches fewer per mode.
     // R <= 32: the Gram's sums, norms and normalisation in one workgroup, with
     // the next mode's FtF from the same launch.
+    h.ainv_for = -1;
     TailJobs tj;
     if (mode < 2)
     {
@@ -717,7 +723,11 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
                 CPTC_TRY(cptc_gram(h.F[g], h.dims[g], R, h.G(g), h.s));
                 h.gram_ok[g] = true;
             }
-        if (h.ftf_for != mode) CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+        if (h.ftf_for != mode)
+        {
+            CPTC_TRY(cptc_hadamard(h.G(p), h.G(q), h.d_FtF, RR, h.s));
+            h.ainv_for = -1;
+        }
         h.ftf_for = -1;
         if (events) CPTC_HIP(hipEventRecord(h.ev_cur[1 + 2 * mode], h.s));
         CPTC_TRY(mttkrp_launch(h, mode, true));
@@ -736,12 +746,13 @@ int enqueue_iteration(Als3& h, double* d_out, bool events = true)
 // The state an iteration leaves behind and finds: every Gram current, mode
 // 0's FtF formed by mode 2's update and FtV not yet cleared for mode 0 (the
 // fit reads it), or already cleared when mode C's one-launch update formed
-// the fit.  Only an iteration that starts there has the captured
-// iteration's launches.
+// the fit, and mode 0's pinv formed by that launch too.  Only an iteration
+// that starts there has the captured iteration's launches.
 bool steady(const Als3& h)
 {
     return h.gram_ok[0] && h.gram_ok[1] && h.gram_ok[2] && h.ftf_for == 0 &&
-           h.ftv_zero_for == ((h.small_upd & 8) ? 0 : -1);
+           h.ftv_zero_for == ((h.small_upd & 8) ? 0 : -1) &&
+           h.ainv_for == ((h.small_upd & 4) ? 0 : -1);
 }
 
 // Captures one steady-state iteration (no events, kernel timing off, the
@@ -762,6 +773,7 @@ int capture_iteration(Als3& h, double* d_out)
     {
         if (g) (void)hipGraphDestroy(g);
         h.ftf_for = -1;   // nothing ran: the next iteration forms its FtF itself
+        h.ainv_for = -1;
         h.ftv_zero_for = -1;
         return rc;
     }
@@ -1160,6 +1172,7 @@ extern "C" int cptc_als3_sgd(void* handle, int iters, double gamma, uint32_t bat
                                  h->o.verbose, batch_rmse, h->s);
     for (bool& g : h->gram_ok) g = false;   // the factors changed
     h->ftf_for = -1;
+    h->ainv_for = -1;
     h->ftv_zero_for = -1;
     return rc;
 }
@@ -1274,6 +1287,7 @@ extern "C" int cptc_als3_set_factor(void* handle, int mode, const double* host_i
     CPTC_HIP(hipStreamSynchronize(h->s));
     h->gram_ok[mode] = false;
     h->ftf_for = -1;
+    h->ainv_for = -1;
     h->ftv_zero_for = -1;
     return CPTC_OK;
 }

@@ -32,9 +32,9 @@ int gram_normalize_absorb_next_tail(double* d_F, size_t rows, int R, double* d_G
 // cptc_update_small3: a small mode's whole update in one launch
 // (rows <= UPDATE3_SMALL_MAX_ROWS, R <= 32)
 constexpr size_t UPDATE3_SMALL_MAX_ROWS = 4096;
-int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
-                  double* d_G, double* d_norms, double* d_lambda, const double* d_other,
-                  double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
+int update3_small(double* d_FtV, double* d_Ainv, double* d_F, size_t rows, int R, double* d_G,
+                  double* d_norms, double* d_lambda, const double* d_other, double* d_FtF,
+                  size_t nzero, const double* d_grams, double* d_fit, int next_pinv,
                   hipStream_t s);
 
 }  // namespace cptc

@@ -1281,6 +1281,88 @@ __device__ __forceinline__ double upd3_keep(double v)
     return v;
 }
 
+// The pinv fast path of sweep_inverse_kernel run by one wave, with no
+// workgroup barrier (the rest of the workgroup does other work meanwhile):
+// A (R x R, row stride ld) read from LDS, lane l keeps row l % RT, columns
+// C (l / RT) .. + C - 1 (C = RT^2 / 64), the pivot column goes through the
+// LDS row colb (a wave's LDS accesses run in order).  Per entry the same
+// operations as sweep_inverse_kernel, so an accepted inverse is the same
+// bits.  Returns 1 with -(swept A) = A^-1 stored to Ainv, or 0 when a pivot
+// is <= 1e-10 max diag (or not finite) or fast_inverse_ok fails: the
+// caller then runs the Jacobi pseudoinverse.  Uniform over the wave.
+template <int RT>
+__device__ int sweep_wave(const double* As, int ld, int R, double* __restrict__ Ainv,
+                          double* colb)
+{
+    constexpr int LPR = WAVE / RT;
+    constexpr int C = RT / LPR;
+    const int l = int(threadIdx.x) % WAVE;
+    const int row = l % RT, part = l / RT, c0 = part * C;
+    double a[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) a[c] = (row < R && c0 + c < R) ? As[row * ld + c0 + c] : 0.0;
+    double md = 0.0, fa = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+    {
+        if (c0 + c == row) md = a[c];
+        fa += a[c] * a[c];
+    }
+#pragma unroll
+    for (int o = WAVE / 2; o >= 1; o >>= 1)
+    {
+        md = fmax(md, __shfl_xor(md, o));
+        fa += __shfl_xor(fa, o);
+    }
+    const double tau = 1e-10 * md;
+    int ok = (md > 0.0 && isfinite(md)) ? 1 : 0;
+#pragma unroll 1
+    for (int kp = 0; kp < LPR && kp * C < R && ok; ++kp)
+    {
+#pragma unroll
+        for (int kc = 0; kc < C; ++kc)
+        {
+            const int k = kp * C + kc;
+            if (k >= R || !ok) continue;   // uniform
+            if (part == kp) colb[row] = a[kc];
+            __builtin_amdgcn_wave_barrier();
+            const double p = colb[k];
+            if (!(p > tau) || !isfinite(p))
+            {
+                ok = 0;
+                continue;
+            }
+            const double ip = 1.0 / p;
+            const double f = colb[row] * ip;
+            const bool prow = row == k;
+            const double g = prow ? 0.0 : f;
+            const double h = prow ? ip : 1.0;
+            double cj[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) cj[c] = colb[c0 + c];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+            {
+                const double up = fma(-g, cj[c], a[c] * h);
+                a[c] = (c == kc && part == kp) ? (prow ? -ip : f) : up;
+            }
+        }
+    }
+    if (!ok) return 0;
+    double fi = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) fi += a[c] * a[c];
+#pragma unroll
+    for (int o = WAVE / 2; o >= 1; o >>= 1) fi += __shfl_xor(fi, o);
+    if (!fast_inverse_ok(fa, fi, R)) return 0;
+    if (row < R)
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (c0 + c < R) Ainv[size_t(row) * R + c0 + c] = -a[c];
+    return 1;
+}
+
 constexpr int UPD3_T = 256;
 constexpr int UPD3_WAVES = UPD3_T / WAVE;
 constexpr int UPD3_MAX_ROWS = 4096;
@@ -1292,15 +1374,16 @@ __global__ __launch_bounds__(UPD3_T) void update3_small_kernel(
     const double* Y, const double* __restrict__ Ainv, double* F, int rows, int R,
     double* __restrict__ G, double* __restrict__ norms, double* lambda,
     const double* __restrict__ other, double* __restrict__ FtF, double* Z, int nz,
-    const double* __restrict__ grams, double* __restrict__ fit_out, double* part)
+    const double* __restrict__ grams, double* __restrict__ fit_out, double* part,
+    double* __restrict__ Anext, double* __restrict__ Vw)
 {
     constexpr int NP = NT * (NT + 1) / 2;   // tile pairs (a <= c) of the Gram
     constexpr int KS = 4 * NT;              // K steps of 4 over R padded to 16 NT
     __shared__ double gl[UPD3_WAVES][NP][256];
-    __shared__ double g_s[32][33];
-    __shared__ double n_s[32], lamn_s[32], fit_s[UPD3_WAVES][32];
-    __shared__ double red2[2][UPD3_WAVES];
-    __shared__ int last_s;
+    __shared__ double g_s[32][33], f_s[32][33];
+    __shared__ double n_s[32], lamn_s[32], fit_s[UPD3_WAVES][32], fs_s[32], colb[32];
+    __shared__ double red2[UPD3_WAVES];
+    __shared__ int last_s, decl_s;
     const int tid = threadIdx.x, w = tid / WAVE, l = tid % WAVE;
     const int lr = l % 16, lk = l / 16;
     const int RR = R * R;
@@ -1427,11 +1510,15 @@ __global__ __launch_bounds__(UPD3_T) void update3_small_kernel(
     // ---- stage 2: the last workgroup --------------------------------------
     __threadfence();   // acquire: the other workgroups' stores are seen
     // every load that does not depend on the sums is issued first: the
-    // factor's first SB entries of this thread's column (thread t: column
-    // t % R, rows t / R + k rpp), the next FtF's other Gram and the fit's
+    // factor's first SB entries of this thread's column (scaling thread t:
+    // column t % R, rows t / R + k rpp; with Anext wave 0 runs the sweep
+    // instead and waves 1.. scale), the next FtF's other Gram and the fit's
     // two Grams (entries tid + q T, RR <= 4 T)
     constexpr int SB = 32;
-    const int c0 = tid % R, rpp = UPD3_T / R, r0 = tid / R;
+    const int nsc = Anext ? UPD3_T - WAVE : UPD3_T;
+    const int st = Anext ? tid - WAVE : tid;
+    const int stc = st < 0 ? 0 : st;
+    const int c0 = stc % R, rpp = nsc / R, r0 = stc / R;
     double fv[SB];
 #pragma unroll
     for (int k = 0; k < SB; ++k) fv[k] = F[size_t(min(r0 + k * rpp, rows - 1)) * R + c0];
@@ -1509,37 +1596,19 @@ __global__ __launch_bounds__(UPD3_T) void update3_small_kernel(
             const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : g_s[i][j] / (ni * nj);
             g_s[i][j] = v;   // each entry read and written by its own thread only
             G[x] = v;
-            if (other) FtF[x] = v * ot[q];
-        }
-    }
-    // the factor scaled in place, SB rows of the thread's column at a time
-    if (r0 < rpp)
-    {
-        const double n = n_s[c0];
-        const bool zero = n < 1e-14;
-#pragma unroll
-        for (int k = 0; k < SB; ++k)
-        {
-            const int i = r0 + k * rpp;
-            if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
-        }
-        for (int i0 = r0 + SB * rpp; i0 < rows; i0 += SB * rpp)
-        {
-#pragma unroll
-            for (int k = 0; k < SB; ++k) fv[k] = F[size_t(min(i0 + k * rpp, rows - 1)) * R + c0];
-#pragma unroll
-            for (int k = 0; k < SB; ++k)
+            if (other)
             {
-                const int i = i0 + k * rpp;
-                if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
+                const double h = v * ot[q];
+                FtF[x] = h;
+                f_s[i][j] = h;
             }
         }
     }
     if (fit_out)   // uniform (a kernel argument)
     {
-        // <F[:, r], FtV[:, r]> = <F_unscaled[:, r], FtV[:, r]> / n_r
-        const double ip =
-            (tid < R) ? lamn_s[tid] * (n_s[tid] < 1e-14 ? 0.0 : fsum / n_s[tid]) : 0.0;
+        // <F[:, r], FtV[:, r]> = <F_unscaled[:, r], FtV[:, r]> / n_r for the
+        // fit wave, and this thread's share of model^2, per wave
+        if (tid < R) fs_s[tid] = (n_s[tid] < 1e-14) ? 0.0 : fsum / n_s[tid];
         double md = 0.0;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -1551,33 +1620,66 @@ __global__ __launch_bounds__(UPD3_T) void update3_small_kernel(
                 md += lamn_s[i] * lamn_s[j] * ga[q] * gb[q] * g_s[i][j];
             }
         }
-        double ipw = ip, mdw = md;
 #pragma unroll
-        for (int o = WAVE / 2; o >= 1; o >>= 1)
-        {
-            ipw += __shfl_xor(ipw, o);
-            mdw += __shfl_xor(mdw, o);
-        }
-        if (l == 0)
-        {
-            red2[0][w] = ipw;
-            red2[1][w] = mdw;
-        }
-        __syncthreads();
-        if (tid == 0)
-        {
-            double a = 0.0, m2 = 0.0;
-#pragma unroll
-            for (int q = 0; q < UPD3_WAVES; ++q)
-            {
-                a += red2[0][q];
-                m2 += red2[1][q];
-            }
-            fit_out[0] = a;
-            fit_out[1] = m2;
-        }
+        for (int o = WAVE / 2; o >= 1; o >>= 1) md += __shfl_xor(md, o);
+        if (l == 0) red2[w] = md;
     }
-    for (int x = tid; x < nz; x += UPD3_T) Z[x] = 0.0;
+    __syncthreads();   // FtF in f_s; the fit's sums
+    if (st < 0)
+    {
+        // wave 0: the next mode's pinv (one-wave sweep)
+        const int okp = sweep_wave<16 * NT>(&f_s[0][0], 33, R, Anext, colb);
+        if (l == 0) decl_s = !okp;
+    }
+    else
+    {
+        if (fit_out && w == 1)
+        {
+            double ip = (l < R) ? lamn_s[l] * fs_s[l] : 0.0;
+#pragma unroll
+            for (int o = WAVE / 2; o >= 1; o >>= 1) ip += __shfl_xor(ip, o);
+            if (l == 0)
+            {
+                double m2 = 0.0;
+#pragma unroll
+                for (int q = 0; q < UPD3_WAVES; ++q) m2 += red2[q];
+                fit_out[0] = ip;
+                fit_out[1] = m2;
+            }
+        }
+        // the factor scaled in place, SB rows of the thread's column at a time
+        if (r0 < rpp)
+        {
+            const double n = n_s[c0];
+            const bool zero = n < 1e-14;
+#pragma unroll
+            for (int k = 0; k < SB; ++k)
+            {
+                const int i = r0 + k * rpp;
+                if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
+            }
+            for (int i0 = r0 + SB * rpp; i0 < rows; i0 += SB * rpp)
+            {
+#pragma unroll
+                for (int k = 0; k < SB; ++k)
+                    fv[k] = F[size_t(min(i0 + k * rpp, rows - 1)) * R + c0];
+#pragma unroll
+                for (int k = 0; k < SB; ++k)
+                {
+                    const int i = i0 + k * rpp;
+                    if (i < rows) F[size_t(i) * R + c0] = zero ? 0.0 : fv[k] / n;
+                }
+            }
+        }
+        for (int x = st; x < nz; x += nsc) Z[x] = 0.0;
+    }
+    if (Anext)   // uniform (a kernel argument)
+    {
+        __syncthreads();
+        // a declined sweep: the Jacobi pseudoinverse of FtF by the whole
+        // workgroup (A in the Gram tiles' LDS, V in global scratch)
+        if (decl_s) jacobi_pinv_body<UPD3_T>(FtF, R, nullptr, Vw, Anext, 1, &gl[0][0][0]);
+    }
     if (tid == 0) upd3_count = 0u;
 }
 
@@ -1595,14 +1697,16 @@ __global__ __launch_bounds__(UPD1_T) void update3_one_kernel(
     const double* Y, const double* __restrict__ Ainv, double* __restrict__ F, int rows, int R,
     double* __restrict__ G, double* __restrict__ norms, double* __restrict__ lambda,
     const double* __restrict__ other, double* __restrict__ FtF, double* Z, int nz,
-    const double* __restrict__ grams, double* __restrict__ fit_out)
+    const double* __restrict__ grams, double* __restrict__ fit_out, double* __restrict__ Anext,
+    double* __restrict__ Vw)
 {
     constexpr int NP = NT * (NT + 1) / 2;
     constexpr int KS = 4 * NT;
     __shared__ double gl[UPD1_WAVES][NP][256];
-    __shared__ double g_s[32][33];
-    __shared__ double n_s[32], lamn_s[32], fit_s[UPD1_WAVES][32];
-    __shared__ double red2[2][UPD1_WAVES];
+    __shared__ double g_s[32][33], f_s[32][33];
+    __shared__ double n_s[32], lamn_s[32], fit_s[UPD1_WAVES][32], colb[32];
+    __shared__ double red2[UPD1_WAVES];
+    __shared__ int decl_s;
     const int tid = threadIdx.x, w = tid / WAVE, l = tid % WAVE;
     const int lr = l % 16, lk = l / 16;
     const int RR = R * R;
@@ -1733,7 +1837,12 @@ __global__ __launch_bounds__(UPD1_T) void update3_one_kernel(
             const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : g_s[i][j] / (ni * nj);
             g_s[i][j] = v;   // each entry read and written by its own thread only
             G[x] = v;
-            if (other) FtF[x] = v * ot[q];
+            if (other)
+            {
+                const double h = v * ot[q];
+                FtF[x] = h;
+                f_s[i][j] = h;
+            }
         }
     }
     double nr[NT], sp[NT];
@@ -1762,21 +1871,14 @@ __global__ __launch_bounds__(UPD1_T) void update3_one_kernel(
     }
     if (fit_out)   // uniform (a kernel argument)
     {
+        // <F, FtV> per rank (the four lanes of a column, then per wave) and
+        // this thread's share of model^2, per wave
 #pragma unroll
         for (int t = 0; t < NT; ++t)
         {
             sp[t] += __shfl_xor(sp[t], 16);
             sp[t] += __shfl_xor(sp[t], 32);
             if (lk == 0) fit_s[w][16 * t + lr] = sp[t];
-        }
-        __syncthreads();
-        double ip = 0.0;
-        if (tid < R)
-        {
-            double s = 0.0;
-#pragma unroll
-            for (int q = 0; q < UPD1_WAVES; ++q) s += fit_s[q][tid];
-            ip = lamn_s[tid] * s;
         }
         double md = 0.0;
 #pragma unroll
@@ -1790,32 +1892,55 @@ __global__ __launch_bounds__(UPD1_T) void update3_one_kernel(
             }
         }
 #pragma unroll
-        for (int o = WAVE / 2; o >= 1; o >>= 1)
+        for (int o = WAVE / 2; o >= 1; o >>= 1) md += __shfl_xor(md, o);
+        if (l == 0) red2[w] = md;
+    }
+    __syncthreads();   // FtF in f_s, the fit partials; every wave's FtV loads are consumed
+    // wave 0: the next mode's pinv (one-wave sweep); wave 1: the fit
+    // scalars; waves 2.. : FtV cleared for the next MTTKRP
+    if (w == 0)
+    {
+        if (Anext)
         {
-            ip += __shfl_xor(ip, o);
-            md += __shfl_xor(md, o);
-        }
-        if (l == 0)
-        {
-            red2[0][w] = ip;
-            red2[1][w] = md;
-        }
-        __syncthreads();
-        if (tid == 0)
-        {
-            double a = 0.0, m2 = 0.0;
-#pragma unroll
-            for (int q = 0; q < UPD1_WAVES; ++q)
-            {
-                a += red2[0][q];
-                m2 += red2[1][q];
-            }
-            fit_out[0] = a;
-            fit_out[1] = m2;
+            const int okp = sweep_wave<16 * NT>(&f_s[0][0], 33, R, Anext, colb);
+            if (l == 0) decl_s = !okp;
         }
     }
-    __syncthreads();   // every wave's FtV loads are consumed
-    for (int x = tid; x < nz; x += UPD1_T) Z[x] = 0.0;
+    else if (w == 1)
+    {
+        if (fit_out)
+        {
+            double ip = 0.0;
+            if (l < R)
+            {
+                double sr = 0.0;
+#pragma unroll
+                for (int q = 0; q < UPD1_WAVES; ++q) sr += fit_s[q][l];
+                ip = lamn_s[l] * sr;
+            }
+#pragma unroll
+            for (int o = WAVE / 2; o >= 1; o >>= 1) ip += __shfl_xor(ip, o);
+            if (l == 0)
+            {
+                double m2 = 0.0;
+#pragma unroll
+                for (int q = 0; q < UPD1_WAVES; ++q) m2 += red2[q];
+                fit_out[0] = ip;
+                fit_out[1] = m2;
+            }
+        }
+    }
+    else
+    {
+        for (int x = tid - 2 * WAVE; x < nz; x += UPD1_T - 2 * WAVE) Z[x] = 0.0;
+    }
+    if (Anext)   // uniform (a kernel argument)
+    {
+        __syncthreads();
+        // a declined sweep: the Jacobi pseudoinverse of FtF by the whole
+        // workgroup (A in the Gram tiles' LDS, V in global scratch)
+        if (decl_s) jacobi_pinv_body<UPD1_T>(FtF, R, nullptr, Vw, Anext, 1, &gl[0][0][0]);
+    }
 }
 
 int partials_for(size_t rows, size_t min_rows)
@@ -1927,9 +2052,9 @@ int gram_normalize_absorb_next_tail(double* d_F, size_t rows, int R, double* d_G
     return scale_launch(d_F, rows, R, d_norms, t, s);
 }
 
-int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
-                  double* d_G, double* d_norms, double* d_lambda, const double* d_other,
-                  double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
+int update3_small(double* d_FtV, double* d_Ainv, double* d_F, size_t rows, int R, double* d_G,
+                  double* d_norms, double* d_lambda, const double* d_other, double* d_FtF,
+                  size_t nzero, const double* d_grams, double* d_fit, int next_pinv,
                   hipStream_t s)
 {
     CPTC_REQUIRE(R >= 1 && R <= 32 && rows >= 1 && rows <= UPDATE3_SMALL_MAX_ROWS,
@@ -1937,15 +2062,25 @@ int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows,
                  R, UPDATE3_SMALL_MAX_ROWS);
     CPTC_REQUIRE(d_FtV && d_Ainv && d_F && d_G && d_norms && d_lambda &&
                      (d_other == nullptr) == (d_FtF == nullptr) && (!d_fit || d_grams) &&
-                     nzero < (size_t(1) << 31),
+                     (!next_pinv || d_FtF) && nzero < (size_t(1) << 31),
                  CPTC_ERR_ARG, "cptc_update_small3: bad arguments");
     static_assert(UPDATE3_SMALL_MAX_ROWS == size_t(UPD3_MAX_ROWS), "row limit");
     const int nb = int((rows + 15) / 16);
     const int P = (nb + UPD3_WAVES - 1) / UPD3_WAVES;   // one 16-row block per wave
+    const size_t RR = size_t(R) * R;
     void* buf = nullptr;
     CPTC_TRY(cptc::scratch_get(cptc::SCR_GRAM, size_t(UPD3_MAX_P) * 32 * (32 + 1) * sizeof(double),
                                &buf));
     double* part = static_cast<double*>(buf);
+    // the Jacobi fallback's V (pinv_launch's scratch layout: [work][V][flag])
+    double* Vw = nullptr;
+    double* Anext = next_pinv ? d_Ainv : nullptr;
+    if (next_pinv)
+    {
+        void* pb = nullptr;
+        CPTC_TRY(cptc::scratch_get(cptc::SCR_PINV, (2 * RR + 2) * sizeof(double), &pb));
+        Vw = static_cast<double*>(pb) + RR;
+    }
     const int nr = int(rows), nz = int(nzero);
     // one workgroup up to 256 rows, the multi-workgroup form above that
     // (CPTC_UPD3_ONE_ROWS overrides the limit, at most 512; 0 = never).
@@ -1960,7 +2095,8 @@ int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows,
         const bool two = nr <= 16 * UPD1_WAVES * 2;
         auto go = [&](auto kern) {
             hipLaunchKernelGGL(kern, dim3(1), dim3(UPD1_T), 0, s, d_FtV, d_Ainv, d_F, nr, R, d_G,
-                               d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams, d_fit);
+                               d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams, d_fit, Anext,
+                               Vw);
         };
         if (R <= 16) two ? go(update3_one_kernel<1, 2>) : go(update3_one_kernel<1, 4>);
         else two ? go(update3_one_kernel<2, 2>) : go(update3_one_kernel<2, 4>);
@@ -1970,24 +2106,25 @@ int update3_small(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows,
     if (R <= 16)
         hipLaunchKernelGGL(update3_small_kernel<1>, dim3(P), dim3(UPD3_T), 0, s, d_FtV, d_Ainv,
                            d_F, nr, R, d_G, d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams,
-                           d_fit, part);
+                           d_fit, part, Anext, Vw);
     else
         hipLaunchKernelGGL(update3_small_kernel<2>, dim3(P), dim3(UPD3_T), 0, s, d_FtV, d_Ainv,
                            d_F, nr, R, d_G, d_norms, d_lambda, d_other, d_FtF, d_FtV, nz, d_grams,
-                           d_fit, part);
+                           d_fit, part, Anext, Vw);
     CPTC_LAUNCHED();
     return CPTC_OK;
 }
 
 }  // namespace cptc
 
-extern "C" int cptc_update_small3(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows,
+extern "C" int cptc_update_small3(double* d_FtV, double* d_Ainv, double* d_F, size_t rows,
                                   int R, double* d_G, double* d_norms, double* d_lambda,
                                   const double* d_other, double* d_FtF, size_t nzero,
-                                  const double* d_grams, double* d_fit, void* stream)
+                                  const double* d_grams, double* d_fit, int next_pinv,
+                                  void* stream)
 {
     return cptc::update3_small(d_FtV, d_Ainv, d_F, rows, R, d_G, d_norms, d_lambda, d_other,
-                               d_FtF, nzero, d_grams, d_fit, cptc::as_stream(stream));
+                               d_FtF, nzero, d_grams, d_fit, next_pinv, cptc::as_stream(stream));
 }
 
 extern "C" int cptc_gram_normalize_absorb(double* d_F, size_t rows, int R, double* d_G,

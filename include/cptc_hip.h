@@ -271,15 +271,18 @@ int cptc_gram_normalize_absorb_next(double* d_F, size_t rows, int R, double* d_G
  * d_FtV[0, nzero) = 0 (the next MTTKRP's output; d_FtV is read before).
  * With d_fit (and d_grams = G_0, G_1 of an order-3 model, this call's G
  * being G_2), also the Gram fit scalars of cptc_fit_gram over the new
- * factor and d_FtV: d_fit[0] = iprod, d_fit[1] = model^2.  Results equal
- * the separate calls' up to summation order (als.cu:480-517, 659-715).
- * Uses the library's Gram scratch and a device counter: calls that overlap
- * on one GPU race.  No reference counterpart: the reference runs these as
- * separate kernels. */
-int cptc_update_small3(double* d_FtV, const double* d_Ainv, double* d_F, size_t rows, int R,
+ * factor and d_FtV: d_fit[0] = iprod, d_fit[1] = model^2.  With next_pinv
+ * (which needs d_other / d_FtF), d_Ainv is then overwritten with
+ * cptc_pinv_sym of the new d_FtF (the same bits when the fast path accepts
+ * it; the Jacobi pseudoinverse otherwise).  Results equal the separate
+ * calls' up to summation order (als.cu:480-517, 659-715; solver.cu:900-1002).
+ * Uses the library's Gram and pinv scratch and a device counter: calls that
+ * overlap on one GPU race.  No reference counterpart: the reference runs
+ * these as separate kernels. */
+int cptc_update_small3(double* d_FtV, double* d_Ainv, double* d_F, size_t rows, int R,
                        double* d_G, double* d_norms, double* d_lambda, const double* d_other,
                        double* d_FtF, size_t nzero, const double* d_grams, double* d_fit,
-                       void* stream);
+                       int next_pinv, void* stream);
 
 /* C = A o B elementwise over n doubles (C may alias A or B).
  * Replaces elementwise_mult_kernel (als.cu:101-106) and g_mul_kernel

@@ -673,15 +673,20 @@ def test_update_small3_matches_steps(ca, dev, R, rows):
     the last workgroup to finish sums the partials and scales) against the
     separate calls it replaces: cptc_apply_pinv with lambda, then
     cptc_gram_normalize_absorb_next with the next FtF, then cptc_fit_gram on
-    the new factor with grams (G_0, G_1, this G).  Factor, norms, lambda, G
-    and FtF within 1e-13 (relative, 2-norm), the fit scalars within 1e-12:
-    the sums run in another order; a dropped block, column or rank term
-    shows at 1e-2 and more.  A zero column of Ainv gives a zero column of F
+    the new factor with grams (G_0, G_1, this G), then cptc_pinv_sym of the
+    next FtF.  Factor, norms, lambda, G and FtF within 1e-13 (relative,
+    2-norm), the fit scalars within 1e-12: the sums run in another order; a
+    dropped block, column or rank term shows at 1e-2 and more.  The next
+    pinv: `other` SPD makes FtF SPD (Schur product), the one-wave sweep
+    accepts it and its inverse equals cptc_pinv_sym of the launch's own FtF
+    bit for bit; with a zero row and column in `other` the sweep meets a zero
+    pivot and the launch's Jacobi pseudoinverse is within 1e-10 of
+    cptc_pinv_sym's.  A zero column of Ainv gives a zero column of F
     (norm < 1e-14): F, lambda and the Gram's row and column are exactly 0.
     FtV[0, nzero) is cleared after its reads and the rest is untouched; a
-    second call without the fit and the next FtF leaves fit and FtF alone.
-    Sizes past 4096 rows or R = 33 are refused.  Two calls in a row check
-    that the workgroup counter is left at zero."""
+    call without fit, next FtF or clearing leaves those alone.  Sizes past
+    4096 rows or R = 33 are refused.  Calls in a row check that the
+    workgroup counter is left at zero."""
     rng = np.random.default_rng(R * 1000 + rows)
     Y = rng.standard_normal((rows, R))
     A = rng.standard_normal((R, R))
@@ -690,7 +695,8 @@ def test_update_small3_matches_steps(ca, dev, R, rows):
     if zc is not None:
         A[:, zc] = 0.0
     lam = rng.random(R) + 0.1
-    other = rng.standard_normal((R, R))
+    B = rng.standard_normal((R, R))
+    other = B @ B.T / R + np.eye(R)
     g01 = rng.random((2, R, R))
     dY, dA, do = to_dev(ca, Y), to_dev(ca, A), to_dev(ca, other)
     # the separate calls
@@ -705,17 +711,18 @@ def test_update_small3_matches_steps(ca, dev, R, rows):
     g3 = to_dev(ca, np.concatenate([g01.ravel(), G1.numpy().ravel()]))
     assert ca.lib.cptc_fit_gram(a_F.data_ptr(), dY.data_ptr(), rows, a_l.data_ptr(),
                                 g3.data_ptr(), 3, R, out1.data_ptr(), stream(ca)) == 0
-    # one launch; FtV in a longer buffer, cleared over nzero entries
+    # one launch; FtV in a longer buffer, cleared over nzero entries; the
+    # next pinv overwrites Ainv
     extra = 40
     Yb = np.concatenate([Y.ravel(), np.full(extra, 7.0)])
     nzero = rows * R + extra // 2
-    dYb = to_dev(ca, Yb)
+    dYb, dA2 = to_dev(ca, Yb), to_dev(ca, A)
     b_F, b_l = zeros(ca, (rows, R)), to_dev(ca, lam)
     n2, G2, H2, out2 = zeros(ca, (R,)), zeros(ca, (R, R)), zeros(ca, (R, R)), zeros(ca, (2,))
     g01d = to_dev(ca, g01)
-    rc = ca.lib.cptc_update_small3(dYb.data_ptr(), dA.data_ptr(), b_F.data_ptr(), rows, R,
+    rc = ca.lib.cptc_update_small3(dYb.data_ptr(), dA2.data_ptr(), b_F.data_ptr(), rows, R,
                                    G2.data_ptr(), n2.data_ptr(), b_l.data_ptr(), do.data_ptr(),
-                                   H2.data_ptr(), nzero, g01d.data_ptr(), out2.data_ptr(),
+                                   H2.data_ptr(), nzero, g01d.data_ptr(), out2.data_ptr(), 1,
                                    stream(ca))
     assert rc == 0, ca.lib.cptc_last_error()
     ca.sync()
@@ -729,20 +736,46 @@ def test_update_small3_matches_steps(ca, dev, R, rows):
     assert np.array_equal(G2.numpy(), G2.numpy().T)
     yb = dYb.numpy()
     assert np.all(yb[:nzero] == 0.0) and np.all(yb[nzero:] == 7.0)
-    # without fit, next FtF or clearing: those outputs are left alone
+    P1 = zeros(ca, (R, R))
+    assert ca.lib.cptc_pinv_sym(H2.data_ptr(), P1.data_ptr(), R, None, stream(ca)) == 0
+    ca.sync()
+    if zc is None:
+        assert np.array_equal(dA2.numpy(), P1.numpy())
+    else:
+        # the zero column of the Gram makes FtF singular: both take Jacobi
+        assert rel_err(dA2.numpy(), P1.numpy()) <= 1e-10
+    # a zero row and column in `other`: a zero pivot, the launch's Jacobi
+    if R > 3:
+        o0 = other.copy()
+        o0[1, :] = 0.0
+        o0[:, 1] = 0.0
+        do0, dA3, H3 = to_dev(ca, o0), to_dev(ca, A), zeros(ca, (R, R))
+        c_F, c_l, n3, G3 = zeros(ca, (rows, R)), to_dev(ca, lam), zeros(ca, (R,)), zeros(ca, (R, R))
+        assert ca.lib.cptc_update_small3(dY.data_ptr(), dA3.data_ptr(), c_F.data_ptr(), rows, R,
+                                         G3.data_ptr(), n3.data_ptr(), c_l.data_ptr(),
+                                         do0.data_ptr(), H3.data_ptr(), 0, None, None, 1,
+                                         stream(ca)) == 0
+        P3 = zeros(ca, (R, R))
+        assert ca.lib.cptc_pinv_sym(H3.data_ptr(), P3.data_ptr(), R, None, stream(ca)) == 0
+        ca.sync()
+        assert rel_err(dA3.numpy(), P3.numpy()) <= 1e-10
+        assert np.all(dA3.numpy()[1] == 0.0) and np.all(dA3.numpy()[:, 1] == 0.0)
+        assert rel_err(c_F.numpy(), a_F.numpy()) <= 1e-13
+    # without fit, next FtF, pinv or clearing: those outputs are left alone
     dY2 = to_dev(ca, Y)
     c_l = to_dev(ca, lam)
     n3, G3 = zeros(ca, (R,)), zeros(ca, (R, R))
     assert ca.lib.cptc_update_small3(dY2.data_ptr(), dA.data_ptr(), b_F.data_ptr(), rows, R,
                                      G3.data_ptr(), n3.data_ptr(), c_l.data_ptr(), None, None, 0,
-                                     None, None, stream(ca)) == 0
+                                     None, None, 0, stream(ca)) == 0
     ca.sync()
     assert rel_err(b_F.numpy(), a_F.numpy()) <= 1e-13
     assert np.array_equal(G3.numpy(), G2.numpy()) and np.array_equal(dY2.numpy(), Y)
-    for bad_rows, bad_R in ((4097, R), (rows, 33), (0, R)):
+    assert np.array_equal(dA.numpy(), A)
+    for bad_rows, bad_R, npv in ((4097, R, 0), (rows, 33, 0), (0, R, 0), (rows, R, 1)):
         assert ca.lib.cptc_update_small3(dY2.data_ptr(), dA.data_ptr(), b_F.data_ptr(), bad_rows,
                                          bad_R, G3.data_ptr(), n3.data_ptr(), c_l.data_ptr(),
-                                         None, None, 0, None, None, stream(ca)) != 0
+                                         None, None, 0, None, None, npv, stream(ca)) != 0
 
 
 @pytest.mark.parametrize("R", [1, 7, 32, 100])
