@@ -86,9 +86,11 @@ void radix_sort_pairs_u64(std::vector<uint64_t>& keys, std::vector<V>& vals, int
 // config 5 (32768 units) slows at anything below 16 (atomic contention on
 // 64-row targets).  CPTC_TILE_GROUP=<n> fixes it (tuning).
 // Smallest tile (unit) x 32-rank-block count for which the drivers take the
-// split-bf16 tile kernel (config 5's 32 768 units at R = 32 gain, config 1's
-// 4096 tiles at R = 32 lose to its extra operand-image launch).
-constexpr size_t TILE_B3_MIN_ITEMS = 16384;
+// split-bf16 tile kernel: config 5's 32 768 units at R = 32 gain, and since
+// the order-3 update runs in one launch, config 1's 4096 tiles at R = 32 do
+// too (0.167-0.169 -> 0.163 ms per iteration; before it, its extra
+// operand-image launch cost more than the kernel saved).
+constexpr size_t TILE_B3_MIN_ITEMS = 4096;
 
 // Tile kernel choice from a switch (ALS_TILE_KERNEL / GEN_TILE_KERNEL):
 // "fp32" -> 0, "bf16x3" -> 1, unset or anything else -> -1 (automatic).
