@@ -68,6 +68,14 @@ def test_version_and_no_device_here(ca):
                                         1, 10, 1, 1, 1, None, 1, (C.c_void_p * 3)(16, 16, 16), 1,
                                         8, None),
     lambda l: l.cptc_pack_level_keys(2, 1, 10, (C.c_int * 2)(33, 1), 1, 8, None),
+    # one-launch update: rows past 4096, R past 32, no rows, the next pinv
+    # without the next FtF, a fit without the Grams, null pointers
+    lambda l: l.cptc_update_small3(8, 8, 8, 4097, 8, 8, 8, 8, None, None, 0, None, None, 0, None),
+    lambda l: l.cptc_update_small3(8, 8, 8, 100, 33, 8, 8, 8, None, None, 0, None, None, 0, None),
+    lambda l: l.cptc_update_small3(8, 8, 8, 0, 8, 8, 8, 8, None, None, 0, None, None, 0, None),
+    lambda l: l.cptc_update_small3(8, 8, 8, 100, 8, 8, 8, 8, None, None, 0, None, None, 1, None),
+    lambda l: l.cptc_update_small3(8, 8, 8, 100, 8, 8, 8, 8, None, None, 0, None, 8, 0, None),
+    lambda l: l.cptc_update_small3(0, 8, 8, 100, 8, 8, 8, 8, None, None, 0, None, None, 0, None),
 ])
 def test_bad_arguments_rejected(ca, call):
     assert call(ca.lib) == -1
