@@ -157,6 +157,19 @@ __global__ __launch_bounds__(256) void compact_split_fill_kernel(const float* __
     }
 }
 
+// A factor entry, or 0 past the factor's rows or ranks: the load is made
+// from a clamped address on every path and zeroed by an AND with a mask an
+// empty asm has made opaque (a `cond ? load : 0` lets the compiler put each
+// load under a branch with a memory wait of its own).
+__device__ __forceinline__ float operand_entry(const double* __restrict__ F, int row, int dim,
+                                               int r, int R)
+{
+    const double v = F[size_t(max(0, min(row, dim - 1))) * R + min(r, R - 1)];
+    long long m = (row < dim && r < R) ? -1LL : 0LL;
+    asm volatile("" : "+v"(m));
+    return float(__longlong_as_double(__double_as_longlong(v) & m));
+}
+
 // Operand images of the split-bf16 kernel for one target slot: the
 // contracted factor Fc split into bf16 hi / lo, 8 rows of one rank per 16
 // bytes ([row / 8][Rq]), and the weight factor in FP32, 16 rows of one rank
@@ -174,8 +187,7 @@ __global__ __launch_bounds__(256) void tile_operands_kernel(
 #pragma unroll
         for (int q = 0; q < 8; ++q)
         {
-            const int row = 8 * b + q;
-            x[q] = (row < cdim && r < R) ? float(Fc[size_t(row) * R + r]) : 0.0f;
+            x[q] = operand_entry(Fc, 8 * b + q, cdim, r, R);
         }
         cptc_k::u32x4 hv, lv;
 #pragma unroll
@@ -197,8 +209,7 @@ __global__ __launch_bounds__(256) void tile_operands_kernel(
 #pragma unroll
         for (int u = 0; u < 16; ++u)
         {
-            const int row = 16 * b + u;
-            x[u] = (row < wdim && r < R) ? float(Fw[size_t(row) * R + r]) : 0.0f;
+            x[u] = operand_entry(Fw, 16 * b + u, wdim, r, R);
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s)

@@ -402,6 +402,74 @@ def test_dense_tiles_bf16x3_split_error(ca, orc, dev):
     assert rc != 0 and b"workspace" in ca.lib.cptc_last_error()
 
 
+def _bf16_rne(x):
+    """float32 -> bf16 bits, round to nearest even (finite values)."""
+    b = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint32)
+
+
+def _operand_images(F, dim, R, Rq):
+    """The split-bf16 kernel's operand images of a factor, restated: as the
+    contracted factor, 8-row blocks of one rank, each 16-byte entry the bf16
+    hi halves of its 8 float32 values (pairs packed low | high << 16), and
+    the same for the lo halves bf16(x - hi); as the weight factor, 16-row
+    blocks of one rank in float32.  Rows past the factor and ranks >= R are 0."""
+    x = np.zeros((((dim + 15) // 16) * 16, Rq), np.float32)
+    x[:dim, :R] = F.astype(np.float32)
+    hi = _bf16_rne(x)
+    lo = _bf16_rne(x - (hi << 16).view(np.float32))
+    def pack(h):   # [row / 8][Rq] entries of 4 words: rows 8b + 2s (low), 8b + 2s + 1 (high)
+        h = h.reshape(-1, 8, Rq).transpose(0, 2, 1).reshape(-1, 4, 2)
+        return (h[..., 0] | (h[..., 1] << 16)).ravel()
+    fw = x.reshape(-1, 16, Rq).transpose(0, 2, 1).ravel()
+    return pack(hi), pack(lo), fw
+
+
+def test_dense_tiles_operand_images(ca, orc, dev):
+    """The operand images the split-bf16 kernel builds per launch (left in
+    its workspace) equal a numpy restatement bit for bit: the contracted
+    factor's bf16 hi / lo split (round to nearest even) and the weight
+    factor in float32, padded rows and ranks zero (R = 40 pads to 64, dims
+    not multiples of 16).  One of the two other factors of the mode must be
+    the contracted one and the other the weight."""
+    rng = np.random.default_rng(5)
+    dims = (40, 37, 50)
+    idx, val = block_tensor(rng, dims)
+    p = orc.partition3(idx[0], idx[1], idx[2], val, dims, 0.03)
+    nt = len(p["tiles"])
+    R, Rq = 40, 64
+    F = [rng.standard_normal((d, R)) for d in dims]
+    dF = [to_dev(ca, f) for f in F]
+    tiles = to_dev(ca, p["tiles"].astype(np.int32))
+    tf = zeros(ca, (nt * 4096,), np.float32)
+    pools = [to_dev(ca, p[k]) for k in ("pool_lid", "pool_val", "pool_off")]   # kept alive
+    assert ca.lib.cptc_dense_tiles_pack3(*(b.data_ptr() for b in pools), nt, tf.data_ptr(),
+                                         stream(ca)) == 0
+    nb = ca.lib.cptc_tile_operands_bytes(max(dims), R)
+    imgs = [_operand_images(F[m], dims[m], R, Rq) for m in range(3)]
+    for mode in range(3):
+        ws = zeros(ca, (nb,), np.uint8)
+        out = zeros(ca, (dims[mode], R))
+        assert ca.lib.cptc_mttkrp_dense_tiles3_ws(mode, tiles.data_ptr(), tf.data_ptr(), nt, None,
+                                                  None, 0, dF[0].data_ptr(), dF[1].data_ptr(),
+                                                  dF[2].data_ptr(), out.data_ptr(), R, *dims,
+                                                  ws.data_ptr(), nb, stream(ca)) == 0
+        ca.sync()
+        w = ws.numpy()
+        o = [m for m in range(3) if m != mode]
+        ok = False
+        for c, wt in ((o[0], o[1]), (o[1], o[0])):
+            hi, lo, fw = imgs[c]
+            n = hi.size * 4
+            got_hi = w[:n].view(np.uint32)
+            got_lo = w[n:2 * n].view(np.uint32)
+            got_fw = w[2 * n:2 * n + imgs[wt][2].size * 4].view(np.float32)
+            if (np.array_equal(got_hi, hi) and np.array_equal(got_lo, lo)
+                    and np.array_equal(got_fw.view(np.uint32), imgs[wt][2].view(np.uint32))):
+                ok = True
+        assert ok, mode
+
+
 def test_dense_tile_pack_last_write_wins(ca, orc, dev):
     rng = np.random.default_rng(1)
     cells = np.array(np.meshgrid(*[np.arange(16)] * 3, indexing="ij")).reshape(3, -1)
