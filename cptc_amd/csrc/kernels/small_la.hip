@@ -1134,18 +1134,44 @@ __global__ __launch_bounds__(FIT_T) void gram_norms_absorb_kernel(double* __rest
     const int c = int(threadIdx.x) % R, r0 = int(threadIdx.x) / R;
     if (r0 >= rpp) return;
     const double nj = nl[c];
+    // entry i of column c: G /= n_i n_j (0 when either norm is below
+    // 1e-14), the division by 1 of a masked 0 standing for the select, so
+    // that neither the load nor the division sits under a branch
+    auto scaled = [&](int i, double g) {
+        const double ni = nl[i];
+        const bool keep = !(ni < 1e-14 || nj < 1e-14);
+        long long m = keep ? -1LL : 0LL;
+        asm volatile("" : "+v"(m));
+        return __longlong_as_double(__double_as_longlong(g) & m) / (keep ? ni * nj : 1.0);
+    };
     auto one = [&](int i) {
         const size_t x = size_t(i) * R + c;
-        const double ni = nl[i];
-        const double v = (ni < 1e-14 || nj < 1e-14) ? 0.0 : G[x] / (ni * nj);
+        const double v = scaled(i, G[x]);
         G[x] = v;
         if (other) FtF[x] = v * other[x];
     };
-    // four rows per round (their loads issued together)
+    // four rows per round, their loads issued before any store (G is
+    // updated in place, so a load after a store would wait for it)
     int i = r0;
     for (; i + 3 * rpp < R; i += 4 * rpp)
+    {
+        double g4[4], o4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) one(i + q * rpp);
+        for (int q = 0; q < 4; ++q)
+        {
+            const size_t x = size_t(i + q * rpp) * R + c;
+            g4[q] = G[x];
+            o4[q] = other ? other[x] : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+        {
+            const size_t x = size_t(i + q * rpp) * R + c;
+            const double v = scaled(i + q * rpp, g4[q]);
+            G[x] = v;
+            if (other) FtF[x] = v * o4[q];
+        }
+    }
     for (; i < R; i += rpp) one(i);
 }
 
